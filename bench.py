@@ -1,0 +1,249 @@
+#!/usr/bin/env python3
+"""Benchmark of the fused quantized MoE layer on one MI355X.
+
+Metric: MoE-layer decode tokens/s + achieved HBM GB/s (% of
+8 TB/s).  A step is one full layer forward (router GEMV -> top-k -> grouped
+w13 + SiLU-gate -> w2 + weighted combine, + the shared expert) over one batch
+of synthetic tokens already resident in HBM.  To keep the weights streaming
+from HBM rather than the 256 MB last-level cache, ``--layers`` independent
+random-init layers (4 x 805 MB for C3) are cycled, one per step, each with a
+fresh activation batch -- the pattern a real decode step has across layers.
+
+Prints ONE JSON line.  ``roofline`` covers the dominant kernel (the w13 stage),
+timed with HIP events on the launch stream; ``cpu_baseline`` times the
+reference's own CPU MoE kernel (python/freetoken/kernel/csrc/cpu_moe/cpu_moe.cpp,
+built unmodified into oracle/_ref) on the same routing.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "freetoken-intel_amd"))
+
+METRIC = "MoE-layer decode tokens/s + achieved HBM GB/s (% of 8 TB/s), bs 1-64"
+HBM_PEAK_GBS = 8000.0
+
+
+def _parse():
+    ap = argparse.ArgumentParser(description=__doc__)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--config", default="c3_fp8")
+    ap.add_argument("--batch", type=int, default=16)
+    ap.add_argument("--layers", type=int, default=4)
+    ap.add_argument("--sweep", default="1,4,16,64", help="extra decode batch sizes to report ('' = none)")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    return ap.parse_args()
+
+
+def _w13_bytes_per_expert(syn) -> int:
+    return sum(t[0].numel() * t.element_size() for k, t in syn.bank.items() if k.endswith("gate_up")) + (
+        syn.bias13[0].numel() * 2 if syn.bias13 is not None else 0)
+
+
+def main() -> int:
+    args = _parse()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one MI355X only: this build has no multi-GPU path "
+              "(expert-parallel sharding is a design note), so --gpus must be 1.", file=sys.stderr)
+        return 2
+
+    import numpy as np
+    import torch
+
+    from ftmoe import _native as nat
+    from ftmoe import synthetic as S
+
+    dev = torch.device("cuda:0")
+    cfg = S.CONFIGS[args.config]
+    T = args.batch
+    NL = max(1, args.layers)
+    NX = 7
+    layers, syns = [], []
+    for s in range(NL):
+        syn = S.generate(cfg, T=T, seed=s, device=dev)
+        syns.append(syn)
+        layers.append(S.build_layer(syn))
+    torch.cuda.synchronize()
+    gx = torch.Generator(device=dev).manual_seed(1234)
+    max_t = max([T] + [int(b) for b in args.sweep.split(",") if b])
+    x_pool = [torch.randn(max_t, cfg.H, generator=gx, device=dev).to(torch.bfloat16) for _ in range(NX)]
+
+    def run_point(Tb: int, steps: int, warmup: int):
+        xs = [x[:Tb].contiguous() for x in x_pool]
+        for i in range(warmup):
+            layers[i % NL].forward(xs[i % NX])
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        w0 = time.perf_counter()
+        e0.record()
+        for i in range(steps):
+            j = warmup + i
+            layers[j % NL].forward(xs[j % NX])
+        e1.record()
+        torch.cuda.synchronize()
+        wall_ms = (time.perf_counter() - w0) * 1e3 / steps
+        ms = e0.elapsed_time(e1) / steps
+        # routing of the same (layer, batch) pairs, untimed: realised unique experts
+        uniq = []
+        for i in range(steps):
+            j = warmup + i
+            _, ids, _, _ = layers[j % NL].forward(xs[j % NX], return_routing=True)
+            uniq.append(int(torch.unique(ids).numel()))
+        b_alg = float(np.mean([S.algorithmic_bytes(cfg, u, Tb) for u in uniq]))
+        return ms, wall_ms, float(np.mean(uniq)), b_alg, xs
+
+    ms, wall_ms, U, b_alg, xs = run_point(T, args.steps, args.warmup)
+    gbs = b_alg / (ms * 1e-3) / 1e9
+
+    # ---- dominant kernel (w13 stage) timed with events on the launch stream
+    out = torch.empty(T, cfg.H, dtype=torch.bfloat16, device=dev)
+    nsteps = min(args.steps, 60)
+    evs = []
+    for i in range(nsteps + 5):
+        L, x = layers[i % NL], xs[i % NX]
+        L.forward_stage(x, out, nat.STAGE_ROUTER)
+        L.forward_stage(x, out, nat.STAGE_TOPK)
+        a0, a1, b1 = (torch.cuda.Event(enable_timing=True) for _ in range(3))
+        a0.record()
+        L.forward_stage(x, out, nat.STAGE_W13)
+        a1.record()
+        L.forward_stage(x, out, nat.STAGE_W2)
+        b1.record()
+        if i >= 5:
+            evs.append((a0, a1, b1, i))
+    torch.cuda.synchronize()
+    dur_a = [a0.elapsed_time(a1) for a0, a1, _, _ in evs]
+    dur_b = [a1.elapsed_time(b1) for _, a1, b1, _ in evs]
+    w13_unit = _w13_bytes_per_expert(syns[0])
+    sh_w13 = 2 * cfg.shared_inter * cfg.H * 2 if cfg.shared_inter else 0
+    bytes_a = []
+    for _, _, _, i in evs:
+        _, ids, _, _ = layers[i % NL].forward(xs[i % NX], return_routing=True)
+        u = int(torch.unique(ids).numel())
+        bytes_a.append(u * w13_unit + sh_w13 + T * cfg.H * 2)
+    ach = float(np.mean(bytes_a)) / (float(np.mean(dur_a)) * 1e-3) / 1e9
+    roofline = {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": None,
+                "kernel": f"k_stage_a<{cfg.fmt}> (w13 + SiLU-gate)",
+                "kernel_avg_us": round(float(np.mean(dur_a)) * 1e3, 2),
+                "bytes_per_launch": int(np.mean(bytes_a)),
+                "unit_bytes": w13_unit, "units_per_launch": round((np.mean(bytes_a) - sh_w13 - T * cfg.H * 2) / w13_unit, 2),
+                "w2_stage_avg_us": round(float(np.mean(dur_b)) * 1e3, 2)}
+
+    # ---- extra decode batch sizes (same layers)
+    sweep = []
+    for tb in [int(b) for b in args.sweep.split(",") if b]:
+        ms_b, _, U_b, balg_b, _ = run_point(tb, 50, 10)
+        g_b = balg_b / (ms_b * 1e-3) / 1e9
+        sweep.append({"T": tb, "tokens_per_s": round(tb / (ms_b * 1e-3), 1), "us_per_layer": round(ms_b * 1e3, 2),
+                      "unique_experts": round(U_b, 1), "GBps": round(g_b, 1), "hbm_frac": round(g_b / HBM_PEAK_GBS, 4)})
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        cpu = _cpu_baseline(cfg, syns[0], layers[0], xs[0], T, args.cpu_seconds)
+
+    line = {
+        "metric": METRIC,
+        "value": round(T / (ms * 1e-3), 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 5),
+        "wall_ms_per_step": round(wall_ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "weights": cfg.fmt,
+        "data": "synthetic (seeded random-init weights at the real layer shape, N(0,1) bf16 tokens)",
+        "config": {"workload": f"{cfg.name} decode T={T}: {cfg.fmt} H={cfg.H} I={cfg.I} E={cfg.E} top-{cfg.k}"
+                               + (f" + shared bf16 I={cfg.shared_inter}" if cfg.shared_inter else ""),
+                   "global_batch": T, "seq_len": 1, "parallelism": "none (1 GPU)", "layers_rotated": NL},
+        "GBps": round(gbs, 1),
+        "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
+        "unique_experts": round(U, 2),
+        "bytes_per_step": int(b_alg),
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+        "sweep": sweep,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+def _cpu_baseline(cfg, syn, layer, x, T, seconds):
+    """The reference's CPU MoE (cpu_moe.cpp freetoken_cpu_moe_forward_fast) on the
+    same layer: banks dequantized to fp32 once outside the timer (by the GPU dequant
+    kernel), routing taken from the GPU run, the shared expert as one more
+    always-routed expert weighted by its sigmoid gate."""
+    import numpy as np
+    import torch
+
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import ftm_oracle as O
+    from ftmoe.kernel._dequant import dequant
+
+    out, ids, w, _ = layer.forward(x, return_routing=True)
+    ids = ids.cpu().numpy()
+    w = w.cpu().numpy()
+    gu = torch.empty(cfg.E + 1, 2 * cfg.I, cfg.H, dtype=torch.float32)
+    dn = torch.empty(cfg.E + 1, cfg.H, cfg.I, dtype=torch.float32)
+    for e in range(cfg.E):
+        gu[e] = dequant(layer.w13, out_dtype=torch.float32, slot=e).cpu()
+        dn[e] = dequant(layer.w2, out_dtype=torch.float32, slot=e).cpu()
+    E_tot = cfg.E
+    if cfg.shared_inter:
+        assert cfg.shared_inter == cfg.I
+        gu[cfg.E] = syn.shared["w13"].float().cpu()
+        dn[cfg.E] = syn.shared["w2"].float().cpu()
+        sl = (x.float() @ syn.shared["gate"].float().T).cpu().numpy()[:, 0]
+        sw = O.round_bf16(1.0 / (1.0 + np.exp(-sl)).astype(np.float32))
+        ids = np.concatenate([ids, np.full((T, 1), cfg.E, np.int32)], axis=1)
+        w = np.concatenate([w, sw[:, None]], axis=1)
+        E_tot += 1
+    gu_np = gu[:E_tot].numpy()
+    dn_np = dn[:E_tot].numpy()
+    xf = x.float().cpu().numpy()
+    threads = min(16, os.cpu_count() or 1)
+    kind = "reference" if O.ref_cpu_moe_available() else "port"
+
+    def call():
+        if kind == "reference":
+            return O.ref_cpu_moe_forward_fast(xf, ids, w, gu_np, dn_np, threads=threads)
+        spec_w13 = O.OracleProj("fp32", gu_np, 2 * cfg.I, cfg.H)
+        spec_w2 = O.OracleProj("fp32", dn_np, cfg.H, cfg.I)
+        return O.moe_experts(spec_w13, spec_w2, xf, ids, w, E=E_tot, h_bf16=False)
+
+    call()
+    n, t0 = 0, time.perf_counter()
+    while True:
+        call()
+        n += 1
+        el = time.perf_counter() - t0
+        if el >= seconds:
+            break
+    model = ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            model = next((l.split(":", 1)[1].strip() for l in f if l.startswith("model name")), "")
+    except OSError:
+        pass
+    return {"value": round(T * n / el, 2), "unit": "tokens/s", "cores": threads if kind == "reference" else 1,
+            "kind": kind,
+            "sample": f"{n} calls x {T} tokens of {cfg.name} in {el:.1f} s on {model or 'host CPU'}: "
+                      "freetoken_cpu_moe_forward_fast (python/freetoken/kernel/csrc/cpu_moe/cpu_moe.cpp, built "
+                      "unmodified), fp32 banks dequantized once outside the timer, routing from the GPU run, "
+                      "shared expert as an always-routed expert; router GEMV not timed"}
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,73 @@
+// ftm_internal.h -- host-side layout of the layer workspace and the kernel
+// launchers shared by the C ABI (ftm_capi.cpp) and the kernel files.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include "ftmoe.h"
+
+namespace ftm {
+
+// ---- control region (first FTM_WS_CTRL_BYTES of a workspace, int32 words).
+// Zero between calls: every counter is reset by the workgroup that consumes it.
+constexpr int kCtrlArriveTopk = 0;  // arrivals of the top-k workgroups
+constexpr int kCtrlNRouted = 1;     // routed experts with >= 1 token (written per call)
+constexpr int kCtrlNU = 2;          // nRouted + shared expert
+constexpr int kCtrlError = 3;       // sticky error bits (bit 0: routed to a non-resident slot)
+constexpr int kCtrlExpertCnt = 16;  // [E] per-expert pair counters (E <= kMaxExperts)
+constexpr int kMaxExperts = 512;
+constexpr int kCtrlTileCnt = kCtrlExpertCnt + kMaxExperts;  // [H/64] combine arrivals
+constexpr int kMaxColTiles = FTM_WS_CTRL_BYTES / 4 - kCtrlTileCnt;
+
+struct WsLayout {
+  size_t misc, logits, wts, ids, lists, uniq, ucnt, hbuf, ybuf, total;
+  int T, E, KP, Imax;
+};
+
+inline size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+
+inline WsLayout ws_layout(const ftm_moe_layer& L, int T) {
+  WsLayout w;
+  w.T = T;
+  w.E = L.num_experts;
+  w.KP = L.topk + (L.shared_inter > 0 ? 1 : 0);
+  w.Imax = L.inter > L.shared_inter ? L.inter : L.shared_inter;
+  const size_t Tt = (size_t)(T > 0 ? T : 1);
+  const size_t act = L.act_dtype == FTM_DT_F32 ? 4 : 2;
+  size_t o = FTM_WS_CTRL_BYTES;
+  w.misc = o;   o = align_up(o + 256, 256);
+  w.logits = o; o = align_up(o + 4 * Tt * (w.E + 1), 256);
+  w.wts = o;    o = align_up(o + 4 * Tt * w.KP, 256);
+  w.ids = o;    o = align_up(o + 4 * Tt * L.topk, 256);
+  w.lists = o;  o = align_up(o + 4 * (size_t)w.E * Tt, 256);
+  w.uniq = o;   o = align_up(o + 4 * (size_t)(w.E + 1), 256);
+  w.ucnt = o;   o = align_up(o + 4 * (size_t)(w.E + 1), 256);
+  w.hbuf = o;   o = align_up(o + act * Tt * w.KP * w.Imax, 256);
+  w.ybuf = o;   o = align_up(o + 4 * Tt * w.KP * (size_t)L.hidden, 256);
+  w.total = o;
+  return w;
+}
+
+// ---- launchers (ftm_moe.hip); all return hipError_t of the launch
+hipError_t launch_router(const ftm_moe_layer& L, const void* x, int T, int row_begin, int row_end, char* ws,
+                         const WsLayout& wl, hipStream_t st);
+hipError_t launch_topk(const ftm_moe_layer& L, int T, const void* logits_in, int logits_dt,
+                       const int32_t* ids_in, const float* w_in, int32_t* ids_out, float* w_out,
+                       float* logits_out, char* ws, const WsLayout& wl, hipStream_t st);
+hipError_t launch_experts(const ftm_moe_layer& L, const void* x, int T, void* out, char* ws,
+                          const WsLayout& wl, hipStream_t st, int which = 3);
+hipError_t launch_linear(const ftm_proj& P, int slot, const void* x, int x_dt, int M, void* out,
+                         int out_dt, const void* bias, int bias_dt, int final_dt, hipStream_t st);
+hipError_t launch_fill_routing(int T, int32_t slot, int32_t* slot_word, int32_t* ids, float* w, hipStream_t st);
+hipError_t launch_ws_init(void* ws, hipStream_t st);
+// ftm_dequant.hip
+hipError_t launch_linear_generic(const ftm_proj& P, int slot, const void* x, int x_dt, int M, void* out,
+                                 int out_dt, const void* bias, int bias_dt, int final_dt, hipStream_t st);
+hipError_t launch_experts_generic(const ftm_moe_layer& L, const void* x, int T, void* out, char* ws,
+                                  const WsLayout& wl, hipStream_t st);
+hipError_t launch_dequant(const ftm_proj& P, int slot, void* out, int out_dt, int transpose,
+                          hipStream_t st);
+
+}  // namespace ftm

@@ -1,0 +1,714 @@
+// ftm_moe.hip -- the fused quantized MoE layer on gfx950.
+//
+// One layer forward is four launches on the caller's stream:
+//   k_router   router GEMV  logits[t, e] = round(x[t] . G[e] (+ b[e]))      (one WG per expert row)
+//   k_topk     softmax / top-k / renorm per token (one wave per token), then
+//              the last-arriving WG compacts the routed experts (ascending id)
+//   k_stage_a  per (routed expert, 16-channel tile): gate and up rows of w13,
+//              K split over the 4 waves, fused activation -> h (act dtype)
+//   k_stage_b  per (expert, 64-column tile of H): w2 . h, bias, router weight,
+//              written to the [T, k(+1), H] fp32 slot buffer; the last WG to
+//              finish a column tile sums its k(+1) slots in fixed order -> out
+// The shared expert (dense bf16) rides along as one more expert in stages A/B.
+// No float atomics anywhere: the output is bitwise reproducible run to run.
+//
+// Reference semantics followed (file:line under /root/reference):
+//   routing      python/freetoken/models/qwen3_5_moe/__init__.py:1224-1227,
+//                python/freetoken/kernel/triton/fused_moe.py:91-97,
+//                python/freetoken/models/gpt_oss/__init__.py:347-352
+//   expert       python/freetoken/kernel/triton/fused_fp8_linear.py:154-175 (fp32 gu,
+//                h rounded to the activation dtype, fp32 down projection)
+//   clamped GLU  python/freetoken/models/gpt_oss/__init__.py:306-310
+//   combine      python/freetoken/models/qwen3_5_moe/__init__.py:1732-1737,1252
+//   shared       python/freetoken/models/qwen3_5_moe/__init__.py:1229,1752-1768
+#include <math.h>
+
+#include "ftm_device.h"
+#include "ftm_internal.h"
+
+namespace ftm {
+
+struct LayerArgs {
+  ftm_moe_layer L;
+  const void* x;
+  void* out;
+  int T, KP, Imax;
+  int32_t* ctrl;
+  float* logits;    // [T, E+1]   (column E = shared-expert gate logit)
+  float* wts;       // [T*KP]     router weight of pair p = t*KP + j (j == k: shared gate)
+  int32_t* ids;     // [T*k]
+  int32_t* lists;   // [E, T]     pair ids routed to expert e (order within an expert is free)
+  int32_t* uniq;    // [E+1]      routed experts with >= 1 pair, ascending
+  int32_t* ucnt;    // [E+1]
+  char* hbuf;       // [T*KP, Imax] act dtype
+  float* ybuf;      // [T*KP, H]
+};
+
+static LayerArgs make_args(const ftm_moe_layer& L, const void* x, void* out, int T, char* ws,
+                           const WsLayout& wl) {
+  LayerArgs a;
+  a.L = L;
+  a.x = x;
+  a.out = out;
+  a.T = T;
+  a.KP = wl.KP;
+  a.Imax = wl.Imax;
+  a.ctrl = (int32_t*)ws;
+  a.logits = (float*)(ws + wl.logits);
+  a.wts = (float*)(ws + wl.wts);
+  a.ids = (int32_t*)(ws + wl.ids);
+  a.lists = (int32_t*)(ws + wl.lists);
+  a.uniq = (int32_t*)(ws + wl.uniq);
+  a.ucnt = (int32_t*)(ws + wl.ucnt);
+  a.hbuf = ws + wl.hbuf;
+  a.ybuf = (float*)(ws + wl.ybuf);
+  return a;
+}
+
+// ============================================================== router GEMV
+// logit = round_act( sum_k x[k]*G[k] (+ b) ).  The fp32 sum has a fixed order
+// (per lane: 8-element chunks c = lane + 64*s in ascending s, fma in element
+// order; then the xor-32/16/8/4/2/1 butterfly) that the C oracle replays with
+// fmaf, so logits and therefore routing indices are bit-reproducible.
+__global__ __launch_bounds__(kBlock) void k_router(const LayerArgs a, int row_begin) {
+  const int r = row_begin + blockIdx.x;
+  const int E = a.L.num_experts, H = a.L.hidden, T = a.T;
+  const uint16_t* grow = (r < E) ? (const uint16_t*)a.L.gate_w + (size_t)r * H
+                                 : (const uint16_t*)a.L.shared_gate;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const uint16_t* xb = (const uint16_t*)a.x;
+  for (int t0 = wave; t0 < T; t0 += 32) {
+    float acc[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) acc[i] = 0.0f;
+    for (int c = lane; 8 * c < H; c += 64) {
+      const u32x4 gv = *(const u32x4*)(grow + 8 * c);
+      const uint32_t gw[4] = {gv.x, gv.y, gv.z, gv.w};
+      float gf[8];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        gf[2 * e] = bf16_to_f32(gw[e] & 0xffffu);
+        gf[2 * e + 1] = bf16_to_f32(gw[e] >> 16);
+      }
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const int t = t0 + 4 * i;
+        if (t < T) {
+          const u32x4 xv = *(const u32x4*)(xb + (size_t)t * H + 8 * c);
+          const uint32_t xw[4] = {xv.x, xv.y, xv.z, xv.w};
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            acc[i] = __builtin_fmaf(bf16_to_f32(xw[e] & 0xffffu), gf[2 * e], acc[i]);
+            acc[i] = __builtin_fmaf(bf16_to_f32(xw[e] >> 16), gf[2 * e + 1], acc[i]);
+          }
+        }
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const float v = wave_sum(acc[i]);
+      const int t = t0 + 4 * i;
+      if (lane == 0 && t < T) {
+        float z = v;
+        if (r < E && a.L.gate_b != nullptr) z = v + bf16_to_f32(((const uint16_t*)a.L.gate_b)[r]);
+        a.logits[(size_t)t * (E + 1) + r] = round_to(z, a.L.act_dtype);
+      }
+    }
+  }
+}
+
+// ============================================================== top-k + grouping
+constexpr int kMaxNV = kMaxExperts / 64;
+
+__device__ __forceinline__ bool key_better(float v, int e, float bv, int be) {
+  return v > bv || (v == bv && e < be);
+}
+
+template <int MODE>
+__global__ __launch_bounds__(kBlock) void k_topk(const LayerArgs a, const void* logits_in, int logits_dt,
+                                                 const int32_t* ids_in, const float* w_in, int32_t* ids_out,
+                                                 float* w_out, float* logits_out) {
+  const int E = a.L.num_experts, k = a.L.topk, T = a.T, KP = a.KP;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int t = blockIdx.x * 4 + wave;
+  const int act_dt = a.L.act_dtype;
+  int32_t* cnt = a.ctrl + kCtrlExpertCnt;
+
+  if (t < T) {
+    int sel_e = -1;
+    float sel_w = 0.0f;
+    if (ids_in != nullptr) {
+      if (lane < k) {
+        sel_e = ids_in[(size_t)t * k + lane];
+        sel_w = w_in[(size_t)t * k + lane];
+      }
+    } else {
+      const int pdt = logits_in ? logits_dt : act_dt;  // dtype the probabilities live in (LOWP)
+      float v[kMaxNV], key[kMaxNV];
+      float vmax = -INFINITY;
+#pragma unroll
+      for (int i = 0; i < kMaxNV; ++i) {
+        const int e = lane + 64 * i;
+        v[i] = -INFINITY;
+        if (e < E) {
+          v[i] = logits_in ? load_scalar(logits_in, (size_t)t * E + e, logits_dt)
+                           : a.logits[(size_t)t * (E + 1) + e];
+          if (logits_out) logits_out[(size_t)t * E + e] = v[i];
+        }
+        vmax = fmaxf(vmax, v[i]);
+      }
+      float m = 0.0f, s = 1.0f;
+      if (MODE != FTM_ROUTE_TOPK_SOFTMAX) {
+        m = wave_max(vmax);
+        float ps = 0.0f;
+#pragma unroll
+        for (int i = 0; i < kMaxNV; ++i)
+          if (lane + 64 * i < E) ps += expf(v[i] - m);
+        s = wave_sum(ps);
+      }
+#pragma unroll
+      for (int i = 0; i < kMaxNV; ++i) {
+        if (MODE == FTM_ROUTE_SOFTMAX_TOPK_LOWP)
+          key[i] = (lane + 64 * i < E) ? round_to(expf(v[i] - m) / s, pdt) : -INFINITY;
+        else
+          key[i] = v[i];
+      }
+      // k rounds of wave arg-max on (key desc, expert id asc).
+      uint32_t taken = 0;
+      float top0 = 0.0f;
+      for (int j = 0; j < k; ++j) {
+        float bv = -INFINITY;
+        int be = 0x7fffffff;
+#pragma unroll
+        for (int i = 0; i < kMaxNV; ++i) {
+          const int e = lane + 64 * i;
+          if (e < E && !((taken >> i) & 1u) && key_better(key[i], e, bv, be)) {
+            bv = key[i];
+            be = e;
+          }
+        }
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) {
+          const float ov = __shfl_xor(bv, off);
+          const int oe = __shfl_xor(be, off);
+          if (key_better(ov, oe, bv, be)) {
+            bv = ov;
+            be = oe;
+          }
+        }
+        if ((be & 63) == lane) taken |= 1u << (be >> 6);
+        if (j == 0) top0 = bv;
+        if (lane == j) {
+          sel_e = be;
+          sel_w = bv;  // the key; converted to a weight below
+        }
+      }
+      // weights
+      float p = 0.0f;
+      if (lane < k) {
+        if (MODE == FTM_ROUTE_SOFTMAX_TOPK) p = expf(sel_w - m) / s;
+        else if (MODE == FTM_ROUTE_SOFTMAX_TOPK_LOWP) p = sel_w;
+        else p = expf(sel_w - top0);
+      }
+      const float tot = wave_sum(lane < k ? p : 0.0f);
+      if (MODE == FTM_ROUTE_SOFTMAX_TOPK) {
+        sel_w = a.L.renormalize ? p / tot : p;
+      } else if (MODE == FTM_ROUTE_SOFTMAX_TOPK_LOWP) {
+        sel_w = a.L.renormalize ? round_to(p / round_to(tot, pdt), pdt) : p;
+      } else {
+        sel_w = p / tot;
+      }
+      sel_w = round_to(sel_w, act_dt);
+    }
+    if (lane < k) {
+      const int p = t * KP + lane;
+      if (sel_e >= 0 && sel_e < E) {
+        a.wts[p] = sel_w;
+        a.ids[(size_t)t * k + lane] = sel_e;
+        if (ids_out) ids_out[(size_t)t * k + lane] = sel_e;
+        if (w_out) w_out[(size_t)t * k + lane] = sel_w;
+        const int pos = atomicAdd(&cnt[sel_e], 1);
+        if (pos < T) {
+          a.lists[(size_t)sel_e * T + pos] = p;
+        } else {  // a token listed the same expert twice (caller-supplied routing)
+          atomicSub(&cnt[sel_e], 1);
+          atomicOr(&a.ctrl[kCtrlError], 4);
+        }
+      } else {
+        atomicOr(&a.ctrl[kCtrlError], 2);
+      }
+    }
+    if (lane == 0 && a.L.shared_inter > 0) {
+      const float sl = a.logits[(size_t)t * (E + 1) + E];
+      a.wts[t * KP + k] = round_to(1.0f / (1.0f + expf(-sl)), act_dt);
+    }
+  }
+
+  // ---- last-arriving workgroup: compact the routed experts (ascending id).
+  __shared__ int s_last;
+  __shared__ int s_wsum[4];
+  __threadfence();
+  __syncthreads();
+  if (threadIdx.x == 0) s_last = (atomicAdd(&a.ctrl[kCtrlArriveTopk], 1) == (int)gridDim.x - 1);
+  __syncthreads();
+  if (!s_last) return;
+  __threadfence();
+  int running = 0;
+  for (int base = 0; base < E; base += kBlock) {
+    const int e = base + threadIdx.x;
+    const int c = (e < E) ? __hip_atomic_load(&cnt[e], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0;
+    const bool f = c > 0;
+    const uint64_t mask = __ballot(f);
+    const int pre = __popcll(mask & ((1ull << lane) - 1ull));
+    if (lane == 0) s_wsum[wave] = __popcll(mask);
+    __syncthreads();
+    int wpre = 0, tot = 0;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      if (w < wave) wpre += s_wsum[w];
+      tot += s_wsum[w];
+    }
+    if (f) {
+      a.uniq[running + wpre + pre] = e;
+      a.ucnt[running + wpre + pre] = c;
+    }
+    if (e < E) cnt[e] = 0;
+    running += tot;
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) {
+    a.ctrl[kCtrlNRouted] = running;
+    a.ctrl[kCtrlNU] = running + (a.L.shared_inter > 0 ? 1 : 0);
+    a.ctrl[kCtrlArriveTopk] = 0;
+  }
+}
+
+// ============================================================== activation
+__device__ __forceinline__ float act_fn(int act, float g, float u, float alpha, float limit) {
+  if (act == FTM_ACT_SILU) return g / (1.0f + expf(-g)) * u;
+  if (act == FTM_ACT_GELU) return 0.5f * g * (1.0f + erff(g * 0.70710678118654752f)) * u;
+  if (act == FTM_ACT_RELU) return fmaxf(g, 0.0f) * u;
+  // FTM_ACT_SWIGLU_OAI
+  g = fminf(g, limit);
+  u = fminf(fmaxf(u, -limit), limit);
+  const float glu = g / (1.0f + expf(-alpha * g));
+  return (u + 1.0f) * glu;
+}
+
+__device__ __forceinline__ ProjSlot shared_view(const void* w, int N, int K) {
+  ProjSlot v;
+  v.w = (const char*)w;
+  v.s = v.z = v.bias = nullptr;
+  v.fmt = FTM_FMT_BF16;
+  v.s_dt = v.bias_dt = FTM_DT_BF16;
+  v.group = 0;
+  v.N = N;
+  v.K = K;
+  return v;
+}
+
+// ============================================================== stage A (w13 + act)
+template <int EFMT, bool SPLIT, int NT>
+__device__ void stage_a_body(const LayerArgs& a, const ProjSlot& W, int Iu, int it, int cnt,
+                             const int32_t* list, int shared_col, f32x4* red) {
+  constexpr bool kG = EFMT == FTM_FMT_GPTQ_INT4;
+  constexpr int NSUB = kG ? 4 : 1;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int H = a.L.hidden, KP = a.KP;
+  const int nL = fmt_loads<EFMT>(H);
+  const int L_lo = wave * nL / 4, L_hi = (wave + 1) * nL / 4;
+  const int col0[2] = {it * NT, Iu + it * NT};
+  const int xsz = dt_size(a.L.act_dtype);
+  for (int mb = 0; mb < cnt; mb += 16) {
+    ARow ar;
+    ar.dt = a.L.act_dtype;
+    ar.mul = 1.0f;
+    ar.p = nullptr;
+    const int m = mb + (lane & 15);
+    if (m < cnt) {
+      const int p = list ? list[m] : m * KP + shared_col;
+      const int t = p / KP;
+      ar.p = (const char*)a.x + (size_t)t * H * xsz;
+      if (a.L.apply_router_weight_on_input && list) ar.mul = a.wts[p];
+    }
+    if constexpr (kG) {
+      f32x4 acc[2][4];
+#pragma unroll
+      for (int r = 0; r < 2; ++r)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) acc[r][c] = (f32x4){0.f, 0.f, 0.f, 0.f};
+      wave_gemm_gptq<2, SPLIT>(W, col0, L_lo, L_hi, ar, acc);
+#pragma unroll
+      for (int r = 0; r < 2; ++r)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) red[((wave * 2 + r) * NSUB + c) * 64 + lane] = acc[r][c];
+    } else {
+      f32x4 acc[2] = {(f32x4){0.f, 0.f, 0.f, 0.f}, (f32x4){0.f, 0.f, 0.f, 0.f}};
+      wave_gemm_kmajor<EFMT, 2, SPLIT>(W, col0, L_lo, L_hi, ar, acc);
+#pragma unroll
+      for (int r = 0; r < 2; ++r) red[(wave * 2 + r) * 64 + lane] = acc[r];
+    }
+    __syncthreads();
+    for (int idx = threadIdx.x; idx < 16 * NT; idx += kBlock) {
+      const int i = idx / NT, j = idx % NT;
+      const int c = kG ? (j & 3) : 0, jj = kG ? (j >> 2) : j;
+      const int ln = jj + 16 * (i >> 2), rr = i & 3;
+      float gs = 0.0f, us = 0.0f;
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        gs += red[((w * 2 + 0) * NSUB + c) * 64 + ln][rr];
+        us += red[((w * 2 + 1) * NSUB + c) * 64 + ln][rr];
+      }
+      const int m2 = mb + i;
+      if (m2 < cnt) {
+        const int ch = it * NT + j;
+        if (W.bias != nullptr) {
+          gs += load_scalar(W.bias, ch, W.bias_dt);
+          us += load_scalar(W.bias, Iu + ch, W.bias_dt);
+        }
+        const float h = act_fn(a.L.act, gs, us, a.L.swiglu_alpha, a.L.swiglu_limit);
+        const int p = list ? list[m2] : m2 * KP + shared_col;
+        store_scalar(a.hbuf, (size_t)p * a.Imax + ch, a.L.act_dtype, h);
+      }
+    }
+    __syncthreads();
+  }
+}
+
+template <int FMT, bool SPLIT>
+__global__ __launch_bounds__(kBlock) void k_stage_a(const LayerArgs a) {
+  constexpr bool kG = FMT == FTM_FMT_GPTQ_INT4;
+  constexpr int NT = kG ? 64 : 16;
+  __shared__ f32x4 red[4 * 2 * (kG ? 4 : 1) * 64];
+  const int nRouted = a.ctrl[kCtrlNRouted];
+  const int I = a.L.inter;
+  const int tilesR = I / NT;
+  int item = blockIdx.x;
+  if (item < nRouted * tilesR) {
+    const int u = item / tilesR, it = item % tilesR;
+    const int e = a.uniq[u], cnt = a.ucnt[u];
+    const int slot = a.L.slot_of_expert ? a.L.slot_of_expert[e] : e;
+    if (slot < 0 || slot >= a.L.w13.num_slots) {
+      if (threadIdx.x == 0) atomicOr(&a.ctrl[kCtrlError], 1);
+      return;
+    }
+    const ProjSlot W = proj_slot(a.L.w13, slot);
+    stage_a_body<FMT, SPLIT, NT>(a, W, I, it, cnt, a.lists + (size_t)e * a.T, 0, red);
+  } else {
+    item -= nRouted * tilesR;
+    const int Is = a.L.shared_inter;
+    if (Is <= 0 || item >= Is / 16) return;
+    const ProjSlot W = shared_view(a.L.shared_w13, 2 * Is, a.L.hidden);
+    stage_a_body<FTM_FMT_BF16, SPLIT, 16>(a, W, Is, item, a.T, nullptr, a.L.topk, red);
+  }
+}
+
+// ============================================================== stage B (w2 + combine)
+template <int EFMT, bool SPLIT>
+__device__ void stage_b_body(const LayerArgs& a, const ProjSlot& W, int cnt, const int32_t* list,
+                             int shared_col, int nt, f32x4* red) {
+  constexpr bool kG = EFMT == FTM_FMT_GPTQ_INT4;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int Ku = W.K;
+  const int H = a.L.hidden, KP = a.KP;
+  const int nL = fmt_loads<EFMT>(Ku);
+  const int L_lo = kG ? wave * nL / 4 : 0;
+  const int L_hi = kG ? (wave + 1) * nL / 4 : nL;
+  const int col0[1] = {kG ? nt * 64 : nt * 64 + 16 * wave};
+  const int hsz = dt_size(a.L.act_dtype);
+  const bool weighted = !(a.L.apply_router_weight_on_input && list);
+  for (int mb = 0; mb < cnt; mb += 16) {
+    ARow ar;
+    ar.dt = a.L.act_dtype;
+    ar.mul = 1.0f;
+    ar.p = nullptr;
+    const int m = mb + (lane & 15);
+    if (m < cnt) {
+      const int p = list ? list[m] : m * KP + shared_col;
+      ar.p = a.hbuf + (size_t)p * a.Imax * hsz;
+    }
+    if constexpr (kG) {
+      f32x4 acc[1][4];
+#pragma unroll
+      for (int c = 0; c < 4; ++c) acc[0][c] = (f32x4){0.f, 0.f, 0.f, 0.f};
+      wave_gemm_gptq<1, SPLIT>(W, col0, L_lo, L_hi, ar, acc);
+#pragma unroll
+      for (int c = 0; c < 4; ++c) red[(wave * 4 + c) * 64 + lane] = acc[0][c];
+      __syncthreads();
+      for (int idx = threadIdx.x; idx < 16 * 64; idx += kBlock) {
+        const int i = idx / 64, j = idx % 64;
+        const int c = j & 3, ln = (j >> 2) + 16 * (i >> 2), rr = i & 3;
+        float y = 0.0f;
+#pragma unroll
+        for (int w = 0; w < 4; ++w) y += red[(w * 4 + c) * 64 + ln][rr];
+        const int m2 = mb + i, n = nt * 64 + j;
+        if (m2 < cnt && n < H) {
+          const int p = list ? list[m2] : m2 * KP + shared_col;
+          if (W.bias != nullptr) y += load_scalar(W.bias, n, W.bias_dt);
+          if (weighted) y *= a.wts[p];
+          a.ybuf[(size_t)p * H + n] = y;
+        }
+      }
+      __syncthreads();
+    } else {
+      f32x4 acc[1] = {(f32x4){0.f, 0.f, 0.f, 0.f}};
+      wave_gemm_kmajor<EFMT, 1, SPLIT>(W, col0, L_lo, L_hi, ar, acc);
+      const int n = col0[0] + (lane & 15);
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) {
+        const int m2 = mb + 4 * (lane >> 4) + rr;
+        if (m2 < cnt && n < H) {
+          const int p = list ? list[m2] : m2 * KP + shared_col;
+          float y = acc[0][rr];
+          if (W.bias != nullptr) y += load_scalar(W.bias, n, W.bias_dt);
+          if (weighted) y *= a.wts[p];
+          a.ybuf[(size_t)p * H + n] = y;
+        }
+      }
+    }
+  }
+}
+
+template <int FMT, bool SPLIT>
+__global__ __launch_bounds__(kBlock) void k_stage_b(const LayerArgs a) {
+  __shared__ f32x4 red[4 * 4 * 64];
+  __shared__ int s_last;
+  const int H = a.L.hidden;
+  const int tiles = H / 64;
+  const int nU = a.ctrl[kCtrlNU], nRouted = a.ctrl[kCtrlNRouted];
+  const int u = blockIdx.x / tiles, nt = blockIdx.x % tiles;
+  if (u >= nU) return;
+  if (u < nRouted) {
+    const int e = a.uniq[u], cnt = a.ucnt[u];
+    const int32_t* list = a.lists + (size_t)e * a.T;
+    const int slot = a.L.slot_of_expert ? a.L.slot_of_expert[e] : e;
+    if (slot < 0 || slot >= a.L.w2.num_slots) {
+      // non-resident expert: contribute zeros, flag the error
+      for (int idx = threadIdx.x; idx < cnt * 64; idx += kBlock) {
+        const int m = idx / 64, n = nt * 64 + idx % 64;
+        a.ybuf[(size_t)list[m] * H + n] = 0.0f;
+      }
+      if (threadIdx.x == 0) atomicOr(&a.ctrl[kCtrlError], 1);
+    } else {
+      const ProjSlot W = proj_slot(a.L.w2, slot);
+      stage_b_body<FMT, SPLIT>(a, W, cnt, list, 0, nt, red);
+    }
+  } else {
+    const ProjSlot W = shared_view(a.L.shared_w2, H, a.L.shared_inter);
+    stage_b_body<FTM_FMT_BF16, SPLIT>(a, W, a.T, nullptr, a.L.topk, nt, red);
+  }
+  // ---- deterministic combine: the last of the nU workgroups of this column
+  // tile sums the KP slots of every token in slot order.
+  int32_t* tilecnt = a.ctrl + kCtrlTileCnt;
+  __threadfence();
+  __syncthreads();
+  if (threadIdx.x == 0) s_last = (atomicAdd(&tilecnt[nt], 1) == nU - 1);
+  __syncthreads();
+  if (!s_last) return;
+  __threadfence();
+  const int KP = a.KP;
+  for (int idx = threadIdx.x; idx < a.T * 64; idx += kBlock) {
+    const int t = idx / 64, n = nt * 64 + (idx % 64);
+    const float* yb = a.ybuf + (size_t)t * KP * H + n;
+    float s = 0.0f;
+    for (int j = 0; j < KP; ++j) s += __builtin_nontemporal_load(yb + (size_t)j * H);
+    store_scalar(a.out, (size_t)t * H + n, a.L.act_dtype, s);
+  }
+  if (threadIdx.x == 0) tilecnt[nt] = 0;
+}
+
+// ============================================================== single projection
+struct LinArgs {
+  ftm_proj P;
+  int slot;
+  const void* x;
+  int x_dt, M;
+  void* out;
+  int out_dt;
+  const void* bias;
+  int bias_dt, final_dt;
+};
+
+template <int FMT, bool SPLIT>
+__global__ __launch_bounds__(kBlock) void k_linear(const LinArgs a) {
+  constexpr bool kG = FMT == FTM_FMT_GPTQ_INT4;
+  __shared__ f32x4 red[4 * 4 * 64];
+  const ProjSlot W = proj_slot(a.P, a.slot);
+  const int N = W.N, K = W.K;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int nt = blockIdx.x, mt = blockIdx.y;
+  const int nL = fmt_loads<FMT>(K);
+  const int L_lo = kG ? wave * nL / 4 : 0;
+  const int L_hi = kG ? (wave + 1) * nL / 4 : nL;
+  const int col0[1] = {kG ? nt * 64 : nt * 64 + 16 * wave};
+  ARow ar;
+  ar.dt = a.x_dt;
+  ar.mul = 1.0f;
+  const int m = mt * 16 + (lane & 15);
+  ar.p = (m < a.M) ? (const char*)a.x + (size_t)m * K * dt_size(a.x_dt) : nullptr;
+  auto emit = [&](int m2, int n, float y) {
+    if (m2 < a.M && n < N) {
+      float v = round_to(y, a.out_dt);
+      if (a.bias != nullptr) v = round_to(v + load_scalar(a.bias, n, a.bias_dt), a.final_dt);
+      store_scalar(a.out, (size_t)m2 * N + n, a.final_dt, v);
+    }
+  };
+  if constexpr (kG) {
+    f32x4 acc[1][4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) acc[0][c] = (f32x4){0.f, 0.f, 0.f, 0.f};
+    wave_gemm_gptq<1, SPLIT>(W, col0, L_lo, L_hi, ar, acc);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) red[(wave * 4 + c) * 64 + lane] = acc[0][c];
+    __syncthreads();
+    for (int idx = threadIdx.x; idx < 16 * 64; idx += kBlock) {
+      const int i = idx / 64, j = idx % 64;
+      const int c = j & 3, ln = (j >> 2) + 16 * (i >> 2), rr = i & 3;
+      float y = 0.0f;
+#pragma unroll
+      for (int w = 0; w < 4; ++w) y += red[(w * 4 + c) * 64 + ln][rr];
+      emit(mt * 16 + i, nt * 64 + j, y);
+    }
+  } else {
+    f32x4 acc[1] = {(f32x4){0.f, 0.f, 0.f, 0.f}};
+    wave_gemm_kmajor<FMT, 1, SPLIT>(W, col0, L_lo, L_hi, ar, acc);
+    const int n = col0[0] + (lane & 15);
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) emit(mt * 16 + 4 * (lane >> 4) + rr, n, acc[0][rr]);
+  }
+}
+
+// ============================================================== small helpers
+__global__ void k_fill_routing(int T, int32_t slot, int32_t* slot_word, int32_t* ids, float* w) {
+  const int t = blockIdx.x * blockDim.x + threadIdx.x;
+  if (t == 0) *slot_word = slot;
+  if (t < T) {
+    ids[t] = 0;
+    w[t] = 1.0f;
+  }
+}
+
+__global__ void k_zero_words(int32_t* p, int n) {
+  for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) p[i] = 0;
+}
+
+// ============================================================== launchers
+hipError_t launch_ws_init(void* ws, hipStream_t st) {
+  hipLaunchKernelGGL(k_zero_words, dim3(4), dim3(kBlock), 0, st, (int32_t*)ws, FTM_WS_CTRL_BYTES / 4);
+  return hipGetLastError();
+}
+
+hipError_t launch_router(const ftm_moe_layer& L, const void* x, int T, int row_begin, int row_end, char* ws,
+                         const WsLayout& wl, hipStream_t st) {
+  const LayerArgs a = make_args(L, x, nullptr, T, ws, wl);
+  if (row_end - row_begin <= 0 || T <= 0) return hipSuccess;
+  hipLaunchKernelGGL(k_router, dim3(row_end - row_begin), dim3(kBlock), 0, st, a, row_begin);
+  return hipGetLastError();
+}
+
+hipError_t launch_topk(const ftm_moe_layer& L, int T, const void* logits_in, int logits_dt,
+                       const int32_t* ids_in, const float* w_in, int32_t* ids_out, float* w_out,
+                       float* logits_out, char* ws, const WsLayout& wl, hipStream_t st) {
+  const LayerArgs a = make_args(L, nullptr, nullptr, T, ws, wl);
+  const dim3 grid((T + 3) / 4 > 0 ? (T + 3) / 4 : 1);
+  switch (L.route_mode) {
+    case FTM_ROUTE_SOFTMAX_TOPK:
+      hipLaunchKernelGGL(k_topk<FTM_ROUTE_SOFTMAX_TOPK>, grid, dim3(kBlock), 0, st, a, logits_in, logits_dt,
+                         ids_in, w_in, ids_out, w_out, logits_out);
+      break;
+    case FTM_ROUTE_SOFTMAX_TOPK_LOWP:
+      hipLaunchKernelGGL(k_topk<FTM_ROUTE_SOFTMAX_TOPK_LOWP>, grid, dim3(kBlock), 0, st, a, logits_in,
+                         logits_dt, ids_in, w_in, ids_out, w_out, logits_out);
+      break;
+    default:
+      hipLaunchKernelGGL(k_topk<FTM_ROUTE_TOPK_SOFTMAX>, grid, dim3(kBlock), 0, st, a, logits_in, logits_dt,
+                         ids_in, w_in, ids_out, w_out, logits_out);
+      break;
+  }
+  return hipGetLastError();
+}
+
+// which: bit 0 = stage A (w13 + act), bit 1 = stage B (w2 + combine)
+template <int FMT, bool SPLIT>
+static void launch_stages(const LayerArgs& a, int gridA, int gridB, hipStream_t st, int which) {
+  if (which & 1) hipLaunchKernelGGL((k_stage_a<FMT, SPLIT>), dim3(gridA), dim3(kBlock), 0, st, a);
+  if (which & 2) hipLaunchKernelGGL((k_stage_b<FMT, SPLIT>), dim3(gridB), dim3(kBlock), 0, st, a);
+}
+
+hipError_t launch_experts(const ftm_moe_layer& L, const void* x, int T, void* out, char* ws,
+                          const WsLayout& wl, hipStream_t st, int which) {
+  const LayerArgs a = make_args(L, x, out, T, ws, wl);
+  const int maxU = L.num_experts < T * L.topk ? L.num_experts : T * L.topk;
+  const int NT = L.w13.fmt == FTM_FMT_GPTQ_INT4 ? 64 : 16;
+  const int has_sh = L.shared_inter > 0 ? 1 : 0;
+  const int gridA = maxU * (L.inter / NT) + (has_sh ? L.shared_inter / 16 : 0);
+  const int gridB = (maxU + has_sh) * (L.hidden / 64);
+  const bool split = L.act_dtype != FTM_DT_BF16;
+  switch (L.w13.fmt) {
+    case FTM_FMT_BF16:
+      split ? launch_stages<FTM_FMT_BF16, true>(a, gridA, gridB, st, which)
+            : launch_stages<FTM_FMT_BF16, false>(a, gridA, gridB, st, which);
+      break;
+    case FTM_FMT_FP8_BLOCK:
+      split ? launch_stages<FTM_FMT_FP8_BLOCK, true>(a, gridA, gridB, st, which)
+            : launch_stages<FTM_FMT_FP8_BLOCK, false>(a, gridA, gridB, st, which);
+      break;
+    case FTM_FMT_GPTQ_INT4:
+      split ? launch_stages<FTM_FMT_GPTQ_INT4, true>(a, gridA, gridB, st, which)
+            : launch_stages<FTM_FMT_GPTQ_INT4, false>(a, gridA, gridB, st, which);
+      break;
+    case FTM_FMT_INT8_PACKED:
+      split ? launch_stages<FTM_FMT_INT8_PACKED, true>(a, gridA, gridB, st, which)
+            : launch_stages<FTM_FMT_INT8_PACKED, false>(a, gridA, gridB, st, which);
+      break;
+    case FTM_FMT_MXFP4:
+      split ? launch_stages<FTM_FMT_MXFP4, true>(a, gridA, gridB, st, which)
+            : launch_stages<FTM_FMT_MXFP4, false>(a, gridA, gridB, st, which);
+      break;
+    default:
+      return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+template <int FMT>
+static void launch_linear_t(const LinArgs& a, dim3 grid, bool split, hipStream_t st) {
+  if (split)
+    hipLaunchKernelGGL((k_linear<FMT, true>), grid, dim3(kBlock), 0, st, a);
+  else
+    hipLaunchKernelGGL((k_linear<FMT, false>), grid, dim3(kBlock), 0, st, a);
+}
+
+hipError_t launch_linear(const ftm_proj& P, int slot, const void* x, int x_dt, int M, void* out, int out_dt,
+                         const void* bias, int bias_dt, int final_dt, hipStream_t st) {
+  LinArgs a;
+  a.P = P;
+  a.slot = slot;
+  a.x = x;
+  a.x_dt = x_dt;
+  a.M = M;
+  a.out = out;
+  a.out_dt = out_dt;
+  a.bias = bias;
+  a.bias_dt = bias_dt;
+  a.final_dt = final_dt;
+  const dim3 grid((P.N + 63) / 64, (M + 15) / 16);
+  const bool split = x_dt != FTM_DT_BF16;
+  switch (P.fmt) {
+    case FTM_FMT_BF16: launch_linear_t<FTM_FMT_BF16>(a, grid, split, st); break;
+    case FTM_FMT_FP8_BLOCK: launch_linear_t<FTM_FMT_FP8_BLOCK>(a, grid, split, st); break;
+    case FTM_FMT_GPTQ_INT4: launch_linear_t<FTM_FMT_GPTQ_INT4>(a, grid, split, st); break;
+    case FTM_FMT_INT8_PACKED: launch_linear_t<FTM_FMT_INT8_PACKED>(a, grid, split, st); break;
+    case FTM_FMT_MXFP4: launch_linear_t<FTM_FMT_MXFP4>(a, grid, split, st); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_fill_routing(int T, int32_t slot, int32_t* slot_word, int32_t* ids, float* w, hipStream_t st) {
+  const int blocks = (T + 255) / 256 > 0 ? (T + 255) / 256 : 1;
+  hipLaunchKernelGGL(k_fill_routing, dim3(blocks), dim3(256), 0, st, T, slot, slot_word, ids, w);
+  return hipGetLastError();
+}
+
+}  // namespace ftm

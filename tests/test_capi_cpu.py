@@ -1,0 +1,113 @@
+"""C ABI on the CPU: the library loads, exports exactly what include/ftmoe.h
+declares, and rejects bad arguments with the reference's error convention
+(python/freetoken/kernel/csrc/cpu_moe/cpu_moe.cpp:733-739) before touching
+the HIP runtime, so every error path is exercised without a GPU."""
+import ctypes
+import os
+import re
+
+import pytest
+
+from ftmoe import _native as nat
+
+HEADER = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "include", "ftmoe.h")
+
+
+def _declared():
+    src = open(HEADER).read()
+    src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
+    return sorted(set(re.findall(r"\b(ftm_[a-z0-9_]+)\s*\(", src)))
+
+
+def test_exports_match_header():
+    L = nat.lib()
+    declared = _declared()
+    assert declared == sorted(nat.EXPORTED)
+    for name in declared:
+        assert hasattr(L, name), name
+    assert L.ftm_version() == nat.ABI_VERSION
+
+
+def _proj(**kw):
+    p = nat.FtmProj()
+    p.w = kw.get("w", 0x1000)
+    p.s = kw.get("s", 0x2000)
+    p.z = kw.get("z", None)
+    p.fmt = kw.get("fmt", nat.FMT_FP8_BLOCK)
+    p.s_dtype = nat.DT_F32
+    p.group = kw.get("group", 128)
+    p.N = kw.get("N", 256)
+    p.K = kw.get("K", 256)
+    p.num_slots = kw.get("num_slots", 1)
+    return p
+
+
+def test_linear_argument_errors():
+    L = nat.lib()
+    x = ctypes.c_void_p(0x4000)
+    out = ctypes.c_void_p(0x8000)
+
+    def call(p, slot=0, M=4, xx=x, oo=out, dt=nat.DT_F32):
+        return L.ftm_linear(ctypes.byref(p) if p is not None else None, slot, xx, dt, M, oo, dt, None, 0, dt, None)
+
+    assert call(None) == nat.ERR_NULL
+    assert call(_proj(w=None)) == nat.ERR_NULL
+    assert call(_proj(s=None)) == nat.ERR_NULL
+    assert call(_proj(N=0)) == nat.ERR_DIM
+    assert call(_proj(fmt=99)) == nat.ERR_FORMAT
+    assert call(_proj(), slot=1) == nat.ERR_DIM
+    assert call(_proj(), M=-1) == nat.ERR_DIM
+    assert call(_proj(), M=0) == nat.OK  # empty batch is a no-op
+    assert call(_proj(), xx=None) == nat.ERR_NULL
+    assert call(_proj(), dt=7) == nat.ERR_FORMAT
+    assert call(_proj(fmt=nat.FMT_GPTQ_INT4, z=None)) == nat.ERR_NULL
+
+
+def _layer(**kw):
+    L = nat.FtmMoeLayer()
+    L.w13 = _proj(N=2 * kw.get("I", 128), K=kw.get("H", 256), num_slots=8)
+    L.w2 = _proj(N=kw.get("H", 256), K=kw.get("I", 128), num_slots=8)
+    L.num_experts = kw.get("E", 8)
+    L.hidden = kw.get("H", 256)
+    L.inter = kw.get("I", 128)
+    L.topk = kw.get("k", 2)
+    L.gate_w = kw.get("gate_w", 0x9000)
+    L.act_dtype = kw.get("act_dtype", nat.DT_BF16)
+    L.route_mode = kw.get("route_mode", nat.ROUTE_SOFTMAX_TOPK)
+    L.act = kw.get("act", nat.ACT_SILU)
+    return L
+
+
+def test_layer_argument_errors():
+    lib = nat.lib()
+    x, out, ws = ctypes.c_void_p(0x10000), ctypes.c_void_p(0x20000), ctypes.c_void_p(0x40000)
+
+    def fwd(L, T=4, wsb=1 << 30, wsp=ws):
+        return lib.ftm_moe_forward(ctypes.byref(L), x, T, out, None, None, None, wsp, wsb, None)
+
+    assert fwd(_layer(E=0)) == nat.ERR_DIM
+    assert fwd(_layer(k=9)) == nat.ERR_DIM  # k > E
+    assert fwd(_layer(E=600, k=2)) == nat.ERR_DIM
+    assert fwd(_layer(gate_w=None)) == nat.ERR_NULL
+    assert fwd(_layer(act_dtype=nat.DT_F16)) == nat.ERR_FORMAT
+    assert fwd(_layer(route_mode=9)) == nat.ERR_FORMAT
+    assert fwd(_layer(act=9)) == nat.ERR_FORMAT
+    assert fwd(_layer(), T=-1) == nat.ERR_DIM
+    assert fwd(_layer(), T=0) == nat.OK
+    assert fwd(_layer(), wsp=None) == nat.ERR_WORKSPACE
+    assert fwd(_layer(), wsb=16) == nat.ERR_WORKSPACE
+    assert fwd(_layer(), wsp=ctypes.c_void_p(0x40010)) == nat.ERR_ALIGN
+    bad = _layer()
+    bad.w2.K = 64  # w2 must be [H, I]
+    assert fwd(bad) == nat.ERR_DIM
+    assert lib.ftm_moe_workspace_bytes(ctypes.byref(_layer()), 4) > nat.WS_CTRL_BYTES
+
+
+def test_copy_slots_argument_errors():
+    lib = nat.lib()
+    ev = (ctypes.c_int32 * 2)(0, 1)
+    assert lib.ftm_copy_slots(None, None, 64, None, None, -1, None, None) == nat.ERR_DIM
+    assert lib.ftm_copy_slots(None, None, 0, None, None, 0, None, None) == nat.ERR_DIM
+    assert lib.ftm_copy_slots(None, None, 64, ev, ev, 2, None, None) == nat.ERR_NULL
+    neg = (ctypes.c_int32 * 1)(-1)
+    assert lib.ftm_copy_slots(ctypes.c_void_p(16), ctypes.c_void_p(32), 64, neg, ev, 1, None, None) == nat.ERR_DIM

@@ -1,0 +1,138 @@
+"""GPU: the whole fused MoE layer through the C ABI against the oracle.
+
+Routing indices and router logits are bit-exact (the router kernel's fp32
+summation order is the oracle's); router weights agree to one bf16 ulp (exp
+differs between the GPU and the host libm); the bf16 layer output is within
+|got - ref| <= 2e-2 + 1e-2 |ref| of the fp32-accumulated oracle.  Covers all
+four quantized formats at reduced shapes, the FP8 + shared-expert layer (C3)
+and the INT8 layer (C1) at their full shapes, caller-supplied routing, the
+dense ``fused`` backend, and run-to-run bitwise determinism."""
+import numpy as np
+import pytest
+import torch
+
+import ftm_oracle as O
+from ftm_helpers import ATOL, RTOL, assert_close, np_, oracle_spec, to_f32
+
+from ftmoe import synthetic as S
+
+pytestmark = pytest.mark.gpu
+
+
+def _run_and_check(syn, gpu, *, check_routing=True):
+    spec = oracle_spec(syn)
+    ref = O.layer_reference(spec, np_(syn.x))
+    dsyn = syn.to(gpu)
+    layer = S.build_layer(dsyn)
+    out, ids, w, logits = layer.forward(dsyn.x, return_routing=True)
+    torch.cuda.synchronize()
+    if check_routing:
+        np.testing.assert_array_equal(to_f32(logits), ref["logits"], err_msg="router logits")
+        np.testing.assert_array_equal(ids.cpu().numpy(), ref["ids"], err_msg="routing indices")
+        np.testing.assert_allclose(w.cpu().numpy(), ref["w"], rtol=2 ** -8, atol=0, err_msg="router weights")
+    assert_close(to_f32(out), ref["out"], what=f"{syn.cfg.name} layer output")
+    return layer, dsyn, ref, out
+
+
+@pytest.mark.parametrize("name", ["c1_int8", "c2_gptq", "c3_fp8", "c4_mxfp4"])
+@pytest.mark.parametrize("T", [1, 5, 16])
+def test_small_layer_matches_oracle(gpu, name, T):
+    syn = S.generate(S.SMALL[name], T=T, seed=11 + T)
+    _run_and_check(syn, gpu)
+
+
+@pytest.mark.parametrize("name", ["c2_gptq", "c3_fp8", "c4_mxfp4"])
+def test_small_layer_routed_matches_oracle(gpu, name):
+    syn = S.generate(S.SMALL[name], T=9, seed=5)
+    spec = oracle_spec(syn)
+    rng = np.random.RandomState(0)
+    ids = np.stack([rng.choice(syn.cfg.E, syn.cfg.k, replace=False) for _ in range(9)]).astype(np.int32)
+    w = O.round_bf16(rng.rand(9, syn.cfg.k).astype(np.float32))
+    ref = O.layer_reference(spec, np_(syn.x), ids=ids, w=w)
+    dsyn = syn.to(gpu)
+    layer = S.build_layer(dsyn)
+    out = layer.forward_routed(dsyn.x, torch.from_numpy(ids).to(gpu), torch.from_numpy(w).to(gpu))
+    assert_close(to_f32(out), ref["out"], what="routed layer")
+
+
+def test_layer_is_bitwise_deterministic(gpu):
+    syn = S.generate(S.SMALL["c3_fp8"], T=16, seed=3).to(gpu)
+    layer = S.build_layer(syn)
+    a = layer.forward(syn.x)
+    b = layer.forward(syn.x)
+    torch.cuda.synchronize()
+    assert torch.equal(a.view(torch.int16), b.view(torch.int16))
+
+
+@pytest.fixture(scope="module")
+def c3_full():
+    return S.generate(S.CONFIGS["c3_fp8"], T=64, seed=0)
+
+
+@pytest.mark.parametrize("T", [1, 4, 16, 64])
+def test_c3_fp8_full_shape_matches_oracle(gpu, c3_full, T):
+    base = c3_full
+    syn = S.SyntheticLayer(base.cfg, base.bank, base.gate_w, base.x[:T].contiguous(), shared=base.shared)
+    _run_and_check(syn, gpu)
+
+
+def test_c1_int8_full_shape_matches_oracle(gpu):
+    syn = S.generate(S.CONFIGS["c1_int8"], T=4, seed=0)
+    _run_and_check(syn, gpu)
+
+
+def test_expert_forward_single_slot(gpu):
+    syn = S.generate(S.SMALL["c3_fp8"], T=7, seed=9)
+    spec = oracle_spec(syn)
+    dsyn = syn.to(gpu)
+    layer = S.build_layer(dsyn)
+    for slot in (0, 5, syn.cfg.E - 1):
+        got = layer.expert_forward(slot, dsyn.x)
+        ref = O.expert_forward(spec["w13"], spec["w2"], slot, O.bf16_bits_to_f32(np_(syn.x)))
+        assert_close(to_f32(got), ref, what=f"expert {slot}")
+
+
+# ---------------------------------------------------------------- fused backend (dense banks)
+def _fused_ref(x, w1, w2, gating, k, renorm, act, on_input, wdt):
+    """Oracle for fused_moe.py:64-161 on dense banks."""
+    E, I2, H = w1.shape
+    xb = x.float().numpy()
+    ids, w = O.route(gating.float().numpy(), k, "softmax_topk_lowp", renorm,
+                     weight_dt="bf16" if x.dtype == torch.bfloat16 else "f32",
+                     prob_dt="bf16" if gating.dtype == torch.bfloat16 else "f32")
+    fmt = "bf16" if wdt == torch.bfloat16 else "fp32"
+    a = np_(w1) if fmt == "bf16" else w1.float().numpy()
+    b = np_(w2) if fmt == "bf16" else w2.float().numpy()
+    p13 = O.OracleProj(fmt, np.ascontiguousarray(a), I2, H)
+    p2 = O.OracleProj(fmt, np.ascontiguousarray(b), H, I2 // 2)
+    bf = x.dtype == torch.bfloat16
+    return O.moe_experts(p13, p2, xb, ids, w, E=E, act=act, h_bf16=bf, on_input=on_input, x_bf16=bf)
+
+
+@pytest.mark.parametrize("renorm,act,on_input", [(True, "silu", False), (True, "silu", True), (False, "gelu", False)])
+def test_fused_backend_fp32_tiny(gpu, renorm, act, on_input):
+    """tests/test_moe_fused.py:58-181 shapes (E=5, H=7, I=4, T=6, k=2) at atol 1e-5."""
+    from ftmoe.moe import create_moe_backend
+
+    g = torch.Generator().manual_seed(1)
+    E, H, I, T, K = 5, 7, 4, 6, 2
+    w1, w2 = torch.randn(E, 2 * I, H, generator=g), torch.randn(E, H, I, generator=g)
+    x, gating = torch.randn(T, H, generator=g), torch.randn(T, E, generator=g)
+    backend = create_moe_backend("fused")
+    got = backend.forward(x.to(gpu), w1.to(gpu), w2.to(gpu), gating.to(gpu), K, renorm, act, on_input)
+    ref = _fused_ref(x, w1, w2, gating, K, renorm, act, on_input, torch.float32)
+    np.testing.assert_allclose(got.cpu().numpy(), ref, atol=1e-5, rtol=1e-5)
+
+
+def test_fused_backend_bf16_serving_shape(gpu):
+    from ftmoe.moe import create_moe_backend
+
+    g = torch.Generator().manual_seed(2)
+    E, H, I, T, K = 64, 1024, 256, 12, 4
+    w1 = (torch.randn(E, 2 * I, H, generator=g) * 0.02).to(torch.bfloat16)
+    w2 = (torch.randn(E, H, I, generator=g) * 0.02).to(torch.bfloat16)
+    x = torch.randn(T, H, generator=g).to(torch.bfloat16)
+    gating = torch.randn(T, E, generator=g).to(torch.bfloat16)
+    got = create_moe_backend("fused").forward(x.to(gpu), w1.to(gpu), w2.to(gpu), gating.to(gpu), K, True, "silu", False)
+    ref = _fused_ref(x, w1, w2, gating, K, True, "silu", False, torch.bfloat16)
+    assert_close(got.float().cpu().numpy(), ref, ATOL, RTOL, what="fused bf16")
