@@ -17,8 +17,8 @@ bool dt_ok(int dt) { return dt == FTM_DT_F32 || dt == FTM_DT_F16 || dt == FTM_DT
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
-// Validate one projection for the MFMA engines.  `need_fast` is always true
-// today: every format path is the register-dequant MFMA engine.
+// Whether the register-dequant MFMA engine takes this projection (else the
+// generic scalar kernels run it).
 int check_proj(const ftm_proj* P) {
   if (P == nullptr || P->w == nullptr) return FTM_ERR_NULL;
   if (P->N <= 0 || P->K <= 0 || P->num_slots <= 0) return FTM_ERR_DIM;
@@ -124,6 +124,7 @@ int check_layer(const ftm_moe_layer* L, bool need_router) {
 // Whether the MFMA engine takes this layer (else the generic scalar path runs).
 bool fast_layer(const ftm_moe_layer* L, const void* x) {
   const int H = L->hidden, I = L->inter;
+  if (L->apply_router_weight_on_input) return false;  // scaled inputs: generic path
   if (check_proj(&L->w13) != FTM_OK || check_proj(&L->w2) != FTM_OK) return false;
   if (H % 64 != 0 || H / 64 > kMaxColTiles) return false;
   const int nt = L->w13.fmt == FTM_FMT_GPTQ_INT4 ? 64 : 16;

@@ -177,77 +177,95 @@ __device__ __forceinline__ u32x4 perm_gptq(u32x4 d) {
   return r;
 }
 
+// ---------------------------------------------------------------- buffer loads
+// Raw buffer loads return 0 for any byte offset at or past the descriptor's
+// size, so padding rows, rows past N and K tails are expressed as an
+// out-of-range offset instead of a branch: every load is issued
+// unconditionally and the waves keep many loads in flight.
+typedef __amdgpu_buffer_rsrc_t Rsrc;
+constexpr uint32_t kOOB = 0x80000000u;
+
+__device__ __forceinline__ Rsrc make_rsrc(const void* p, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, 0x00020000);
+}
+__device__ __forceinline__ u32x4 bload16(Rsrc r, uint32_t off) {
+  return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+}
+__device__ __forceinline__ uint32_t bload4(Rsrc r, uint32_t off) {
+  return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
+}
+__device__ __forceinline__ uint32_t bload2(Rsrc r, uint32_t off) {
+  return (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0);
+}
+__device__ __forceinline__ uint32_t bload1(Rsrc r, uint32_t off) {
+  return (uint32_t)__builtin_amdgcn_raw_buffer_load_b8(r, off, 0, 0);
+}
+// Scalars are fetched as the aligned 4-byte word holding element i (0 when
+// !ok) and decoded later, so no dtype-dependent code sits between the loads.
+__device__ __forceinline__ uint32_t bload_scalar_word(Rsrc r, uint32_t i, int dt, bool ok) {
+  const uint32_t byte = dt == FTM_DT_F32 ? 4u * i : 2u * i;
+  return bload4(r, ok ? (byte & ~3u) : kOOB);
+}
+// Branch-free (selects only): a branch here would separate an MFMA from the
+// VALU read of its result by a block boundary (see wave_gemm_kmajor).
+__device__ __forceinline__ float decode_scalar_word(uint32_t w, uint32_t i, int dt) {
+  const uint32_t h = (w >> ((i & 1u) * 16u)) & 0xffffu;
+  const float f16v = f16_to_f32((uint16_t)h);
+  const float bf16v = __uint_as_float(h << 16);
+  const float narrow = dt == FTM_DT_F16 ? f16v : bf16v;
+  return dt == FTM_DT_F32 ? __uint_as_float(w) : narrow;
+}
+
 // ---------------------------------------------------------------- A operand
-// Each lane owns one A row (its l % 16) of the current 16-row M tile.
-struct ARow {
-  const char* p;  // row base, NULL -> zero row
-  float mul;      // multiplier applied before rounding (router weight on input), 1 = none
-  int dt;         // FTM_DT_* of the row
+// Each lane owns one A row (its l % 16) of the current 16-row M tile: the
+// byte offset of that row in the activation buffer, or kOOB for a padding row.
+// AT is the activation dtype: bf16 feeds the MFMA directly; fp32 / fp16 are
+// split into bf16 hi + lo halves (16 significant bits) and cost two MFMAs.
+template <int AT>
+struct AType {
+  static constexpr bool kSplit = AT != FTM_DT_BF16;
+  static constexpr int kBytes = AT == FTM_DT_F32 ? 4 : 2;
 };
 
-// 8 consecutive activations starting at element kk, as bf16 hi (+ lo remainder
-// when the source is fp32/fp16, so hi + lo carries 16 significant bits).
-template <bool SPLIT>
-__device__ __forceinline__ void load_a8(const ARow& a, int kk, u32x4& hi, u32x4& lo) {
-  if (a.p == nullptr) {
-    hi = (u32x4){0, 0, 0, 0};
-    lo = hi;
-    return;
-  }
-  if (a.dt == FTM_DT_BF16 && a.mul == 1.0f) {
-    hi = *(const u32x4*)(a.p + 2 * (int64_t)kk);
+template <int AT>
+__device__ __forceinline__ void load_a8(Rsrc r, uint32_t row_off, int kk, u32x4& hi, u32x4& lo) {
+  if constexpr (AT == FTM_DT_BF16) {
+    hi = bload16(r, row_off + 2u * (uint32_t)kk);
     lo = (u32x4){0, 0, 0, 0};
-    return;
-  }
-  float v[8];
-  if (a.dt == FTM_DT_F32) {
-    u32x4 q0 = *(const u32x4*)(a.p + 4 * (int64_t)kk);
-    u32x4 q1 = *(const u32x4*)(a.p + 4 * (int64_t)kk + 16);
-    v[0] = __uint_as_float(q0.x); v[1] = __uint_as_float(q0.y);
-    v[2] = __uint_as_float(q0.z); v[3] = __uint_as_float(q0.w);
-    v[4] = __uint_as_float(q1.x); v[5] = __uint_as_float(q1.y);
-    v[6] = __uint_as_float(q1.z); v[7] = __uint_as_float(q1.w);
   } else {
-    u32x4 q = *(const u32x4*)(a.p + 2 * (int64_t)kk);
-    uint32_t w[4] = {q.x, q.y, q.z, q.w};
+    float v[8];
+    if constexpr (AT == FTM_DT_F32) {
+      const u32x4 q0 = bload16(r, row_off + 4u * (uint32_t)kk);
+      const u32x4 q1 = bload16(r, row_off + 4u * (uint32_t)kk + 16u);
+      v[0] = __uint_as_float(q0.x); v[1] = __uint_as_float(q0.y);
+      v[2] = __uint_as_float(q0.z); v[3] = __uint_as_float(q0.w);
+      v[4] = __uint_as_float(q1.x); v[5] = __uint_as_float(q1.y);
+      v[6] = __uint_as_float(q1.z); v[7] = __uint_as_float(q1.w);
+    } else {
+      const u32x4 q = bload16(r, row_off + 2u * (uint32_t)kk);
+      const uint32_t w[4] = {q.x, q.y, q.z, q.w};
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      if (a.dt == FTM_DT_BF16) {
-        v[2 * i] = bf16_to_f32(w[i] & 0xffffu);
-        v[2 * i + 1] = bf16_to_f32(w[i] >> 16);
-      } else {
+      for (int i = 0; i < 4; ++i) {
         v[2 * i] = f16_to_f32((uint16_t)(w[i] & 0xffffu));
         v[2 * i + 1] = f16_to_f32((uint16_t)(w[i] >> 16));
       }
     }
-  }
-  if (a.mul != 1.0f) {
-    // x * router_weight rounded to the activation dtype (fused_moe.py:139-140).
+    uint32_t h[4], l[4];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) v[i] = round_to(v[i] * a.mul, a.dt);
-  }
-  uint32_t h[4], l[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    h[i] = pack_bf16x2(v[2 * i], v[2 * i + 1]);
-    if (SPLIT) {
-      float r0 = v[2 * i] - bf16_to_f32(h[i] & 0xffffu);
-      float r1 = v[2 * i + 1] - bf16_to_f32(h[i] >> 16);
-      l[i] = pack_bf16x2(r0, r1);
-    } else {
-      l[i] = 0;
+    for (int i = 0; i < 4; ++i) {
+      h[i] = pack_bf16x2(v[2 * i], v[2 * i + 1]);
+      l[i] = pack_bf16x2(v[2 * i] - bf16_to_f32(h[i] & 0xffffu), v[2 * i + 1] - bf16_to_f32(h[i] >> 16));
     }
+    hi = (u32x4){h[0], h[1], h[2], h[3]};
+    lo = (u32x4){l[0], l[1], l[2], l[3]};
   }
-  hi = (u32x4){h[0], h[1], h[2], h[3]};
-  lo = (u32x4){l[0], l[1], l[2], l[3]};
 }
 
-// Sum of the 8 activations a lane feeds for element offset kk (fp32), used by
-// the GPTQ zero-point correction.
+// Sum of the 8 activations a lane feeds (hi + lo), for the GPTQ zero-point correction.
 __device__ __forceinline__ float sum_a8(u32x4 hi, u32x4 lo) {
   float s = 0.0f;
-  uint32_t h[4] = {hi.x, hi.y, hi.z, hi.w};
-  uint32_t l[4] = {lo.x, lo.y, lo.z, lo.w};
+  const uint32_t h[4] = {hi.x, hi.y, hi.z, hi.w};
+  const uint32_t l[4] = {lo.x, lo.y, lo.z, lo.w};
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     s += bf16_to_f32(h[i] & 0xffffu) + bf16_to_f32(l[i] & 0xffffu);
@@ -257,7 +275,7 @@ __device__ __forceinline__ float sum_a8(u32x4 hi, u32x4 lo) {
 }
 
 // ---------------------------------------------------------------- projection view
-// One slot of one projection, resolved to raw pointers.
+// One slot of one projection: raw pointers and the byte sizes of its banks.
 struct ProjSlot {
   const char* w;
   const char* s;
@@ -284,160 +302,176 @@ __device__ __forceinline__ ProjSlot proj_slot(const ftm_proj& P, int slot) {
 // ---------------------------------------------------------------- K-major engine
 // Formats whose weight rows are contiguous along K: FP8 block, INT8 packed,
 // MXFP4, BF16.  One "wave-load" = every lane loading 16 bytes of its row
-// (row = col0 + l%16, 4 lane groups side by side along K).
+// (row = col0 + l%16, the 4 lane groups side by side along K).
 template <int FMT>
 struct KMajor;
 
 template <>
 struct KMajor<FTM_FMT_FP8_BLOCK> {
-  static constexpr int kLaneK = 16, kLoadK = 64, kMfma = 2, kChunk = 8;
+  static constexpr int kLaneK = 16, kLoadK = 64, kMfma = 2;
   static constexpr bool kPostScale = true;
-  __device__ static int64_t row_bytes(int K) { return K; }
-  __device__ static int64_t elem_off(int kk) { return kk; }
+  __device__ static uint32_t row_bytes(int K) { return (uint32_t)K; }
+  __device__ static uint32_t elem_off(int kk) { return (uint32_t)kk; }
 };
 template <>
 struct KMajor<FTM_FMT_INT8_PACKED> {
-  static constexpr int kLaneK = 16, kLoadK = 64, kMfma = 2, kChunk = 8;
+  static constexpr int kLaneK = 16, kLoadK = 64, kMfma = 2;
   static constexpr bool kPostScale = true;
-  __device__ static int64_t row_bytes(int K) { return K; }
-  __device__ static int64_t elem_off(int kk) { return kk; }
+  __device__ static uint32_t row_bytes(int K) { return (uint32_t)K; }
+  __device__ static uint32_t elem_off(int kk) { return (uint32_t)kk; }
 };
 template <>
 struct KMajor<FTM_FMT_MXFP4> {
-  static constexpr int kLaneK = 32, kLoadK = 128, kMfma = 4, kChunk = 4;
+  static constexpr int kLaneK = 32, kLoadK = 128, kMfma = 4;
   static constexpr bool kPostScale = false;
-  __device__ static int64_t row_bytes(int K) { return K / 2; }
-  __device__ static int64_t elem_off(int kk) { return kk / 2; }
+  __device__ static uint32_t row_bytes(int K) { return (uint32_t)K / 2; }
+  __device__ static uint32_t elem_off(int kk) { return (uint32_t)kk / 2; }
 };
 template <>
 struct KMajor<FTM_FMT_BF16> {
-  static constexpr int kLaneK = 8, kLoadK = 32, kMfma = 1, kChunk = 8;
+  static constexpr int kLaneK = 8, kLoadK = 32, kMfma = 1;
   static constexpr bool kPostScale = false;
-  __device__ static int64_t row_bytes(int K) { return 2 * (int64_t)K; }
-  __device__ static int64_t elem_off(int kk) { return 2 * (int64_t)kk; }
+  __device__ static uint32_t row_bytes(int K) { return 2u * (uint32_t)K; }
+  __device__ static uint32_t elem_off(int kk) { return 2u * (uint32_t)kk; }
 };
 
-// Number of wave-loads covering K for a format.
-template <int FMT>
-__device__ __forceinline__ int kmajor_loads(int K) {
-  return (K + KMajor<FMT>::kLoadK - 1) / KMajor<FMT>::kLoadK;
-}
-
-// Wave-loads covering K for any format (GPTQ: 32 k per wave-load).
 template <int FMT>
 __device__ __forceinline__ int fmt_loads(int K) {
   if constexpr (FMT == FTM_FMT_GPTQ_INT4) {
     return (K + 31) / 32;
   } else {
-    return kmajor_loads<FMT>(K);
+    return (K + KMajor<FMT>::kLoadK - 1) / KMajor<FMT>::kLoadK;
   }
 }
 
-// acc[r] += sum over wave-loads [L_lo, L_hi) of A(16 x K) * W(rows col0[r]..+16)^T.
+// Wave-loads issued together before their MFMAs (registers vs loads in flight).
+template <int FMT, int NR, int AT>
+struct Chunk {
+  static constexpr int v = (KMajor<FMT>::kMfma >= 4 || AType<AT>::kSplit || NR > 1) ? 4 : 8;
+};
+
+// acc[r] += A(16 x K-range) * W(rows col0[r] .. +16)^T over wave-loads [L_lo, L_hi).
 // Rows >= N and k >= K read as zero.  For post-scaled formats the partial sum of
 // each quantisation group is multiplied by the group's fp32 scale before it
 // joins acc (FP8: one scale per 128x128 block; INT8: one per (row, group)).
-template <int FMT, int NR, bool SPLIT>
-__device__ __forceinline__ void wave_gemm_kmajor(const ProjSlot& W, const int (&col0)[NR], int L_lo,
-                                                 int L_hi, const ARow& ar, f32x4 (&acc)[NR]) {
+template <int FMT, int NR, int AT>
+__device__ __forceinline__ void wave_gemm_kmajor(const ProjSlot& W, const int (&col0)[NR], int L_lo, int L_hi,
+                                                 Rsrc ares, uint32_t arow, f32x4 (&acc)[NR]) {
   using F = KMajor<FMT>;
-  constexpr int CH = SPLIT ? (F::kChunk / 2 > 0 ? F::kChunk / 2 : 1) : F::kChunk;
+  constexpr bool SPLIT = AType<AT>::kSplit;
+  constexpr int CH = Chunk<FMT, NR, AT>::v;
   const int lane = threadIdx.x & 63;
   const int g = lane >> 4;
   const int rl = lane & 15;
   const int K = W.K;
-  const int64_t rb = F::row_bytes(K);
-
-  const char* wrow[NR];
-  const char* srow[NR];
+  const uint32_t rb = F::row_bytes(K);
+  const Rsrc wres = make_rsrc(W.w, rb * (uint32_t)W.N);
+  uint32_t woff[NR];
+  Rsrc sres = wres;
+  uint32_t soff[NR];
+  if constexpr (FMT == FTM_FMT_FP8_BLOCK) {
+    const int nkb = (K + W.group - 1) / W.group;
+    const int nrb = (W.N + W.group - 1) / W.group;
+    sres = make_rsrc(W.s, (uint32_t)(nrb * nkb) * (W.s_dt == FTM_DT_F32 ? 4u : 2u));
 #pragma unroll
-  for (int r = 0; r < NR; ++r) {
-    const int n = col0[r] + rl;
-    wrow[r] = (n < W.N) ? W.w + (int64_t)n * rb : nullptr;
-    srow[r] = nullptr;
-    if (FMT == FTM_FMT_FP8_BLOCK) {
-      // scale row of the 128-row block holding this 16-row tile
-      const int nkb = (K + W.group - 1) / W.group;
-      srow[r] = (col0[r] < W.N) ? W.s + (int64_t)(col0[r] / W.group) * nkb * (W.s_dt == FTM_DT_F32 ? 4 : 2)
-                                : nullptr;
-    } else if (FMT == FTM_FMT_INT8_PACKED) {
-      const int ng = K / W.group;
-      srow[r] = (n < W.N) ? W.s + (int64_t)n * ng * (W.s_dt == FTM_DT_F32 ? 4 : 2) : nullptr;
-    } else if (FMT == FTM_FMT_MXFP4) {
-      srow[r] = (n < W.N) ? W.s + (int64_t)n * (K / 32) : nullptr;
-    }
+    for (int r = 0; r < NR; ++r) soff[r] = (col0[r] < W.N) ? (uint32_t)((col0[r] / W.group) * nkb) : kOOB;
+  } else if constexpr (FMT == FTM_FMT_INT8_PACKED) {
+    const int ng = K / W.group;
+    sres = make_rsrc(W.s, (uint32_t)(W.N * ng) * (W.s_dt == FTM_DT_F32 ? 4u : 2u));
+#pragma unroll
+    for (int r = 0; r < NR; ++r) soff[r] = (col0[r] + rl < W.N) ? (uint32_t)((col0[r] + rl) * ng) : kOOB;
+  } else if constexpr (FMT == FTM_FMT_MXFP4) {
+    sres = make_rsrc(W.s, (uint32_t)W.N * (uint32_t)(K / 32));
+#pragma unroll
+    for (int r = 0; r < NR; ++r) soff[r] = (col0[r] + rl < W.N) ? (uint32_t)((col0[r] + rl) * (K / 32)) : kOOB;
   }
+#pragma unroll
+  for (int r = 0; r < NR; ++r) woff[r] = (col0[r] + rl < W.N) ? (uint32_t)(col0[r] + rl) * rb : kOOB;
 
   f32x4 tmp[NR];
 #pragma unroll
   for (int r = 0; r < NR; ++r) tmp[r] = (f32x4){0.f, 0.f, 0.f, 0.f};
 
+  // Post-scaled formats: wave-loads per quantisation group (the host requires
+  // group % kLoadK == 0 or a single group), and the group / position of the
+  // current wave-load, advanced by selects rather than per-load divisions.
+  const int lpg = F::kPostScale ? (W.group + F::kLoadK - 1) / F::kLoadK : 1;
+  int gcur = L_lo / lpg;
+  int gpos = L_lo - gcur * lpg;
+
   for (int Lc = L_lo; Lc < L_hi; Lc += CH) {
     u32x4 raw[NR][CH];
-    float msc[NR][CH];
+    float sc[NR][CH];      // MXFP4: e8m0 factor of the lane's block
+    uint32_t scw[NR][CH];  // FP8 / INT8: raw scale word of the wave-load's group
+    int grp_b[CH];         // FP8 / INT8: group of wave-load b
+    bool last_b[CH];       // FP8 / INT8: wave-load b ends its group or the range
     u32x4 ahi[CH][F::kMfma], alo[CH][F::kMfma];
 #pragma unroll
     for (int b = 0; b < CH; ++b) {
       const int L = Lc + b;
       const int kk = L * F::kLoadK + F::kLaneK * g;
       const bool kok = (L < L_hi) && (kk < K);
+      if constexpr (F::kPostScale) {
+        const bool wrap = gpos == lpg - 1;
+        grp_b[b] = gcur;
+        last_b[b] = wrap | (L + 1 == L_hi);
+        gpos = wrap ? 0 : gpos + 1;
+        gcur += wrap ? 1 : 0;
+      }
 #pragma unroll
       for (int r = 0; r < NR; ++r) {
-        raw[r][b] = (kok && wrow[r]) ? *(const u32x4*)(wrow[r] + F::elem_off(kk)) : (u32x4){0, 0, 0, 0};
-        if (FMT == FTM_FMT_MXFP4)
-          msc[r][b] = (kok && srow[r]) ? e8m0_to_f32((uint8_t)srow[r][kk / 32]) : 0.0f;
-      }
-#pragma unroll
-      for (int q = 0; q < F::kMfma; ++q) {
-        if (kok) {
-          load_a8<SPLIT>(ar, kk + 8 * q, ahi[b][q], alo[b][q]);
-        } else {
-          ahi[b][q] = (u32x4){0, 0, 0, 0};
-          alo[b][q] = ahi[b][q];
+        raw[r][b] = bload16(wres, kok ? woff[r] + F::elem_off(kk) : kOOB);
+        if constexpr (FMT == FTM_FMT_MXFP4) {
+          sc[r][b] = e8m0_to_f32(bload1(sres, kok ? soff[r] + (uint32_t)(kk / 32) : kOOB));
+        } else if constexpr (F::kPostScale) {
+          scw[r][b] = bload_scalar_word(sres, soff[r] + (uint32_t)grp_b[b], W.s_dt, L < L_hi && soff[r] != kOOB);
         }
       }
+#pragma unroll
+      for (int q = 0; q < F::kMfma; ++q) load_a8<AT>(ares, kok ? arow : kOOB, kk + 8 * q, ahi[b][q], alo[b][q]);
     }
+    // Wave-loads past L_hi read zeros, so the MFMAs below are unconditional
+    // (no branch the compiler could sink the loads into).
 #pragma unroll
     for (int b = 0; b < CH; ++b) {
       const int L = Lc + b;
-      if (L >= L_hi) break;
 #pragma unroll
       for (int q = 0; q < F::kMfma; ++q) {
 #pragma unroll
         for (int r = 0; r < NR; ++r) {
           u32x4 bq;
-          if (FMT == FTM_FMT_FP8_BLOCK) {
+          if constexpr (FMT == FTM_FMT_FP8_BLOCK) {
             bq = q == 0 ? fp8x8_to_bf16(raw[r][b].x, raw[r][b].y) : fp8x8_to_bf16(raw[r][b].z, raw[r][b].w);
-          } else if (FMT == FTM_FMT_INT8_PACKED) {
+          } else if constexpr (FMT == FTM_FMT_INT8_PACKED) {
             bq = q == 0 ? i8x8_to_bf16(raw[r][b].x, raw[r][b].y) : i8x8_to_bf16(raw[r][b].z, raw[r][b].w);
-          } else if (FMT == FTM_FMT_MXFP4) {
+          } else if constexpr (FMT == FTM_FMT_MXFP4) {
             const uint32_t wq = q == 0 ? raw[r][b].x : q == 1 ? raw[r][b].y : q == 2 ? raw[r][b].z : raw[r][b].w;
-            bq = fp4x8_to_bf16(wq, msc[r][b]);
+            bq = fp4x8_to_bf16(wq, sc[r][b]);
           } else {
             bq = raw[r][b];
           }
           tmp[r] = mfma_bf16(ahi[b][q], bq, tmp[r]);
-          if (SPLIT) tmp[r] = mfma_bf16(alo[b][q], bq, tmp[r]);
+          if constexpr (SPLIT) tmp[r] = mfma_bf16(alo[b][q], bq, tmp[r]);
         }
       }
-      if (F::kPostScale) {
-        const int k_first = L * F::kLoadK;
-        const int grp = k_first / W.group;
-        const bool last = (L + 1 == L_hi) || (((L + 1) * F::kLoadK) / W.group != grp);
-        if (last) {
+      if constexpr (F::kPostScale) {
+        // End of a quantisation group (or of the wave's range): fold in its
+        // scale.  Straight-line code on purpose: with a branch between the
+        // MFMAs above and these reads of tmp, the gfx950 compiler has placed
+        // too few wait states on the taken path and read stale accumulators.
+        const bool fold = last_b[b] & (L < L_hi);
 #pragma unroll
-          for (int r = 0; r < NR; ++r) {
-            // FP8: one scale for the whole 16-row tile; INT8: the scale of row
-            // col0 + l%16, which is exactly the D column this lane holds.
-            const float s = (srow[r] != nullptr) ? load_scalar(srow[r], grp, W.s_dt) : 0.0f;
-            acc[r] += tmp[r] * s;
-            tmp[r] = (f32x4){0.f, 0.f, 0.f, 0.f};
-          }
+        for (int r = 0; r < NR; ++r) {
+          const float s_grp = decode_scalar_word(scw[r][b], soff[r] + (uint32_t)grp_b[b], W.s_dt);
+          const float f = fold ? s_grp : 0.0f;
+          acc[r] += tmp[r] * f;
+          const float keep = last_b[b] ? 0.0f : 1.0f;
+          tmp[r] *= keep;
         }
       }
     }
   }
-  if (!F::kPostScale) {
+  if constexpr (!F::kPostScale) {
 #pragma unroll
     for (int r = 0; r < NR; ++r) acc[r] += tmp[r];
   }
@@ -448,11 +482,14 @@ __device__ __forceinline__ void wave_gemm_kmajor(const ProjSlot& W, const int (&
 // reads packed row 4L+g (k = 32L + 8g .. +8) for columns col0 + 4*(l%16) + c,
 // c = 0..3 (16 bytes).  A wave therefore produces 64 columns as 4 interleaved
 // MFMA sub-tiles: sub-tile c, MFMA column j <-> output column col0 + 4j + c.
-// Per quantisation group the zero point and the +128 decode bias are removed
-// with  acc += s * (tmp - (128 + zp) * sum_k x_k)  (gptq_linear.py:88-99).
-template <int NR, bool SPLIT>
-__device__ __forceinline__ void wave_gemm_gptq(const ProjSlot& W, const int (&col0)[NR], int L_lo, int L_hi,
-                                               const ARow& ar, f32x4 (&acc)[NR][4]) {
+// The wave walks whole quantisation groups [grp_lo, grp_hi); each group's
+// scales and zero word are loaded with its first weights, and at the group's
+// end the zero point and the +128 decode bias are removed in fp32:
+//   acc += s * (tmp - (128 + zp) * sum_k x_k)        (gptq_linear.py:88-99)
+template <int NR, int AT>
+__device__ __forceinline__ void wave_gemm_gptq(const ProjSlot& W, const int (&col0)[NR], int grp_lo, int grp_hi,
+                                               Rsrc ares, uint32_t arow, f32x4 (&acc)[NR][4]) {
+  constexpr bool SPLIT = AType<AT>::kSplit;
   constexpr int CH = 4;
   const int lane = threadIdx.x & 63;
   const int g = lane >> 4;
@@ -461,92 +498,91 @@ __device__ __forceinline__ void wave_gemm_gptq(const ProjSlot& W, const int (&co
   const int K = W.K;
   const int G = W.group;
   const int ngroups = (K + G - 1) / G;
+  const int nL = (K + 31) / 32;
+  const uint32_t sbytes = W.s_dt == FTM_DT_F32 ? 4u : 2u;
+  const Rsrc wres = make_rsrc(W.w, (uint32_t)(K / 8) * (uint32_t)N * 4u);
+  const Rsrc zres = make_rsrc(W.z, (uint32_t)ngroups * (uint32_t)(N / 8) * 4u);
+  const Rsrc sres = make_rsrc(W.s, (uint32_t)ngroups * (uint32_t)N * sbytes);
+  uint32_t ncol[NR];
+#pragma unroll
+  for (int r = 0; r < NR; ++r) ncol[r] = (col0[r] + 4 * rl < N) ? (uint32_t)(col0[r] + 4 * rl) : kOOB;
 
-  f32x4 tmp[NR][4];
+  for (int grp = grp_lo; grp < grp_hi; ++grp) {
+    const int L0 = grp * G / 32;
+    const int L1 = min((grp + 1) * G / 32, nL);
+    // this group's 4 scales and zero word per row tile (16 bytes covers 4 fp32 or 8 fp16 scales)
+    u32x4 scv[NR];
+    uint32_t zw[NR];
 #pragma unroll
-  for (int r = 0; r < NR; ++r)
+    for (int r = 0; r < NR; ++r) {
+      const bool ok = ncol[r] != kOOB;
+      scv[r] = bload16(sres, ok ? ((uint32_t)grp * (uint32_t)N + ncol[r]) * sbytes : kOOB);
+      zw[r] = bload4(zres, ok ? ((uint32_t)grp * (uint32_t)(N / 8) + ncol[r] / 8) * 4u : kOOB);
+    }
+    f32x4 tmp[NR][4];
 #pragma unroll
-    for (int c = 0; c < 4; ++c) tmp[r][c] = (f32x4){0.f, 0.f, 0.f, 0.f};
-  float xs = 0.0f;  // this lane's partial sum of x over the current group
-
-  for (int Lc = L_lo; Lc < L_hi; Lc += CH) {
-    u32x4 raw[NR][CH];
-    u32x4 ahi[CH], alo[CH];
+    for (int r = 0; r < NR; ++r)
 #pragma unroll
-    for (int b = 0; b < CH; ++b) {
-      const int L = Lc + b;
-      const int prow = 4 * L + g;
-      const bool kok = (L < L_hi) && (8 * prow < K);
+      for (int c = 0; c < 4; ++c) tmp[r][c] = (f32x4){0.f, 0.f, 0.f, 0.f};
+    float xs = 0.0f;
+    for (int Lc = L0; Lc < L1; Lc += CH) {
+      u32x4 raw[NR][CH];
+      u32x4 ahi[CH], alo[CH];
 #pragma unroll
-      for (int r = 0; r < NR; ++r) {
-        const int n = col0[r] + 4 * rl;
-        raw[r][b] = (kok && n < N) ? *(const u32x4*)(W.w + ((int64_t)prow * N + n) * 4) : (u32x4){0, 0, 0, 0};
-      }
-      if (kok) {
+      for (int b = 0; b < CH; ++b) {
+        const int L = Lc + b;
+        const int prow = 4 * L + g;
+        const bool kok = (L < L1) && (8 * prow < K);
+#pragma unroll
+        for (int r = 0; r < NR; ++r)
+          raw[r][b] = bload16(wres, (kok && ncol[r] != kOOB) ? ((uint32_t)prow * (uint32_t)N + ncol[r]) * 4u : kOOB);
         u32x4 h, l;
-        load_a8<SPLIT>(ar, 8 * prow, h, l);
+        load_a8<AT>(ares, kok ? arow : kOOB, 8 * prow, h, l);
         ahi[b] = perm_gptq(h);
         alo[b] = perm_gptq(l);
-      } else {
-        ahi[b] = (u32x4){0, 0, 0, 0};
-        alo[b] = ahi[b];
       }
-    }
+      // wave-loads past the group read zeros: x sums and MFMAs stay unconditional
 #pragma unroll
-    for (int b = 0; b < CH; ++b) {
-      const int L = Lc + b;
-      if (L >= L_hi) break;
-      xs += sum_a8(ahi[b], alo[b]);
+      for (int b = 0; b < CH; ++b) {
+        xs += sum_a8(ahi[b], alo[b]);
 #pragma unroll
-      for (int r = 0; r < NR; ++r) {
-        const uint32_t wv[4] = {raw[r][b].x, raw[r][b].y, raw[r][b].z, raw[r][b].w};
+        for (int r = 0; r < NR; ++r) {
+          const uint32_t wv[4] = {raw[r][b].x, raw[r][b].y, raw[r][b].z, raw[r][b].w};
 #pragma unroll
-        for (int c = 0; c < 4; ++c) {
-          const u32x4 bq = gptq_word_to_bf16(wv[c]);
-          tmp[r][c] = mfma_bf16(ahi[b], bq, tmp[r][c]);
-          if (SPLIT) tmp[r][c] = mfma_bf16(alo[b], bq, tmp[r][c]);
-        }
-      }
-      const int grp = (32 * L) / G;
-      const bool last = (L + 1 == L_hi) || ((32 * (L + 1)) / G != grp);
-      if (last) {
-        // Row sums of x over this group: reduce the 4 lane groups (same l%16).
-        float sx = xs;
-        sx += __shfl_xor(sx, 16);
-        sx += __shfl_xor(sx, 32);
-        // D row i = 4*(l/16) + rr lives at lane i's sum.
-        float sxr[4];
-#pragma unroll
-        for (int rr = 0; rr < 4; ++rr) sxr[rr] = __shfl(sx, 4 * g + rr);
-        xs = 0.0f;
-        if (grp < ngroups) {
-#pragma unroll
-          for (int r = 0; r < NR; ++r) {
-            const int nb = col0[r] + 4 * rl;  // columns nb + c
-            float sc[4], zp[4];
-            if (nb < N) {
-              const uint32_t zw = *(const uint32_t*)(W.z + ((int64_t)grp * (N / 8) + nb / 8) * 4);
-#pragma unroll
-              for (int c = 0; c < 4; ++c) {
-                sc[c] = load_scalar(W.s, (int64_t)grp * N + nb + c, W.s_dt);
-                zp[c] = (float)(((zw >> (4 * ((nb + c) & 7))) & 0xfu) + 1u);
-              }
-            } else {
-#pragma unroll
-              for (int c = 0; c < 4; ++c) { sc[c] = 0.0f; zp[c] = 0.0f; }
-            }
-#pragma unroll
-            for (int c = 0; c < 4; ++c) {
-              f32x4 corr;
-              corr.x = tmp[r][c].x - (128.0f + zp[c]) * sxr[0];
-              corr.y = tmp[r][c].y - (128.0f + zp[c]) * sxr[1];
-              corr.z = tmp[r][c].z - (128.0f + zp[c]) * sxr[2];
-              corr.w = tmp[r][c].w - (128.0f + zp[c]) * sxr[3];
-              acc[r][c] += corr * sc[c];
-              tmp[r][c] = (f32x4){0.f, 0.f, 0.f, 0.f};
-            }
+          for (int c = 0; c < 4; ++c) {
+            const u32x4 bq = gptq_word_to_bf16(wv[c]);
+            tmp[r][c] = mfma_bf16(ahi[b], bq, tmp[r][c]);
+            if constexpr (SPLIT) tmp[r][c] = mfma_bf16(alo[b], bq, tmp[r][c]);
           }
         }
+      }
+    }
+    // Row sums of x over this group: reduce the 4 lane groups (same l%16), then
+    // fetch the sums of the D rows this lane holds (row 4g+rr lives at lane 4g+rr).
+    float sx = xs;
+    sx += __shfl_xor(sx, 16);
+    sx += __shfl_xor(sx, 32);
+    float sxr[4];
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) sxr[rr] = __shfl(sx, 4 * g + rr);
+#pragma unroll
+    for (int r = 0; r < NR; ++r) {
+      const uint32_t sw[4] = {scv[r].x, scv[r].y, scv[r].z, scv[r].w};
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        float sc;
+        if (sbytes == 4u) sc = __uint_as_float(sw[c]);
+        else {
+          const uint32_t h = (sw[c >> 1] >> (16 * (c & 1))) & 0xffffu;
+          sc = W.s_dt == FTM_DT_F16 ? f16_to_f32((uint16_t)h) : bf16_to_f32(h);
+        }
+        const float zp = (float)(((zw[r] >> (4 * ((ncol[r] + c) & 7))) & 0xfu) + 1u);
+        f32x4 corr;
+        corr.x = tmp[r][c].x - (128.0f + zp) * sxr[0];
+        corr.y = tmp[r][c].y - (128.0f + zp) * sxr[1];
+        corr.z = tmp[r][c].z - (128.0f + zp) * sxr[2];
+        corr.w = tmp[r][c].w - (128.0f + zp) * sxr[3];
+        acc[r][c] += corr * sc;
       }
     }
   }

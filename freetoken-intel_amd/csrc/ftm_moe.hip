@@ -1,14 +1,14 @@
 // ftm_moe.hip -- the fused quantized MoE layer on gfx950.
 //
-// One layer forward is four launches on the caller's stream:
+// One layer forward is five launches on the caller's stream:
 //   k_router   router GEMV  logits[t, e] = round(x[t] . G[e] (+ b[e]))      (one WG per expert row)
 //   k_topk     softmax / top-k / renorm per token (one wave per token), then
 //              the last-arriving WG compacts the routed experts (ascending id)
 //   k_stage_a  per (routed expert, 16-channel tile): gate and up rows of w13,
 //              K split over the 4 waves, fused activation -> h (act dtype)
 //   k_stage_b  per (expert, 64-column tile of H): w2 . h, bias, router weight,
-//              written to the [T, k(+1), H] fp32 slot buffer; the last WG to
-//              finish a column tile sums its k(+1) slots in fixed order -> out
+//              written to the [T, k(+1), H] fp32 slot buffer
+//   k_combine  out[t] = sum of the token's k(+1) slots in fixed order
 // The shared expert (dense bf16) rides along as one more expert in stages A/B.
 // No float atomics anywhere: the output is bitwise reproducible run to run.
 //
@@ -308,28 +308,38 @@ __device__ __forceinline__ ProjSlot shared_view(const void* w, int N, int K) {
 }
 
 // ============================================================== stage A (w13 + act)
-template <int EFMT, bool SPLIT, int NT>
+// Split-K over the 4 waves: wave-load range of wave w (GPTQ: whole groups).
+template <int EFMT>
+__device__ __forceinline__ void wave_k_range(const ProjSlot& W, int wave, int nwaves, int& lo, int& hi) {
+  if constexpr (EFMT == FTM_FMT_GPTQ_INT4) {
+    const int ng = (W.K + W.group - 1) / W.group;
+    lo = wave * ng / nwaves;
+    hi = (wave + 1) * ng / nwaves;
+  } else {
+    const int nL = fmt_loads<EFMT>(W.K);
+    lo = wave * nL / nwaves;
+    hi = (wave + 1) * nL / nwaves;
+  }
+}
+
+template <int EFMT, int AT, int NT>
 __device__ void stage_a_body(const LayerArgs& a, const ProjSlot& W, int Iu, int it, int cnt,
                              const int32_t* list, int shared_col, f32x4* red) {
   constexpr bool kG = EFMT == FTM_FMT_GPTQ_INT4;
   constexpr int NSUB = kG ? 4 : 1;
+  constexpr int XB = AType<AT>::kBytes;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int H = a.L.hidden, KP = a.KP;
-  const int nL = fmt_loads<EFMT>(H);
-  const int L_lo = wave * nL / 4, L_hi = (wave + 1) * nL / 4;
+  int lo, hi;
+  wave_k_range<EFMT>(W, wave, 4, lo, hi);
   const int col0[2] = {it * NT, Iu + it * NT};
-  const int xsz = dt_size(a.L.act_dtype);
+  const Rsrc xres = make_rsrc(a.x, (uint32_t)a.T * (uint32_t)H * XB);
   for (int mb = 0; mb < cnt; mb += 16) {
-    ARow ar;
-    ar.dt = a.L.act_dtype;
-    ar.mul = 1.0f;
-    ar.p = nullptr;
     const int m = mb + (lane & 15);
+    uint32_t arow = kOOB;
     if (m < cnt) {
       const int p = list ? list[m] : m * KP + shared_col;
-      const int t = p / KP;
-      ar.p = (const char*)a.x + (size_t)t * H * xsz;
-      if (a.L.apply_router_weight_on_input && list) ar.mul = a.wts[p];
+      arow = (uint32_t)(p / KP) * (uint32_t)H * XB;
     }
     if constexpr (kG) {
       f32x4 acc[2][4];
@@ -337,14 +347,14 @@ __device__ void stage_a_body(const LayerArgs& a, const ProjSlot& W, int Iu, int 
       for (int r = 0; r < 2; ++r)
 #pragma unroll
         for (int c = 0; c < 4; ++c) acc[r][c] = (f32x4){0.f, 0.f, 0.f, 0.f};
-      wave_gemm_gptq<2, SPLIT>(W, col0, L_lo, L_hi, ar, acc);
+      wave_gemm_gptq<2, AT>(W, col0, lo, hi, xres, arow, acc);
 #pragma unroll
       for (int r = 0; r < 2; ++r)
 #pragma unroll
         for (int c = 0; c < 4; ++c) red[((wave * 2 + r) * NSUB + c) * 64 + lane] = acc[r][c];
     } else {
       f32x4 acc[2] = {(f32x4){0.f, 0.f, 0.f, 0.f}, (f32x4){0.f, 0.f, 0.f, 0.f}};
-      wave_gemm_kmajor<EFMT, 2, SPLIT>(W, col0, L_lo, L_hi, ar, acc);
+      wave_gemm_kmajor<EFMT, 2, AT>(W, col0, lo, hi, xres, arow, acc);
 #pragma unroll
       for (int r = 0; r < 2; ++r) red[(wave * 2 + r) * 64 + lane] = acc[r];
     }
@@ -368,14 +378,14 @@ __device__ void stage_a_body(const LayerArgs& a, const ProjSlot& W, int Iu, int 
         }
         const float h = act_fn(a.L.act, gs, us, a.L.swiglu_alpha, a.L.swiglu_limit);
         const int p = list ? list[m2] : m2 * KP + shared_col;
-        store_scalar(a.hbuf, (size_t)p * a.Imax + ch, a.L.act_dtype, h);
+        store_scalar(a.hbuf, (size_t)p * a.Imax + ch, AT, h);
       }
     }
     __syncthreads();
   }
 }
 
-template <int FMT, bool SPLIT>
+template <int FMT, int AT>
 __global__ __launch_bounds__(kBlock) void k_stage_a(const LayerArgs a) {
   constexpr bool kG = FMT == FTM_FMT_GPTQ_INT4;
   constexpr int NT = kG ? 64 : 16;
@@ -393,45 +403,48 @@ __global__ __launch_bounds__(kBlock) void k_stage_a(const LayerArgs a) {
       return;
     }
     const ProjSlot W = proj_slot(a.L.w13, slot);
-    stage_a_body<FMT, SPLIT, NT>(a, W, I, it, cnt, a.lists + (size_t)e * a.T, 0, red);
+    stage_a_body<FMT, AT, NT>(a, W, I, it, cnt, a.lists + (size_t)e * a.T, 0, red);
   } else {
     item -= nRouted * tilesR;
     const int Is = a.L.shared_inter;
     if (Is <= 0 || item >= Is / 16) return;
     const ProjSlot W = shared_view(a.L.shared_w13, 2 * Is, a.L.hidden);
-    stage_a_body<FTM_FMT_BF16, SPLIT, 16>(a, W, Is, item, a.T, nullptr, a.L.topk, red);
+    stage_a_body<FTM_FMT_BF16, AT, 16>(a, W, Is, item, a.T, nullptr, a.L.topk, red);
   }
 }
 
-// ============================================================== stage B (w2 + combine)
-template <int EFMT, bool SPLIT>
+// ============================================================== stage B (w2 -> slot buffer)
+// 64 output columns per workgroup.  K-major formats: 4 waves side by side,
+// 16 columns each, full K.  GPTQ: one 64-column wave tile, K split over the
+// 4 waves on group edges and reduced through LDS.
+template <int EFMT, int AT>
 __device__ void stage_b_body(const LayerArgs& a, const ProjSlot& W, int cnt, const int32_t* list,
                              int shared_col, int nt, f32x4* red) {
   constexpr bool kG = EFMT == FTM_FMT_GPTQ_INT4;
+  constexpr int XB = AType<AT>::kBytes;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int Ku = W.K;
   const int H = a.L.hidden, KP = a.KP;
-  const int nL = fmt_loads<EFMT>(Ku);
-  const int L_lo = kG ? wave * nL / 4 : 0;
-  const int L_hi = kG ? (wave + 1) * nL / 4 : nL;
+  int lo, hi;
+  if (kG) {
+    wave_k_range<EFMT>(W, wave, 4, lo, hi);
+  } else {
+    lo = 0;
+    hi = fmt_loads<EFMT>(W.K);
+  }
   const int col0[1] = {kG ? nt * 64 : nt * 64 + 16 * wave};
-  const int hsz = dt_size(a.L.act_dtype);
-  const bool weighted = !(a.L.apply_router_weight_on_input && list);
+  const Rsrc hres = make_rsrc(a.hbuf, (uint32_t)a.T * (uint32_t)KP * (uint32_t)a.Imax * XB);
   for (int mb = 0; mb < cnt; mb += 16) {
-    ARow ar;
-    ar.dt = a.L.act_dtype;
-    ar.mul = 1.0f;
-    ar.p = nullptr;
     const int m = mb + (lane & 15);
+    uint32_t arow = kOOB;
     if (m < cnt) {
       const int p = list ? list[m] : m * KP + shared_col;
-      ar.p = a.hbuf + (size_t)p * a.Imax * hsz;
+      arow = (uint32_t)p * (uint32_t)a.Imax * XB;
     }
     if constexpr (kG) {
       f32x4 acc[1][4];
 #pragma unroll
       for (int c = 0; c < 4; ++c) acc[0][c] = (f32x4){0.f, 0.f, 0.f, 0.f};
-      wave_gemm_gptq<1, SPLIT>(W, col0, L_lo, L_hi, ar, acc);
+      wave_gemm_gptq<1, AT>(W, col0, lo, hi, hres, arow, acc);
 #pragma unroll
       for (int c = 0; c < 4; ++c) red[(wave * 4 + c) * 64 + lane] = acc[0][c];
       __syncthreads();
@@ -445,14 +458,14 @@ __device__ void stage_b_body(const LayerArgs& a, const ProjSlot& W, int cnt, con
         if (m2 < cnt && n < H) {
           const int p = list ? list[m2] : m2 * KP + shared_col;
           if (W.bias != nullptr) y += load_scalar(W.bias, n, W.bias_dt);
-          if (weighted) y *= a.wts[p];
+          y *= a.wts[p];  // router weight (routed) or sigmoid gate (shared)
           a.ybuf[(size_t)p * H + n] = y;
         }
       }
       __syncthreads();
     } else {
       f32x4 acc[1] = {(f32x4){0.f, 0.f, 0.f, 0.f}};
-      wave_gemm_kmajor<EFMT, 1, SPLIT>(W, col0, L_lo, L_hi, ar, acc);
+      wave_gemm_kmajor<EFMT, 1, AT>(W, col0, lo, hi, hres, arow, acc);
       const int n = col0[0] + (lane & 15);
 #pragma unroll
       for (int rr = 0; rr < 4; ++rr) {
@@ -461,7 +474,7 @@ __device__ void stage_b_body(const LayerArgs& a, const ProjSlot& W, int cnt, con
           const int p = list ? list[m2] : m2 * KP + shared_col;
           float y = acc[0][rr];
           if (W.bias != nullptr) y += load_scalar(W.bias, n, W.bias_dt);
-          if (weighted) y *= a.wts[p];
+          y *= a.wts[p];  // router weight (routed) or sigmoid gate (shared)
           a.ybuf[(size_t)p * H + n] = y;
         }
       }
@@ -469,10 +482,9 @@ __device__ void stage_b_body(const LayerArgs& a, const ProjSlot& W, int cnt, con
   }
 }
 
-template <int FMT, bool SPLIT>
+template <int FMT, int AT>
 __global__ __launch_bounds__(kBlock) void k_stage_b(const LayerArgs a) {
   __shared__ f32x4 red[4 * 4 * 64];
-  __shared__ int s_last;
   const int H = a.L.hidden;
   const int tiles = H / 64;
   const int nU = a.ctrl[kCtrlNU], nRouted = a.ctrl[kCtrlNRouted];
@@ -491,30 +503,34 @@ __global__ __launch_bounds__(kBlock) void k_stage_b(const LayerArgs a) {
       if (threadIdx.x == 0) atomicOr(&a.ctrl[kCtrlError], 1);
     } else {
       const ProjSlot W = proj_slot(a.L.w2, slot);
-      stage_b_body<FMT, SPLIT>(a, W, cnt, list, 0, nt, red);
+      stage_b_body<FMT, AT>(a, W, cnt, list, 0, nt, red);
     }
   } else {
     const ProjSlot W = shared_view(a.L.shared_w2, H, a.L.shared_inter);
-    stage_b_body<FTM_FMT_BF16, SPLIT>(a, W, a.T, nullptr, a.L.topk, nt, red);
+    stage_b_body<FTM_FMT_BF16, AT>(a, W, a.T, nullptr, a.L.topk, nt, red);
   }
-  // ---- deterministic combine: the last of the nU workgroups of this column
-  // tile sums the KP slots of every token in slot order.
-  int32_t* tilecnt = a.ctrl + kCtrlTileCnt;
-  __threadfence();
-  __syncthreads();
-  if (threadIdx.x == 0) s_last = (atomicAdd(&tilecnt[nt], 1) == nU - 1);
-  __syncthreads();
-  if (!s_last) return;
-  __threadfence();
-  const int KP = a.KP;
-  for (int idx = threadIdx.x; idx < a.T * 64; idx += kBlock) {
-    const int t = idx / 64, n = nt * 64 + (idx % 64);
-    const float* yb = a.ybuf + (size_t)t * KP * H + n;
-    float s = 0.0f;
-    for (int j = 0; j < KP; ++j) s += __builtin_nontemporal_load(yb + (size_t)j * H);
-    store_scalar(a.out, (size_t)t * H + n, a.L.act_dtype, s);
+}
+
+// ============================================================== combine
+// out[t, n] = sum_j ybuf[t*KP + j, n] in slot order (deterministic, no atomics).
+template <int AT>
+__global__ __launch_bounds__(kBlock) void k_combine(const LayerArgs a) {
+  const int H = a.L.hidden, KP = a.KP;
+  const int H4 = H / 4;
+  const int idx = blockIdx.x * kBlock + threadIdx.x;
+  if (idx >= a.T * H4) return;
+  const int t = idx / H4, n4 = idx % H4;
+  const f32x4* yb = (const f32x4*)(a.ybuf + (size_t)t * KP * H) + n4;
+  f32x4 s = yb[0];
+  for (int j = 1; j < KP; ++j) s += yb[(size_t)j * H4];
+  if constexpr (AT == FTM_DT_F32) {
+    ((f32x4*)a.out)[(size_t)t * H4 + n4] = s;
+  } else {
+    u32x2 o;
+    o.x = pack_bf16x2(s.x, s.y);
+    o.y = pack_bf16x2(s.z, s.w);
+    ((u32x2*)a.out)[(size_t)t * H4 + n4] = o;
   }
-  if (threadIdx.x == 0) tilecnt[nt] = 0;
 }
 
 // ============================================================== single projection
@@ -522,30 +538,33 @@ struct LinArgs {
   ftm_proj P;
   int slot;
   const void* x;
-  int x_dt, M;
+  int M;
   void* out;
   int out_dt;
   const void* bias;
   int bias_dt, final_dt;
 };
 
-template <int FMT, bool SPLIT>
+template <int FMT, int AT>
 __global__ __launch_bounds__(kBlock) void k_linear(const LinArgs a) {
   constexpr bool kG = FMT == FTM_FMT_GPTQ_INT4;
+  constexpr int XB = AType<AT>::kBytes;
   __shared__ f32x4 red[4 * 4 * 64];
   const ProjSlot W = proj_slot(a.P, a.slot);
   const int N = W.N, K = W.K;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int nt = blockIdx.x, mt = blockIdx.y;
-  const int nL = fmt_loads<FMT>(K);
-  const int L_lo = kG ? wave * nL / 4 : 0;
-  const int L_hi = kG ? (wave + 1) * nL / 4 : nL;
+  int lo, hi;
+  if (kG) {
+    wave_k_range<FMT>(W, wave, 4, lo, hi);
+  } else {
+    lo = 0;
+    hi = fmt_loads<FMT>(K);
+  }
   const int col0[1] = {kG ? nt * 64 : nt * 64 + 16 * wave};
-  ARow ar;
-  ar.dt = a.x_dt;
-  ar.mul = 1.0f;
+  const Rsrc xres = make_rsrc(a.x, (uint32_t)a.M * (uint32_t)K * XB);
   const int m = mt * 16 + (lane & 15);
-  ar.p = (m < a.M) ? (const char*)a.x + (size_t)m * K * dt_size(a.x_dt) : nullptr;
+  const uint32_t arow = (m < a.M) ? (uint32_t)m * (uint32_t)K * XB : kOOB;
   auto emit = [&](int m2, int n, float y) {
     if (m2 < a.M && n < N) {
       float v = round_to(y, a.out_dt);
@@ -557,7 +576,7 @@ __global__ __launch_bounds__(kBlock) void k_linear(const LinArgs a) {
     f32x4 acc[1][4];
 #pragma unroll
     for (int c = 0; c < 4; ++c) acc[0][c] = (f32x4){0.f, 0.f, 0.f, 0.f};
-    wave_gemm_gptq<1, SPLIT>(W, col0, L_lo, L_hi, ar, acc);
+    wave_gemm_gptq<1, AT>(W, col0, lo, hi, xres, arow, acc);
 #pragma unroll
     for (int c = 0; c < 4; ++c) red[(wave * 4 + c) * 64 + lane] = acc[0][c];
     __syncthreads();
@@ -571,7 +590,7 @@ __global__ __launch_bounds__(kBlock) void k_linear(const LinArgs a) {
     }
   } else {
     f32x4 acc[1] = {(f32x4){0.f, 0.f, 0.f, 0.f}};
-    wave_gemm_kmajor<FMT, 1, SPLIT>(W, col0, L_lo, L_hi, ar, acc);
+    wave_gemm_kmajor<FMT, 1, AT>(W, col0, lo, hi, xres, arow, acc);
     const int n = col0[0] + (lane & 15);
 #pragma unroll
     for (int rr = 0; rr < 4; ++rr) emit(mt * 16 + 4 * (lane >> 4) + rr, n, acc[0][rr]);
@@ -628,11 +647,23 @@ hipError_t launch_topk(const ftm_moe_layer& L, int T, const void* logits_in, int
   return hipGetLastError();
 }
 
-// which: bit 0 = stage A (w13 + act), bit 1 = stage B (w2 + combine)
-template <int FMT, bool SPLIT>
+// which: bit 0 = stage A (w13 + act), bit 1 = stage B (w2) + combine
+template <int FMT, int AT>
 static void launch_stages(const LayerArgs& a, int gridA, int gridB, hipStream_t st, int which) {
-  if (which & 1) hipLaunchKernelGGL((k_stage_a<FMT, SPLIT>), dim3(gridA), dim3(kBlock), 0, st, a);
-  if (which & 2) hipLaunchKernelGGL((k_stage_b<FMT, SPLIT>), dim3(gridB), dim3(kBlock), 0, st, a);
+  if (which & 1) hipLaunchKernelGGL((k_stage_a<FMT, AT>), dim3(gridA), dim3(kBlock), 0, st, a);
+  if (which & 2) {
+    hipLaunchKernelGGL((k_stage_b<FMT, AT>), dim3(gridB), dim3(kBlock), 0, st, a);
+    const int n4 = a.T * (a.L.hidden / 4);
+    hipLaunchKernelGGL((k_combine<AT>), dim3((n4 + kBlock - 1) / kBlock), dim3(kBlock), 0, st, a);
+  }
+}
+
+template <int FMT>
+static void launch_stages_dt(const LayerArgs& a, int gridA, int gridB, hipStream_t st, int which) {
+  if (a.L.act_dtype == FTM_DT_F32)
+    launch_stages<FMT, FTM_DT_F32>(a, gridA, gridB, st, which);
+  else
+    launch_stages<FMT, FTM_DT_BF16>(a, gridA, gridB, st, which);
 }
 
 hipError_t launch_experts(const ftm_moe_layer& L, const void* x, int T, void* out, char* ws,
@@ -643,40 +674,25 @@ hipError_t launch_experts(const ftm_moe_layer& L, const void* x, int T, void* ou
   const int has_sh = L.shared_inter > 0 ? 1 : 0;
   const int gridA = maxU * (L.inter / NT) + (has_sh ? L.shared_inter / 16 : 0);
   const int gridB = (maxU + has_sh) * (L.hidden / 64);
-  const bool split = L.act_dtype != FTM_DT_BF16;
   switch (L.w13.fmt) {
-    case FTM_FMT_BF16:
-      split ? launch_stages<FTM_FMT_BF16, true>(a, gridA, gridB, st, which)
-            : launch_stages<FTM_FMT_BF16, false>(a, gridA, gridB, st, which);
-      break;
-    case FTM_FMT_FP8_BLOCK:
-      split ? launch_stages<FTM_FMT_FP8_BLOCK, true>(a, gridA, gridB, st, which)
-            : launch_stages<FTM_FMT_FP8_BLOCK, false>(a, gridA, gridB, st, which);
-      break;
-    case FTM_FMT_GPTQ_INT4:
-      split ? launch_stages<FTM_FMT_GPTQ_INT4, true>(a, gridA, gridB, st, which)
-            : launch_stages<FTM_FMT_GPTQ_INT4, false>(a, gridA, gridB, st, which);
-      break;
-    case FTM_FMT_INT8_PACKED:
-      split ? launch_stages<FTM_FMT_INT8_PACKED, true>(a, gridA, gridB, st, which)
-            : launch_stages<FTM_FMT_INT8_PACKED, false>(a, gridA, gridB, st, which);
-      break;
-    case FTM_FMT_MXFP4:
-      split ? launch_stages<FTM_FMT_MXFP4, true>(a, gridA, gridB, st, which)
-            : launch_stages<FTM_FMT_MXFP4, false>(a, gridA, gridB, st, which);
-      break;
-    default:
-      return hipErrorInvalidValue;
+    case FTM_FMT_BF16: launch_stages_dt<FTM_FMT_BF16>(a, gridA, gridB, st, which); break;
+    case FTM_FMT_FP8_BLOCK: launch_stages_dt<FTM_FMT_FP8_BLOCK>(a, gridA, gridB, st, which); break;
+    case FTM_FMT_GPTQ_INT4: launch_stages_dt<FTM_FMT_GPTQ_INT4>(a, gridA, gridB, st, which); break;
+    case FTM_FMT_INT8_PACKED: launch_stages_dt<FTM_FMT_INT8_PACKED>(a, gridA, gridB, st, which); break;
+    case FTM_FMT_MXFP4: launch_stages_dt<FTM_FMT_MXFP4>(a, gridA, gridB, st, which); break;
+    default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
 }
 
 template <int FMT>
-static void launch_linear_t(const LinArgs& a, dim3 grid, bool split, hipStream_t st) {
-  if (split)
-    hipLaunchKernelGGL((k_linear<FMT, true>), grid, dim3(kBlock), 0, st, a);
+static void launch_linear_t(const LinArgs& a, dim3 grid, int x_dt, hipStream_t st) {
+  if (x_dt == FTM_DT_F32)
+    hipLaunchKernelGGL((k_linear<FMT, FTM_DT_F32>), grid, dim3(kBlock), 0, st, a);
+  else if (x_dt == FTM_DT_F16)
+    hipLaunchKernelGGL((k_linear<FMT, FTM_DT_F16>), grid, dim3(kBlock), 0, st, a);
   else
-    hipLaunchKernelGGL((k_linear<FMT, false>), grid, dim3(kBlock), 0, st, a);
+    hipLaunchKernelGGL((k_linear<FMT, FTM_DT_BF16>), grid, dim3(kBlock), 0, st, a);
 }
 
 hipError_t launch_linear(const ftm_proj& P, int slot, const void* x, int x_dt, int M, void* out, int out_dt,
@@ -685,7 +701,6 @@ hipError_t launch_linear(const ftm_proj& P, int slot, const void* x, int x_dt, i
   a.P = P;
   a.slot = slot;
   a.x = x;
-  a.x_dt = x_dt;
   a.M = M;
   a.out = out;
   a.out_dt = out_dt;
@@ -693,13 +708,12 @@ hipError_t launch_linear(const ftm_proj& P, int slot, const void* x, int x_dt, i
   a.bias_dt = bias_dt;
   a.final_dt = final_dt;
   const dim3 grid((P.N + 63) / 64, (M + 15) / 16);
-  const bool split = x_dt != FTM_DT_BF16;
   switch (P.fmt) {
-    case FTM_FMT_BF16: launch_linear_t<FTM_FMT_BF16>(a, grid, split, st); break;
-    case FTM_FMT_FP8_BLOCK: launch_linear_t<FTM_FMT_FP8_BLOCK>(a, grid, split, st); break;
-    case FTM_FMT_GPTQ_INT4: launch_linear_t<FTM_FMT_GPTQ_INT4>(a, grid, split, st); break;
-    case FTM_FMT_INT8_PACKED: launch_linear_t<FTM_FMT_INT8_PACKED>(a, grid, split, st); break;
-    case FTM_FMT_MXFP4: launch_linear_t<FTM_FMT_MXFP4>(a, grid, split, st); break;
+    case FTM_FMT_BF16: launch_linear_t<FTM_FMT_BF16>(a, grid, x_dt, st); break;
+    case FTM_FMT_FP8_BLOCK: launch_linear_t<FTM_FMT_FP8_BLOCK>(a, grid, x_dt, st); break;
+    case FTM_FMT_GPTQ_INT4: launch_linear_t<FTM_FMT_GPTQ_INT4>(a, grid, x_dt, st); break;
+    case FTM_FMT_INT8_PACKED: launch_linear_t<FTM_FMT_INT8_PACKED>(a, grid, x_dt, st); break;
+    case FTM_FMT_MXFP4: launch_linear_t<FTM_FMT_MXFP4>(a, grid, x_dt, st); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
