@@ -40,7 +40,26 @@ def _parse():
     ap.add_argument("--sweep", default="1,4,16,64", help="extra decode batch sizes to report ('' = none)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-probe-mib", type=int, default=0,
+                    help="after the bench, copy a buffer of this many MiB 3 times (a plain copy kernel of known "
+                         "size, the reference point for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE)")
     return ap.parse_args()
+
+
+def _pmc_traffic(config: str, T: int):
+    """HBM bytes per launch of the w13 kernel from the committed rocprofv3 PMC
+    summary (FETCH_SIZE + WRITE_SIZE per dispatch, scaled by the factor the
+    same counters read for a copy kernel of known size), if one exists for
+    this workload."""
+    path = os.path.join(ROOT, "profiles", f"k_stage_a__{config}_T{T}__pmc.md")
+    try:
+        with open(path) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return {"bytes": int(line.split(":", 1)[1].strip()), "source": os.path.relpath(path, ROOT)}
+    except OSError:
+        pass
+    return None
 
 
 def _w13_bytes_per_expert(syn) -> int:
@@ -76,6 +95,33 @@ def main() -> int:
     max_t = max([T] + [int(b) for b in args.sweep.split(",") if b])
     x_pool = [torch.randn(max_t, cfg.H, generator=gx, device=dev).to(torch.bfloat16) for _ in range(NX)]
 
+    cap_stream = torch.cuda.Stream(device=dev)
+
+    def graphs_for(xs):
+        """One HIP graph per (layer, batch) pair of the rotation: a serving loop
+        replays a captured layer forward instead of paying Python launch cost."""
+        pairs = [(l, j) for l in range(NL) for j in range(NX)]
+        cap_stream.wait_stream(torch.cuda.current_stream(dev))
+        with torch.cuda.stream(cap_stream):
+            for l, j in pairs:  # allocates this stream's workspace outside capture
+                layers[l].forward(xs[j])
+        torch.cuda.current_stream(dev).wait_stream(cap_stream)
+        torch.cuda.synchronize()
+        gs = {}
+        for l, j in pairs:
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, stream=cap_stream):
+                o = layers[l].forward(xs[j])
+            gs[(l, j)] = (g, o)
+        # replays must equal the eager forward bit for bit (deterministic kernels)
+        ok = True
+        for (l, j), (g, o) in list(gs.items())[:3]:
+            g.replay()
+            ref = layers[l].forward(xs[j])
+            torch.cuda.synchronize()
+            ok = ok and bool(torch.equal(o, ref))
+        return gs, ok
+
     def run_point(Tb: int, steps: int, warmup: int):
         xs = [x[:Tb].contiguous() for x in x_pool]
         for i in range(warmup):
@@ -91,6 +137,20 @@ def main() -> int:
         torch.cuda.synchronize()
         wall_ms = (time.perf_counter() - w0) * 1e3 / steps
         ms = e0.elapsed_time(e1) / steps
+        # the same steps as HIP-graph replays (one captured forward per pair)
+        gs, graph_ok = graphs_for(xs)
+        for i in range(warmup):
+            gs[(i % NL, i % NX)][0].replay()
+        torch.cuda.synchronize()
+        f0, f1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        f0.record()
+        for i in range(steps):
+            j = warmup + i
+            gs[(j % NL, j % NX)][0].replay()
+        f1.record()
+        torch.cuda.synchronize()
+        graph_ms = f0.elapsed_time(f1) / steps
+        del gs
         # routing of the same (layer, batch) pairs, untimed: realised unique experts
         uniq = []
         for i in range(steps):
@@ -98,53 +158,74 @@ def main() -> int:
             _, ids, _, _ = layers[j % NL].forward(xs[j % NX], return_routing=True)
             uniq.append(int(torch.unique(ids).numel()))
         b_alg = float(np.mean([S.algorithmic_bytes(cfg, u, Tb) for u in uniq]))
-        return ms, wall_ms, float(np.mean(uniq)), b_alg, xs
+        return ms, wall_ms, float(np.mean(uniq)), b_alg, xs, graph_ms, graph_ok
 
-    ms, wall_ms, U, b_alg, xs = run_point(T, args.steps, args.warmup)
+    ms, wall_ms, U, b_alg, xs, graph_ms, graph_ok = run_point(T, args.steps, args.warmup)
     gbs = b_alg / (ms * 1e-3) / 1e9
 
-    # ---- dominant kernel (w13 stage) timed with events on the launch stream
+    # ---- per-kernel durations.  Each of the five launches of a forward is
+    # timed as a group of NL consecutive launches, one per rotated layer (each
+    # layer with its own workspace, so the groups keep every layer's stage
+    # order), between two events on the launch stream; a sleep kernel queued
+    # first lets the host run ahead, so no host gap falls inside a group.
     out = torch.empty(T, cfg.H, dtype=torch.bfloat16, device=dev)
-    nsteps = min(args.steps, 60)
-    evs = []
-    for i in range(nsteps + 5):
-        L, x = layers[i % NL], xs[i % NX]
-        L.forward_stage(x, out, nat.STAGE_ROUTER)
-        L.forward_stage(x, out, nat.STAGE_TOPK)
-        a0, a1, b1 = (torch.cuda.Event(enable_timing=True) for _ in range(3))
-        a0.record()
-        L.forward_stage(x, out, nat.STAGE_W13)
-        a1.record()
-        L.forward_stage(x, out, nat.STAGE_W2)
-        b1.record()
-        if i >= 5:
-            evs.append((a0, a1, b1, i))
+    nsteps = max(1, min(args.steps, 60) // NL)
+    stages = (nat.STAGE_ROUTER, nat.STAGE_TOPK, nat.STAGE_W13, nat.STAGE_W2, nat.STAGE_COMBINE)
+    wss = [torch.zeros(layers[l].workspace_bytes(T), dtype=torch.uint8, device=dev) for l in range(NL)]
+    for st in stages:
+        for l in range(NL):
+            layers[l].forward_stage(xs[l % NX], out, st, ws=wss[l])
     torch.cuda.synchronize()
-    dur_a = [a0.elapsed_time(a1) for a0, a1, _, _ in evs]
-    dur_b = [a1.elapsed_time(b1) for _, a1, b1, _ in evs]
+    if hasattr(torch.cuda, "_sleep"):
+        torch.cuda._sleep(100_000_000)
+    evs = []
+    for i in range(nsteps):
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(len(stages) + 1)]
+        for k, st in enumerate(stages):
+            ev[k].record()
+            for l in range(NL):
+                layers[l].forward_stage(xs[(i + l) % NX], out, st, ws=wss[l])
+        ev[-1].record()
+        evs.append((ev, i))
+    torch.cuda.synchronize()
+    kern_us = {name: float(np.mean([ev[k].elapsed_time(ev[k + 1]) for ev, _ in evs])) * 1e3 / NL
+               for k, name in enumerate(("router", "topk", "w13", "w2", "combine"))}
     w13_unit = _w13_bytes_per_expert(syns[0])
     sh_w13 = 2 * cfg.shared_inter * cfg.H * 2 if cfg.shared_inter else 0
     bytes_a = []
-    for _, _, _, i in evs:
-        _, ids, _, _ = layers[i % NL].forward(xs[i % NX], return_routing=True)
-        u = int(torch.unique(ids).numel())
-        bytes_a.append(u * w13_unit + sh_w13 + T * cfg.H * 2)
-    ach = float(np.mean(bytes_a)) / (float(np.mean(dur_a)) * 1e-3) / 1e9
+    for _, i in evs:
+        for l in range(NL):
+            _, ids, _, _ = layers[l].forward(xs[(i + l) % NX], return_routing=True)
+            u = int(torch.unique(ids).numel())
+            bytes_a.append(u * w13_unit + sh_w13 + T * cfg.H * 2)
+    ach = float(np.mean(bytes_a)) / (kern_us["w13"] * 1e-6) / 1e9
+    traffic = _pmc_traffic(cfg.name, T)
     roofline = {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": None,
+                "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": traffic["bytes"] if traffic else None,
                 "kernel": f"k_stage_a<{cfg.fmt}> (w13 + SiLU-gate)",
-                "kernel_avg_us": round(float(np.mean(dur_a)) * 1e3, 2),
+                "kernel_avg_us": round(kern_us["w13"], 2),
                 "bytes_per_launch": int(np.mean(bytes_a)),
                 "unit_bytes": w13_unit, "units_per_launch": round((np.mean(bytes_a) - sh_w13 - T * cfg.H * 2) / w13_unit, 2),
-                "w2_stage_avg_us": round(float(np.mean(dur_b)) * 1e3, 2)}
+                "traffic_source": traffic["source"] if traffic else None,
+                "kernels_us": {k: round(v, 2) for k, v in kern_us.items()}}
 
     # ---- extra decode batch sizes (same layers)
     sweep = []
     for tb in [int(b) for b in args.sweep.split(",") if b]:
-        ms_b, _, U_b, balg_b, _ = run_point(tb, 50, 10)
+        ms_b, _, U_b, balg_b, _, graph_b, _ = run_point(tb, 50, 10)
         g_b = balg_b / (ms_b * 1e-3) / 1e9
         sweep.append({"T": tb, "tokens_per_s": round(tb / (ms_b * 1e-3), 1), "us_per_layer": round(ms_b * 1e3, 2),
+                      "graph_us_per_layer": round(graph_b * 1e3, 2),
                       "unique_experts": round(U_b, 1), "GBps": round(g_b, 1), "hbm_frac": round(g_b / HBM_PEAK_GBS, 4)})
+
+    if args.copy_probe_mib > 0:
+        n = args.copy_probe_mib * (1 << 20) // 4
+        src = torch.ones(n, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -159,6 +240,10 @@ def main() -> int:
         "warmup": args.warmup,
         "ms_per_step": round(ms, 5),
         "wall_ms_per_step": round(wall_ms, 5),
+        "graph_ms_per_step": round(graph_ms, 5),
+        "timing": "events around K layer forwards launched back to back from Python (one ctypes call each); "
+                  "graph = the same steps as HIP-graph replays (checked bitwise against eager: %s)"
+                  % ("ok" if graph_ok else "MISMATCH"),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,

@@ -194,7 +194,7 @@ int ftm_moe_forward_stage(const ftm_moe_layer* layer, const void* x, int32_t num
                           void* workspace, size_t ws_bytes, void* stream) {
   int rc = check_layer(layer, true);
   if (rc != FTM_OK) return rc;
-  if (stage < FTM_STAGE_ROUTER || stage > FTM_STAGE_W2) return FTM_ERR_DIM;
+  if (stage < FTM_STAGE_ROUTER || stage > FTM_STAGE_COMBINE) return FTM_ERR_DIM;
   if (num_tokens < 0) return FTM_ERR_DIM;
   if (num_tokens == 0) return FTM_OK;
   if (x == nullptr || out == nullptr) return FTM_ERR_NULL;
@@ -211,7 +211,8 @@ int ftm_moe_forward_stage(const ftm_moe_layer* layer, const void* x, int32_t num
   else if (stage == FTM_STAGE_TOPK)
     e = launch_topk(*layer, num_tokens, nullptr, 0, nullptr, nullptr, nullptr, nullptr, nullptr, ws, wl, st);
   else
-    e = launch_experts(*layer, x, num_tokens, out, ws, wl, st, stage == FTM_STAGE_W13 ? 1 : 2);
+    e = launch_experts(*layer, x, num_tokens, out, ws, wl, st,
+                       stage == FTM_STAGE_W13 ? 1 : stage == FTM_STAGE_W2 ? 2 : 4);
   return hip_rc(e);
 }
 

@@ -1,9 +1,12 @@
 // ftm_moe.hip -- the fused quantized MoE layer on gfx950.
 //
 // One layer forward is five launches on the caller's stream:
-//   k_router   router GEMV  logits[t, e] = round(x[t] . G[e] (+ b[e]))      (one WG per expert row)
-//   k_topk     softmax / top-k / renorm per token (one wave per token), then
-//              the last-arriving WG compacts the routed experts (ascending id)
+//   k_router   router GEMV  logits[t, e] = round(x[t] . G[e] (+ b[e]))
+//              (one WG per expert row and 16-token block)
+//   k_topk1    softmax / top-k / renorm, one wave per token, and compaction
+//              of the routed experts (ascending id); one WG for T <= 256
+//   k_topk     the same for larger T over many WGs; the last-arriving WG
+//              compacts
 //   k_stage_a  per (routed expert, 16-channel tile): gate and up rows of w13,
 //              K split over the 4 waves, fused activation -> h (act dtype)
 //   k_stage_b  per (expert, 64-column tile of H): w2 . h, bias, router weight,
@@ -70,181 +73,340 @@ static LayerArgs make_args(const ftm_moe_layer& L, const void* x, void* out, int
 // (per lane: 8-element chunks c = lane + 64*s in ascending s, fma in element
 // order; then the xor-32/16/8/4/2/1 butterfly) that the C oracle replays with
 // fmaf, so logits and therefore routing indices are bit-reproducible.
+// Grid: (expert row [+ the shared-gate row], block of 16 tokens); wave w
+// takes tokens 16*blockIdx.y + w + 4*i, i < 4.  Every load of a step group
+// (4 chunk steps: the gate row and the wave's 4 token rows) is issued before
+// any fma, with buffer loads that read zeros past the end, so one wave has
+// 20 x 16 B per lane in flight.  Chunks past H are masked by a select.
+constexpr int kRouterTPW = 4;  // tokens per wave
+constexpr int kRouterSteps = 4;  // 512-element chunk steps per load group
+
 __global__ __launch_bounds__(kBlock) void k_router(const LayerArgs a, int row_begin) {
   const int r = row_begin + blockIdx.x;
   const int E = a.L.num_experts, H = a.L.hidden, T = a.T;
-  const uint16_t* grow = (r < E) ? (const uint16_t*)a.L.gate_w + (size_t)r * H
-                                 : (const uint16_t*)a.L.shared_gate;
+  const void* grow = (r < E) ? (const void*)((const uint16_t*)a.L.gate_w + (size_t)r * H) : a.L.shared_gate;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const uint16_t* xb = (const uint16_t*)a.x;
-  for (int t0 = wave; t0 < T; t0 += 32) {
-    float acc[8];
+  const int tb = blockIdx.y * 4 * kRouterTPW + wave;
+  const Rsrc gres = make_rsrc(grow, (uint32_t)H * 2u);
+  const Rsrc xres = make_rsrc(a.x, (uint32_t)T * (uint32_t)H * 2u);
+  const int nsteps = (H + 511) / 512;
+  float acc[kRouterTPW];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) acc[i] = 0.0f;
-    for (int c = lane; 8 * c < H; c += 64) {
-      const u32x4 gv = *(const u32x4*)(grow + 8 * c);
-      const uint32_t gw[4] = {gv.x, gv.y, gv.z, gv.w};
-      float gf[8];
+  for (int i = 0; i < kRouterTPW; ++i) acc[i] = 0.0f;
+  for (int s0 = 0; s0 < nsteps; s0 += kRouterSteps) {
+    u32x4 gv[kRouterSteps], xv[kRouterSteps][kRouterTPW];
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        gf[2 * e] = bf16_to_f32(gw[e] & 0xffffu);
-        gf[2 * e + 1] = bf16_to_f32(gw[e] >> 16);
-      }
+    for (int q = 0; q < kRouterSteps; ++q) {
+      const int c = lane + 64 * (s0 + q);
+      const bool ok = (s0 + q < nsteps) && (8 * c < H);
+      gv[q] = bload16(gres, ok ? 16u * (uint32_t)c : kOOB);
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const int t = t0 + 4 * i;
-        if (t < T) {
-          const u32x4 xv = *(const u32x4*)(xb + (size_t)t * H + 8 * c);
-          const uint32_t xw[4] = {xv.x, xv.y, xv.z, xv.w};
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            acc[i] = __builtin_fmaf(bf16_to_f32(xw[e] & 0xffffu), gf[2 * e], acc[i]);
-            acc[i] = __builtin_fmaf(bf16_to_f32(xw[e] >> 16), gf[2 * e + 1], acc[i]);
-          }
-        }
+      for (int i = 0; i < kRouterTPW; ++i) {
+        const int t = tb + 4 * i;
+        xv[q][i] = bload16(xres, (ok && t < T) ? ((uint32_t)t * (uint32_t)H + 8u * (uint32_t)c) * 2u : kOOB);
       }
     }
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const float v = wave_sum(acc[i]);
-      const int t = t0 + 4 * i;
-      if (lane == 0 && t < T) {
-        float z = v;
-        if (r < E && a.L.gate_b != nullptr) z = v + bf16_to_f32(((const uint16_t*)a.L.gate_b)[r]);
-        a.logits[(size_t)t * (E + 1) + r] = round_to(z, a.L.act_dtype);
+    for (int q = 0; q < kRouterSteps; ++q) {
+      const int c = lane + 64 * (s0 + q);
+      const bool ok = (s0 + q < nsteps) && (8 * c < H);
+      const uint32_t gw[4] = {gv[q].x, gv[q].y, gv[q].z, gv[q].w};
+#pragma unroll
+      for (int i = 0; i < kRouterTPW; ++i) {
+        const uint32_t xw[4] = {xv[q][i].x, xv[q][i].y, xv[q][i].z, xv[q][i].w};
+        float t8 = acc[i];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          t8 = __builtin_fmaf(bf16_to_f32(xw[e] & 0xffffu), bf16_to_f32(gw[e] & 0xffffu), t8);
+          t8 = __builtin_fmaf(bf16_to_f32(xw[e] >> 16), bf16_to_f32(gw[e] >> 16), t8);
+        }
+        acc[i] = ok ? t8 : acc[i];
       }
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < kRouterTPW; ++i) {
+    const float v = wave_sum(acc[i]);
+    const int t = tb + 4 * i;
+    if (lane == 0 && t < T) {
+      float z = v;
+      if (r < E && a.L.gate_b != nullptr) z = v + bf16_to_f32(((const uint16_t*)a.L.gate_b)[r]);
+      a.logits[(size_t)t * (E + 1) + r] = round_to(z, a.L.act_dtype);
     }
   }
 }
 
 // ============================================================== top-k + grouping
-constexpr int kMaxNV = kMaxExperts / 64;
 
-__device__ __forceinline__ bool key_better(float v, int e, float bv, int be) {
-  return v > bv || (v == bv && e < be);
+// Selection keys: (key desc, expert id asc) packed into one u64 that orders
+// the same way -- the key's order-preserving bit image (+0 for either zero,
+// the bottom for NaN) above ~expert.  0 is below every real key.
+__device__ __forceinline__ uint64_t pack_key(float v, int e) {
+  uint32_t b = __float_as_uint(v == 0.0f ? 0.0f : v);
+  b = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+  b = (v != v) ? 0u : b;
+  return ((uint64_t)b << 32) | (uint32_t)~(uint32_t)e;
+}
+__device__ __forceinline__ float key_value(uint64_t k) {
+  const uint32_t b = (uint32_t)(k >> 32);
+  return __uint_as_float((b & 0x80000000u) ? (b & 0x7fffffffu) : ~b);
+}
+__device__ __forceinline__ int key_expert(uint64_t k) { return (int)~(uint32_t)k; }
+
+template <int CTRL>
+__device__ __forceinline__ uint64_t dpp_u64(uint64_t x) {
+  const uint32_t lo = (uint32_t)dpp_i<CTRL>((int)(uint32_t)x);
+  const uint32_t hi = (uint32_t)dpp_i<CTRL>((int)(uint32_t)(x >> 32));
+  return ((uint64_t)hi << 32) | lo;
+}
+__device__ __forceinline__ uint64_t umax64(uint64_t a, uint64_t b) { return a > b ? a : b; }
+
+// Wave max of a u64 (DPP within rows, v_readlane across rows); all lanes get it.
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t x) {
+  x = umax64(x, dpp_u64<kDppXor1>(x));
+  x = umax64(x, dpp_u64<kDppXor2>(x));
+  x = umax64(x, dpp_u64<kDppHalfMirror>(x));
+  x = umax64(x, dpp_u64<kDppMirror>(x));
+  uint64_t r[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)x, 16 * q);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(x >> 32), 16 * q);
+    r[q] = ((uint64_t)hi << 32) | lo;
+  }
+  return umax64(umax64(r[0], r[1]), umax64(r[2], r[3]));
 }
 
-template <int MODE>
+__device__ __forceinline__ void cas_desc(uint64_t& a, uint64_t& b) {
+  const uint64_t hi = umax64(a, b), lo = a > b ? b : a;
+  a = hi;
+  b = lo;
+}
+// Descending sorting networks for a lane's candidates (4: 5 comparators,
+// 8: Batcher's 19).
+template <int NV>
+__device__ __forceinline__ void sort_desc(uint64_t (&k)[NV]) {
+  if constexpr (NV == 4) {
+    cas_desc(k[0], k[1]); cas_desc(k[2], k[3]);
+    cas_desc(k[0], k[2]); cas_desc(k[1], k[3]);
+    cas_desc(k[1], k[2]);
+  } else {
+    static_assert(NV == 8, "4 or 8 candidates per lane");
+    cas_desc(k[0], k[1]); cas_desc(k[2], k[3]); cas_desc(k[4], k[5]); cas_desc(k[6], k[7]);
+    cas_desc(k[0], k[2]); cas_desc(k[1], k[3]); cas_desc(k[4], k[6]); cas_desc(k[5], k[7]);
+    cas_desc(k[1], k[2]); cas_desc(k[5], k[6]);
+    cas_desc(k[0], k[4]); cas_desc(k[1], k[5]); cas_desc(k[2], k[6]); cas_desc(k[3], k[7]);
+    cas_desc(k[2], k[4]); cas_desc(k[3], k[5]);
+    cas_desc(k[1], k[2]); cas_desc(k[3], k[4]); cas_desc(k[5], k[6]);
+  }
+}
+
+// Routing of token t by one wave: lanes j < k end with (sel_e, sel_w).
+// NV = candidates per lane (E <= 64 * NV).
+template <int MODE, int NV>
+__device__ __forceinline__ void route_token(const LayerArgs& a, int t, const void* logits_in, int logits_dt,
+                                            const int32_t* ids_in, const float* w_in, float* logits_out,
+                                            int& sel_e, float& sel_w) {
+  const int E = a.L.num_experts, k = a.L.topk;
+  const int lane = threadIdx.x & 63;
+  const int act_dt = a.L.act_dtype;
+  sel_e = -1;
+  sel_w = 0.0f;
+  if (ids_in != nullptr) {
+    if (lane < k) {
+      sel_e = ids_in[(size_t)t * k + lane];
+      sel_w = w_in[(size_t)t * k + lane];
+    }
+    return;
+  }
+  const int pdt = logits_in ? logits_dt : act_dt;  // dtype the probabilities live in (LOWP)
+  float v[NV], key[NV];
+  float vmax = -INFINITY;
+  if (logits_in == nullptr) {
+    // the router's [T, E+1] fp32 logits: all loads issued before any use
+    const Rsrc lres = make_rsrc(a.logits, (uint32_t)a.T * (uint32_t)(E + 1) * 4u);
+    uint32_t raw[NV];
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const int e = lane + 64 * i;
+      raw[i] = bload4(lres, e < E ? ((uint32_t)t * (uint32_t)(E + 1) + (uint32_t)e) * 4u : kOOB);
+    }
+#pragma unroll
+    for (int i = 0; i < NV; ++i) v[i] = (lane + 64 * i < E) ? __uint_as_float(raw[i]) : -INFINITY;
+  } else {
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const int e = lane + 64 * i;
+      v[i] = (e < E) ? load_scalar(logits_in, (size_t)t * E + e, logits_dt) : -INFINITY;
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int e = lane + 64 * i;
+    if (logits_out && e < E) logits_out[(size_t)t * E + e] = v[i];
+    vmax = fmaxf(vmax, v[i]);
+  }
+  float m = 0.0f, s = 1.0f;
+  if (MODE != FTM_ROUTE_TOPK_SOFTMAX) {
+    m = wave_max_dpp(vmax);
+    float ps = 0.0f;
+#pragma unroll
+    for (int i = 0; i < NV; ++i)
+      if (lane + 64 * i < E) ps += expf(v[i] - m);
+    s = wave_sum_dpp(ps);
+  }
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    if (MODE == FTM_ROUTE_SOFTMAX_TOPK_LOWP)
+      key[i] = (lane + 64 * i < E) ? round_to(expf(v[i] - m) / s, pdt) : -INFINITY;
+    else
+      key[i] = v[i];
+  }
+  // Each lane sorts its candidates; k rounds take the wave max of the lanes'
+  // heads, and the lane holding it pops its head.
+  uint64_t lst[NV];
+#pragma unroll
+  for (int i = 0; i < NV; ++i) lst[i] = (lane + 64 * i < E) ? pack_key(key[i], lane + 64 * i) : 0ull;
+  sort_desc<NV>(lst);
+  uint64_t mine = 0ull, first = 0ull;
+  for (int j = 0; j < k; ++j) {
+    const uint64_t best = wave_max_u64(lst[0]);
+    first = j == 0 ? best : first;
+    mine = lane == j ? best : mine;
+    const bool pop = lst[0] == best;
+#pragma unroll
+    for (int i = 0; i + 1 < NV; ++i) lst[i] = pop ? lst[i + 1] : lst[i];
+    lst[NV - 1] = pop ? 0ull : lst[NV - 1];
+  }
+  const float top0 = key_value(first);
+  if (lane < k) {
+    sel_e = key_expert(mine);
+    sel_w = key_value(mine);  // the key; converted to a weight below
+  }
+  float p = 0.0f;
+  if (lane < k) {
+    if (MODE == FTM_ROUTE_SOFTMAX_TOPK) p = expf(sel_w - m) / s;
+    else if (MODE == FTM_ROUTE_SOFTMAX_TOPK_LOWP) p = sel_w;
+    else p = expf(sel_w - top0);
+  }
+  const float tot = wave_sum_dpp(lane < k ? p : 0.0f);
+  if (MODE == FTM_ROUTE_SOFTMAX_TOPK) {
+    sel_w = a.L.renormalize ? p / tot : p;
+  } else if (MODE == FTM_ROUTE_SOFTMAX_TOPK_LOWP) {
+    sel_w = a.L.renormalize ? round_to(p / round_to(tot, pdt), pdt) : p;
+  } else {
+    sel_w = p / tot;
+  }
+  sel_w = round_to(sel_w, act_dt);
+}
+
+// Record token t's selection: weights, ids, and one list entry per pair in
+// the expert's list (cnt: per-expert counters, in LDS or global memory).
+__device__ __forceinline__ void emit_token(const LayerArgs& a, int t, int sel_e, float sel_w, int32_t* ids_out,
+                                           float* w_out, int32_t* cnt) {
+  const int E = a.L.num_experts, k = a.L.topk, T = a.T, KP = a.KP;
+  const int lane = threadIdx.x & 63;
+  if (lane < k) {
+    const int p = t * KP + lane;
+    if (sel_e >= 0 && sel_e < E) {
+      a.wts[p] = sel_w;
+      a.ids[(size_t)t * k + lane] = sel_e;
+      if (ids_out) ids_out[(size_t)t * k + lane] = sel_e;
+      if (w_out) w_out[(size_t)t * k + lane] = sel_w;
+      const int pos = atomicAdd(&cnt[sel_e], 1);
+      if (pos < T) {
+        a.lists[(size_t)sel_e * T + pos] = p;
+      } else {  // a token listed the same expert twice (caller-supplied routing)
+        atomicSub(&cnt[sel_e], 1);
+        atomicOr(&a.ctrl[kCtrlError], 4);
+      }
+    } else {
+      atomicOr(&a.ctrl[kCtrlError], 2);
+    }
+  }
+  if (lane == 0 && a.L.shared_inter > 0) {
+    const float sl = a.logits[(size_t)t * (E + 1) + E];
+    a.wts[t * KP + k] = round_to(1.0f / (1.0f + expf(-sl)), a.L.act_dtype);
+  }
+}
+
+// Compaction of the routed experts (ascending id) by one workgroup of NW
+// waves from the per-expert counters; counters are cleared when global.
+template <int NW>
+__device__ __forceinline__ void compact_experts(const LayerArgs& a, int32_t* cnt, bool global_cnt, int* s_wsum) {
+  const int E = a.L.num_experts;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  int running = 0;
+  for (int base = 0; base < E; base += NW * 64) {
+    const int e = base + threadIdx.x;
+    int c = 0;
+    if (e < E) c = global_cnt ? __hip_atomic_load(&cnt[e], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : cnt[e];
+    const bool f = c > 0;
+    const uint64_t mask = __ballot(f);
+    const int pre = __popcll(mask & ((1ull << lane) - 1ull));
+    if (lane == 0) s_wsum[wave] = __popcll(mask);
+    __syncthreads();
+    int wpre = 0, tot = 0;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) {
+      if (w < wave) wpre += s_wsum[w];
+      tot += s_wsum[w];
+    }
+    if (f) {
+      a.uniq[running + wpre + pre] = e;
+      a.ucnt[running + wpre + pre] = c;
+    }
+    if (global_cnt && e < E) cnt[e] = 0;
+    running += tot;
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) {
+    a.ctrl[kCtrlNRouted] = running;
+    a.ctrl[kCtrlNU] = running + (a.L.shared_inter > 0 ? 1 : 0);
+  }
+}
+
+// Small batches: one workgroup of 16 waves routes every token (wave w takes
+// t = w, w + 16, ...) with per-expert counters in LDS, then compacts.  No
+// cross-workgroup traffic, so no device-scope fences.
+constexpr int kTopk1Waves = 16;
+constexpr int kTopk1MaxT = 256;
+
+template <int MODE, int NV>
+__global__ __launch_bounds__(64 * kTopk1Waves) void k_topk1(const LayerArgs a, const void* logits_in,
+                                                            int logits_dt, const int32_t* ids_in,
+                                                            const float* w_in, int32_t* ids_out, float* w_out,
+                                                            float* logits_out) {
+  __shared__ int32_t s_cnt[kMaxExperts];
+  __shared__ int s_wsum[kTopk1Waves];
+  const int E = a.L.num_experts, T = a.T;
+  for (int e = threadIdx.x; e < E; e += 64 * kTopk1Waves) s_cnt[e] = 0;
+  __syncthreads();
+  for (int t = threadIdx.x >> 6; t < T; t += kTopk1Waves) {
+    int sel_e;
+    float sel_w;
+    route_token<MODE, NV>(a, t, logits_in, logits_dt, ids_in, w_in, logits_out, sel_e, sel_w);
+    emit_token(a, t, sel_e, sel_w, ids_out, w_out, s_cnt);
+  }
+  __syncthreads();
+  compact_experts<kTopk1Waves>(a, s_cnt, false, s_wsum);
+}
+
+// Large batches: one wave per token, 4 per workgroup; the last-arriving
+// workgroup compacts from the global counters and clears them.
+template <int MODE, int NV>
 __global__ __launch_bounds__(kBlock) void k_topk(const LayerArgs a, const void* logits_in, int logits_dt,
                                                  const int32_t* ids_in, const float* w_in, int32_t* ids_out,
                                                  float* w_out, float* logits_out) {
-  const int E = a.L.num_experts, k = a.L.topk, T = a.T, KP = a.KP;
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int t = blockIdx.x * 4 + wave;
-  const int act_dt = a.L.act_dtype;
+  const int T = a.T;
+  const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
   int32_t* cnt = a.ctrl + kCtrlExpertCnt;
-
   if (t < T) {
-    int sel_e = -1;
-    float sel_w = 0.0f;
-    if (ids_in != nullptr) {
-      if (lane < k) {
-        sel_e = ids_in[(size_t)t * k + lane];
-        sel_w = w_in[(size_t)t * k + lane];
-      }
-    } else {
-      const int pdt = logits_in ? logits_dt : act_dt;  // dtype the probabilities live in (LOWP)
-      float v[kMaxNV], key[kMaxNV];
-      float vmax = -INFINITY;
-#pragma unroll
-      for (int i = 0; i < kMaxNV; ++i) {
-        const int e = lane + 64 * i;
-        v[i] = -INFINITY;
-        if (e < E) {
-          v[i] = logits_in ? load_scalar(logits_in, (size_t)t * E + e, logits_dt)
-                           : a.logits[(size_t)t * (E + 1) + e];
-          if (logits_out) logits_out[(size_t)t * E + e] = v[i];
-        }
-        vmax = fmaxf(vmax, v[i]);
-      }
-      float m = 0.0f, s = 1.0f;
-      if (MODE != FTM_ROUTE_TOPK_SOFTMAX) {
-        m = wave_max(vmax);
-        float ps = 0.0f;
-#pragma unroll
-        for (int i = 0; i < kMaxNV; ++i)
-          if (lane + 64 * i < E) ps += expf(v[i] - m);
-        s = wave_sum(ps);
-      }
-#pragma unroll
-      for (int i = 0; i < kMaxNV; ++i) {
-        if (MODE == FTM_ROUTE_SOFTMAX_TOPK_LOWP)
-          key[i] = (lane + 64 * i < E) ? round_to(expf(v[i] - m) / s, pdt) : -INFINITY;
-        else
-          key[i] = v[i];
-      }
-      // k rounds of wave arg-max on (key desc, expert id asc).
-      uint32_t taken = 0;
-      float top0 = 0.0f;
-      for (int j = 0; j < k; ++j) {
-        float bv = -INFINITY;
-        int be = 0x7fffffff;
-#pragma unroll
-        for (int i = 0; i < kMaxNV; ++i) {
-          const int e = lane + 64 * i;
-          if (e < E && !((taken >> i) & 1u) && key_better(key[i], e, bv, be)) {
-            bv = key[i];
-            be = e;
-          }
-        }
-#pragma unroll
-        for (int off = 32; off >= 1; off >>= 1) {
-          const float ov = __shfl_xor(bv, off);
-          const int oe = __shfl_xor(be, off);
-          if (key_better(ov, oe, bv, be)) {
-            bv = ov;
-            be = oe;
-          }
-        }
-        if ((be & 63) == lane) taken |= 1u << (be >> 6);
-        if (j == 0) top0 = bv;
-        if (lane == j) {
-          sel_e = be;
-          sel_w = bv;  // the key; converted to a weight below
-        }
-      }
-      // weights
-      float p = 0.0f;
-      if (lane < k) {
-        if (MODE == FTM_ROUTE_SOFTMAX_TOPK) p = expf(sel_w - m) / s;
-        else if (MODE == FTM_ROUTE_SOFTMAX_TOPK_LOWP) p = sel_w;
-        else p = expf(sel_w - top0);
-      }
-      const float tot = wave_sum(lane < k ? p : 0.0f);
-      if (MODE == FTM_ROUTE_SOFTMAX_TOPK) {
-        sel_w = a.L.renormalize ? p / tot : p;
-      } else if (MODE == FTM_ROUTE_SOFTMAX_TOPK_LOWP) {
-        sel_w = a.L.renormalize ? round_to(p / round_to(tot, pdt), pdt) : p;
-      } else {
-        sel_w = p / tot;
-      }
-      sel_w = round_to(sel_w, act_dt);
-    }
-    if (lane < k) {
-      const int p = t * KP + lane;
-      if (sel_e >= 0 && sel_e < E) {
-        a.wts[p] = sel_w;
-        a.ids[(size_t)t * k + lane] = sel_e;
-        if (ids_out) ids_out[(size_t)t * k + lane] = sel_e;
-        if (w_out) w_out[(size_t)t * k + lane] = sel_w;
-        const int pos = atomicAdd(&cnt[sel_e], 1);
-        if (pos < T) {
-          a.lists[(size_t)sel_e * T + pos] = p;
-        } else {  // a token listed the same expert twice (caller-supplied routing)
-          atomicSub(&cnt[sel_e], 1);
-          atomicOr(&a.ctrl[kCtrlError], 4);
-        }
-      } else {
-        atomicOr(&a.ctrl[kCtrlError], 2);
-      }
-    }
-    if (lane == 0 && a.L.shared_inter > 0) {
-      const float sl = a.logits[(size_t)t * (E + 1) + E];
-      a.wts[t * KP + k] = round_to(1.0f / (1.0f + expf(-sl)), act_dt);
-    }
+    int sel_e;
+    float sel_w;
+    route_token<MODE, NV>(a, t, logits_in, logits_dt, ids_in, w_in, logits_out, sel_e, sel_w);
+    emit_token(a, t, sel_e, sel_w, ids_out, w_out, cnt);
   }
-
-  // ---- last-arriving workgroup: compact the routed experts (ascending id).
   __shared__ int s_last;
   __shared__ int s_wsum[4];
   __threadfence();
@@ -253,34 +415,8 @@ __global__ __launch_bounds__(kBlock) void k_topk(const LayerArgs a, const void* 
   __syncthreads();
   if (!s_last) return;
   __threadfence();
-  int running = 0;
-  for (int base = 0; base < E; base += kBlock) {
-    const int e = base + threadIdx.x;
-    const int c = (e < E) ? __hip_atomic_load(&cnt[e], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0;
-    const bool f = c > 0;
-    const uint64_t mask = __ballot(f);
-    const int pre = __popcll(mask & ((1ull << lane) - 1ull));
-    if (lane == 0) s_wsum[wave] = __popcll(mask);
-    __syncthreads();
-    int wpre = 0, tot = 0;
-#pragma unroll
-    for (int w = 0; w < 4; ++w) {
-      if (w < wave) wpre += s_wsum[w];
-      tot += s_wsum[w];
-    }
-    if (f) {
-      a.uniq[running + wpre + pre] = e;
-      a.ucnt[running + wpre + pre] = c;
-    }
-    if (e < E) cnt[e] = 0;
-    running += tot;
-    __syncthreads();
-  }
-  if (threadIdx.x == 0) {
-    a.ctrl[kCtrlNRouted] = running;
-    a.ctrl[kCtrlNU] = running + (a.L.shared_inter > 0 ? 1 : 0);
-    a.ctrl[kCtrlArriveTopk] = 0;
-  }
+  compact_experts<4>(a, cnt, true, s_wsum);
+  if (threadIdx.x == 0) a.ctrl[kCtrlArriveTopk] = 0;
 }
 
 // ============================================================== activation
@@ -390,13 +526,15 @@ __global__ __launch_bounds__(kBlock) void k_stage_a(const LayerArgs a) {
   constexpr bool kG = FMT == FTM_FMT_GPTQ_INT4;
   constexpr int NT = kG ? 64 : 16;
   __shared__ f32x4 red[4 * 2 * (kG ? 4 : 1) * 64];
-  const int nRouted = a.ctrl[kCtrlNRouted];
   const int I = a.L.inter;
   const int tilesR = I / NT;
   int item = blockIdx.x;
+  // The expert table is read before the routed count so both loads are in
+  // flight together (uniq / ucnt hold E + 1 entries).
+  const int u = min(item / tilesR, a.L.num_experts), it = item % tilesR;
+  const int e = a.uniq[u], cnt = a.ucnt[u];
+  const int nRouted = a.ctrl[kCtrlNRouted];
   if (item < nRouted * tilesR) {
-    const int u = item / tilesR, it = item % tilesR;
-    const int e = a.uniq[u], cnt = a.ucnt[u];
     const int slot = a.L.slot_of_expert ? a.L.slot_of_expert[e] : e;
     if (slot < 0 || slot >= a.L.w13.num_slots) {
       if (threadIdx.x == 0) atomicOr(&a.ctrl[kCtrlError], 1);
@@ -487,11 +625,12 @@ __global__ __launch_bounds__(kBlock) void k_stage_b(const LayerArgs a) {
   __shared__ f32x4 red[4 * 4 * 64];
   const int H = a.L.hidden;
   const int tiles = H / 64;
-  const int nU = a.ctrl[kCtrlNU], nRouted = a.ctrl[kCtrlNRouted];
   const int u = blockIdx.x / tiles, nt = blockIdx.x % tiles;
+  const int uc = min(u, a.L.num_experts);  // uniq / ucnt hold E + 1 entries
+  const int e = a.uniq[uc], cnt = a.ucnt[uc];
+  const int nU = a.ctrl[kCtrlNU], nRouted = a.ctrl[kCtrlNRouted];
   if (u >= nU) return;
   if (u < nRouted) {
-    const int e = a.uniq[u], cnt = a.ucnt[u];
     const int32_t* list = a.lists + (size_t)e * a.T;
     const int slot = a.L.slot_of_expert ? a.L.slot_of_expert[e] : e;
     if (slot < 0 || slot >= a.L.w2.num_slots) {
@@ -621,7 +760,8 @@ hipError_t launch_router(const ftm_moe_layer& L, const void* x, int T, int row_b
                          const WsLayout& wl, hipStream_t st) {
   const LayerArgs a = make_args(L, x, nullptr, T, ws, wl);
   if (row_end - row_begin <= 0 || T <= 0) return hipSuccess;
-  hipLaunchKernelGGL(k_router, dim3(row_end - row_begin), dim3(kBlock), 0, st, a, row_begin);
+  const int tpb = 4 * kRouterTPW;
+  hipLaunchKernelGGL(k_router, dim3(row_end - row_begin, (T + tpb - 1) / tpb), dim3(kBlock), 0, st, a, row_begin);
   return hipGetLastError();
 }
 
@@ -629,30 +769,37 @@ hipError_t launch_topk(const ftm_moe_layer& L, int T, const void* logits_in, int
                        const int32_t* ids_in, const float* w_in, int32_t* ids_out, float* w_out,
                        float* logits_out, char* ws, const WsLayout& wl, hipStream_t st) {
   const LayerArgs a = make_args(L, nullptr, nullptr, T, ws, wl);
-  const dim3 grid((T + 3) / 4 > 0 ? (T + 3) / 4 : 1);
-  switch (L.route_mode) {
-    case FTM_ROUTE_SOFTMAX_TOPK:
-      hipLaunchKernelGGL(k_topk<FTM_ROUTE_SOFTMAX_TOPK>, grid, dim3(kBlock), 0, st, a, logits_in, logits_dt,
-                         ids_in, w_in, ids_out, w_out, logits_out);
-      break;
-    case FTM_ROUTE_SOFTMAX_TOPK_LOWP:
-      hipLaunchKernelGGL(k_topk<FTM_ROUTE_SOFTMAX_TOPK_LOWP>, grid, dim3(kBlock), 0, st, a, logits_in,
-                         logits_dt, ids_in, w_in, ids_out, w_out, logits_out);
-      break;
-    default:
-      hipLaunchKernelGGL(k_topk<FTM_ROUTE_TOPK_SOFTMAX>, grid, dim3(kBlock), 0, st, a, logits_in, logits_dt,
-                         ids_in, w_in, ids_out, w_out, logits_out);
-      break;
+  const bool one = T <= kTopk1MaxT;
+  const dim3 grid(one ? 1 : (T + 3) / 4), block(one ? 64 * kTopk1Waves : kBlock);
+#define FTM_TOPK_LAUNCH(M, NV)                                                                                 \
+  if (one)                                                                                                     \
+    hipLaunchKernelGGL((k_topk1<M, NV>), grid, block, 0, st, a, logits_in, logits_dt, ids_in, w_in, ids_out,    \
+                       w_out, logits_out);                                                                     \
+  else                                                                                                         \
+    hipLaunchKernelGGL((k_topk<M, NV>), grid, block, 0, st, a, logits_in, logits_dt, ids_in, w_in, ids_out,     \
+                       w_out, logits_out);
+#define FTM_TOPK_NV(M)            \
+  if (L.num_experts <= 256) {     \
+    FTM_TOPK_LAUNCH(M, 4)         \
+  } else {                        \
+    FTM_TOPK_LAUNCH(M, 8)         \
   }
+  switch (L.route_mode) {
+    case FTM_ROUTE_SOFTMAX_TOPK: FTM_TOPK_NV(FTM_ROUTE_SOFTMAX_TOPK) break;
+    case FTM_ROUTE_SOFTMAX_TOPK_LOWP: FTM_TOPK_NV(FTM_ROUTE_SOFTMAX_TOPK_LOWP) break;
+    default: FTM_TOPK_NV(FTM_ROUTE_TOPK_SOFTMAX) break;
+  }
+#undef FTM_TOPK_NV
+#undef FTM_TOPK_LAUNCH
   return hipGetLastError();
 }
 
-// which: bit 0 = stage A (w13 + act), bit 1 = stage B (w2) + combine
+// which: bit 0 = stage A (w13 + act), bit 1 = stage B (w2), bit 2 = combine
 template <int FMT, int AT>
 static void launch_stages(const LayerArgs& a, int gridA, int gridB, hipStream_t st, int which) {
   if (which & 1) hipLaunchKernelGGL((k_stage_a<FMT, AT>), dim3(gridA), dim3(kBlock), 0, st, a);
-  if (which & 2) {
-    hipLaunchKernelGGL((k_stage_b<FMT, AT>), dim3(gridB), dim3(kBlock), 0, st, a);
+  if (which & 2) hipLaunchKernelGGL((k_stage_b<FMT, AT>), dim3(gridB), dim3(kBlock), 0, st, a);
+  if (which & 4) {
     const int n4 = a.T * (a.L.hidden / 4);
     hipLaunchKernelGGL((k_combine<AT>), dim3((n4 + kBlock - 1) / kBlock), dim3(kBlock), 0, st, a);
   }

@@ -53,6 +53,7 @@ STAGE_ROUTER = 0
 STAGE_TOPK = 1
 STAGE_W13 = 2
 STAGE_W2 = 3
+STAGE_COMBINE = 4
 
 _ERR_TEXT = {
     ERR_NULL: "a required pointer is NULL",

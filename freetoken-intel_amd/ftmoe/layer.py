@@ -155,11 +155,17 @@ class MoeLayer:
             return out, ids, w, logits
         return out
 
-    def forward_stage(self, x: torch.Tensor, out: torch.Tensor, stage: int) -> None:
+    def forward_stage(self, x: torch.Tensor, out: torch.Tensor, stage: int,
+                      ws: Optional[torch.Tensor] = None) -> None:
         """Launch one stage (``ftmoe._native.STAGE_*``) of :meth:`forward` into ``out``
-        (for per-kernel timing; stages 0..3 in order equal one forward)."""
+        (for per-kernel timing; stages 0..4 in order equal one forward).  ``ws``:
+        an explicit workspace (uint8, zero-initialised, at least
+        :meth:`workspace_bytes`), so several layers' stages can interleave."""
         T = x.shape[0]
-        ws = workspace(x.device, self.workspace_bytes(T))
+        if ws is None:
+            ws = workspace(x.device, self.workspace_bytes(T))
+        elif ws.numel() < self.workspace_bytes(T):
+            raise ValueError("workspace too small")
         rc = nat.lib().ftm_moe_forward_stage(ctypes.byref(self.c()), x.data_ptr(), T, out.data_ptr(), int(stage),
                                              ws.data_ptr(), ws.numel(), nat.stream_of(x))
         nat.check(rc, "ftm_moe_forward_stage")

@@ -153,12 +153,14 @@ int ftm_moe_forward(const ftm_moe_layer* layer, const void* x, int32_t num_token
 
 /* One stage of ftm_moe_forward, for per-kernel timing with events on `stream`:
  *   0 = router GEMV, 1 = softmax/top-k/grouping, 2 = w13 + activation,
- *   3 = w2 + router-weighted combine.  Calling stages 0..3 in order on one
- * stream launches exactly the kernels ftm_moe_forward launches. */
+ *   3 = w2 (router-weighted slots), 4 = combine of the slots into `out`.
+ * Calling stages 0..4 in order on one stream launches exactly the kernels
+ * ftm_moe_forward launches. */
 #define FTM_STAGE_ROUTER 0
 #define FTM_STAGE_TOPK 1
 #define FTM_STAGE_W13 2
 #define FTM_STAGE_W2 3
+#define FTM_STAGE_COMBINE 4
 int ftm_moe_forward_stage(const ftm_moe_layer* layer, const void* x, int32_t num_tokens, void* out,
                           int32_t stage, void* workspace, size_t ws_bytes, void* stream);
 
