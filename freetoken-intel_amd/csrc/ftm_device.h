@@ -465,6 +465,15 @@ __device__ __forceinline__ void wave_gemm_kmajor(const ProjSlot& W, const int (&
           scw[r][b] = bload_scalar_word(sres, soff[r] + (uint32_t)grp_b[b], W.s_dt, L < L_hi && soff[r] != kOOB);
         }
       }
+    }
+    // Activation fragments after every weight load of the chunk: their row
+    // offsets come from the expert's token list, so the weight stream is not
+    // held up behind that dependent load.
+#pragma unroll
+    for (int b = 0; b < CH; ++b) {
+      const int L = Lc + b;
+      const int kk = L * F::kLoadK + F::kLaneK * g;
+      const bool kok = (L < L_hi) && (kk < K);
 #pragma unroll
       for (int q = 0; q < F::kMfma; ++q) load_a8<AT>(ares, kok ? arow : kOOB, kk + 8 * q, ahi[b][q], alo[b][q]);
     }
@@ -513,6 +522,131 @@ __device__ __forceinline__ void wave_gemm_kmajor(const ProjSlot& W, const int (&
 #pragma unroll
     for (int r = 0; r < NR; ++r) acc[r] += tmp[r];
   }
+}
+
+// ---------------------------------------------------------------- row-item engine
+// A 4-byte word at a wave-uniform byte offset, read through the constant
+// address space so the compiler emits a scalar (s_load) read.
+__device__ __forceinline__ uint32_t sload4(const void* base, uint32_t off) {
+  typedef const __attribute__((address_space(4))) uint32_t* CPtr;
+  return *(CPtr)((const char*)base + off);
+}
+
+// acc += A(16 tokens x K range) * W(16 rows)^T, where lane l supplies weight
+// row lrow (its MFMA column l % 16; -1 = no row, reads zero).  Unlike
+// wave_gemm_kmajor the 16 rows need not be consecutive: stage A pairs 8 gate
+// rows with their 8 up rows.  FP8 block scales are read with scalar loads:
+// lanes l % 16 < 8 use scale row-block sb_lo, the others sb_hi (each uniform).
+template <int FMT, int AT, int CH>
+__device__ __forceinline__ void wave_rows_kmajor(const ProjSlot& W, int lrow, int sb_lo, int sb_hi, int L_lo,
+                                                 int L_hi, Rsrc ares, uint32_t arow, f32x4& acc) {
+  using F = KMajor<FMT>;
+  constexpr bool SPLIT = AType<AT>::kSplit;
+  const int lane = threadIdx.x & 63;
+  const int g = lane >> 4;
+  const bool upper = (lane & 15) >= 8;
+  const int K = W.K;
+  const uint32_t rb = F::row_bytes(K);
+  const Rsrc wres = make_rsrc(W.w, rb * (uint32_t)W.N);
+  const uint32_t woff = lrow >= 0 ? (uint32_t)lrow * rb : kOOB;
+  Rsrc sres = wres;
+  uint32_t soff = kOOB;
+  uint32_t fp8_lo = 0, fp8_hi = 0;  // FP8: byte offsets of the two scale rows
+  int gmax = 0;                     // FP8: last K block (clamps the scalar reads)
+  const uint32_t sesz = W.s_dt == FTM_DT_F32 ? 4u : 2u;
+  if constexpr (FMT == FTM_FMT_FP8_BLOCK) {
+    const int nkb = (K + W.group - 1) / W.group;
+    gmax = nkb - 1;
+    fp8_lo = (uint32_t)(sb_lo * nkb) * sesz;
+    fp8_hi = (uint32_t)(sb_hi * nkb) * sesz;
+  } else if constexpr (FMT == FTM_FMT_INT8_PACKED) {
+    const int ng = K / W.group;
+    sres = make_rsrc(W.s, (uint32_t)(W.N * ng) * sesz);
+    soff = lrow >= 0 ? (uint32_t)(lrow * ng) : kOOB;
+  } else if constexpr (FMT == FTM_FMT_MXFP4) {
+    sres = make_rsrc(W.s, (uint32_t)W.N * (uint32_t)(K / 32));
+    soff = lrow >= 0 ? (uint32_t)(lrow * (K / 32)) : kOOB;
+  }
+  const int lpg = F::kPostScale ? (W.group + F::kLoadK - 1) / F::kLoadK : 1;
+  int gcur = L_lo / lpg;
+  int gpos = L_lo - gcur * lpg;
+  f32x4 tmp = (f32x4){0.f, 0.f, 0.f, 0.f};
+
+  for (int Lc = L_lo; Lc < L_hi; Lc += CH) {
+    u32x4 raw[CH];
+    float sc[CH];       // MXFP4: e8m0 factor of the lane's block
+    uint32_t scw[CH];   // FP8 / INT8: raw scale word of the wave-load's group
+    int grp_b[CH];
+    bool last_b[CH];
+    u32x4 ahi[CH][F::kMfma], alo[CH][F::kMfma];
+#pragma unroll
+    for (int b = 0; b < CH; ++b) {
+      const int L = Lc + b;
+      const int kk = L * F::kLoadK + F::kLaneK * g;
+      const bool kok = (L < L_hi) && (kk < K);
+      if constexpr (F::kPostScale) {
+        const bool wrap = gpos == lpg - 1;
+        grp_b[b] = gcur;
+        last_b[b] = wrap | (L + 1 == L_hi);
+        gpos = wrap ? 0 : gpos + 1;
+        gcur += wrap ? 1 : 0;
+      }
+      raw[b] = bload16(wres, kok ? woff + F::elem_off(kk) : kOOB);
+      if constexpr (FMT == FTM_FMT_MXFP4) {
+        sc[b] = e8m0_to_f32(bload1(sres, kok ? soff + (uint32_t)(kk / 32) : kOOB));
+      } else if constexpr (FMT == FTM_FMT_FP8_BLOCK) {
+        // both halves' words, uniform offsets -> scalar loads
+        const uint32_t gb = (uint32_t)min(grp_b[b], gmax) * sesz;
+        const uint32_t w_lo = sload4(W.s, (fp8_lo + gb) & ~3u);
+        const uint32_t w_hi = sload4(W.s, (fp8_hi + gb) & ~3u);
+        scw[b] = upper ? w_hi : w_lo;
+      } else if constexpr (FMT == FTM_FMT_INT8_PACKED) {
+        scw[b] = bload_scalar_word(sres, soff + (uint32_t)grp_b[b], W.s_dt, L < L_hi && soff != kOOB);
+      }
+    }
+#pragma unroll
+    for (int b = 0; b < CH; ++b) {
+      const int L = Lc + b;
+      const int kk = L * F::kLoadK + F::kLaneK * g;
+      const bool kok = (L < L_hi) && (kk < K);
+#pragma unroll
+      for (int q = 0; q < F::kMfma; ++q) load_a8<AT>(ares, kok ? arow : kOOB, kk + 8 * q, ahi[b][q], alo[b][q]);
+    }
+#pragma unroll
+    for (int b = 0; b < CH; ++b) {
+      const int L = Lc + b;
+#pragma unroll
+      for (int q = 0; q < F::kMfma; ++q) {
+        u32x4 bq;
+        if constexpr (FMT == FTM_FMT_FP8_BLOCK) {
+          bq = q == 0 ? fp8x8_to_bf16(raw[b].x, raw[b].y) : fp8x8_to_bf16(raw[b].z, raw[b].w);
+        } else if constexpr (FMT == FTM_FMT_INT8_PACKED) {
+          bq = q == 0 ? i8x8_to_bf16(raw[b].x, raw[b].y) : i8x8_to_bf16(raw[b].z, raw[b].w);
+        } else if constexpr (FMT == FTM_FMT_MXFP4) {
+          const uint32_t wq = q == 0 ? raw[b].x : q == 1 ? raw[b].y : q == 2 ? raw[b].z : raw[b].w;
+          bq = fp4x8_to_bf16(wq, sc[b]);
+        } else {
+          bq = raw[b];
+        }
+        tmp = mfma_bf16(ahi[b][q], bq, tmp);
+        if constexpr (SPLIT) tmp = mfma_bf16(alo[b][q], bq, tmp);
+      }
+      if constexpr (F::kPostScale) {
+        // group end (or range end): fold in the group's scale; straight-line
+        // code, see wave_gemm_kmajor
+        const bool fold = last_b[b] & (L < L_hi);
+        uint32_t sidx;
+        if constexpr (FMT == FTM_FMT_FP8_BLOCK)
+          sidx = ((upper ? fp8_hi : fp8_lo) / sesz) + (uint32_t)grp_b[b];
+        else
+          sidx = soff + (uint32_t)grp_b[b];
+        const float s_grp = decode_scalar_word(scw[b], sidx, W.s_dt);
+        acc += tmp * (fold ? s_grp : 0.0f);
+        tmp *= last_b[b] ? 0.0f : 1.0f;
+      }
+    }
+  }
+  if constexpr (!F::kPostScale) acc += tmp;
 }
 
 // ---------------------------------------------------------------- GPTQ engine

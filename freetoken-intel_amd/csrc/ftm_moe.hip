@@ -68,6 +68,14 @@ static LayerArgs make_args(const ftm_moe_layer& L, const void* x, void* out, int
   return a;
 }
 
+// Pair slot p of row m of an expert's token list (the shared expert has no
+// list: its rows are the tokens, p = m*KP + shared_col), or -1 past cnt.
+// A buffer load, so callers issue it early without a branch around it.
+__device__ __forceinline__ int pair_of_row(Rsrc lres, bool has_list, int m, int cnt, int KP, int shared_col) {
+  const uint32_t v = bload4(lres, (has_list && m < cnt) ? 4u * (uint32_t)m : kOOB);
+  return m < cnt ? (has_list ? (int)v : m * KP + shared_col) : -1;
+}
+
 // ============================================================== router GEMV
 // logit = round_act( sum_k x[k]*G[k] (+ b) ).  The fp32 sum has a fixed order
 // (per lane: 8-element chunks c = lane + 64*s in ascending s, fma in element
@@ -464,19 +472,30 @@ __device__ void stage_a_body(const LayerArgs& a, const ProjSlot& W, int Iu, int 
   constexpr bool kG = EFMT == FTM_FMT_GPTQ_INT4;
   constexpr int NSUB = kG ? 4 : 1;
   constexpr int XB = AType<AT>::kBytes;
+  constexpr int EPI = 16 * NT / kBlock;  // epilogue elements per thread
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int H = a.L.hidden, KP = a.KP;
   int lo, hi;
   wave_k_range<EFMT>(W, wave, 4, lo, hi);
   const int col0[2] = {it * NT, Iu + it * NT};
   const Rsrc xres = make_rsrc(a.x, (uint32_t)a.T * (uint32_t)H * XB);
+  const Rsrc lres = make_rsrc(list, list ? (uint32_t)cnt * 4u : 0u);
+  // epilogue element q of this thread: row i, channel j of the tile
+  float bias_g[EPI], bias_u[EPI];
+#pragma unroll
+  for (int q = 0; q < EPI; ++q) {
+    const int j = (threadIdx.x + q * kBlock) % NT;
+    bias_g[q] = W.bias != nullptr ? load_scalar(W.bias, it * NT + j, W.bias_dt) : 0.0f;
+    bias_u[q] = W.bias != nullptr ? load_scalar(W.bias, Iu + it * NT + j, W.bias_dt) : 0.0f;
+  }
   for (int mb = 0; mb < cnt; mb += 16) {
-    const int m = mb + (lane & 15);
-    uint32_t arow = kOOB;
-    if (m < cnt) {
-      const int p = list ? list[m] : m * KP + shared_col;
-      arow = (uint32_t)(p / KP) * (uint32_t)H * XB;
-    }
+    // every list lookup of this row block is issued before the weight stream
+    const int pa = pair_of_row(lres, list != nullptr, mb + (lane & 15), cnt, KP, shared_col);
+    int pe[EPI];
+#pragma unroll
+    for (int q = 0; q < EPI; ++q)
+      pe[q] = pair_of_row(lres, list != nullptr, mb + (threadIdx.x + q * kBlock) / NT, cnt, KP, shared_col);
+    const uint32_t arow = pa >= 0 ? (uint32_t)(pa / KP) * (uint32_t)H * XB : kOOB;
     if constexpr (kG) {
       f32x4 acc[2][4];
 #pragma unroll
@@ -495,26 +514,23 @@ __device__ void stage_a_body(const LayerArgs& a, const ProjSlot& W, int Iu, int 
       for (int r = 0; r < 2; ++r) red[(wave * 2 + r) * 64 + lane] = acc[r];
     }
     __syncthreads();
-    for (int idx = threadIdx.x; idx < 16 * NT; idx += kBlock) {
+#pragma unroll
+    for (int q = 0; q < EPI; ++q) {
+      const int idx = threadIdx.x + q * kBlock;
       const int i = idx / NT, j = idx % NT;
       const int c = kG ? (j & 3) : 0, jj = kG ? (j >> 2) : j;
       const int ln = jj + 16 * (i >> 2), rr = i & 3;
-      float gs = 0.0f, us = 0.0f;
+      float g4 = 0.0f, u4 = 0.0f;
 #pragma unroll
       for (int w = 0; w < 4; ++w) {
-        gs += red[((w * 2 + 0) * NSUB + c) * 64 + ln][rr];
-        us += red[((w * 2 + 1) * NSUB + c) * 64 + ln][rr];
+        g4 += red[((w * 2 + 0) * NSUB + c) * 64 + ln][rr];
+        u4 += red[((w * 2 + 1) * NSUB + c) * 64 + ln][rr];
       }
-      const int m2 = mb + i;
-      if (m2 < cnt) {
-        const int ch = it * NT + j;
-        if (W.bias != nullptr) {
-          gs += load_scalar(W.bias, ch, W.bias_dt);
-          us += load_scalar(W.bias, Iu + ch, W.bias_dt);
-        }
+      const float gs = W.bias != nullptr ? g4 + bias_g[q] : g4;
+      const float us = W.bias != nullptr ? u4 + bias_u[q] : u4;
+      if (pe[q] >= 0) {
         const float h = act_fn(a.L.act, gs, us, a.L.swiglu_alpha, a.L.swiglu_limit);
-        const int p = list ? list[m2] : m2 * KP + shared_col;
-        store_scalar(a.hbuf, (size_t)p * a.Imax + ch, AT, h);
+        store_scalar(a.hbuf, (size_t)pe[q] * a.Imax + it * NT + j, AT, h);
       }
     }
     __syncthreads();
@@ -551,6 +567,95 @@ __global__ __launch_bounds__(kBlock) void k_stage_a(const LayerArgs a) {
   }
 }
 
+// ---------------------------------------------------------------- stage A, K-major formats
+// Work item: 8 channels of one expert = 16 weight rows (the 8 gate rows and
+// their 8 up rows), K split over the 4 waves of a workgroup and reduced
+// through LDS.  Lanes l % 16 < 8 produce gate sums, the others the matching
+// up sums; a DPP row shift brings each up sum next to its gate sum for the
+// activation.  Compared with 16-channel tiles (16 gate + 16 up rows), the
+// workgroup needs half the activation registers per weight byte in flight.
+constexpr int kDppRowShl8 = 0x108;  // lane i <- lane i + 8 within a 16-lane row
+
+template <int EFMT, int AT>
+__device__ void stage_a_rows(const LayerArgs& a, const ProjSlot& W, int Iu, int c0, int cnt, const int32_t* list,
+                             int shared_col, int kp, f32x4* red) {
+  constexpr int CH = 4;
+  constexpr int KS = 4;
+  const int lane = threadIdx.x & 63;
+  const int n = lane & 15;
+  const int H = a.L.hidden, KP = a.KP;
+  constexpr int XB = AType<AT>::kBytes;
+  const int lrow = n < 8 ? c0 + n : Iu + c0 + (n - 8);
+  const int sb_lo = W.group > 0 ? c0 / W.group : 0;
+  const int sb_hi = W.group > 0 ? (Iu + c0) / W.group : 0;
+  const int nL = fmt_loads<EFMT>(W.K);
+  const int L_lo = kp * nL / KS, L_hi = (kp + 1) * nL / KS;
+  const Rsrc xres = make_rsrc(a.x, (uint32_t)a.T * (uint32_t)H * XB);
+  const Rsrc lres = make_rsrc(list, list ? (uint32_t)cnt * 4u : 0u);
+  float bg = 0.0f, bu = 0.0f;
+  if (W.bias != nullptr && n < 8) {
+    bg = load_scalar(W.bias, c0 + n, W.bias_dt);
+    bu = load_scalar(W.bias, Iu + c0 + n, W.bias_dt);
+  }
+  for (int mb = 0; mb < cnt; mb += 16) {
+    const int pa = pair_of_row(lres, list != nullptr, mb + n, cnt, KP, shared_col);
+    int pe[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) pe[r] = pair_of_row(lres, list != nullptr, mb + 4 * (lane >> 4) + r, cnt, KP, shared_col);
+    const uint32_t arow = pa >= 0 ? (uint32_t)(pa / KP) * (uint32_t)H * XB : kOOB;
+    f32x4 acc = (f32x4){0.f, 0.f, 0.f, 0.f};
+    wave_rows_kmajor<EFMT, AT, CH>(W, lrow, sb_lo, sb_hi, L_lo, L_hi, xres, arow, acc);
+    red[kp * 64 + lane] = acc;
+    __syncthreads();
+    if (kp == 0) {
+      acc = red[lane];
+#pragma unroll
+      for (int j = 1; j < KS; ++j) acc += red[j * 64 + lane];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float gs = acc[r] + bg;
+        const float us = dpp_f<kDppRowShl8>(acc[r]) + bu;
+        if (n < 8 && pe[r] >= 0) {
+          const float h = act_fn(a.L.act, gs, us, a.L.swiglu_alpha, a.L.swiglu_limit);
+          store_scalar(a.hbuf, (size_t)pe[r] * a.Imax + c0 + n, AT, h);
+        }
+      }
+    }
+    __syncthreads();
+  }
+}
+
+// One 8-channel item per workgroup (routed items first, then the shared expert's).
+template <int FMT, int AT>
+__global__ __launch_bounds__(kBlock) void k_stage_a_rows(const LayerArgs a) {
+  __shared__ f32x4 red[4 * 64];
+  // wave index as a wave-uniform (scalar) value, so the FP8 scale addresses
+  // stay in SGPRs and use scalar loads
+  const int kp = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int I = a.L.inter;
+  const int t8 = I / 8;
+  const int item = blockIdx.x;
+  // expert table and routed count in flight together (uniq / ucnt hold E + 1)
+  const int u = min(item / t8, a.L.num_experts);
+  const int e = a.uniq[u], cnt = a.ucnt[u];
+  const int nRouted = a.ctrl[kCtrlNRouted];
+  if (item < nRouted * t8) {
+    const int slot = a.L.slot_of_expert ? a.L.slot_of_expert[e] : e;
+    if (slot < 0 || slot >= a.L.w13.num_slots) {
+      if (threadIdx.x == 0) atomicOr(&a.ctrl[kCtrlError], 1);
+      return;
+    }
+    const ProjSlot W = proj_slot(a.L.w13, slot);
+    stage_a_rows<FMT, AT>(a, W, I, (item % t8) * 8, cnt, a.lists + (size_t)e * a.T, 0, kp, red);
+  } else {
+    const int sitem = item - nRouted * t8;
+    const int Is = a.L.shared_inter;
+    if (Is <= 0 || sitem >= Is / 8) return;
+    const ProjSlot W = shared_view(a.L.shared_w13, 2 * Is, a.L.hidden);
+    stage_a_rows<FTM_FMT_BF16, AT>(a, W, Is, sitem * 8, a.T, nullptr, a.L.topk, kp, red);
+  }
+}
+
 // ============================================================== stage B (w2 -> slot buffer)
 // 64 output columns per workgroup.  K-major formats: 4 waves side by side,
 // 16 columns each, full K.  GPTQ: one 64-column wave tile, K split over the
@@ -560,6 +665,7 @@ __device__ void stage_b_body(const LayerArgs& a, const ProjSlot& W, int cnt, con
                              int shared_col, int nt, f32x4* red) {
   constexpr bool kG = EFMT == FTM_FMT_GPTQ_INT4;
   constexpr int XB = AType<AT>::kBytes;
+  constexpr int EPI = kG ? 16 * 64 / kBlock : 4;  // output elements per thread
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int H = a.L.hidden, KP = a.KP;
   int lo, hi;
@@ -571,13 +677,42 @@ __device__ void stage_b_body(const LayerArgs& a, const ProjSlot& W, int cnt, con
   }
   const int col0[1] = {kG ? nt * 64 : nt * 64 + 16 * wave};
   const Rsrc hres = make_rsrc(a.hbuf, (uint32_t)a.T * (uint32_t)KP * (uint32_t)a.Imax * XB);
-  for (int mb = 0; mb < cnt; mb += 16) {
-    const int m = mb + (lane & 15);
-    uint32_t arow = kOOB;
-    if (m < cnt) {
-      const int p = list ? list[m] : m * KP + shared_col;
-      arow = (uint32_t)p * (uint32_t)a.Imax * XB;
+  const Rsrc lres = make_rsrc(list, list ? (uint32_t)cnt * 4u : 0u);
+  const Rsrc wres = make_rsrc(a.wts, (uint32_t)a.T * (uint32_t)KP * 4u);
+  // output element q of this thread: (row, column)
+  auto elem = [&](int q, int& i, int& n) {
+    if constexpr (kG) {
+      const int idx = threadIdx.x + q * kBlock;
+      i = idx / 64;
+      n = nt * 64 + idx % 64;
+    } else {
+      i = 4 * (lane >> 4) + q;
+      n = col0[0] + (lane & 15);
     }
+  };
+  float bias_n[EPI];
+#pragma unroll
+  for (int q = 0; q < EPI; ++q) {
+    int i, n;
+    elem(q, i, n);
+    bias_n[q] = (W.bias != nullptr && n < H) ? load_scalar(W.bias, n, W.bias_dt) : 0.0f;
+  }
+  for (int mb = 0; mb < cnt; mb += 16) {
+    // list lookups and router weights of the block are issued before the
+    // weight stream; only the activation loads wait for them
+    const int pa = pair_of_row(lres, list != nullptr, mb + (lane & 15), cnt, KP, shared_col);
+    int pe[EPI];
+    float we[EPI];
+#pragma unroll
+    for (int q = 0; q < EPI; ++q) {
+      int i, n;
+      elem(q, i, n);
+      pe[q] = pair_of_row(lres, list != nullptr, mb + i, cnt, KP, shared_col);
+    }
+#pragma unroll
+    for (int q = 0; q < EPI; ++q) we[q] = __uint_as_float(bload4(wres, pe[q] >= 0 ? 4u * (uint32_t)pe[q] : kOOB));
+    const uint32_t arow = pa >= 0 ? (uint32_t)pa * (uint32_t)a.Imax * XB : kOOB;
+    float yv[EPI];
     if constexpr (kG) {
       f32x4 acc[1][4];
 #pragma unroll
@@ -586,35 +721,32 @@ __device__ void stage_b_body(const LayerArgs& a, const ProjSlot& W, int cnt, con
 #pragma unroll
       for (int c = 0; c < 4; ++c) red[(wave * 4 + c) * 64 + lane] = acc[0][c];
       __syncthreads();
-      for (int idx = threadIdx.x; idx < 16 * 64; idx += kBlock) {
+#pragma unroll
+      for (int q = 0; q < EPI; ++q) {
+        const int idx = threadIdx.x + q * kBlock;
         const int i = idx / 64, j = idx % 64;
         const int c = j & 3, ln = (j >> 2) + 16 * (i >> 2), rr = i & 3;
         float y = 0.0f;
 #pragma unroll
         for (int w = 0; w < 4; ++w) y += red[(w * 4 + c) * 64 + ln][rr];
-        const int m2 = mb + i, n = nt * 64 + j;
-        if (m2 < cnt && n < H) {
-          const int p = list ? list[m2] : m2 * KP + shared_col;
-          if (W.bias != nullptr) y += load_scalar(W.bias, n, W.bias_dt);
-          y *= a.wts[p];  // router weight (routed) or sigmoid gate (shared)
-          a.ybuf[(size_t)p * H + n] = y;
-        }
+        yv[q] = y;
       }
       __syncthreads();
     } else {
       f32x4 acc[1] = {(f32x4){0.f, 0.f, 0.f, 0.f}};
       wave_gemm_kmajor<EFMT, 1, AT>(W, col0, lo, hi, hres, arow, acc);
-      const int n = col0[0] + (lane & 15);
 #pragma unroll
-      for (int rr = 0; rr < 4; ++rr) {
-        const int m2 = mb + 4 * (lane >> 4) + rr;
-        if (m2 < cnt && n < H) {
-          const int p = list ? list[m2] : m2 * KP + shared_col;
-          float y = acc[0][rr];
-          if (W.bias != nullptr) y += load_scalar(W.bias, n, W.bias_dt);
-          y *= a.wts[p];  // router weight (routed) or sigmoid gate (shared)
-          a.ybuf[(size_t)p * H + n] = y;
-        }
+      for (int q = 0; q < EPI; ++q) yv[q] = acc[0][q];
+    }
+#pragma unroll
+    for (int q = 0; q < EPI; ++q) {
+      int i, n;
+      elem(q, i, n);
+      if (pe[q] >= 0 && n < H) {
+        float y = yv[q];
+        if (W.bias != nullptr) y += bias_n[q];
+        y *= we[q];  // router weight (routed) or sigmoid gate (shared)
+        a.ybuf[(size_t)pe[q] * H + n] = y;
       }
     }
   }
@@ -797,7 +929,16 @@ hipError_t launch_topk(const ftm_moe_layer& L, int T, const void* logits_in, int
 // which: bit 0 = stage A (w13 + act), bit 1 = stage B (w2), bit 2 = combine
 template <int FMT, int AT>
 static void launch_stages(const LayerArgs& a, int gridA, int gridB, hipStream_t st, int which) {
-  if (which & 1) hipLaunchKernelGGL((k_stage_a<FMT, AT>), dim3(gridA), dim3(kBlock), 0, st, a);
+  if (which & 1) {
+    if constexpr (FMT == FTM_FMT_GPTQ_INT4) {
+      hipLaunchKernelGGL((k_stage_a<FMT, AT>), dim3(gridA), dim3(kBlock), 0, st, a);
+    } else {
+      // one workgroup per 8-channel item (routed upper bound + shared)
+      const int maxU = a.L.num_experts < a.T * a.L.topk ? a.L.num_experts : a.T * a.L.topk;
+      const int items = maxU * (a.L.inter / 8) + (a.L.shared_inter > 0 ? a.L.shared_inter / 8 : 0);
+      hipLaunchKernelGGL((k_stage_a_rows<FMT, AT>), dim3(items), dim3(kBlock), 0, st, a);
+    }
+  }
   if (which & 2) hipLaunchKernelGGL((k_stage_b<FMT, AT>), dim3(gridB), dim3(kBlock), 0, st, a);
   if (which & 4) {
     const int n4 = a.T * (a.L.hidden / 4);
