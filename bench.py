@@ -51,7 +51,7 @@ def _pmc_traffic(config: str, T: int):
     summary (FETCH_SIZE + WRITE_SIZE per dispatch, scaled by the factor the
     same counters read for a copy kernel of known size), if one exists for
     this workload."""
-    path = os.path.join(ROOT, "profiles", f"k_stage_a__{config}_T{T}__pmc.md")
+    path = os.path.join(ROOT, "profiles", f"k_stage_a_rows__{config}_T{T}__pmc.md")
     try:
         with open(path) as f:
             for line in f:
@@ -202,7 +202,7 @@ def main() -> int:
     traffic = _pmc_traffic(cfg.name, T)
     roofline = {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": traffic["bytes"] if traffic else None,
-                "kernel": f"k_stage_a<{cfg.fmt}> (w13 + SiLU-gate)",
+                "kernel": f"k_stage_a_rows<{cfg.fmt}> (w13 + activation)",
                 "kernel_avg_us": round(kern_us["w13"], 2),
                 "bytes_per_launch": int(np.mean(bytes_a)),
                 "unit_bytes": w13_unit, "units_per_launch": round((np.mean(bytes_a) - sh_w13 - T * cfg.H * 2) / w13_unit, 2),
