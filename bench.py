@@ -40,6 +40,10 @@ def _parse():
     ap.add_argument("--sweep", default="1,4,16,64", help="extra decode batch sizes to report ('' = none)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--offload", action="store_true",
+                    help="run the C5 offload decode benchmark instead (64 HBM slots, 256 pinned host banks)")
+    ap.add_argument("--offload-steps", type=int, default=200)
+    ap.add_argument("--offload-slots", type=int, default=64)
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="after the bench, copy a buffer of this many MiB 3 times (a plain copy kernel of known "
                          "size, the reference point for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE)")
@@ -79,6 +83,9 @@ def main() -> int:
 
     from ftmoe import _native as nat
     from ftmoe import synthetic as S
+
+    if args.offload:
+        return _offload_bench(args)
 
     dev = torch.device("cuda:0")
     cfg = S.CONFIGS[args.config]
@@ -260,6 +267,108 @@ def main() -> int:
         "roofline": roofline,
         "cpu_baseline": cpu,
         "sweep": sweep,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+def _zipf_routing(rng, steps: int, T: int, E: int, k: int, s_exp: float = 1.1):
+    """Per token k distinct experts drawn Zipf(s) over ranks mapped through a
+    seeded permutation; router weights = softmax of N(0, 1) logits over the k."""
+    import numpy as np
+
+    perm = rng.permutation(E)
+    p = 1.0 / np.arange(1, E + 1) ** s_exp
+    p /= p.sum()
+    ids = np.empty((steps, T, k), np.int32)
+    for st in range(steps):
+        for t in range(T):
+            ids[st, t] = perm[rng.choice(E, k, replace=False, p=p)]
+    z = rng.randn(steps, T, k)
+    w = np.exp(z - z.max(-1, keepdims=True))
+    return ids, (w / w.sum(-1, keepdims=True)).astype(np.float32)
+
+
+def _offload_bench(args) -> int:
+    """C5: the C3 FP8 layer with only ``--offload-slots`` expert slots in HBM and
+    all 256 banks in pinned host memory.  Each step: LRU (host) -> copies of the
+    misses on a side stream -> grouped layer call over the slot pool (+ shared
+    expert).  Reports tokens/s, the hit rate over unique expert requests and the
+    achieved H2D GB/s next to a pinned 256 MiB host-to-device copy."""
+    import numpy as np
+    import torch
+
+    from ftmoe import synthetic as S
+    from ftmoe.moe.offload_cache import OffloadMoeCache, moe_grouped_forward
+
+    dev = torch.device("cuda:0")
+    cfg = S.CONFIGS["c3_fp8"]
+    T, steps, slots = args.batch, args.offload_steps, args.offload_slots
+    syn = S.generate(cfg, T=T, seed=0, device=dev)
+    bank_host = {k: v.cpu() for k, v in syn.bank.items()}
+    del syn.bank
+    torch.cuda.empty_cache()
+    cache = OffloadMoeCache(1, cfg.E, slots, dev, quant_format="fp8_block", decode_only=slots < cfg.E)
+    cache.set_bank_sources({b: [bank_host[b]] for b in cache.bank_schema})
+    del bank_host
+    rng = np.random.RandomState(0)
+    ids_all, w_all = _zipf_routing(rng, steps + 10, T, cfg.E, cfg.k)
+    ids_dev = torch.from_numpy(ids_all).to(dev)
+    w_dev = torch.from_numpy(w_all).to(dev)
+    gx = torch.Generator(device=dev).manual_seed(1234)
+    xs = [torch.randn(T, cfg.H, generator=gx, device=dev).to(torch.bfloat16) for _ in range(7)]
+    slot_bytes = sum(cache.bank_caches[b][0].numel() * cache.bank_caches[b].element_size() for b in cache.bank_schema)
+
+    def step(i):
+        cache.ensure_experts(0, torch.from_numpy(ids_all[i]))
+        misses = int(cache.num_indices.item())
+        cache.copy_missing()
+        moe_grouped_forward(xs[i % 7], ids_dev[i], w_dev[i], cache, 0, intermediate=cfg.I, shared=syn.shared)
+        return misses
+
+    for i in range(10):  # warm the pool and the kernels
+        step(steps + i)
+    torch.cuda.synchronize()
+    cache.reset_stats()
+    uniq = [len(np.unique(ids_all[i])) for i in range(steps)]
+    over = sum(u > slots for u in uniq)
+    misses = 0
+    t0 = time.perf_counter()
+    for i in range(steps):
+        misses += step(i)
+    torch.cuda.synchronize()
+    el = time.perf_counter() - t0
+    req = int(np.sum(uniq))
+    h2d = misses * slot_bytes
+
+    # the achievable pinned H2D rate on this box
+    src = torch.empty(256 << 20, dtype=torch.uint8, pin_memory=True)
+    dst = torch.empty(256 << 20, dtype=torch.uint8, device=dev)
+    dst.copy_(src, non_blocking=True)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(5):
+        dst.copy_(src, non_blocking=True)
+    e1.record()
+    torch.cuda.synchronize()
+    peak = 5 * (256 << 20) / (e0.elapsed_time(e1) * 1e-3) / 1e9
+
+    line = {
+        "metric": "offload decode tokens/s (C5: C3 FP8 layer, 64 HBM slots, 256 pinned host banks)",
+        "value": round(steps * T / el, 1), "unit": "tokens/s", "n_gpus": 1, "steps": steps, "warmup": 10,
+        "ms_per_step": round(el * 1e3 / steps, 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "bf16", "weights": cfg.fmt,
+        "data": "synthetic (seeded random-init FP8 banks at the C3 shape; Zipf(1.1) routing over a seeded "
+                "expert permutation, softmax weights of N(0,1) logits)",
+        "config": {"workload": f"c5 offload: {cfg.name} T={T}, slots={slots} of E={cfg.E}, one layer",
+                   "global_batch": T, "seq_len": 1, "parallelism": "none (1 GPU)"},
+        "hit_rate": round(1.0 - misses / req, 4), "misses_per_step": round(misses / steps, 2),
+        "unique_experts_per_step": round(float(np.mean(uniq)), 2), "steps_with_more_experts_than_slots": over,
+        "h2d_bytes_per_slot": slot_bytes, "h2d_GBps": round(h2d / el / 1e9, 2),
+        "h2d_pinned_copy_peak_GBps": round(peak, 2),
+        "h2d_frac_of_copy_peak": round(h2d / el / 1e9 / peak, 4),
+        "timing": "wall clock around the steps (host LRU + side-stream copies + kernels), synchronised at both ends",
     }
     print(json.dumps(line), flush=True)
     return 0

@@ -1,0 +1,505 @@
+"""Global timestamp-LRU pool of HBM expert slots fed by pinned host banks.
+
+The slot API of python/freetoken/moe/offload_cache.py:218-694
+(:class:`OffloadMoeCache`) and its per-slot weight view (:697-1128,
+:class:`SlotWeightAccessor`), kept name for name, with the pool on the GPU:
+
+* the LRU bookkeeping (``slot_for_id``, ``id_of_slot``, ``usage``, ``step`` and
+  the copy plan ``evict_slots`` / ``src_indices`` / ``num_indices``) lives in
+  host memory and is updated by the native ``ftm_lru_ensure`` /
+  ``ftm_lru_materialize`` (one C++ pass instead of per-slot ``.item()``
+  calls); the policy is the reference's: hits stamp ``usage = step``, the
+  misses (ascending expert id) each take the ``argmin (usage, slot)`` victim,
+  prefill first takes the lowest free slot;
+* the host banks are held in pinned memory and :meth:`copy_missing` enqueues
+  the staged rows with ``ftm_copy_slots`` (``hipMemcpyAsync``, contiguous runs
+  merged) on a side stream that first waits for the compute stream (a slot
+  being overwritten may still be read by earlier work); the compute stream
+  then waits on the copy's event, so the next layer forward sees the new
+  bytes without a host synchronisation;
+* ``slot_of_expert(layer)`` is the device ``int32 [E]`` map the layer kernels
+  read (``-1`` = not resident).
+
+A pool on the CPU (``device="cpu"``) keeps the bookkeeping usable for
+host-only tests, but :meth:`copy_missing` and every compute path need the GPU.
+"""
+from __future__ import annotations
+
+from typing import Optional
+
+import torch
+
+from .. import _native as nat
+
+# Bank names of each format (python/freetoken/moe/offload_cache.py:140-173).
+_BANK_SCHEMAS: dict = {
+    "bf16": ("gate_up", "down"),
+    "gptq_int4": ("qweight_gate_up", "qzeros_gate_up", "scales_gate_up", "qweight_down", "qzeros_down",
+                  "scales_down"),
+    "fp8_block": ("weight_gate_up", "scale_gate_up", "weight_down", "scale_down"),
+    "mxfp4": ("blocks_gate_up", "scales_gate_up", "blocks_down", "scales_down"),
+    "int8_channel": ("weight_packed_gate_up", "weight_scale_gate_up", "weight_packed_down", "weight_scale_down"),
+    "gguf_kquant": ("raw_gate", "raw_up", "raw_down"),
+}
+
+# Formats whose expert math the gfx950 kernels implement.
+_COMPUTE_FORMATS = ("bf16", "gptq_int4", "fp8_block", "mxfp4", "int8_channel")
+
+
+def gptq_int4_bytes_per_expert_slot(hidden_size: int, moe_intermediate_size: int, group_size: int, *,
+                                    qweight_bytes: int = 4, scale_bytes: int = 2) -> int:
+    """Packed bytes of one ``gptq_int4`` expert slot (offload_cache.py:176-215):
+    per projection ``[K, N]``: qweight ``K/8 x N`` words, qzeros
+    ``ceil(K/g) x N/8`` words, scales ``ceil(K/g) x N``; gate_up has
+    ``K = hidden``, ``N = 2 * inter``, down the reverse."""
+    if hidden_size <= 0 or moe_intermediate_size <= 0 or group_size <= 0:
+        raise ValueError(
+            "gptq_int4_bytes_per_expert_slot needs positive hidden_size / "
+            "moe_intermediate_size / group_size"
+        )
+
+    def proj(k: int, n: int) -> int:
+        groups = -(-k // group_size)
+        return (k // 8) * n * qweight_bytes + groups * (n // 8) * qweight_bytes + groups * n * scale_bytes
+
+    return proj(hidden_size, 2 * moe_intermediate_size) + proj(moe_intermediate_size, hidden_size)
+
+
+class OffloadMoeCache:
+    """A timestamp-LRU pool of device slots fed by per-layer host expert banks.
+
+    Args:
+        num_layers: MoE layers (``L``).
+        num_experts: experts per layer (``E``).
+        cache_size: device slots (``S >= E``).
+        device: the slot pool's device (a ROCm GPU; ``"cpu"`` for bookkeeping only).
+        quant_format: bank schema (``_BANK_SCHEMAS`` key).
+        prefill_overlap: accepted for signature compatibility.
+        decode_only: allow ``cache_size < num_experts`` (a pool that never holds
+            a whole layer, e.g. 64 slots for 256 experts); :meth:`materialize_layer`
+            then refuses.  Not in the reference, whose pool always fits a layer.
+    """
+
+    def __init__(self, num_layers: int, num_experts: int, cache_size: int, device, quant_format: str = "bf16",
+                 prefill_overlap: bool = False, *, decode_only: bool = False) -> None:
+        if quant_format not in _BANK_SCHEMAS:
+            raise ValueError(f"unknown quant_format {quant_format!r}")
+        self.decode_only = decode_only
+        if cache_size < 2 or (cache_size < num_experts and not decode_only):
+            raise ValueError(
+                f"cache_size {cache_size} must be >= num_experts {num_experts} "
+                "(the prefill double buffer borrows the first 2*num_experts slots)"
+            )
+        self.num_layers = num_layers
+        self.num_experts = num_experts
+        self.cache_size = cache_size
+        self.device = torch.device(device)
+        self.quant_format = quant_format
+        self.bank_schema = _BANK_SCHEMAS[quant_format]
+        self.prefill_overlap = prefill_overlap
+        self._alloc_bookkeeping(cache_size)
+        self.active_mask = torch.zeros((num_experts,), dtype=torch.int32)
+        self.step = torch.zeros((), dtype=torch.int64)
+        self.stat_missing = torch.zeros((), dtype=torch.int64)
+        self.stat_calls = torch.zeros((), dtype=torch.int64)
+        self.bank_sources: dict = {}
+        self.bank_caches: dict = {}
+        self.banks: list = []
+        self.extra_metadata: dict = {}
+        self._pending_src_layer: Optional[int] = None
+        self._pending_whole_layer = False
+        self._side_stream = None
+        self._copy_done = None
+        self._slot_dev: Optional[torch.Tensor] = None  # device mirror of slot_for_id
+
+    def _alloc_bookkeeping(self, cache_size: int) -> None:
+        self.slot_for_id = torch.full((self.num_layers, self.num_experts), -1, dtype=torch.int32)
+        self.id_of_slot = torch.full((cache_size,), -1, dtype=torch.int32)
+        self.usage = torch.zeros((cache_size,), dtype=torch.int64)
+        plan = max(self.num_experts, cache_size)
+        self.evict_slots = torch.zeros((plan,), dtype=torch.int32)
+        self.src_indices = torch.zeros((plan,), dtype=torch.int32)
+        self.num_indices = torch.zeros((1,), dtype=torch.int64)
+        self._staged = torch.zeros((1,), dtype=torch.int32)
+
+    # -- bank wiring ---------------------------------------------------------------
+
+    @property
+    def is_gpu(self) -> bool:
+        return self.device.type == "cuda"
+
+    @property
+    def is_xpu(self) -> bool:
+        """The reference's accelerator flag (offload_cache.py:691-694): true when
+        the pool lives on the accelerator (here a ROCm GPU)."""
+        return self.is_gpu
+
+    def set_bank_sources(self, sources: dict) -> None:
+        """Attach the host banks (``{bank: [num_layers x [E, ...] host tensor]}``)
+        and allocate one ``[cache_size, ...]`` device pool per bank.  Host banks
+        are kept in pinned memory (copied there if they are not already)."""
+        if set(sources) != set(self.bank_schema):
+            raise ValueError(
+                f"banks {sorted(sources)} do not match the {self.quant_format!r} schema {self.bank_schema}")
+        self.banks = []
+        for bank in self.bank_schema:
+            per_layer = sources[bank]
+            if len(per_layer) != self.num_layers:
+                raise ValueError(f"bank {bank!r} has {len(per_layer)} layers, expected {self.num_layers}")
+            hosts = []
+            for t in per_layer:
+                if t.device.type != "cpu":
+                    raise ValueError(f"bank {bank!r}: host sources must live in host memory")
+                t = t.contiguous()
+                if self.is_gpu and not t.is_pinned():
+                    t = t.pin_memory()
+                hosts.append(t)
+            row_shape = hosts[0].shape[1:]
+            cache = torch.zeros((self.cache_size, *row_shape), dtype=hosts[0].dtype, device=self.device)
+            self.bank_sources[bank] = hosts
+            self.bank_caches[bank] = cache
+            self.banks.append((hosts, cache))
+
+    def set_extra_metadata(self, name: str, per_layer: list) -> None:
+        if len(per_layer) != self.num_layers:
+            raise ValueError(f"extra metadata {name!r} has {len(per_layer)} layers, expected {self.num_layers}")
+        self.extra_metadata[name] = list(per_layer)
+
+    def get_extra_metadata(self, name: str, layer_id: int):
+        return self.extra_metadata[name][layer_id]
+
+    def rebuild(self, cache_size: int) -> None:
+        """Re-allocate the device pool at ``cache_size`` and clear the LRU state
+        (offload_cache.py:342-388); the host banks are kept."""
+        if cache_size < 2 or (cache_size < self.num_experts and not self.decode_only):
+            raise ValueError(f"rebuild cache_size {cache_size} must be >= num_experts {self.num_experts}")
+        self.cache_size = cache_size
+        self._alloc_bookkeeping(cache_size)
+        if self.bank_sources:
+            for bank in self.bank_schema:
+                hosts = self.bank_sources[bank]
+                self.bank_caches[bank] = torch.zeros((cache_size, *hosts[0].shape[1:]), dtype=hosts[0].dtype,
+                                                     device=self.device)
+            self.banks = [(self.bank_sources[b], self.bank_caches[b]) for b in self.bank_schema]
+        self.step.zero_()
+        self.active_mask.zero_()
+        self._pending_src_layer = None
+        self._pending_whole_layer = False
+        self._slot_dev = None
+
+    def bank_views(self, n: Optional[int] = None) -> tuple:
+        """Per-bank device pools in schema order: all ``S`` slots, or the first ``n``."""
+        if not self.banks:
+            raise AssertionError("set_bank_sources must register the banks first")
+        if n is None:
+            return tuple(cache for _, cache in self.banks)
+        return tuple(cache[:n] for _, cache in self.banks)
+
+    # -- reset -------------------------------------------------------------------
+
+    def _resync_slot_for_id(self) -> None:
+        """Rebuild ``slot_for_id`` from ``id_of_slot`` (the authoritative map)."""
+        E = self.num_experts
+        self.slot_for_id.fill_(-1)
+        ids = self.id_of_slot.to(torch.int64)
+        slots = (ids >= 0).nonzero(as_tuple=True)[0]
+        valid = ids[slots]
+        self.slot_for_id[valid // E, valid % E] = slots.to(torch.int32)
+        self._slot_dev = None
+
+    def reset(self) -> None:
+        self.slot_for_id.fill_(-1)
+        self.id_of_slot.fill_(-1)
+        self.usage.zero_()
+        self.step.zero_()
+        self.active_mask.zero_()
+        self.num_indices.zero_()
+        self._pending_src_layer = None
+        self._pending_whole_layer = False
+        self._slot_dev = None
+        for cache in self.bank_caches.values():
+            cache.zero_()
+        self.reset_stats()
+
+    def reset_stats(self) -> None:
+        self.stat_missing.zero_()
+        self.stat_calls.zero_()
+
+    def decode_miss_stats(self) -> dict:
+        return {"missing": int(self.stat_missing.item()), "calls": int(self.stat_calls.item())}
+
+    # -- LRU -----------------------------------------------------------------------
+
+    def _lru_args(self):
+        # host tensors updated in place by the native LRU
+        return (self.slot_for_id.data_ptr(), self.id_of_slot.data_ptr(), self.usage.data_ptr(),
+                self.step.data_ptr(), self.evict_slots.data_ptr(), self.src_indices.data_ptr(),
+                self._staged.data_ptr())
+
+    def materialize_layer(self, layer_id: int, expert_ids: Optional[torch.Tensor] = None) -> None:
+        """Make every expert of ``layer_id`` resident for a prefill forward
+        (offload_cache.py:461-556); ``expert_ids`` is accepted and left untouched."""
+        if not (0 <= layer_id < self.num_layers):
+            raise ValueError(f"Invalid materialize layer id {layer_id}")
+        if self.cache_size < self.num_experts:
+            raise ValueError(f"cache_size {self.cache_size} < num_experts {self.num_experts}: "
+                             "cannot materialize a whole layer")
+        self.active_mask.fill_(1)
+        rc = nat.lib().ftm_lru_materialize(layer_id, self.num_layers, self.num_experts, self.cache_size,
+                                           *self._lru_args())
+        nat.check(rc, "ftm_lru_materialize")
+        self._after_plan(layer_id, int(self._staged[0]), whole=True)
+
+    def ensure_experts(self, layer_id: int, expert_ids: torch.Tensor) -> None:
+        """Make this layer's routed experts resident (offload_cache.py:560-647):
+        hits keep their slots, each miss evicts the global LRU slot and is
+        staged for :meth:`copy_missing`.  ``expert_ids`` is read (a device
+        tensor is copied to the host) and never rewritten."""
+        if not (0 <= layer_id < self.num_layers):
+            raise ValueError(f"Invalid layer id {layer_id}")
+        if self.banks and self.cache_size < 2:
+            raise RuntimeError(
+                f"cache_size {self.cache_size} < 2: the pool cannot hold a routed expert plus "
+                "a victim to evict; raise moe_cache_size"
+            )
+        ids = expert_ids.reshape(-1).to("cpu", torch.int64).contiguous()
+        if ids.numel() and (int(ids.min()) < 0 or int(ids.max()) >= self.num_experts):
+            raise ValueError(f"expert ids must lie in [0, {self.num_experts})")
+        self.active_mask.zero_()
+        if ids.numel():
+            self.active_mask[ids] = 1
+        rc = nat.lib().ftm_lru_ensure(layer_id, self.num_layers, self.num_experts, self.cache_size,
+                                      ids.data_ptr() if ids.numel() else None, int(ids.numel()),
+                                      *self._lru_args())
+        nat.check(rc, "ftm_lru_ensure")
+        self._after_plan(layer_id, int(self._staged[0]), whole=False)
+
+    def _after_plan(self, layer_id: int, staged: int, whole: bool) -> None:
+        self.num_indices.fill_(staged)
+        self.stat_missing += staged
+        self.stat_calls += 1
+        self._pending_src_layer = layer_id
+        self._pending_whole_layer = whole
+        self._slot_dev = None
+
+    # -- copy engine -----------------------------------------------------------------
+
+    def copy_missing(self) -> None:
+        """Stream the staged (slot, host row) pairs of every bank into the device
+        pools on a side stream (pinned host -> HBM), ordered after the work
+        already queued on the current stream, and make the current stream wait
+        for the copies."""
+        if not self.banks:
+            raise AssertionError("set_bank_sources must register the banks first")
+        layer_id = self._pending_src_layer
+        if layer_id is None:
+            return
+        if not self.is_gpu:
+            raise RuntimeError("copy_missing streams into a GPU slot pool; this cache lives on the CPU")
+        n = int(self.num_indices.item())
+        if n:
+            cur = torch.cuda.current_stream(self.device)
+            if self._side_stream is None:
+                self._side_stream = torch.cuda.Stream(device=self.device)
+                self._copy_done = torch.cuda.Event()
+            side = self._side_stream
+            side.wait_stream(cur)
+            for hosts, cache in self.banks:
+                host = hosts[layer_id]
+                row_bytes = host[0].numel() * host.element_size()
+                rc = nat.lib().ftm_copy_slots(cache.data_ptr(), host.data_ptr(), row_bytes,
+                                              self.evict_slots.data_ptr(), self.src_indices.data_ptr(), n,
+                                              side.cuda_stream, None)
+                nat.check(rc, "ftm_copy_slots")
+            self._copy_done.record(side)
+            cur.wait_event(self._copy_done)
+        self._pending_src_layer = None
+        self._pending_whole_layer = False
+
+    # -- device helpers ----------------------------------------------------------------
+
+    def slot_of_expert(self, layer_id: int) -> torch.Tensor:
+        """Device ``int32 [E]``: the slot holding each expert of ``layer_id``, -1 if
+        not resident (what the layer kernels read)."""
+        if self._slot_dev is None:
+            src = self.slot_for_id.pin_memory() if self.is_gpu else self.slot_for_id
+            self._slot_dev = src.to(self.device, non_blocking=True)
+        return self._slot_dev[layer_id]
+
+    def resident_slots(self, layer_id: int) -> list:
+        E = self.num_experts
+        base = layer_id * E
+        ids = self.id_of_slot
+        return [s for s in range(self.cache_size) if base <= int(ids[s]) < base + E]
+
+
+class SlotWeightAccessor:
+    """Per-slot expert weights of one MoE layer over an :class:`OffloadMoeCache`
+    pool (offload_cache.py:697-1128): packed views (``get_*_packed``), dense
+    dequantized ``(gate [I, H], up [I, H], down [H, I])`` (:meth:`get`, the GPU
+    dequant kernel, cached per instance) and :meth:`expert_forward` (the fused
+    gfx950 expert kernel up to the format's crossover, dequant + matmul above).
+
+    Args:
+        cache: the slot pool (its banks must be registered).
+        intermediate: ``I`` (moe_intermediate_size).
+        dtype: the activation dtype (the dequant output dtype).
+        layer_id: accepted for signature compatibility (``gguf_kquant`` only).
+    """
+
+    def __init__(self, cache: OffloadMoeCache, intermediate: int, dtype: torch.dtype, *,
+                 layer_id: Optional[int] = None) -> None:
+        self.quant_format = getattr(cache, "quant_format", "bf16")
+        self._intermediate = int(intermediate)
+        self._dtype = dtype
+        self._cache_obj = cache
+        self._cache: dict = {}
+        self._layer = None
+        fmt = self.quant_format
+        if fmt not in _COMPUTE_FORMATS:
+            raise ValueError(f"SlotWeightAccessor: quant_format {fmt!r} has no gfx950 kernel in this build")
+        self._banks = dict(zip(cache.bank_schema, cache.bank_views()))
+        if fmt == "gptq_int4":
+            group_size = getattr(cache, "gptq_group_size", None)
+            if group_size is None:
+                raise ValueError(
+                    "OffloadMoeCache.gptq_group_size is not set -- the loader must set it "
+                    "from the checkpoint's quantization_config.group_size before any "
+                    "gptq_int4 forward pass runs (SlotWeightAccessor refuses to guess)"
+                )
+            self._group_size = int(group_size)
+        elif fmt == "fp8_block":
+            self._fp8_block = int(getattr(cache, "fp8_block_size", None) or 128)
+        elif fmt == "int8_channel":
+            k_gate_up = getattr(cache, "int8_k_gate_up", None)
+            k_down = getattr(cache, "int8_k_down", None)
+            if k_gate_up is None or k_down is None:
+                raise ValueError(
+                    "OffloadMoeCache.int8_k_gate_up / int8_k_down are not set -- the loader "
+                    "must set them from the checkpoint's real weight_shape before any "
+                    "int8_channel forward pass runs (SlotWeightAccessor refuses to guess)"
+                )
+            self._int8_k_gate_up = int(k_gate_up)
+            self._int8_k_down = int(k_down)
+        if fmt == "bf16":
+            self._gu, self._dn = cache.bank_views()
+
+    # -- packed views ----------------------------------------------------------------
+
+    def _require(self, fmt: str, what: str) -> None:
+        if self.quant_format != fmt:
+            raise ValueError(f"{what} is {fmt}-only, got quant_format={self.quant_format!r}")
+
+    def get_gptq_packed(self, s_i: int):
+        self._require("gptq_int4", "get_gptq_packed")
+        b = self._banks
+        return (b["qweight_gate_up"][s_i], b["qzeros_gate_up"][s_i], b["scales_gate_up"][s_i],
+                b["qweight_down"][s_i], b["qzeros_down"][s_i], b["scales_down"][s_i], self._group_size)
+
+    def get_fp8_packed(self, s_i: int):
+        self._require("fp8_block", "get_fp8_packed")
+        b = self._banks
+        return (b["weight_gate_up"][s_i], b["scale_gate_up"][s_i], b["weight_down"][s_i], b["scale_down"][s_i],
+                self._fp8_block)
+
+    def get_mxfp4_packed(self, s_i: int):
+        self._require("mxfp4", "get_mxfp4_packed")
+        b = self._banks
+        return (b["blocks_gate_up"][s_i], b["scales_gate_up"][s_i], b["blocks_down"][s_i], b["scales_down"][s_i])
+
+    def get_int8_packed(self, s_i: int):
+        self._require("int8_channel", "get_int8_packed")
+        b = self._banks
+        return (b["weight_packed_gate_up"][s_i], b["weight_scale_gate_up"][s_i], b["weight_packed_down"][s_i],
+                b["weight_scale_down"][s_i], self._int8_k_gate_up, self._int8_k_down)
+
+    # -- the pool as one MoE layer (expert = slot) -----------------------------------
+
+    def _hidden(self) -> int:
+        b, fmt = self._banks, self.quant_format
+        if fmt == "bf16":
+            return int(self._gu.shape[-1])
+        if fmt == "fp8_block":
+            return int(b["weight_gate_up"].shape[-1])
+        if fmt == "gptq_int4":
+            return int(b["qweight_gate_up"].shape[1]) * 8
+        if fmt == "int8_channel":
+            return self._int8_k_gate_up
+        return int(b["blocks_gate_up"].shape[2]) * 32  # mxfp4
+
+    def pool_layer(self):
+        """The slot pool as a :class:`~ftmoe.layer.MoeLayer` whose expert ``s`` is
+        slot ``s`` (no router): what :meth:`expert_forward` runs on."""
+        if self._layer is None:
+            from ..banks import proj_from_bank
+            from ..layer import MoeLayer
+
+            I, H, fmt = self._intermediate, self._hidden(), self.quant_format
+            group = {"gptq_int4": getattr(self, "_group_size", None), "fp8_block": getattr(self, "_fp8_block", None),
+                     "mxfp4": 32}.get(fmt)
+            kd = self._int8_k_down if fmt == "int8_channel" else I
+            w13 = proj_from_bank(fmt, self._banks, which="gate_up", N=2 * I, K=H, group=group)
+            w2 = proj_from_bank(fmt, self._banks, which="down", N=H, K=kd, group=group)
+            self._layer = MoeLayer(w13=w13, w2=w2, num_experts=w13.num_slots, hidden=H, inter=I, topk=1,
+                                   act_dtype=self._dtype)
+        return self._layer
+
+    def expert_forward(self, s_i: int, x: torch.Tensor) -> torch.Tensor:
+        """``down(silu(gate(x)) * up(x))`` for slot ``s_i``: the fused expert kernel
+        (fp32 accumulation, ``h`` rounded to the activation dtype) when the
+        format's ``prefer_fused_over_dequant(rows)`` holds, else the dense
+        weights of :meth:`get` through torch matmuls on the GPU."""
+        nat.require_gpu(x, "x")
+        from ..kernel import fused_fp8_linear, fused_int8_linear, fused_mxfp4_linear, gptq_fused_linear
+
+        prefer = {"fp8_block": fused_fp8_linear.prefer_fused_over_dequant,
+                  "int8_channel": fused_int8_linear.prefer_fused_over_dequant,
+                  "mxfp4": fused_mxfp4_linear.prefer_fused_over_dequant,
+                  "gptq_int4": gptq_fused_linear.prefer_fused_over_dequant}.get(self.quant_format)
+        if self.quant_format == "bf16" or (prefer is not None and prefer(x.shape[0])):
+            return self.pool_layer().expert_forward(int(s_i), x.to(self._dtype))
+        gate_w, up_w, down_w = self.get(s_i)
+        return (torch.nn.functional.silu(x @ gate_w.t()) * (x @ up_w.t())) @ down_w.t()
+
+    def get(self, s_i: int):
+        """``(gate_w [I, H], up_w [I, H], down_w [H, I])`` of slot ``s_i`` in the
+        accessor's dtype, dequantized once per instance by the GPU kernel."""
+        I = self._intermediate
+        if self.quant_format == "bf16":
+            return self._gu[s_i, 0:I], self._gu[s_i, I:2 * I], self._dn[s_i]
+        cached = self._cache.get(s_i)
+        if cached is not None:
+            return cached
+        from ..kernel._dequant import dequant
+
+        layer = self.pool_layer()
+        gu = dequant(layer.w13, out_dtype=self._dtype, slot=int(s_i))
+        dn = dequant(layer.w2, out_dtype=self._dtype, slot=int(s_i))
+        result = (gu[0:I], gu[I:2 * I], dn)
+        self._cache[s_i] = result
+        return result
+
+
+def moe_grouped_forward(flat: torch.Tensor, top_idx: torch.Tensor, top_w: torch.Tensor, cache: OffloadMoeCache,
+                        layer_id: int, *, intermediate: int, act: str = "silu", shared: Optional[dict] = None,
+                        swiglu_alpha: float = 1.702, swiglu_limit: float = 7.0) -> torch.Tensor:
+    """One grouped call for a layer whose experts sit in the slot pool: replaces
+    the per-(token, expert) loop of ``_forward_offload_core``
+    (python/freetoken/models/qwen3_5_moe/__init__.py:1706-1737).  ``top_idx`` /
+    ``top_w`` ``[T, k]`` are expert ids and router weights; the layer must have
+    been made resident with :meth:`OffloadMoeCache.ensure_experts` and
+    :meth:`~OffloadMoeCache.copy_missing` (a routed expert that is not resident
+    contributes zeros and sets the workspace error bit)."""
+    acc = SlotWeightAccessor(cache, intermediate, flat.dtype)
+    pool = acc.pool_layer()
+    from ..layer import MoeLayer
+
+    layer = MoeLayer(w13=pool.w13, w2=pool.w2, num_experts=cache.num_experts, hidden=pool.hidden,
+                     inter=intermediate, topk=int(top_idx.shape[1]), shared=shared, act=act,
+                     swiglu_alpha=swiglu_alpha, swiglu_limit=swiglu_limit,
+                     slot_of_expert=cache.slot_of_expert(layer_id), act_dtype=flat.dtype)
+    return layer.forward_routed(flat, top_idx, top_w)
+
+
+__all__ = ["OffloadMoeCache", "SlotWeightAccessor", "_BANK_SCHEMAS", "gptq_int4_bytes_per_expert_slot",
+           "moe_grouped_forward"]

@@ -1,0 +1,110 @@
+"""GPU: the offload slot pool (OffloadMoeCache + SlotWeightAccessor + the grouped
+layer call over resident slots).
+
+* copy_missing streams exactly the staged host rows into the staged slots
+  (distinguishable banks, restating tests/test_moe_offload_cache.py:66-292);
+* a two-layer FP8 pool smaller than one layer's experts: every decode step
+  (route -> ensure_experts -> copy_missing -> moe_grouped_forward) matches the
+  oracle computed from the full host bank, to the layer tolerance;
+* SlotWeightAccessor.get is the bit-exact dequantization of the slot and
+  expert_forward matches the oracle's expert."""
+import numpy as np
+import pytest
+import torch
+
+import ftm_oracle as O
+from ftm_helpers import assert_close, np_, oracle_proj, oracle_spec, to_f32
+
+from ftmoe import synthetic as S
+from ftmoe.moe.offload_cache import OffloadMoeCache, SlotWeightAccessor, moe_grouped_forward
+
+pytestmark = pytest.mark.gpu
+
+L, E, SL = 2, 4, 8
+H, I = 16, 8
+
+
+def _bank_values(layer, expert):
+    base = 100 * (layer + 1) + 10 * (expert + 1)
+    gate_up = torch.cat([torch.full((I, H), base + 0.0), torch.full((I, H), base + 1.0)])
+    return gate_up, torch.full((H, I), base + 2.0)
+
+
+def _sources():
+    return {"gate_up": [torch.stack([_bank_values(l, e)[0] for e in range(E)]) for l in range(L)],
+            "down": [torch.stack([_bank_values(l, e)[1] for e in range(E)]) for l in range(L)]}
+
+
+def test_copy_missing_streams_the_staged_rows(gpu):
+    c = OffloadMoeCache(L, E, E, gpu)
+    c.set_bank_sources(_sources())
+    c.materialize_layer(0)
+    c.copy_missing()
+    torch.cuda.synchronize()
+    for e in range(E):
+        gu, dn = _bank_values(0, e)
+        assert torch.equal(c.bank_caches["gate_up"][e].cpu(), gu)
+        assert torch.equal(c.bank_caches["down"][e].cpu(), dn)
+    c.step.fill_(3)
+    c.usage[:] = torch.arange(E, dtype=torch.int64) + 1
+    c.ensure_experts(1, torch.tensor([0], device=gpu))  # evicts the LRU slot 0
+    assert int(c.slot_for_id[1, 0]) == 0
+    c.copy_missing()
+    torch.cuda.synchronize()
+    assert torch.equal(c.bank_caches["gate_up"][0].cpu(), _bank_values(1, 0)[0])
+    assert torch.equal(c.bank_caches["down"][0].cpu(), _bank_values(1, 0)[1])
+    for e in range(1, E):  # untouched slots keep layer 0
+        assert torch.equal(c.bank_caches["down"][e].cpu(), _bank_values(0, e)[1])
+    sl = c.slot_of_expert(1)
+    assert sl.is_cuda and sl.dtype == torch.int32 and sl.tolist() == [0, -1, -1, -1]
+
+
+def _fp8_pool(gpu, slots, seeds=(31, 32)):
+    cfg = S.SMALL["c3_fp8"]
+    syns = [S.generate(cfg, T=12, seed=s) for s in seeds]
+    c = OffloadMoeCache(len(syns), cfg.E, slots, gpu, quant_format="fp8_block", decode_only=slots < cfg.E)
+    c.set_bank_sources({b: [syn.bank[b] for syn in syns] for b in c.bank_schema})
+    return cfg, syns, c
+
+
+def test_fp8_pool_decode_steps_match_oracle(gpu):
+    cfg, syns, c = _fp8_pool(gpu, slots=24)  # 24 slots for 2 layers x 32 experts (decode-only pool)
+    rng = np.random.RandomState(5)
+    T = 5  # at most 20 routed experts per step: all of them fit the 24 slots at once
+    for step in range(6):
+        layer_id = step % 2
+        syn = syns[layer_id]
+        x = syn.x[:T]
+        ids = np.stack([rng.choice(cfg.E, cfg.k, replace=False) for _ in range(T)]).astype(np.int32)
+        w = O.round_bf16(rng.rand(T, cfg.k).astype(np.float32))
+        c.ensure_experts(layer_id, torch.from_numpy(ids).to(gpu))
+        c.copy_missing()
+        shared = {k: v.to(gpu) for k, v in syn.shared.items()}
+        out = moe_grouped_forward(x.to(gpu), torch.from_numpy(ids).to(gpu), torch.from_numpy(w).to(gpu), c,
+                                  layer_id, intermediate=cfg.I, shared=shared)
+        ref = O.layer_reference(oracle_spec(syn), np_(x), ids=ids, w=w)
+        assert_close(to_f32(out), ref["out"], what=f"pool step {step}")
+    st = c.decode_miss_stats()
+    assert st["calls"] == 6 and st["missing"] > 0
+
+
+def test_accessor_get_and_expert_forward(gpu):
+    cfg, syns, c = _fp8_pool(gpu, slots=32, seeds=(33,))
+    c.materialize_layer(0)
+    c.copy_missing()
+    acc = SlotWeightAccessor(c, cfg.I, torch.bfloat16)
+    spec13 = oracle_proj(cfg.fmt, syns[0].bank, "gate_up", 2 * cfg.I, cfg.H, cfg.group)
+    spec2 = oracle_proj(cfg.fmt, syns[0].bank, "down", cfg.H, cfg.I, cfg.group)
+    for slot in (0, 5, 31):
+        e = int(c.id_of_slot[slot]) % cfg.E
+        gate, up, down = acc.get(slot)
+        gu_ref = O.round_bf16(O.dequant(spec13, e))
+        np.testing.assert_array_equal(to_f32(gate), gu_ref[:cfg.I])
+        np.testing.assert_array_equal(to_f32(up), gu_ref[cfg.I:])
+        np.testing.assert_array_equal(to_f32(down), O.round_bf16(O.dequant(spec2, e)))
+        x = syns[0].x[:3].to(gpu)
+        got = acc.expert_forward(slot, x)
+        ref = O.expert_forward(spec13, spec2, e, O.bf16_bits_to_f32(np_(x)))
+        assert_close(to_f32(got), ref, what=f"expert slot {slot}")
+    fp8 = acc.get_fp8_packed(0)
+    assert fp8[0].shape == (2 * cfg.I, cfg.H) and fp8[4] == 128
