@@ -1,0 +1,501 @@
+// ftm_gemm.hip -- the MoE expert stages above the token crossover: grouped,
+// LDS-tiled GEMMs on bf16 MFMA (v_mfma_f32_16x16x32_bf16).
+//
+// Below the crossover every expert sees a handful of tokens and the stages are
+// weight-streaming GEMVs (ftm_moe.hip).  Above it (prefill) each expert's
+// weights are reused by many tokens, so a tile of 64 tokens x 64 channels
+// loads its weights once per K step into LDS, decoded to bf16 exactly (FP8
+// e4m3 and INT8 codes are exact in bf16, MXFP4 e2m1 times its power-of-two
+// scale is exact), and four waves run 16x16x32 MFMAs out of LDS.  FP8 block
+// and INT8 group scales multiply the fp32 partial sums of each quantisation
+// group, as in the GEMV path, so both paths share one numerical contract.
+//
+// Tiles: the routed experts' token lists are cut into 64-row M tiles
+// (ascending compact expert index u), then the shared expert's tokens.  Stage
+// A (w13 + activation): a tile covers 64 channels, i.e. the 64 gate rows and
+// the matching 64 up rows of w13, and writes h.  Stage B (w2): a tile covers
+// 64 output columns and writes router-weighted fp32 rows into the slot buffer
+// that k_combine reduces.
+#include "ftm_layer.h"
+
+namespace ftm {
+
+constexpr int kGM = 64;            // tokens per tile
+constexpr int kGK = 64;            // K per step
+constexpr int kGPitch = kGK + 8;   // LDS row pitch in bf16 (144 B: rows do not share a bank period)
+// Crossover, in average tokens per routed expert.  Measured on MI355X (C3 FP8
+// and C4 MXFP4 layers): the tiles win from 16 on (C3 T=512: 466 us against
+// 723 us on the GEMVs; C4 T=128: 360 us against 380 us) and lose at 8 and
+// below (C4 T=64: 341 us against 236 us; C4 T=32: 333 us against 193 us).
+constexpr int kGemmMinRows = 16;
+
+// Weight bytes per element and 16-byte pieces per tile row per K step.
+template <int WFMT>
+struct GemmW {
+  static constexpr int kPieces = WFMT == FTM_FMT_BF16 ? 8 : WFMT == FTM_FMT_MXFP4 ? 2 : 4;
+  static constexpr int kElems = kGK / kPieces;  // elements per piece
+  static constexpr bool kPostScale = WFMT == FTM_FMT_FP8_BLOCK || WFMT == FTM_FMT_INT8_PACKED;
+  __device__ static uint32_t row_bytes(int K) {
+    return WFMT == FTM_FMT_BF16 ? 2u * (uint32_t)K : WFMT == FTM_FMT_MXFP4 ? (uint32_t)K / 2 : (uint32_t)K;
+  }
+};
+
+// M tile -> (compact expert u, first row, token count).  u == nRouted is the
+// shared expert; u < 0: past the last tile.  Every lane of the calling wave
+// gets the same answer (wave-uniform, no LDS).
+struct GemmTile {
+  int u, m0, cnt;
+};
+
+__device__ __forceinline__ GemmTile gemm_find_tile(const LayerArgs& a, int mtile, int nRouted, bool shared) {
+  const int lane = threadIdx.x & 63;
+  // lane l owns compact experts 8l .. 8l+7 (E <= 512)
+  const Rsrc cres = make_rsrc(a.ucnt, (uint32_t)(a.L.num_experts + 1) * 4u);
+  int v[8], c[8];
+  int lsum = 0;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int u = 8 * lane + j;
+    c[j] = u < nRouted ? (int)bload4(cres, 4u * (uint32_t)u) : 0;
+    v[j] = (c[j] + kGM - 1) / kGM;
+    lsum += v[j];
+  }
+  // exclusive prefix over lanes
+  int incl = lsum;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int o = __shfl_up(incl, off);
+    if (lane >= off) incl += o;
+  }
+  const int total = __shfl(incl, 63);
+  GemmTile t = {-1, 0, 0};
+  if (mtile < total) {
+    int base = incl - lsum;
+    int found_u = -1, found_m0 = 0, found_cnt = 0;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      if (found_u < 0 && mtile >= base && mtile < base + v[j]) {
+        found_u = 8 * lane + j;
+        found_m0 = (mtile - base) * kGM;
+        found_cnt = c[j];
+      }
+      base += v[j];
+    }
+    const uint64_t who = __ballot(found_u >= 0);
+    const int src = (int)__builtin_ctzll(who);
+    t.u = __shfl(found_u, src);
+    t.m0 = __shfl(found_m0, src);
+    t.cnt = __shfl(found_cnt, src);
+  } else if (shared) {
+    const int st = mtile - total;
+    if (st * kGM < a.T) {
+      t.u = nRouted;
+      t.m0 = st * kGM;
+      t.cnt = a.T;
+    }
+  }
+  return t;
+}
+
+// Routed M tiles (device total) for the item -> tile mapping of a stage whose
+// routed part has ntn N tiles per M tile.
+__device__ __forceinline__ int gemm_routed_mtiles(const LayerArgs& a, int nRouted) {
+  const int lane = threadIdx.x & 63;
+  const Rsrc cres = make_rsrc(a.ucnt, (uint32_t)(a.L.num_experts + 1) * 4u);
+  int lsum = 0;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int u = 8 * lane + j;
+    lsum += u < nRouted ? ((int)bload4(cres, 4u * (uint32_t)u) + kGM - 1) / kGM : 0;
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) lsum += __shfl_xor(lsum, off);
+  return lsum;
+}
+
+// One 64-token x (NWR weight rows) tile over the whole K range.
+//   WFMT: weight format; NWR = 128 (stage A: 64 gate + 64 up rows) or 64 (stage B)
+//   grow(r): global weight row of tile row r
+//   arow[i]: byte offset of the activation row of A piece i of this thread (kOOB = zero row)
+//   acc[mi][nj]: wave (wm, wn) tile: tokens 32wm + 16mi, tile rows nrow(nj)
+template <int WFMT, int NWR, int AXB>
+struct GemmTileRun {
+  static constexpr int NB = NWR == 128 ? 4 : 2;  // 16-column MFMA blocks per wave
+  static constexpr int kWPieces = NWR * GemmW<WFMT>::kPieces;
+  static constexpr int kWLoads = (kWPieces + kBlock - 1) / kBlock;
+
+  // tile row of MFMA column block nj of wave column wn
+  __device__ static int nrow(int nj, int wn) {
+    if constexpr (NWR == 128) return nj < 2 ? 32 * wn + 16 * nj : 64 + 32 * wn + 16 * (nj - 2);
+    return 32 * wn + 16 * nj;
+  }
+};
+
+template <int WFMT, int NWR>
+__device__ __forceinline__ void gemm_tile(const ProjSlot& W, int c0, int Iu, Rsrc ares, const uint32_t (&arow)[2],
+                                          uint16_t* sA, uint16_t* sB, f32x4 (&acc)[2][NWR == 128 ? 4 : 2]) {
+  using G = GemmW<WFMT>;
+  using R = GemmTileRun<WFMT, NWR, 2>;
+  constexpr int NB = R::NB;
+  constexpr int kSA = kGM * kGPitch, kSB = NWR * kGPitch;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave & 1, wn = wave >> 1;
+  const int K = W.K;
+  const int nsteps = (K + kGK - 1) / kGK;
+  auto grow = [&](int r) { return NWR == 128 ? (r < 64 ? c0 + r : Iu + c0 + (r - 64)) : c0 + r; };
+
+  const uint32_t rb = G::row_bytes(K);
+  const Rsrc wres = make_rsrc(W.w, rb * (uint32_t)W.N);
+  uint32_t woff[R::kWLoads];
+  int wtr[R::kWLoads], wpc[R::kWLoads];
+#pragma unroll
+  for (int i = 0; i < R::kWLoads; ++i) {
+    const int c = tid + kBlock * i;
+    wtr[i] = c / G::kPieces;
+    wpc[i] = c % G::kPieces;
+    const int r = grow(wtr[i]);
+    woff[i] = (c < R::kWPieces && r < W.N) ? (uint32_t)r * rb + (uint32_t)wpc[i] * 16u : kOOB;
+  }
+  Rsrc sres = wres;  // MXFP4 e8m0 scales: one byte per (row, 32 elements)
+  uint32_t moff[R::kWLoads];
+  if constexpr (WFMT == FTM_FMT_MXFP4) {
+    sres = make_rsrc(W.s, (uint32_t)W.N * (uint32_t)(K / 32));
+#pragma unroll
+    for (int i = 0; i < R::kWLoads; ++i) {
+      const int r = grow(wtr[i]);
+      moff[i] = woff[i] != kOOB ? (uint32_t)(r * (K / 32) + wpc[i]) : kOOB;
+    }
+  }
+  // post-scale sources: FP8 block rows (uniform per column block), INT8 rows (per lane)
+  const int lpg = G::kPostScale ? W.group / kGK : 1;
+  int srow[NB];
+#pragma unroll
+  for (int nj = 0; nj < NB; ++nj) srow[nj] = grow(R::nrow(nj, wn));
+  const uint32_t sesz = W.s_dt == FTM_DT_F32 ? 4u : 2u;
+  Rsrc i8res = wres;
+  if constexpr (WFMT == FTM_FMT_INT8_PACKED) i8res = make_rsrc(W.s, (uint32_t)(W.N * (K / W.group)) * sesz);
+
+  u32x4 rw[R::kWLoads], ra[2];
+  uint32_t rs[R::kWLoads];
+  auto issue = [&](int kb) {
+    const uint32_t kbyte = (uint32_t)kb * (uint32_t)(kGK * (WFMT == FTM_FMT_BF16 ? 2 : 1));
+    const uint32_t kbw = WFMT == FTM_FMT_MXFP4 ? kbyte / 2 : kbyte;
+#pragma unroll
+    for (int i = 0; i < R::kWLoads; ++i) {
+      rw[i] = bload16(wres, woff[i] != kOOB ? woff[i] + kbw : kOOB);
+      if constexpr (WFMT == FTM_FMT_MXFP4) rs[i] = bload1(sres, moff[i] != kOOB ? moff[i] + (uint32_t)(2 * kb) : kOOB);
+    }
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int piece = (tid + kBlock * i) & 7;
+      ra[i] = bload16(ares, arow[i] != kOOB ? arow[i] + (uint32_t)(kb * kGK + piece * 8) * 2u : kOOB);
+    }
+  };
+  auto stage = [&](int buf) {
+    uint16_t* a_ = sA + buf * kSA;
+    uint16_t* b_ = sB + buf * kSB;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int c = tid + kBlock * i;
+      *(u32x4*)(a_ + (c >> 3) * kGPitch + (c & 7) * 8) = ra[i];
+    }
+#pragma unroll
+    for (int i = 0; i < R::kWLoads; ++i) {
+      if (tid + kBlock * i >= R::kWPieces) continue;
+      uint16_t* dst = b_ + wtr[i] * kGPitch + wpc[i] * G::kElems;
+      if constexpr (WFMT == FTM_FMT_FP8_BLOCK) {
+        *(u32x4*)dst = fp8x8_to_bf16(rw[i].x, rw[i].y);
+        *(u32x4*)(dst + 8) = fp8x8_to_bf16(rw[i].z, rw[i].w);
+      } else if constexpr (WFMT == FTM_FMT_INT8_PACKED) {
+        *(u32x4*)dst = i8x8_to_bf16(rw[i].x, rw[i].y);
+        *(u32x4*)(dst + 8) = i8x8_to_bf16(rw[i].z, rw[i].w);
+      } else if constexpr (WFMT == FTM_FMT_MXFP4) {
+        const float sc = e8m0_to_f32(rs[i]);
+        *(u32x4*)dst = fp4x8_to_bf16(rw[i].x, sc);
+        *(u32x4*)(dst + 8) = fp4x8_to_bf16(rw[i].y, sc);
+        *(u32x4*)(dst + 16) = fp4x8_to_bf16(rw[i].z, sc);
+        *(u32x4*)(dst + 24) = fp4x8_to_bf16(rw[i].w, sc);
+      } else {
+        *(u32x4*)dst = rw[i];
+      }
+    }
+  };
+
+  f32x4 tmp[2][NB];
+#pragma unroll
+  for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+    for (int nj = 0; nj < NB; ++nj) tmp[mi][nj] = (f32x4){0.f, 0.f, 0.f, 0.f};
+
+  issue(0);
+  for (int kb = 0; kb < nsteps; ++kb) {
+    const int buf = kb & 1;
+    stage(buf);
+    __syncthreads();
+    if (kb + 1 < nsteps) issue(kb + 1);
+    const uint16_t* a_ = sA + buf * kSA;
+    const uint16_t* b_ = sB + buf * kSB;
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      const int ko = ks * 32 + 8 * (lane >> 4);
+      u32x4 af[2], bf[NB];
+#pragma unroll
+      for (int mi = 0; mi < 2; ++mi) af[mi] = *(const u32x4*)(a_ + (32 * wm + 16 * mi + (lane & 15)) * kGPitch + ko);
+#pragma unroll
+      for (int nj = 0; nj < NB; ++nj) bf[nj] = *(const u32x4*)(b_ + (R::nrow(nj, wn) + (lane & 15)) * kGPitch + ko);
+#pragma unroll
+      for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+        for (int nj = 0; nj < NB; ++nj) tmp[mi][nj] = mfma_bf16(af[mi], bf[nj], tmp[mi][nj]);
+    }
+    if constexpr (G::kPostScale) {
+      // end of a quantisation group: acc += group partial * scale (straight-line)
+      const bool last = ((kb + 1) % lpg == 0) | (kb + 1 == nsteps);
+      const int grp = kb / lpg;
+#pragma unroll
+      for (int nj = 0; nj < NB; ++nj) {
+        float s;
+        if constexpr (WFMT == FTM_FMT_FP8_BLOCK) {
+          const int nkb = (K + W.group - 1) / W.group;
+          const uint32_t idx = (uint32_t)((srow[nj] / W.group) * nkb + grp);
+          s = decode_scalar_word(sload4(W.s, (idx * sesz) & ~3u), idx, W.s_dt);
+        } else {
+          const uint32_t idx = (uint32_t)((srow[nj] + (lane & 15)) * (K / W.group) + grp);
+          s = decode_scalar_word(bload_scalar_word(i8res, idx, W.s_dt, srow[nj] + (lane & 15) < W.N), idx, W.s_dt);
+        }
+        const float f = last ? s : 0.0f;
+        const float keep = last ? 0.0f : 1.0f;
+#pragma unroll
+        for (int mi = 0; mi < 2; ++mi) {
+          acc[mi][nj] += tmp[mi][nj] * f;
+          tmp[mi][nj] *= keep;
+        }
+      }
+    }
+  }
+  if constexpr (!G::kPostScale) {
+#pragma unroll
+    for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+      for (int nj = 0; nj < NB; ++nj) acc[mi][nj] += tmp[mi][nj];
+  }
+  __syncthreads();  // the LDS tiles are reused by the caller's next tile
+}
+
+// ---------------------------------------------------------------- stage A (w13 + activation)
+template <int WFMT>
+__device__ void gemm_a_body(const LayerArgs& a, const ProjSlot& W, int Iu, int c0, int m0, int cnt,
+                            const int32_t* list, int shared_col, uint16_t* sA, uint16_t* sB) {
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave & 1, wn = wave >> 1;
+  const int H = a.L.hidden, KP = a.KP;
+  const Rsrc lres = make_rsrc(list, list ? (uint32_t)a.T * 4u : 0u);
+  const Rsrc xres = make_rsrc(a.x, (uint32_t)a.T * (uint32_t)H * 2u);
+  uint32_t arow[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int p = pair_of_row(lres, list != nullptr, m0 + ((tid + kBlock * i) >> 3), cnt, KP, shared_col);
+    arow[i] = p >= 0 ? (uint32_t)(p / KP) * (uint32_t)H * 2u : kOOB;
+  }
+  int pe[2][4];
+#pragma unroll
+  for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      pe[mi][r] = pair_of_row(lres, list != nullptr, m0 + 32 * wm + 16 * mi + 4 * (lane >> 4) + r, cnt, KP,
+                              shared_col);
+  float bg[2], bu[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int ch = c0 + 32 * wn + 16 * j + (lane & 15);
+    bg[j] = W.bias != nullptr ? load_scalar(W.bias, ch, W.bias_dt) : 0.0f;
+    bu[j] = W.bias != nullptr ? load_scalar(W.bias, Iu + ch, W.bias_dt) : 0.0f;
+  }
+  f32x4 acc[2][4];
+#pragma unroll
+  for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+    for (int nj = 0; nj < 4; ++nj) acc[mi][nj] = (f32x4){0.f, 0.f, 0.f, 0.f};
+  gemm_tile<WFMT, 128>(W, c0, Iu, xres, arow, sA, sB, acc);
+#pragma unroll
+  for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int ch = c0 + 32 * wn + 16 * j + (lane & 15);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        if (pe[mi][r] >= 0) {
+          const float h = act_fn(a.L.act, acc[mi][j][r] + bg[j], acc[mi][2 + j][r] + bu[j], a.L.swiglu_alpha,
+                                 a.L.swiglu_limit);
+          store_scalar(a.hbuf, (size_t)pe[mi][r] * a.Imax + ch, FTM_DT_BF16, h);
+        }
+      }
+    }
+}
+
+template <int FMT>
+__global__ __launch_bounds__(kBlock) void k_gemm_a(const LayerArgs a) {
+  __shared__ __attribute__((aligned(16))) uint16_t sA[2 * kGM * kGPitch];
+  __shared__ __attribute__((aligned(16))) uint16_t sB[2 * 128 * kGPitch];
+  const int I = a.L.inter, Is = a.L.shared_inter;
+  const int nRouted = a.ctrl[kCtrlNRouted];
+  const int ntn = I / 64;
+  const int routed_items = gemm_routed_mtiles(a, nRouted) * ntn;
+  const int item = blockIdx.x;
+  if (item < routed_items) {
+    const GemmTile t = gemm_find_tile(a, item / ntn, nRouted, false);
+    if (t.u < 0) return;
+    const int e = a.uniq[t.u];
+    const int slot = a.L.slot_of_expert ? a.L.slot_of_expert[e] : e;
+    if (slot < 0 || slot >= a.L.w13.num_slots) {
+      if (threadIdx.x == 0) atomicOr(&a.ctrl[kCtrlError], 1);
+      return;
+    }
+    const ProjSlot W = proj_slot(a.L.w13, slot);
+    gemm_a_body<FMT>(a, W, I, (item % ntn) * 64, t.m0, t.cnt, a.lists + (size_t)e * a.T, 0, sA, sB);
+  } else if (Is > 0) {
+    const int sitem = item - routed_items, nts = Is / 64;
+    const int m0 = (sitem / nts) * kGM;
+    if (m0 >= a.T) return;
+    const ProjSlot W = shared_view(a.L.shared_w13, 2 * Is, a.L.hidden);
+    gemm_a_body<FTM_FMT_BF16>(a, W, Is, (sitem % nts) * 64, m0, a.T, nullptr, a.L.topk, sA, sB);
+  }
+}
+
+// ---------------------------------------------------------------- stage B (w2 -> slot buffer)
+template <int WFMT>
+__device__ void gemm_b_body(const LayerArgs& a, const ProjSlot& W, int n0, int m0, int cnt, const int32_t* list,
+                            int shared_col, uint16_t* sA, uint16_t* sB) {
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave & 1, wn = wave >> 1;
+  const int H = a.L.hidden, KP = a.KP;
+  const Rsrc lres = make_rsrc(list, list ? (uint32_t)a.T * 4u : 0u);
+  const Rsrc hres = make_rsrc(a.hbuf, (uint32_t)a.T * (uint32_t)KP * (uint32_t)a.Imax * 2u);
+  const Rsrc wres = make_rsrc(a.wts, (uint32_t)a.T * (uint32_t)KP * 4u);
+  uint32_t arow[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int p = pair_of_row(lres, list != nullptr, m0 + ((tid + kBlock * i) >> 3), cnt, KP, shared_col);
+    arow[i] = p >= 0 ? (uint32_t)p * (uint32_t)a.Imax * 2u : kOOB;
+  }
+  int pe[2][4];
+  float we[2][4];
+#pragma unroll
+  for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      pe[mi][r] = pair_of_row(lres, list != nullptr, m0 + 32 * wm + 16 * mi + 4 * (lane >> 4) + r, cnt, KP,
+                              shared_col);
+      we[mi][r] = __uint_as_float(bload4(wres, pe[mi][r] >= 0 ? 4u * (uint32_t)pe[mi][r] : kOOB));
+    }
+  float bn[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int n = n0 + 32 * wn + 16 * j + (lane & 15);
+    bn[j] = W.bias != nullptr ? load_scalar(W.bias, n, W.bias_dt) : 0.0f;
+  }
+  f32x4 acc[2][2];
+#pragma unroll
+  for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+    for (int nj = 0; nj < 2; ++nj) acc[mi][nj] = (f32x4){0.f, 0.f, 0.f, 0.f};
+  gemm_tile<WFMT, 64>(W, n0, 0, hres, arow, sA, sB, acc);
+#pragma unroll
+  for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int n = n0 + 32 * wn + 16 * j + (lane & 15);
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        if (pe[mi][r] >= 0) {
+          float y = acc[mi][j][r];
+          if (W.bias != nullptr) y += bn[j];
+          a.ybuf[(size_t)pe[mi][r] * H + n] = y * we[mi][r];
+        }
+    }
+}
+
+template <int FMT>
+__global__ __launch_bounds__(kBlock) void k_gemm_b(const LayerArgs a) {
+  __shared__ __attribute__((aligned(16))) uint16_t sA[2 * kGM * kGPitch];
+  __shared__ __attribute__((aligned(16))) uint16_t sB[2 * 64 * kGPitch];
+  const int H = a.L.hidden, Is = a.L.shared_inter;
+  const int nRouted = a.ctrl[kCtrlNRouted];
+  const int ntn = H / 64;
+  const int routed_items = gemm_routed_mtiles(a, nRouted) * ntn;
+  const int item = blockIdx.x;
+  if (item < routed_items) {
+    const GemmTile t = gemm_find_tile(a, item / ntn, nRouted, false);
+    if (t.u < 0) return;
+    const int e = a.uniq[t.u];
+    const int32_t* list = a.lists + (size_t)e * a.T;
+    const int slot = a.L.slot_of_expert ? a.L.slot_of_expert[e] : e;
+    const int n0 = (item % ntn) * 64;
+    if (slot < 0 || slot >= a.L.w2.num_slots) {
+      // non-resident expert: its rows contribute zeros
+      for (int idx = threadIdx.x; idx < kGM * 64; idx += kBlock) {
+        const int m = t.m0 + idx / 64;
+        if (m < t.cnt) a.ybuf[(size_t)list[m] * H + n0 + idx % 64] = 0.0f;
+      }
+      if (threadIdx.x == 0) atomicOr(&a.ctrl[kCtrlError], 1);
+      return;
+    }
+    const ProjSlot W = proj_slot(a.L.w2, slot);
+    gemm_b_body<FMT>(a, W, n0, t.m0, t.cnt, list, 0, sA, sB);
+  } else if (Is > 0) {
+    const int sitem = item - routed_items;
+    const int m0 = (sitem / ntn) * kGM;
+    if (m0 >= a.T) return;
+    const ProjSlot W = shared_view(a.L.shared_w2, H, Is);
+    gemm_b_body<FTM_FMT_BF16>(a, W, (sitem % ntn) * 64, m0, a.T, nullptr, a.L.topk, sA, sB);
+  }
+}
+
+// ---------------------------------------------------------------- launch
+bool gemm_path_ok(const ftm_moe_layer& L, int T) {
+  if (L.act_dtype != FTM_DT_BF16) return false;
+  const int f = L.w13.fmt;
+  if (f != FTM_FMT_FP8_BLOCK && f != FTM_FMT_INT8_PACKED && f != FTM_FMT_MXFP4 && f != FTM_FMT_BF16) return false;
+  if (L.hidden % 64 != 0 || L.inter % 64 != 0 || (L.shared_inter > 0 && L.shared_inter % 64 != 0)) return false;
+  if ((f == FTM_FMT_FP8_BLOCK || f == FTM_FMT_INT8_PACKED) &&
+      (L.w13.group % kGK != 0 || L.w2.group % kGK != 0))
+    return false;
+  if (L.apply_router_weight_on_input) return false;
+  // above the crossover: on average at least kGemmMinRows tokens per routed expert
+  const long pairs = (long)T * L.topk;
+  const long maxU = L.num_experts < pairs ? L.num_experts : pairs;
+  return pairs >= (long)kGemmMinRows * maxU;
+}
+
+template <int FMT>
+static void launch_gemm_t(const LayerArgs& a, hipStream_t st, int which) {
+  const ftm_moe_layer& L = a.L;
+  const long pairs = (long)a.T * L.topk;
+  const long maxU = L.num_experts < pairs ? L.num_experts : pairs;
+  const long mt_routed = pairs / kGM + maxU + 1;
+  const long mt_shared = L.shared_inter > 0 ? (a.T + kGM - 1) / kGM : 0;
+  if (which & 1) {
+    const long items = mt_routed * (L.inter / 64) + mt_shared * (L.shared_inter > 0 ? L.shared_inter / 64 : 0);
+    hipLaunchKernelGGL((k_gemm_a<FMT>), dim3((unsigned)items), dim3(kBlock), 0, st, a);
+  }
+  if (which & 2) {
+    const long items = (mt_routed + mt_shared) * (L.hidden / 64);
+    hipLaunchKernelGGL((k_gemm_b<FMT>), dim3((unsigned)items), dim3(kBlock), 0, st, a);
+  }
+}
+
+void launch_gemm_stages(const ftm_moe_layer& L, const void* x, int T, void* out, char* ws, const WsLayout& wl,
+                        hipStream_t st, int which) {
+  const LayerArgs a = make_args(L, x, out, T, ws, wl);
+  switch (L.w13.fmt) {
+    case FTM_FMT_FP8_BLOCK: launch_gemm_t<FTM_FMT_FP8_BLOCK>(a, st, which); break;
+    case FTM_FMT_INT8_PACKED: launch_gemm_t<FTM_FMT_INT8_PACKED>(a, st, which); break;
+    case FTM_FMT_MXFP4: launch_gemm_t<FTM_FMT_MXFP4>(a, st, which); break;
+    default: launch_gemm_t<FTM_FMT_BF16>(a, st, which); break;
+  }
+}
+
+}  // namespace ftm

@@ -58,6 +58,11 @@ hipError_t launch_topk(const ftm_moe_layer& L, int T, const void* logits_in, int
                        float* logits_out, char* ws, const WsLayout& wl, hipStream_t st);
 hipError_t launch_experts(const ftm_moe_layer& L, const void* x, int T, void* out, char* ws,
                           const WsLayout& wl, hipStream_t st, int which = 7);
+// Prefill side of the crossover (ftm_gemm.hip): whether the tiled GEMM stages
+// take this layer at T tokens, and their launch (which: bit 0 = w13, bit 1 = w2).
+bool gemm_path_ok(const ftm_moe_layer& L, int T);
+void launch_gemm_stages(const ftm_moe_layer& L, const void* x, int T, void* out, char* ws, const WsLayout& wl,
+                        hipStream_t st, int which);
 hipError_t launch_linear(const ftm_proj& P, int slot, const void* x, int x_dt, int M, void* out,
                          int out_dt, const void* bias, int bias_dt, int final_dt, hipStream_t st);
 hipError_t launch_fill_routing(int T, int32_t slot, int32_t* slot_word, int32_t* ids, float* w, hipStream_t st);

@@ -29,7 +29,7 @@ def _run_and_check(syn, gpu, *, check_routing=True):
     if check_routing:
         np.testing.assert_array_equal(to_f32(logits), ref["logits"], err_msg="router logits")
         np.testing.assert_array_equal(ids.cpu().numpy(), ref["ids"], err_msg="routing indices")
-        np.testing.assert_allclose(w.cpu().numpy(), ref["w"], rtol=2 ** -8, atol=0, err_msg="router weights")
+        np.testing.assert_allclose(w.cpu().numpy(), ref["w"], rtol=2 ** -7, atol=0, err_msg="router weights (one bf16 ulp)")
     assert_close(to_f32(out), ref["out"], what=f"{syn.cfg.name} layer output")
     return layer, dsyn, ref, out
 
@@ -192,3 +192,31 @@ def test_many_experts_routing(gpu, E, k):
     cfg = replace(S.SMALL["c3_fp8"], name=f"c3_e{E}", E=E, k=k)
     syn = S.generate(cfg, T=12, seed=24)
     _run_and_check(syn, gpu)
+
+
+# ---------------------------------------------------------------- above the token crossover (tiled GEMMs)
+@pytest.mark.parametrize("name,T", [("c3_fp8", 512), ("c1_int8", 256), ("c4_mxfp4", 256), ("c3_fp8", 700)])
+def test_prefill_gemm_path_matches_oracle(gpu, name, T):
+    """At >= 16 tokens per routed expert the expert stages are the LDS-tiled
+    GEMMs (FP8 block, INT8 per-channel, MXFP4 with biases and the clamped
+    SwiGLU, the bf16 shared expert); same contract as the GEMV path."""
+    syn = S.generate(S.SMALL[name], T=T, seed=40 + T)
+    _run_and_check(syn, gpu)
+
+
+def test_prefill_gemm_full_c3_token_subset(gpu):
+    """C3 at its prefill size (T=2048, all 256 experts hit): the layer runs on
+    the whole batch; a token's output depends only on its own row, so 48
+    sampled tokens are checked against the oracle run on just those rows."""
+    syn = S.generate(S.CONFIGS["c3_fp8"], T=2048, seed=7)
+    dsyn = syn.to(gpu)
+    layer = S.build_layer(dsyn)
+    out, ids, _, _ = layer.forward(dsyn.x, return_routing=True)
+    torch.cuda.synchronize()
+    rows = np.sort(np.random.RandomState(0).choice(2048, 48, replace=False))
+    ref = O.layer_reference(oracle_spec(syn), np_(syn.x)[rows])
+    np.testing.assert_array_equal(ids.cpu().numpy()[rows], ref["ids"])
+    assert_close(to_f32(out)[rows], ref["out"], what="C3 prefill rows")
+    again = layer.forward(dsyn.x)
+    torch.cuda.synchronize()
+    assert torch.equal(out, again)
