@@ -531,6 +531,17 @@ __device__ __forceinline__ uint32_t sload4(const void* base, uint32_t off) {
   typedef const __attribute__((address_space(4))) uint32_t* CPtr;
   return *(CPtr)((const char*)base + off);
 }
+// Element i (wave-uniform) of an int32 table written by an earlier kernel,
+// e.g. the routed-expert list: a scalar load keeps the value (and every
+// address derived from it) in SGPRs whatever the rest of the kernel does.
+__device__ __forceinline__ int sload_i32(const int32_t* p, int i) { return (int)sload4(p, 4u * (uint32_t)i); }
+typedef uint32_t u32x8 __attribute__((ext_vector_type(8)));
+// Eight consecutive int32 at a wave-uniform, 32-byte aligned address (one
+// scalar load).
+__device__ __forceinline__ u32x8 sload32(const void* base, uint32_t off) {
+  typedef const __attribute__((address_space(4))) u32x8* CPtr;
+  return *(CPtr)((const char*)base + off);
+}
 
 // acc += A(16 tokens x K range) * W(16 rows)^T, where lane l supplies weight
 // row lrow (its MFMA column l % 16; -1 = no row, reads zero).  Unlike
@@ -647,6 +658,171 @@ __device__ __forceinline__ void wave_rows_kmajor(const ProjSlot& W, int lrow, in
     }
   }
   if constexpr (!F::kPostScale) acc += tmp;
+}
+
+// ---------------------------------------------------------------- prefetched row streams
+// The per-lane-row GEMV of wave_rows_kmajor split into a weight half and an
+// activation half.  rows_issue starts up to NLW wave-loads [Lw, min(Lw + NLW,
+// L_hi)) of the lane's row (plus their scale words) and returns at once, so a
+// workgroup's whole weight window is in flight behind one memory latency while
+// the caller resolves its tokens; rows_consume_lds then runs the MFMAs with
+// the activations taken from LDS.
+//   lrow         weight row of lane l (its MFMA column l % 16); < 0 reads zero
+//   sb_lo/sb_hi  FP8 only: 128-row scale block of lanes l % 16 < 8 / >= 8;
+//                PAIRED = false when every lane's row is in block sb_lo
+template <int FMT, int NLW>
+struct RowStream {
+  u32x4 raw[NLW];
+  uint32_t sw[NLW];  // FP8 / INT8: scale word of the wave-load's group; MXFP4: e8m0 byte
+};
+
+template <int FMT>
+struct RowGeom {
+  Rsrc wres, sres;
+  uint32_t woff, soff;   // lane's row start in w / in its scale row (INT8, MXFP4)
+  uint32_t fp8_lo, fp8_hi, sesz;
+  int gmax, lpg;
+  __device__ __forceinline__ RowGeom() = default;
+  __device__ __forceinline__ RowGeom(const ProjSlot& W, int lrow, int sb_lo, int sb_hi) {
+    using F = KMajor<FMT>;
+    const int K = W.K;
+    const uint32_t rb = F::row_bytes(K);
+    wres = make_rsrc(W.w, rb * (uint32_t)W.N);
+    woff = lrow >= 0 ? (uint32_t)lrow * rb : kOOB;
+    sres = wres;
+    soff = kOOB;
+    fp8_lo = fp8_hi = 0;
+    gmax = 0;
+    sesz = W.s_dt == FTM_DT_F32 ? 4u : 2u;
+    if constexpr (FMT == FTM_FMT_FP8_BLOCK) {
+      const int nkb = (K + W.group - 1) / W.group;
+      const int nrb = (W.N + W.group - 1) / W.group;
+      gmax = nkb - 1;
+      fp8_lo = (uint32_t)(sb_lo * nkb) * sesz;
+      fp8_hi = (uint32_t)(sb_hi * nkb) * sesz;
+      sres = make_rsrc(W.s, (uint32_t)(nrb * nkb) * sesz);
+    } else if constexpr (FMT == FTM_FMT_INT8_PACKED) {
+      const int ng = K / W.group;
+      sres = make_rsrc(W.s, (uint32_t)(W.N * ng) * sesz);
+      soff = lrow >= 0 ? (uint32_t)(lrow * ng) : kOOB;
+    } else if constexpr (FMT == FTM_FMT_MXFP4) {
+      sres = make_rsrc(W.s, (uint32_t)W.N * (uint32_t)(K / 32));
+      soff = lrow >= 0 ? (uint32_t)(lrow * (K / 32)) : kOOB;
+    }
+    lpg = F::kPostScale ? (W.group + F::kLoadK - 1) / F::kLoadK : 1;
+  }
+};
+
+template <int FMT, int NLW, bool PAIRED>
+__device__ __forceinline__ void rows_issue(const ProjSlot& W, const RowGeom<FMT>& G, int Lw, int L_hi,
+                                           RowStream<FMT, NLW>& S) {
+  using F = KMajor<FMT>;
+  const int g = (threadIdx.x & 63) >> 4;
+  const bool upper = (threadIdx.x & 15) >= 8;
+  const int K = W.K;
+  int gcur = Lw / G.lpg;
+  int gpos = Lw - gcur * G.lpg;
+#pragma unroll
+  for (int b = 0; b < NLW; ++b) {
+    const int L = Lw + b;
+    const int kk = L * F::kLoadK + F::kLaneK * g;
+    const bool kok = (L < L_hi) && (kk < K);
+    S.raw[b] = bload16(G.wres, kok ? G.woff + F::elem_off(kk) : kOOB);
+    if constexpr (FMT == FTM_FMT_MXFP4) {
+      S.sw[b] = bload1(G.sres, kok ? G.soff + (uint32_t)(kk / 32) : kOOB);
+    } else if constexpr (FMT == FTM_FMT_FP8_BLOCK) {
+      // each lane reads its own row block's word with the weights (a vector
+      // load: nothing waits for it until the MFMAs)
+      const uint32_t gb = (uint32_t)min(gcur, G.gmax) * G.sesz;
+      const uint32_t rb = (PAIRED && upper) ? G.fp8_hi : G.fp8_lo;
+      S.sw[b] = bload4(G.sres, (L < L_hi) ? ((rb + gb) & ~3u) : kOOB);
+    } else if constexpr (FMT == FTM_FMT_INT8_PACKED) {
+      S.sw[b] = bload_scalar_word(G.sres, G.soff + (uint32_t)gcur, W.s_dt, L < L_hi && G.soff != kOOB);
+    }
+    if constexpr (F::kPostScale) {
+      const bool wrap = gpos == G.lpg - 1;
+      gpos = wrap ? 0 : gpos + 1;
+      gcur += wrap ? 1 : 0;
+    }
+  }
+}
+
+// rows_consume_lds: the MFMAs of NT row tiles at once, activations from LDS.  xs
+// holds the current block's token rows from element k0 on (bf16, `pitch`
+// elements apart, nb of them); lane l feeds token row l % 16 of the MFMA and
+// rows >= nb read as zero.  Each activation read feeds all NT tiles' MFMAs.
+// Post-scaled formats accumulate each quantisation group in its own register
+// (LPG wave-loads per group, the window starting on a group boundary, or the
+// whole window inside one group when LPG == NLW) and apply the scales once at
+// the end, so no MFMA waits on a VALU read of its own result mid-window.
+template <int FMT, int NLW, int NT, int LPG, bool PAIRED>
+__device__ __forceinline__ void rows_consume_lds(const ProjSlot& W, const RowGeom<FMT> (&G)[NT], int Lw, int L_hi,
+                                                 const RowStream<FMT, NLW> (&S)[NT], const uint16_t* xs, int k0,
+                                                 int pitch, int nb, f32x4 (&acc)[NT]) {
+  using F = KMajor<FMT>;
+  static_assert(NLW % LPG == 0, "groups tile the window");
+  const int lane = threadIdx.x & 63;
+  const int g = lane >> 4;
+  const int m = lane & 15;
+  const bool upper = m >= 8;
+  const int K = W.K;
+  const bool mok = m < nb;
+  const uint16_t* xrow = xs + (mok ? m : 0) * pitch;
+  const u32x4 zero = (u32x4){0u, 0u, 0u, 0u};
+  constexpr int NP = F::kPostScale ? NLW / LPG : 1;
+  f32x4 part[NT][NP];
+#pragma unroll
+  for (int t = 0; t < NT; ++t)
+#pragma unroll
+    for (int i = 0; i < NP; ++i) part[t][i] = (f32x4){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int b = 0; b < NLW; ++b) {
+    const int L = Lw + b;
+    const int kk = L * F::kLoadK + F::kLaneK * g;
+    const bool ok = mok && (L < L_hi) && (kk < K);
+#pragma unroll
+    for (int q = 0; q < F::kMfma; ++q) {
+      const u32x4 xa = *(const u32x4*)(xrow + (ok ? kk + 8 * q - k0 : 0));
+      const u32x4 av = ok ? xa : zero;
+#pragma unroll
+      for (int t = 0; t < NT; ++t) {
+        const u32x4 r = S[t].raw[b];
+        u32x4 bq;
+        if constexpr (FMT == FTM_FMT_FP8_BLOCK) {
+          bq = q == 0 ? fp8x8_to_bf16(r.x, r.y) : fp8x8_to_bf16(r.z, r.w);
+        } else if constexpr (FMT == FTM_FMT_INT8_PACKED) {
+          bq = q == 0 ? i8x8_to_bf16(r.x, r.y) : i8x8_to_bf16(r.z, r.w);
+        } else if constexpr (FMT == FTM_FMT_MXFP4) {
+          const uint32_t wq = q == 0 ? r.x : q == 1 ? r.y : q == 2 ? r.z : r.w;
+          bq = fp4x8_to_bf16(wq, e8m0_to_f32(S[t].sw[b]));
+        } else {
+          bq = r;
+        }
+        f32x4& pt = part[t][F::kPostScale ? b / LPG : 0];
+        pt = mfma_bf16(av, bq, pt);
+      }
+    }
+  }
+  if constexpr (F::kPostScale) {
+    const int g0 = Lw / G[0].lpg;
+#pragma unroll
+    for (int i = 0; i < NP; ++i) {
+      const int b = i * LPG;  // first wave-load of the group
+#pragma unroll
+      for (int t = 0; t < NT; ++t) {
+        uint32_t sidx;
+        if constexpr (FMT == FTM_FMT_FP8_BLOCK)
+          sidx = (((PAIRED && upper) ? G[t].fp8_hi : G[t].fp8_lo) / G[t].sesz) + (uint32_t)(g0 + i);
+        else
+          sidx = G[t].soff + (uint32_t)(g0 + i);
+        const float s_grp = decode_scalar_word(S[t].sw[b], sidx, W.s_dt);
+        acc[t] += part[t][i] * ((Lw + b < L_hi) ? s_grp : 0.0f);
+      }
+    }
+  } else {
+#pragma unroll
+    for (int t = 0; t < NT; ++t) acc[t] += part[t][0];
+  }
 }
 
 // ---------------------------------------------------------------- GPTQ engine

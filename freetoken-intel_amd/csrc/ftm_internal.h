@@ -12,6 +12,18 @@ namespace ftm {
 
 // ---- control region (first FTM_WS_CTRL_BYTES of a workspace, int32 words).
 // Zero between calls: every counter is reset by the workgroup that consumes it.
+// Work record of routed expert u (recs[u], kRecWords int32): expert id, token
+// count, bank slot (-1 = not resident), the pairs of its first kRecPairs
+// tokens (-1 past the count), one pad word.  Written by the top-k compaction,
+// read by the decode stages with one scalar load.
+constexpr int kRecWords = 8;
+constexpr int kRecPairs = 4;
+// Batches up to kXlMaxT tokens run the decode stages with activations in LDS
+// and per-expert work records (latency-bound there); larger batches keep the
+// register-fed chunked kernels, which sustain more bytes in flight per CU.
+// Measured on MI355X (C3 layer, w13 + w2 us): T=1 15.9 vs 16.7, T=4 30.7 vs
+// 34.5, T=8 54.5 vs 54.5, T=16 92.4 vs 88.1.
+constexpr int kXlMaxT = 4;
 constexpr int kCtrlArriveTopk = 0;  // arrivals of the top-k workgroups
 constexpr int kCtrlNRouted = 1;     // routed experts with >= 1 token (written per call)
 constexpr int kCtrlNU = 2;          // nRouted + shared expert
@@ -22,7 +34,7 @@ constexpr int kCtrlTileCnt = kCtrlExpertCnt + kMaxExperts;  // [H/64] combine ar
 constexpr int kMaxColTiles = FTM_WS_CTRL_BYTES / 4 - kCtrlTileCnt;
 
 struct WsLayout {
-  size_t misc, logits, wts, ids, lists, uniq, ucnt, hbuf, ybuf, total;
+  size_t misc, logits, wts, ids, lists, uniq, ucnt, recs, hbuf, ybuf, total;
   int T, E, KP, Imax;
 };
 
@@ -44,6 +56,7 @@ inline WsLayout ws_layout(const ftm_moe_layer& L, int T) {
   w.lists = o;  o = align_up(o + 4 * (size_t)w.E * Tt, 256);
   w.uniq = o;   o = align_up(o + 4 * (size_t)(w.E + 1), 256);
   w.ucnt = o;   o = align_up(o + 4 * (size_t)(w.E + 1), 256);
+  w.recs = o;   o = align_up(o + 4 * (size_t)kRecWords * (w.E + 1), 256);
   w.hbuf = o;   o = align_up(o + act * Tt * w.KP * w.Imax, 256);
   w.ybuf = o;   o = align_up(o + 4 * Tt * w.KP * (size_t)L.hidden, 256);
   w.total = o;

@@ -22,6 +22,7 @@ struct LayerArgs {
   int32_t* lists;   // [E, T]     pair ids routed to expert e (order within an expert is free)
   int32_t* uniq;    // [E+1]      routed experts with >= 1 pair, ascending
   int32_t* ucnt;    // [E+1]
+  int32_t* recs;    // [E+1, kRecWords] work records of the routed experts
   char* hbuf;       // [T*KP, Imax] act dtype
   float* ybuf;      // [T*KP, H]
 };
@@ -42,6 +43,7 @@ inline LayerArgs make_args(const ftm_moe_layer& L, const void* x, void* out, int
   a.lists = (int32_t*)(ws + wl.lists);
   a.uniq = (int32_t*)(ws + wl.uniq);
   a.ucnt = (int32_t*)(ws + wl.ucnt);
+  a.recs = (int32_t*)(ws + wl.recs);
   a.hbuf = ws + wl.hbuf;
   a.ybuf = (float*)(ws + wl.ybuf);
   return a;

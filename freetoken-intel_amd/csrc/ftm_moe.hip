@@ -28,6 +28,9 @@
 
 #include "ftm_layer.h"
 
+#include <algorithm>
+#include <mutex>
+
 namespace ftm {
 
 // ============================================================== router GEMV
@@ -315,8 +318,25 @@ __device__ __forceinline__ void compact_experts(const LayerArgs& a, int32_t* cnt
       tot += s_wsum[w];
     }
     if (f) {
-      a.uniq[running + wpre + pre] = e;
-      a.ucnt[running + wpre + pre] = c;
+      const int u = running + wpre + pre;
+      a.uniq[u] = e;
+      a.ucnt[u] = c;
+    }
+    if (f && a.T <= kXlMaxT) {
+      // work record for the LDS-activation stages: the list of expert e is
+      // complete here
+      const int u = running + wpre + pre;
+      const int32_t* list = a.lists + (size_t)e * a.T;
+      int rec[kRecWords];
+      rec[0] = e;
+      rec[1] = c;
+      rec[2] = a.L.slot_of_expert ? a.L.slot_of_expert[e] : e;
+#pragma unroll
+      for (int i = 0; i < kRecPairs; ++i) rec[3 + i] = i < c ? list[i] : -1;
+      rec[kRecWords - 1] = 0;
+      int32_t* dst = a.recs + (size_t)u * kRecWords;
+#pragma unroll
+      for (int i = 0; i < kRecWords; ++i) dst[i] = rec[i];
     }
     if (global_cnt && e < E) cnt[e] = 0;
     running += tot;
@@ -482,10 +502,10 @@ __global__ __launch_bounds__(kBlock) void k_stage_a(const LayerArgs a) {
   // The expert table is read before the routed count so both loads are in
   // flight together (uniq / ucnt hold E + 1 entries).
   const int u = min(item / tilesR, a.L.num_experts), it = item % tilesR;
-  const int e = a.uniq[u], cnt = a.ucnt[u];
-  const int nRouted = a.ctrl[kCtrlNRouted];
+  const int e = sload_i32(a.uniq, u), cnt = sload_i32(a.ucnt, u);
+  const int nRouted = sload_i32(a.ctrl, kCtrlNRouted);
   if (item < nRouted * tilesR) {
-    const int slot = a.L.slot_of_expert ? a.L.slot_of_expert[e] : e;
+    const int slot = a.L.slot_of_expert ? sload_i32(a.L.slot_of_expert, e) : e;
     if (slot < 0 || slot >= a.L.w13.num_slots) {
       if (threadIdx.x == 0) atomicOr(&a.ctrl[kCtrlError], 1);
       return;
@@ -509,6 +529,8 @@ __global__ __launch_bounds__(kBlock) void k_stage_a(const LayerArgs a) {
 // activation.  Compared with 16-channel tiles (16 gate + 16 up rows), the
 // workgroup needs half the activation registers per weight byte in flight.
 constexpr int kDppRowShl8 = 0x108;  // lane i <- lane i + 8 within a 16-lane row
+
+constexpr int kRowsNLW = 8;  // wave-loads of a wave's K range in one prefetch window
 
 template <int EFMT, int AT>
 __device__ void stage_a_rows(const LayerArgs& a, const ProjSlot& W, int Iu, int c0, int cnt, const int32_t* list,
@@ -716,6 +738,281 @@ __global__ __launch_bounds__(kBlock) void k_stage_b(const LayerArgs a) {
   }
 }
 
+// ============================================================== decode stages, activations in LDS
+// Each wave starts its weight window as soon as the expert is known, then
+// resolves the token list with scalar loads and copies its K range of the
+// block's token rows into its own LDS region by direct global->LDS loads.
+// Those copies complete behind the weights (vector loads finish in issue
+// order) but hold no registers and depend on nothing the weights wait for,
+// so the whole dependent chain (expert table -> token list -> activations)
+// overlaps the weight latency.  The MFMAs read the activations from LDS right
+// where they are used.  Tokens are taken kXT at a time (MFMA rows kXT..15
+// read zero).
+constexpr int kXT = 4;
+extern __shared__ __align__(16) uint16_t ftm_xl_lds[];
+
+// LDS elements per token row of one wave's region: its K range plus 8 (shifts
+// banks).  A wave's range is ceil(ceil(K / kLoadK) / split) wave-loads, at most
+// ceil(ceil(K / 128) / split) * 128 elements for every format (kLoadK = 32,
+// 64 or 128).
+__host__ __device__ __forceinline__ int xl_pitch(int K, int split) {
+  return ((K + 127) / 128 + split - 1) / split * 128 + 8;
+}
+
+// Work record of routed expert u (see kRecWords).
+struct ExpertRec {
+  int e, cnt, slot;
+  int p[kRecPairs];
+};
+__device__ __forceinline__ ExpertRec load_rec(const LayerArgs& a, int u) {
+  const u32x8 v = sload32(a.recs, (uint32_t)u * (uint32_t)(4 * kRecWords));
+  ExpertRec r;
+  r.e = (int)v[0];
+  r.cnt = (int)v[1];
+  r.slot = (int)v[2];
+#pragma unroll
+  for (int i = 0; i < kRecPairs; ++i) r.p[i] = (int)v[3 + i];
+  return r;
+}
+
+// Pairs of tokens [mb, mb + kXT) of a routed expert (block 0 from its record,
+// later blocks from its list) or of the shared expert; -1 past cnt.
+__device__ __forceinline__ void block_pairs(const LayerArgs& a, const ExpertRec* rec, const int32_t* list,
+                                            int shared_col, int cnt, int mb, int (&pr)[kXT]) {
+  static_assert(kXT <= kRecPairs, "block 0 pairs come from the record");
+#pragma unroll
+  for (int i = 0; i < kXT; ++i) {
+    const bool ok = mb + i < cnt;
+    int p;
+    if (list == nullptr)
+      p = (mb + i) * a.KP + shared_col;
+    else if (mb == 0)
+      p = rec->p[i];
+    else
+      p = ok ? sload_i32(list, mb + i) : -1;
+    pr[i] = ok ? p : -1;
+  }
+}
+
+// Copies elements [k0, k1) of the rows of the pairs pr (-1 = none) into xw
+// (row i at xw + i * pitch).  Row of pair p: src + (p / div) * row_elems
+// elements.  Returns after issuing the direct global->LDS loads.
+__device__ __forceinline__ void xl_fill_wave(const int (&pr)[kXT], const void* src, int div, int row_elems, int k0,
+                                             int k1, uint16_t* xw, int pitch) {
+  typedef __attribute__((address_space(1))) const void* GPtr;
+  typedef __attribute__((address_space(3))) void* LPtr;
+  const uint32_t lane = threadIdx.x & 63;
+  const uint32_t nbytes = 2u * (uint32_t)(k1 - k0);
+#pragma unroll
+  for (int i = 0; i < kXT; ++i) {
+    if (pr[i] >= 0) {
+      const char* row = (const char*)src + ((size_t)(pr[i] / div) * (size_t)row_elems + (size_t)k0) * 2u;
+      char* dst = (char*)(xw + i * pitch);
+      for (uint32_t c = 0; c < nbytes; c += 16u * kWave) {
+        if (c + 16u * lane < nbytes)
+          __builtin_amdgcn_global_load_lds((GPtr)(row + c + 16u * lane), (LPtr)(dst + c), 16, 0, 0);
+      }
+    }
+  }
+}
+
+// Stage A item body: NT x 8 channels (per tile 8 gate + 8 up rows) of one
+// expert, K split over the 4 waves and reduced through LDS.
+template <int EFMT, int NT, int LPG>
+__device__ void stage_a_xl_body(const LayerArgs& a, const ProjSlot& W, int Iu, int c0, int cnt,
+                                const ExpertRec* rec, const int32_t* list, int shared_col, int kp, f32x4* red) {
+  using F = KMajor<EFMT>;
+  constexpr int KS = 4;
+  const int lane = threadIdx.x & 63;
+  const int n = lane & 15;
+  const int H = a.L.hidden;
+  const int nL = fmt_loads<EFMT>(W.K);
+  const int L_lo = kp * nL / KS, L_hi = (kp + 1) * nL / KS;
+  const bool multi = L_hi - L_lo > kRowsNLW;
+  RowGeom<EFMT> G[NT];
+  RowStream<EFMT, kRowsNLW> S[NT];
+#pragma unroll
+  for (int t = 0; t < NT; ++t) {
+    const int ct = c0 + 8 * t;
+    const int lrow = n < 8 ? ct + n : Iu + ct + (n - 8);
+    G[t] = RowGeom<EFMT>(W, lrow, W.group > 0 ? ct / W.group : 0, W.group > 0 ? (Iu + ct) / W.group : 0);
+    rows_issue<EFMT, kRowsNLW, true>(W, G[t], L_lo, L_hi, S[t]);
+  }
+  const int pitch = xl_pitch(H, KS);
+  uint16_t* xw = ftm_xl_lds + kp * kXT * pitch;
+  const int k0 = L_lo * F::kLoadK, k1 = min(L_hi * F::kLoadK, W.K);
+  float bg[NT], bu[NT];
+#pragma unroll
+  for (int t = 0; t < NT; ++t) {
+    bg[t] = bu[t] = 0.0f;
+    if (W.bias != nullptr && n < 8 && kp == 0) {
+      bg[t] = load_scalar(W.bias, c0 + 8 * t + n, W.bias_dt);
+      bu[t] = load_scalar(W.bias, Iu + c0 + 8 * t + n, W.bias_dt);
+    }
+  }
+  for (int mb = 0; mb < cnt; mb += kXT) {
+    const int nb = min(kXT, cnt - mb);
+    int pr[kXT];
+    block_pairs(a, rec, list, shared_col, cnt, mb, pr);
+    xl_fill_wave(pr, a.x, a.KP, H, k0, k1, xw, pitch);
+    f32x4 acc[NT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) acc[t] = (f32x4){0.f, 0.f, 0.f, 0.f};
+    for (int Lw = L_lo; Lw < L_hi; Lw += kRowsNLW) {
+      // further windows, or the first again for a later token block when the
+      // range needs several (re-reads hit L2)
+      if (Lw != L_lo || (mb > 0 && multi)) {
+#pragma unroll
+        for (int t = 0; t < NT; ++t) rows_issue<EFMT, kRowsNLW, true>(W, G[t], Lw, L_hi, S[t]);
+      }
+      __builtin_amdgcn_s_waitcnt(0);  // weights and this wave's LDS copy have landed
+      rows_consume_lds<EFMT, kRowsNLW, NT, LPG, true>(W, G, Lw, L_hi, S, xw, k0, pitch, nb, acc);
+    }
+    // MFMA rows 0..kXT-1 (the block's tokens) live in lanes 0..15
+    if (lane < 16) {
+#pragma unroll
+      for (int t = 0; t < NT; ++t) red[(t * KS + kp) * 16 + lane] = acc[t];
+    }
+    __syncthreads();
+    if (kp == 0) {
+#pragma unroll
+      for (int t = 0; t < NT; ++t) {
+        f32x4 v = red[t * KS * 16 + n];
+#pragma unroll
+        for (int j = 1; j < KS; ++j) v += red[(t * KS + j) * 16 + n];
+#pragma unroll
+        for (int r = 0; r < kXT; ++r) {
+          const float gs = v[r] + bg[t];
+          const float us = dpp_f<kDppRowShl8>(v[r]) + bu[t];
+          if (lane < 8 && r < nb) {
+            const float h = act_fn(a.L.act, gs, us, a.L.swiglu_alpha, a.L.swiglu_limit);
+            store_scalar(a.hbuf, (size_t)pr[r] * a.Imax + c0 + 8 * t + n, FTM_DT_BF16, h);
+          }
+        }
+      }
+    }
+    __syncthreads();
+  }
+}
+
+// NT x 8 channels per workgroup: routed items first, then the shared expert's.
+template <int FMT, int NT, int LPG>
+__global__ __launch_bounds__(kBlock) void k_stage_a_xl(const LayerArgs a) {
+  __shared__ f32x4 red[NT * 4 * 16];
+  const int kp = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int I = a.L.inter;
+  const int ti = I / (8 * NT);
+  const int item = blockIdx.x;
+  const int u = min(item / ti, a.L.num_experts);
+  const ExpertRec rec = load_rec(a, u);
+  const int nRouted = sload_i32(a.ctrl, kCtrlNRouted);
+  if (item < nRouted * ti) {
+    if (rec.slot < 0 || rec.slot >= a.L.w13.num_slots) {
+      if (threadIdx.x == 0) atomicOr(&a.ctrl[kCtrlError], 1);
+      return;
+    }
+    const ProjSlot W = proj_slot(a.L.w13, rec.slot);
+    stage_a_xl_body<FMT, NT, LPG>(a, W, I, (item % ti) * 8 * NT, rec.cnt, &rec, a.lists + (size_t)rec.e * a.T, 0,
+                                  kp, red);
+  } else {
+    const int sitem = item - nRouted * ti;
+    const int Is = a.L.shared_inter;
+    if (Is <= 0 || sitem >= Is / (8 * NT)) return;
+    const ProjSlot W = shared_view(a.L.shared_w13, 2 * Is, a.L.hidden);
+    stage_a_xl_body<FTM_FMT_BF16, NT, kRowsNLW>(a, W, Is, sitem * 8 * NT, a.T, nullptr, nullptr, a.L.topk, kp, red);
+  }
+}
+
+// Stage B item body: NT x 64 output columns of one expert; in each 64-column
+// tile wave w owns columns 16w .. 16w + 15, over the full K (no cross-wave
+// reduction).
+template <int EFMT, int NT, int LPG>
+__device__ void stage_b_xl_body(const LayerArgs& a, const ProjSlot& W, int cnt, const ExpertRec* rec,
+                                const int32_t* list, int shared_col, int nt, int wv) {
+  const int lane = threadIdx.x & 63;
+  const int n = lane & 15;
+  const int H = a.L.hidden;
+  const int lo = 0, hi = fmt_loads<EFMT>(W.K);
+  const bool multi = hi - lo > kRowsNLW;
+  RowGeom<EFMT> G[NT];
+  RowStream<EFMT, kRowsNLW> S[NT];
+  int brow[NT];
+  float bias_n[NT];
+#pragma unroll
+  for (int t = 0; t < NT; ++t) {
+    const int col0 = (nt * NT + t) * 64 + 16 * wv;
+    brow[t] = col0 + n;
+    const int sb = W.group > 0 ? col0 / W.group : 0;
+    G[t] = RowGeom<EFMT>(W, brow[t] < W.N ? brow[t] : -1, sb, sb);
+    rows_issue<EFMT, kRowsNLW, false>(W, G[t], lo, hi, S[t]);
+    bias_n[t] = (W.bias != nullptr && brow[t] < H) ? load_scalar(W.bias, brow[t], W.bias_dt) : 0.0f;
+  }
+  const int K = W.K;
+  const int pitch = xl_pitch(a.Imax, 1);
+  uint16_t* xw = ftm_xl_lds + wv * kXT * pitch;
+  for (int mb = 0; mb < cnt; mb += kXT) {
+    const int nb = min(kXT, cnt - mb);
+    int pr[kXT];
+    block_pairs(a, rec, list, shared_col, cnt, mb, pr);
+    xl_fill_wave(pr, a.hbuf, 1, a.Imax, 0, K, xw, pitch);
+    float wr[kXT];
+#pragma unroll
+    for (int r = 0; r < kXT; ++r) wr[r] = pr[r] >= 0 ? __uint_as_float(sload4(a.wts, 4u * (uint32_t)pr[r])) : 0.0f;
+    f32x4 acc[NT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) acc[t] = (f32x4){0.f, 0.f, 0.f, 0.f};
+    for (int Lw = lo; Lw < hi; Lw += kRowsNLW) {
+      if (Lw != lo || (mb > 0 && multi)) {
+#pragma unroll
+        for (int t = 0; t < NT; ++t) rows_issue<EFMT, kRowsNLW, false>(W, G[t], Lw, hi, S[t]);
+      }
+      __builtin_amdgcn_s_waitcnt(0);  // weights and this wave's LDS copy have landed
+      rows_consume_lds<EFMT, kRowsNLW, NT, LPG, false>(W, G, Lw, hi, S, xw, 0, pitch, nb, acc);
+    }
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+#pragma unroll
+      for (int r = 0; r < kXT; ++r) {
+        if (lane < 16 && r < nb && brow[t] < H) {
+          float y = acc[t][r];
+          if (W.bias != nullptr) y += bias_n[t];
+          y *= wr[r];  // router weight (routed) or sigmoid gate (shared)
+          a.ybuf[(size_t)pr[r] * H + brow[t]] = y;
+        }
+      }
+    }
+  }
+}
+
+template <int FMT, int NT, int LPG>
+__global__ __launch_bounds__(kBlock) void k_stage_b_xl(const LayerArgs a) {
+  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int H = a.L.hidden;
+  const int tiles = H / (64 * NT);
+  const int u = blockIdx.x / tiles, nt = blockIdx.x % tiles;
+  const int uc = min(u, a.L.num_experts);
+  const ExpertRec rec = load_rec(a, uc);
+  const int nU = sload_i32(a.ctrl, kCtrlNU), nRouted = sload_i32(a.ctrl, kCtrlNRouted);
+  if (u >= nU) return;
+  if (u < nRouted) {
+    const int32_t* list = a.lists + (size_t)rec.e * a.T;
+    if (rec.slot < 0 || rec.slot >= a.L.w2.num_slots) {
+      // non-resident expert: contribute zeros, flag the error
+      for (int idx = threadIdx.x; idx < rec.cnt * 64 * NT; idx += kBlock) {
+        const int m = idx / (64 * NT), c = nt * 64 * NT + idx % (64 * NT);
+        a.ybuf[(size_t)list[m] * H + c] = 0.0f;
+      }
+      if (threadIdx.x == 0) atomicOr(&a.ctrl[kCtrlError], 1);
+      return;
+    }
+    const ProjSlot W = proj_slot(a.L.w2, rec.slot);
+    stage_b_xl_body<FMT, NT, LPG>(a, W, rec.cnt, &rec, list, 0, nt, wv);
+  } else {
+    const ProjSlot W = shared_view(a.L.shared_w2, H, a.L.shared_inter);
+    stage_b_xl_body<FTM_FMT_BF16, NT, kRowsNLW>(a, W, a.T, nullptr, nullptr, a.L.topk, nt, wv);
+  }
+}
+
 // ============================================================== combine
 // out[t, n] = sum_j ybuf[t*KP + j, n] in slot order (deterministic, no atomics).
 template <int AT>
@@ -860,6 +1157,92 @@ hipError_t launch_topk(const ftm_moe_layer& L, int T, const void* logits_in, int
   return hipGetLastError();
 }
 
+// Does one prefetch window hold a wave's share of K when K is split over
+// `split` waves?  (A wave's range is at most ceil(loads / split) wave-loads.)
+template <int FMT>
+static bool pf_window_fits(int K, int split) {
+  if constexpr (FMT == FTM_FMT_GPTQ_INT4) {
+    return false;
+  } else {
+    const int kload = FMT == FTM_FMT_MXFP4 ? 128 : FMT == FTM_FMT_BF16 ? 32 : 64;
+    const int loads = (K + kload - 1) / kload;
+    return (loads + split - 1) / split <= kRowsNLW;
+  }
+}
+
+// Launch plan of the LDS-activation decode stages: eligible (bf16
+// activations, K-major format, a wave's K range in one prefetch window, its
+// quantisation groups aligned as rows_consume_lds needs), row tiles per
+// workgroup and wave-loads per scale group.
+struct XlPlan {
+  bool ok;
+  int nt, lpg;
+};
+#ifndef FTM_XL_NT_MAX
+#define FTM_XL_NT_MAX 1
+#endif
+
+
+template <int FMT>
+static int kload_of() {
+  return FMT == FTM_FMT_MXFP4 ? 128 : FMT == FTM_FMT_BF16 ? 32 : 64;
+}
+
+// Group layout for one projection whose K is split over `split` waves: 2 =
+// two wave-loads per group with every wave range starting on a group
+// boundary; kRowsNLW = every wave range inside one group (or no post-scale);
+// 0 = neither.
+template <int FMT>
+static int xl_lpg(const ftm_proj& P, int split) {
+  if (FMT != FTM_FMT_FP8_BLOCK && FMT != FTM_FMT_INT8_PACKED) return kRowsNLW;
+  const int kload = kload_of<FMT>();
+  const int nL = (P.K + kload - 1) / kload;
+  if (P.group <= 0 || (P.group % kload != 0 && P.group < P.K)) return 0;
+  const int lpg = P.group >= P.K ? nL : P.group / kload;
+  bool two = lpg == 2, one = true;
+  for (int w = 0; w < split; ++w) {
+    const int lo = w * nL / split, hi = (w + 1) * nL / split;
+    if (lo % 2 != 0) two = false;
+    if (hi > lo && lo / lpg != (hi - 1) / lpg) one = false;
+  }
+  return two ? 2 : one ? kRowsNLW : 0;
+}
+
+template <int FMT, int AT>
+static XlPlan xl_plan_a(const ftm_moe_layer& L, int T) {
+  XlPlan p{false, 1, kRowsNLW};
+  if constexpr (FMT == FTM_FMT_GPTQ_INT4 || AT != FTM_DT_BF16) {
+    return p;
+  } else {
+    if (T > kXlMaxT) return p;
+    // routed rows: one window per wave (the bf16 shared rows may take several)
+    if (!pf_window_fits<FMT>(L.hidden, 4)) return p;
+    if (L.hidden % 8 != 0) return p;
+    p.lpg = xl_lpg<FMT>(L.w13, 4);
+    if (p.lpg == 0) return p;
+    p.nt = (FTM_XL_NT_MAX >= 2 && L.inter % 16 == 0 && (L.shared_inter <= 0 || L.shared_inter % 16 == 0)) ? 2 : 1;
+    p.ok = true;
+    return p;
+  }
+}
+
+template <int FMT, int AT>
+static XlPlan xl_plan_b(const ftm_moe_layer& L, int T) {
+  XlPlan p{false, 1, kRowsNLW};
+  if constexpr (FMT == FTM_FMT_GPTQ_INT4 || AT != FTM_DT_BF16) {
+    return p;
+  } else {
+    if (T > kXlMaxT) return p;
+    if (!pf_window_fits<FMT>(L.inter, 1)) return p;
+    if (L.inter % 8 != 0 || (L.shared_inter > 0 && L.shared_inter % 8 != 0)) return p;
+    p.lpg = xl_lpg<FMT>(L.w2, 1);
+    if (p.lpg == 0) return p;
+    p.nt = (FTM_XL_NT_MAX >= 2 && L.hidden % 128 == 0) ? 2 : 1;
+    p.ok = true;
+    return p;
+  }
+}
+
 // which: bit 0 = stage A (w13 + act), bit 1 = stage B (w2), bit 2 = combine
 template <int FMT, int AT>
 static void launch_stages(const LayerArgs& a, int gridA, int gridB, hipStream_t st, int which) {
@@ -870,10 +1253,43 @@ static void launch_stages(const LayerArgs& a, int gridA, int gridB, hipStream_t 
       // one workgroup per 8-channel item (routed upper bound + shared)
       const int maxU = a.L.num_experts < a.T * a.L.topk ? a.L.num_experts : a.T * a.L.topk;
       const int items = maxU * (a.L.inter / 8) + (a.L.shared_inter > 0 ? a.L.shared_inter / 8 : 0);
-      hipLaunchKernelGGL((k_stage_a_rows<FMT, AT>), dim3(items), dim3(kBlock), 0, st, a);
+      const XlPlan pa = xl_plan_a<FMT, AT>(a.L, a.T);
+      if (pa.ok) {
+        const size_t lds = 4u * kXT * (size_t)xl_pitch(a.L.hidden, 4) * 2u;
+        const int nt = pa.nt;
+        const int itemsx = maxU * (a.L.inter / (8 * nt)) + (a.L.shared_inter > 0 ? a.L.shared_inter / (8 * nt) : 0);
+#define FTM_XLA(NT, LPG) hipLaunchKernelGGL((k_stage_a_xl<FMT, NT, LPG>), dim3(itemsx), dim3(kBlock), lds, st, a)
+        if (nt == 2) {
+          if (pa.lpg == 2) FTM_XLA(2, 2); else FTM_XLA(2, kRowsNLW);
+        } else {
+          if (pa.lpg == 2) FTM_XLA(1, 2); else FTM_XLA(1, kRowsNLW);
+        }
+#undef FTM_XLA
+      } else {
+        hipLaunchKernelGGL((k_stage_a_rows<FMT, AT>), dim3(items), dim3(kBlock), 0, st, a);
+      }
     }
   }
-  if (which & 2) hipLaunchKernelGGL((k_stage_b<FMT, AT>), dim3(gridB), dim3(kBlock), 0, st, a);
+  if (which & 2) {
+    const XlPlan pb = xl_plan_b<FMT, AT>(a.L, a.T);
+    if constexpr (FMT == FTM_FMT_GPTQ_INT4) {
+      hipLaunchKernelGGL((k_stage_b<FMT, AT>), dim3(gridB), dim3(kBlock), 0, st, a);
+    } else if (pb.ok) {
+      const size_t lds = 4u * kXT * (size_t)xl_pitch(a.Imax, 1) * 2u;
+      const int nt = pb.nt;
+      const int maxU = a.L.num_experts < a.T * a.L.topk ? a.L.num_experts : a.T * a.L.topk;
+      const int gridx = (maxU + (a.L.shared_inter > 0 ? 1 : 0)) * (a.L.hidden / (64 * nt));
+#define FTM_XLB(NT, LPG) hipLaunchKernelGGL((k_stage_b_xl<FMT, NT, LPG>), dim3(gridx), dim3(kBlock), lds, st, a)
+      if (nt == 2) {
+        if (pb.lpg == 2) FTM_XLB(2, 2); else FTM_XLB(2, kRowsNLW);
+      } else {
+        if (pb.lpg == 2) FTM_XLB(1, 2); else FTM_XLB(1, kRowsNLW);
+      }
+#undef FTM_XLB
+    } else {
+      hipLaunchKernelGGL((k_stage_b<FMT, AT>), dim3(gridB), dim3(kBlock), 0, st, a);
+    }
+  }
   if (which & 4) {
     const int n4 = a.T * (a.L.hidden / 4);
     hipLaunchKernelGGL((k_combine<AT>), dim3((n4 + kBlock - 1) / kBlock), dim3(kBlock), 0, st, a);

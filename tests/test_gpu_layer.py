@@ -220,3 +220,33 @@ def test_prefill_gemm_full_c3_token_subset(gpu):
     again = layer.forward(dsyn.x)
     torch.cuda.synchronize()
     assert torch.equal(out, again)
+
+
+@pytest.mark.parametrize("T", [2, 9])
+def test_non_resident_expert_contributes_zero_and_flags(gpu, T):
+    """A routed expert whose slot is -1 (not resident in an offload pool)
+    contributes nothing to its tokens and sets bit 0 of the workspace error
+    word; the rest of the layer is unaffected.  T=2 takes the decode stages
+    with activations in LDS, T=9 the register-fed ones."""
+    from ftmoe.layer import workspace
+
+    syn = S.generate(S.SMALL["c3_fp8"], T=T, seed=50 + T)
+    spec = oracle_spec(syn)
+    ref_full = O.layer_reference(spec, np_(syn.x))
+    ids = ref_full["ids"].astype(np.int32)
+    w = ref_full["w"].astype(np.float32)
+    missing = int(ids[0, 0])
+    w_ref = np.where(ids == missing, 0.0, w).astype(np.float32)
+    ref = O.layer_reference(spec, np_(syn.x), ids=ids, w=w_ref)
+    dsyn = syn.to(gpu)
+    slots = torch.arange(syn.cfg.E, dtype=torch.int32, device=gpu)
+    slots[missing] = -1
+    layer = S.build_layer(dsyn, slot_of_expert=slots)
+    ws = workspace(gpu, layer.workspace_bytes(T))
+    ws[:16].zero_()
+    out = layer.forward_routed(dsyn.x, torch.from_numpy(ids).to(gpu), torch.from_numpy(w).to(gpu))
+    torch.cuda.synchronize()
+    err = int(ws[12:16].view(torch.int32).item())
+    ws[12:16].zero_()
+    assert err & 1, "error bit for a non-resident routed expert"
+    assert_close(to_f32(out), ref["out"], what="layer output without the missing expert")
