@@ -1178,9 +1178,6 @@ struct XlPlan {
   bool ok;
   int nt, lpg;
 };
-#ifndef FTM_XL_NT_MAX
-#define FTM_XL_NT_MAX 1
-#endif
 
 
 template <int FMT>
@@ -1220,7 +1217,7 @@ static XlPlan xl_plan_a(const ftm_moe_layer& L, int T) {
     if (L.hidden % 8 != 0) return p;
     p.lpg = xl_lpg<FMT>(L.w13, 4);
     if (p.lpg == 0) return p;
-    p.nt = (FTM_XL_NT_MAX >= 2 && L.inter % 16 == 0 && (L.shared_inter <= 0 || L.shared_inter % 16 == 0)) ? 2 : 1;
+    p.nt = 1;
     p.ok = true;
     return p;
   }
@@ -1237,7 +1234,7 @@ static XlPlan xl_plan_b(const ftm_moe_layer& L, int T) {
     if (L.inter % 8 != 0 || (L.shared_inter > 0 && L.shared_inter % 8 != 0)) return p;
     p.lpg = xl_lpg<FMT>(L.w2, 1);
     if (p.lpg == 0) return p;
-    p.nt = (FTM_XL_NT_MAX >= 2 && L.hidden % 128 == 0) ? 2 : 1;
+    p.nt = 1;
     p.ok = true;
     return p;
   }
@@ -1259,11 +1256,7 @@ static void launch_stages(const LayerArgs& a, int gridA, int gridB, hipStream_t 
         const int nt = pa.nt;
         const int itemsx = maxU * (a.L.inter / (8 * nt)) + (a.L.shared_inter > 0 ? a.L.shared_inter / (8 * nt) : 0);
 #define FTM_XLA(NT, LPG) hipLaunchKernelGGL((k_stage_a_xl<FMT, NT, LPG>), dim3(itemsx), dim3(kBlock), lds, st, a)
-        if (nt == 2) {
-          if (pa.lpg == 2) FTM_XLA(2, 2); else FTM_XLA(2, kRowsNLW);
-        } else {
-          if (pa.lpg == 2) FTM_XLA(1, 2); else FTM_XLA(1, kRowsNLW);
-        }
+        if (pa.lpg == 2) FTM_XLA(1, 2); else FTM_XLA(1, kRowsNLW);
 #undef FTM_XLA
       } else {
         hipLaunchKernelGGL((k_stage_a_rows<FMT, AT>), dim3(items), dim3(kBlock), 0, st, a);
@@ -1280,11 +1273,7 @@ static void launch_stages(const LayerArgs& a, int gridA, int gridB, hipStream_t 
       const int maxU = a.L.num_experts < a.T * a.L.topk ? a.L.num_experts : a.T * a.L.topk;
       const int gridx = (maxU + (a.L.shared_inter > 0 ? 1 : 0)) * (a.L.hidden / (64 * nt));
 #define FTM_XLB(NT, LPG) hipLaunchKernelGGL((k_stage_b_xl<FMT, NT, LPG>), dim3(gridx), dim3(kBlock), lds, st, a)
-      if (nt == 2) {
-        if (pb.lpg == 2) FTM_XLB(2, 2); else FTM_XLB(2, kRowsNLW);
-      } else {
-        if (pb.lpg == 2) FTM_XLB(1, 2); else FTM_XLB(1, kRowsNLW);
-      }
+      if (pb.lpg == 2) FTM_XLB(1, 2); else FTM_XLB(1, kRowsNLW);
 #undef FTM_XLB
     } else {
       hipLaunchKernelGGL((k_stage_b<FMT, AT>), dim3(gridB), dim3(kBlock), 0, st, a);
