@@ -322,7 +322,7 @@ __device__ __forceinline__ void compact_experts(const LayerArgs& a, int32_t* cnt
       a.uniq[u] = e;
       a.ucnt[u] = c;
     }
-    if (f && a.T <= kXlMaxT) {
+    if (f && (a.T <= kXlMaxT || a.lean)) {
       // work record for the LDS-activation stages: the list of expert e is
       // complete here
       const int u = running + wpre + pre;
@@ -1013,6 +1013,294 @@ __global__ __launch_bounds__(kBlock) void k_stage_b_xl(const LayerArgs a) {
   }
 }
 
+// ============================================================== lean decode stages (FP8 block-128 layers)
+// The hot decode shape (FP8 block-128 experts with fp32 scales, bf16
+// activations, no projection biases, optional dense bf16 shared expert) gets
+// kernels with nothing else in them: per wave one window of weights issued as
+// soon as the expert record is read, the scale words with two scalar loads,
+// the block's activation rows copied to LDS by one direct global->LDS load per
+// token, LDS reads at fixed offsets (MFMA rows past the block read a zero
+// row), one accumulator per quantisation group.  Measured with a stripped
+// probe of this pattern on MI355X: 6.1 TB/s on the C3 T=16 w13 bytes, where
+// per-lane activation loads cap the same stream at 4.7 TB/s (they triple the
+// vector memory instructions per weight byte).
+constexpr int kLeanXT = 4;  // tokens per block (MFMA rows 0..3; rows 4..15 read the zero row)
+
+// LDS elements per token row of a wave's region (K range + 8: shifts banks).
+__host__ __device__ __forceinline__ constexpr int lean_pitch(int KR) { return KR + 8; }
+
+// One wave's weight window: NLW wave-loads of 16 bytes per lane.
+template <int NLW>
+struct LeanWin {
+  u32x4 raw[NLW];
+};
+
+// Issue window [w0, w0 + NLW) wave-loads of a row-major weight matrix:
+// lane (n, g) reads row `row` (< 0: none) at byte (kbase + (w0 + b) * 64 + 16 g).
+template <int NLW>
+__device__ __forceinline__ void lean_issue(Rsrc wres, int row, uint32_t row_bytes, uint32_t kbase, int w0,
+                                           LeanWin<NLW>& S) {
+  const int g = (threadIdx.x & 63) >> 4;
+  const uint32_t base = row >= 0 ? (uint32_t)row * row_bytes + kbase + 16u * (uint32_t)g : kOOB;
+#pragma unroll
+  for (int b = 0; b < NLW; ++b) S.raw[b] = bload16(wres, base == kOOB ? kOOB : base + 64u * (uint32_t)(w0 + b));
+}
+
+// Copy elements [k0, k0 + KR) of the rows of pairs pr[0..nb) into xw (row r at
+// xw + r * pitch); row of pair p at src + (p / div) * row_elems elements.
+template <int KR>
+__device__ __forceinline__ void lean_fill(const int (&pr)[kLeanXT], int nb, const void* src, int div, int row_elems,
+                                          int k0, uint16_t* xw) {
+  typedef __attribute__((address_space(1))) const void* GPtr;
+  typedef __attribute__((address_space(3))) void* LPtr;
+  const uint32_t lane = threadIdx.x & 63;
+#pragma unroll
+  for (int r = 0; r < kLeanXT; ++r) {
+    if (r < nb) {
+      const char* row = (const char*)src + ((size_t)(pr[r] / div) * (size_t)row_elems + (size_t)k0) * 2u;
+#pragma unroll
+      for (int c = 0; c < (2 * KR + 1023) / 1024; ++c) {
+        if (c * 1024 + 16 * (int)lane < 2 * KR)
+          __builtin_amdgcn_global_load_lds((GPtr)(row + c * 1024 + 16 * lane),
+                                           (LPtr)((char*)(xw + r * lean_pitch(KR)) + c * 1024), 16, 0, 0);
+      }
+    }
+  }
+}
+
+// MFMAs of one window.  FP8: wave-load b of window w belongs to group
+// (w * NLW + b) / 2 (64 K per wave-load, 128 per group), accumulated in
+// part[]; BF16: one accumulator part[0].  xrow: this lane's LDS row
+// (token l % 16, or the zero row), element kw = the window's first K offset
+// within the wave's range.
+template <bool FP8, int NLW, int NP>
+__device__ __forceinline__ void lean_mfma(const LeanWin<NLW>& S, const uint16_t* xrow, int kw, f32x4 (&part)[NP],
+                                          int pbase) {
+  const int g = (threadIdx.x & 63) >> 4;
+  constexpr int kLoadK = FP8 ? 64 : 32, kLaneK = FP8 ? 16 : 8;
+  const uint16_t* xl = xrow + kw + kLaneK * g;
+#pragma unroll
+  for (int b = 0; b < NLW; ++b) {
+    const u32x4 r = S.raw[b];
+    if constexpr (FP8) {
+      const u32x4 x0 = *(const u32x4*)(xl + b * kLoadK);
+      const u32x4 x1 = *(const u32x4*)(xl + b * kLoadK + 8);
+      f32x4& t = part[pbase + b / 2];
+      t = mfma_bf16(x0, fp8x8_to_bf16(r.x, r.y), t);
+      t = mfma_bf16(x1, fp8x8_to_bf16(r.z, r.w), t);
+    } else {
+      const u32x4 x0 = *(const u32x4*)(xl + b * kLoadK);
+      part[0] = mfma_bf16(x0, r, part[0]);
+    }
+  }
+}
+
+// Pairs of tokens [mb, mb + kLeanXT): block 0 of a routed expert from its
+// record, later blocks from its list, the shared expert's from the token index.
+__device__ __forceinline__ void lean_pairs(const LayerArgs& a, const ExpertRec* rec, const int32_t* list,
+                                           int shared_col, int cnt, int mb, int (&pr)[kLeanXT]) {
+#pragma unroll
+  for (int i = 0; i < kLeanXT; ++i) {
+    int p = -1;
+    if (mb + i < cnt) p = list == nullptr ? (mb + i) * a.KP + shared_col : mb == 0 ? rec->p[i] : sload_i32(list, mb + i);
+    pr[i] = p;
+  }
+}
+
+// Stage A item: 8 channels (8 gate + 8 up rows) of one expert, the hidden K
+// split over the 4 waves (KR = H / 4 each).  FP8: one window of KR / 64
+// wave-loads, fp32 scale words sc_lo (gate rows' block) / sc_hi (up rows').
+// BF16 (shared expert): NWIN windows of KR / (32 NWIN) wave-loads.
+template <bool FP8, int KR, int NWIN>
+__device__ void lean_a_item(const LayerArgs& a, const char* w, const float* sc, int Iu, int c0, int cnt,
+                            const ExpertRec* rec, const int32_t* list, int shared_col, int kp, f32x4* red) {
+  constexpr int NLW = (FP8 ? KR / 64 : KR / 32) / NWIN;
+  constexpr int NP = FP8 ? NLW / 2 : 1;
+  static_assert(!FP8 || NWIN == 1, "FP8 rows: one window per wave");
+  const int lane = threadIdx.x & 63;
+  const int n = lane & 15;
+  const int H = a.L.hidden;
+  const uint32_t row_bytes = (FP8 ? 1u : 2u) * (uint32_t)H;
+  const Rsrc wres = make_rsrc(w, row_bytes * (uint32_t)(2 * Iu));
+  const int lrow = n < 8 ? c0 + n : Iu + c0 + (n - 8);
+  const int k0 = kp * KR;
+  const uint32_t kbase = (FP8 ? 1u : 2u) * (uint32_t)k0;
+  LeanWin<NLW> S;
+  lean_issue<NLW>(wres, lrow, row_bytes, kbase, 0, S);
+  // fp32 scale words of this wave's K blocks: gate rows' block, up rows' block
+  float s_lo[NP], s_hi[NP];
+  if constexpr (FP8) {
+    const int nkb = H / 128;
+    const uint32_t lo = (uint32_t)(((c0 / 128) * nkb + k0 / 128) * 4);
+    const uint32_t hi = (uint32_t)((((Iu + c0) / 128) * nkb + k0 / 128) * 4);
+#pragma unroll
+    for (int i = 0; i < NP; ++i) {
+      s_lo[i] = __uint_as_float(sload4(sc, lo + 4u * (uint32_t)i));
+      s_hi[i] = __uint_as_float(sload4(sc, hi + 4u * (uint32_t)i));
+    }
+  }
+  constexpr int pitch = lean_pitch(KR);
+  uint16_t* xw = ftm_xl_lds + kp * (kLeanXT + 1) * pitch;
+  // zero row for MFMA rows without a token (this wave's region only)
+  for (int e = 8 * lane; e < KR; e += 8 * 64) *(u32x4*)(xw + kLeanXT * pitch + e) = (u32x4){0u, 0u, 0u, 0u};
+  for (int mb = 0; mb < cnt; mb += kLeanXT) {
+    const int nb = min(kLeanXT, cnt - mb);
+    int pr[kLeanXT];
+    lean_pairs(a, rec, list, shared_col, cnt, mb, pr);
+    lean_fill<KR>(pr, nb, a.x, a.KP, H, k0, xw);
+    const uint16_t* xrow = xw + ((n < nb) ? n : kLeanXT) * pitch;
+    f32x4 part[NP];
+#pragma unroll
+    for (int i = 0; i < NP; ++i) part[i] = (f32x4){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int wi = 0; wi < NWIN; ++wi) {
+      if (wi > 0 || (NWIN > 1 && mb > 0)) lean_issue<NLW>(wres, lrow, row_bytes, kbase, wi * NLW, S);
+      __builtin_amdgcn_s_waitcnt(0);  // weights and this wave's LDS rows have landed
+      lean_mfma<FP8, NLW, NP>(S, xrow, wi * NLW * (FP8 ? 64 : 32), part, 0);
+    }
+    f32x4 acc;
+    if constexpr (FP8) {
+      const bool upper = n >= 8;
+      acc = part[0] * (upper ? s_hi[0] : s_lo[0]);
+#pragma unroll
+      for (int i = 1; i < NP; ++i) acc += part[i] * (upper ? s_hi[i] : s_lo[i]);
+    } else {
+      acc = part[0];
+    }
+    if (lane < 16) red[kp * 16 + lane] = acc;
+    __syncthreads();
+    if (kp == 0) {
+      f32x4 t = red[n] + red[16 + n] + red[32 + n] + red[48 + n];
+#pragma unroll
+      for (int r = 0; r < kLeanXT; ++r) {
+        const float gs = t[r];
+        const float us = dpp_f<kDppRowShl8>(t[r]);
+        if (lane < 8 && r < nb) {
+          const float h = act_fn(a.L.act, gs, us, a.L.swiglu_alpha, a.L.swiglu_limit);
+          ((uint16_t*)a.hbuf)[(size_t)pr[r] * a.Imax + c0 + n] = f32_to_bf16(h);
+        }
+      }
+    }
+    __syncthreads();
+  }
+}
+
+template <int KR, int NWS>
+__global__ __launch_bounds__(kBlock) void k_stage_a_lean(const LayerArgs a) {
+  __shared__ f32x4 red[4 * 16];
+  const int kp = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int I = a.L.inter;
+  const int t8 = I / 8;
+  // shared-expert items first: each takes every token, so they start early
+  // instead of trailing the grid
+  const int nShared = a.L.shared_inter > 0 ? a.L.shared_inter / 8 : 0;
+  if ((int)blockIdx.x < nShared) {
+    lean_a_item<false, KR, NWS>(a, (const char*)a.L.shared_w13, nullptr, a.L.shared_inter, blockIdx.x * 8, a.T,
+                                nullptr, nullptr, a.L.topk, kp, red);
+    return;
+  }
+  const int item = blockIdx.x - nShared;
+  const ExpertRec rec = load_rec(a, min(item / t8, a.L.num_experts));
+  const int nRouted = sload_i32(a.ctrl, kCtrlNRouted);
+  if (item >= nRouted * t8) return;
+  if (rec.slot < 0 || rec.slot >= a.L.w13.num_slots) {
+    if (threadIdx.x == 0) atomicOr(&a.ctrl[kCtrlError], 1);
+    return;
+  }
+  const char* w = (const char*)a.L.w13.w + (int64_t)rec.slot * a.L.w13.w_stride;
+  const float* sc = (const float*)((const char*)a.L.w13.s + (int64_t)rec.slot * a.L.w13.s_stride);
+  lean_a_item<true, KR, 1>(a, w, sc, I, (item % t8) * 8, rec.cnt, &rec, a.lists + (size_t)rec.e * a.T, 0, kp, red);
+}
+
+// Stage B item: 64 output columns of one expert, wave w owns 16 of them over
+// the full K (= I routed / Is shared); y = acc * router weight -> slot buffer.
+template <bool FP8, int KB, int NWIN>
+__device__ void lean_b_item(const LayerArgs& a, const char* w, const float* sc, int cnt, const ExpertRec* rec,
+                            const int32_t* list, int shared_col, int nt, int wv) {
+  constexpr int NLW = (FP8 ? KB / 64 : KB / 32) / NWIN;
+  constexpr int NP = FP8 ? NLW / 2 : 1;
+  static_assert(!FP8 || NWIN == 1, "FP8 rows: one window per wave");
+  const int lane = threadIdx.x & 63;
+  const int n = lane & 15;
+  const int H = a.L.hidden;
+  const uint32_t row_bytes = (FP8 ? 1u : 2u) * (uint32_t)KB;
+  const Rsrc wres = make_rsrc(w, row_bytes * (uint32_t)H);
+  const int col0 = nt * 64 + 16 * wv;
+  const int brow = col0 + n;
+  LeanWin<NLW> S;
+  lean_issue<NLW>(wres, brow, row_bytes, 0u, 0, S);
+  float sv[NP];
+  if constexpr (FP8) {
+    const uint32_t off = (uint32_t)((col0 / 128) * (KB / 128) * 4);
+#pragma unroll
+    for (int i = 0; i < NP; ++i) sv[i] = __uint_as_float(sload4(sc, off + 4u * (uint32_t)i));
+  }
+  constexpr int pitch = lean_pitch(KB);
+  uint16_t* xw = ftm_xl_lds + wv * (kLeanXT + 1) * pitch;
+  for (int e = 8 * lane; e < KB; e += 8 * 64) *(u32x4*)(xw + kLeanXT * pitch + e) = (u32x4){0u, 0u, 0u, 0u};
+  for (int mb = 0; mb < cnt; mb += kLeanXT) {
+    const int nb = min(kLeanXT, cnt - mb);
+    int pr[kLeanXT];
+    lean_pairs(a, rec, list, shared_col, cnt, mb, pr);
+    lean_fill<KB>(pr, nb, a.hbuf, 1, a.Imax, 0, xw);
+    float wr[kLeanXT];
+#pragma unroll
+    for (int r = 0; r < kLeanXT; ++r) wr[r] = r < nb ? __uint_as_float(sload4(a.wts, 4u * (uint32_t)pr[r])) : 0.0f;
+    const uint16_t* xrow = xw + ((n < nb) ? n : kLeanXT) * pitch;
+    f32x4 part[NP];
+#pragma unroll
+    for (int i = 0; i < NP; ++i) part[i] = (f32x4){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int wi = 0; wi < NWIN; ++wi) {
+      if (wi > 0 || (NWIN > 1 && mb > 0)) lean_issue<NLW>(wres, brow, row_bytes, 0u, wi * NLW, S);
+      __builtin_amdgcn_s_waitcnt(0);  // weights and this wave's LDS rows have landed
+      lean_mfma<FP8, NLW, NP>(S, xrow, wi * NLW * (FP8 ? 64 : 32), part, 0);
+    }
+    f32x4 acc;
+    if constexpr (FP8) {
+      acc = part[0] * sv[0];
+#pragma unroll
+      for (int i = 1; i < NP; ++i) acc += part[i] * sv[i];
+    } else {
+      acc = part[0];
+    }
+#pragma unroll
+    for (int r = 0; r < kLeanXT; ++r)
+      if (lane < 16 && r < nb) a.ybuf[(size_t)pr[r] * H + brow] = acc[r] * wr[r];
+  }
+}
+
+template <int KB, int NWS>
+__global__ __launch_bounds__(kBlock) void k_stage_b_lean(const LayerArgs a) {
+  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int H = a.L.hidden;
+  const int tiles = H / 64;
+  // the shared expert's column tiles first (see k_stage_a_lean)
+  const int hasSh = a.L.shared_inter > 0 ? 1 : 0;
+  const int u0 = (int)blockIdx.x / tiles, nt = (int)blockIdx.x % tiles;
+  if (u0 < hasSh) {
+    lean_b_item<false, KB, NWS>(a, (const char*)a.L.shared_w2, nullptr, a.T, nullptr, nullptr, a.L.topk, nt, wv);
+    return;
+  }
+  const int u = u0 - hasSh;
+  const ExpertRec rec = load_rec(a, min(u, a.L.num_experts));
+  const int nRouted = sload_i32(a.ctrl, kCtrlNRouted);
+  if (u >= nRouted) return;
+  const int32_t* list = a.lists + (size_t)rec.e * a.T;
+  if (rec.slot < 0 || rec.slot >= a.L.w2.num_slots) {
+    // non-resident expert: contribute zeros, flag the error
+    for (int idx = threadIdx.x; idx < rec.cnt * 64; idx += kBlock) {
+      const int m = idx / 64, c = nt * 64 + idx % 64;
+      a.ybuf[(size_t)list[m] * H + c] = 0.0f;
+    }
+    if (threadIdx.x == 0) atomicOr(&a.ctrl[kCtrlError], 1);
+    return;
+  }
+  const char* w = (const char*)a.L.w2.w + (int64_t)rec.slot * a.L.w2.w_stride;
+  const float* sc = (const float*)((const char*)a.L.w2.s + (int64_t)rec.slot * a.L.w2.s_stride);
+  lean_b_item<true, KB, 1>(a, w, sc, rec.cnt, &rec, list, 0, nt, wv);
+}
+
 // ============================================================== combine
 // out[t, n] = sum_j ybuf[t*KP + j, n] in slot order (deterministic, no atomics).
 template <int AT>
@@ -1243,6 +1531,20 @@ static XlPlan xl_plan_b(const ftm_moe_layer& L, int T) {
 // which: bit 0 = stage A (w13 + act), bit 1 = stage B (w2), bit 2 = combine
 template <int FMT, int AT>
 static void launch_stages(const LayerArgs& a, int gridA, int gridB, hipStream_t st, int which) {
+  const bool lean = FMT == FTM_FMT_FP8_BLOCK && AT == FTM_DT_BF16 && a.lean;
+  if (lean) {
+    const int maxU = a.L.num_experts < a.T * a.L.topk ? a.L.num_experts : a.T * a.L.topk;
+    const size_t lds = 4u * (kLeanXT + 1) * (size_t)lean_pitch(512) * 2u;
+    if (which & 1) {
+      const int items = maxU * (a.L.inter / 8) + a.L.shared_inter / 8;
+      hipLaunchKernelGGL((k_stage_a_lean<512, 2>), dim3(items), dim3(kBlock), lds, st, a);
+    }
+    if (which & 2) {
+      const int grid = (maxU + (a.L.shared_inter > 0 ? 1 : 0)) * (a.L.hidden / 64);
+      hipLaunchKernelGGL((k_stage_b_lean<512, 2>), dim3(grid), dim3(kBlock), lds, st, a);
+    }
+    which &= 4;
+  }
   if (which & 1) {
     if constexpr (FMT == FTM_FMT_GPTQ_INT4) {
       hipLaunchKernelGGL((k_stage_a<FMT, AT>), dim3(gridA), dim3(kBlock), 0, st, a);
