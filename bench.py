@@ -50,12 +50,12 @@ def _parse():
     return ap.parse_args()
 
 
-def _pmc_traffic(config: str, T: int):
+def _pmc_traffic(kernel: str, config: str, T: int):
     """HBM bytes per launch of the w13 kernel from the committed rocprofv3 PMC
     summary (FETCH_SIZE + WRITE_SIZE per dispatch, scaled by the factor the
     same counters read for a copy kernel of known size), if one exists for
-    this workload."""
-    path = os.path.join(ROOT, "profiles", f"k_stage_a_rows__{config}_T{T}__pmc.md")
+    this kernel and workload."""
+    path = os.path.join(ROOT, "profiles", f"{kernel}__{config}_T{T}__pmc.md")
     try:
         with open(path) as f:
             for line in f:
@@ -206,10 +206,11 @@ def main() -> int:
             u = int(torch.unique(ids).numel())
             bytes_a.append(u * w13_unit + sh_w13 + T * cfg.H * 2)
     ach = float(np.mean(bytes_a)) / (kern_us["w13"] * 1e-6) / 1e9
-    traffic = _pmc_traffic(cfg.name, T)
+    w13_kernel = layers[0].stage_kernel(T, nat.STAGE_W13)
+    traffic = _pmc_traffic(w13_kernel, cfg.name, T)
     roofline = {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": traffic["bytes"] if traffic else None,
-                "kernel": f"k_stage_a_rows<{cfg.fmt}> (w13 + activation)",
+                "kernel": f"{w13_kernel} ({cfg.fmt} w13 + activation)",
                 "kernel_avg_us": round(kern_us["w13"], 2),
                 "bytes_per_launch": int(np.mean(bytes_a)),
                 "unit_bytes": w13_unit, "units_per_launch": round((np.mean(bytes_a) - sh_w13 - T * cfg.H * 2) / w13_unit, 2),

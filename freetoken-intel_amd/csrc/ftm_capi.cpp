@@ -216,6 +216,13 @@ int ftm_moe_forward_stage(const ftm_moe_layer* layer, const void* x, int32_t num
   return hip_rc(e);
 }
 
+const char* ftm_moe_stage_kernel(const ftm_moe_layer* layer, int32_t num_tokens, int32_t stage) {
+  if (check_layer(layer, true) != FTM_OK || num_tokens <= 0) return nullptr;
+  // x only matters for its alignment, which the caller guarantees when it launches
+  if (!fast_layer(layer, reinterpret_cast<const void*>(uintptr_t{256}))) return nullptr;
+  return stage_kernel_name(*layer, num_tokens, stage);
+}
+
 int ftm_moe_forward_routed(const ftm_moe_layer* layer, const void* x, int32_t num_tokens,
                            const int32_t* topk_ids, const float* topk_w, void* out, void* workspace,
                            size_t ws_bytes, void* stream) {

@@ -80,6 +80,8 @@ hipError_t launch_linear(const ftm_proj& P, int slot, const void* x, int x_dt, i
                          int out_dt, const void* bias, int bias_dt, int final_dt, hipStream_t st);
 hipError_t launch_fill_routing(int T, int32_t slot, int32_t* slot_word, int32_t* ids, float* w, hipStream_t st);
 hipError_t launch_ws_init(void* ws, hipStream_t st);
+// Base name of the kernel a stage (FTM_STAGE_*) launches for L at T tokens.
+const char* stage_kernel_name(const ftm_moe_layer& L, int T, int stage);
 // ftm_dequant.hip
 hipError_t launch_linear_generic(const ftm_proj& P, int slot, const void* x, int x_dt, int M, void* out,
                                  int out_dt, const void* bias, int bias_dt, int final_dt, hipStream_t st);

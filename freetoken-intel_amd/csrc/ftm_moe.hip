@@ -1620,6 +1620,48 @@ hipError_t launch_experts(const ftm_moe_layer& L, const void* x, int T, void* ou
   return hipGetLastError();
 }
 
+// Name of the kernel launch_router / launch_topk / launch_experts start for
+// `stage` (FTM_STAGE_*) of layer L at T tokens: the same predicates as the
+// launchers above, for profilers and benchmarks that attribute time by name.
+template <int FMT, int AT>
+static const char* expert_kernel_name(const ftm_moe_layer& L, int T, int stage) {
+  const bool lean = FMT == FTM_FMT_FP8_BLOCK && AT == FTM_DT_BF16 && lean_ok(L, T);
+  if (stage == FTM_STAGE_W13) {
+    if (lean) return "k_stage_a_lean";
+    if (FMT == FTM_FMT_GPTQ_INT4) return "k_stage_a";
+    return xl_plan_a<FMT, AT>(L, T).ok ? "k_stage_a_xl" : "k_stage_a_rows";
+  }
+  if (lean) return "k_stage_b_lean";
+  if (FMT == FTM_FMT_GPTQ_INT4) return "k_stage_b";
+  return xl_plan_b<FMT, AT>(L, T).ok ? "k_stage_b_xl" : "k_stage_b";
+}
+
+template <int FMT>
+static const char* expert_kernel_name_dt(const ftm_moe_layer& L, int T, int stage) {
+  return L.act_dtype == FTM_DT_F32 ? expert_kernel_name<FMT, FTM_DT_F32>(L, T, stage)
+                                   : expert_kernel_name<FMT, FTM_DT_BF16>(L, T, stage);
+}
+
+const char* stage_kernel_name(const ftm_moe_layer& L, int T, int stage) {
+  switch (stage) {
+    case FTM_STAGE_ROUTER: return "k_router";
+    case FTM_STAGE_TOPK: return T <= kTopk1MaxT ? "k_topk1" : "k_topk";
+    case FTM_STAGE_COMBINE: return "k_combine";
+    case FTM_STAGE_W13:
+    case FTM_STAGE_W2: break;
+    default: return nullptr;
+  }
+  if (gemm_path_ok(L, T)) return stage == FTM_STAGE_W13 ? "k_gemm_a" : "k_gemm_b";
+  switch (L.w13.fmt) {
+    case FTM_FMT_BF16: return expert_kernel_name_dt<FTM_FMT_BF16>(L, T, stage);
+    case FTM_FMT_FP8_BLOCK: return expert_kernel_name_dt<FTM_FMT_FP8_BLOCK>(L, T, stage);
+    case FTM_FMT_GPTQ_INT4: return expert_kernel_name_dt<FTM_FMT_GPTQ_INT4>(L, T, stage);
+    case FTM_FMT_INT8_PACKED: return expert_kernel_name_dt<FTM_FMT_INT8_PACKED>(L, T, stage);
+    case FTM_FMT_MXFP4: return expert_kernel_name_dt<FTM_FMT_MXFP4>(L, T, stage);
+    default: return nullptr;
+  }
+}
+
 template <int FMT>
 static void launch_linear_t(const LinArgs& a, dim3 grid, int x_dt, hipStream_t st) {
   if (x_dt == FTM_DT_F32)

@@ -123,6 +123,7 @@ EXPORTED = (
     "ftm_workspace_init",
     "ftm_moe_forward",
     "ftm_moe_forward_stage",
+    "ftm_moe_stage_kernel",
     "ftm_moe_forward_routed",
     "ftm_route",
     "ftm_linear",
@@ -160,6 +161,8 @@ def lib() -> ctypes.CDLL:
     L.ftm_moe_forward.argtypes = [P_layer, vp, i32, vp, vp, vp, vp, vp, sz, vp]
     L.ftm_moe_forward_stage.restype = ctypes.c_int
     L.ftm_moe_forward_stage.argtypes = [P_layer, vp, i32, vp, i32, vp, sz, vp]
+    L.ftm_moe_stage_kernel.restype = ctypes.c_char_p
+    L.ftm_moe_stage_kernel.argtypes = [P_layer, i32, i32]
     L.ftm_moe_forward_routed.restype = ctypes.c_int
     L.ftm_moe_forward_routed.argtypes = [P_layer, vp, i32, vp, vp, vp, vp, sz, vp]
     L.ftm_route.restype = ctypes.c_int

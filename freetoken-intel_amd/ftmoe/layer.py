@@ -170,6 +170,12 @@ class MoeLayer:
                                              ws.data_ptr(), ws.numel(), nat.stream_of(x))
         nat.check(rc, "ftm_moe_forward_stage")
 
+    def stage_kernel(self, num_tokens: int, stage: int) -> Optional[str]:
+        """Base name of the kernel :meth:`forward_stage` launches for ``stage`` at
+        ``num_tokens`` tokens (None on the generic path); no device work."""
+        name = nat.lib().ftm_moe_stage_kernel(ctypes.byref(self.c()), int(num_tokens), int(stage))
+        return name.decode() if name is not None else None
+
     def forward_routed(self, x: torch.Tensor, topk_ids: torch.Tensor, topk_w: torch.Tensor) -> torch.Tensor:
         """Routed experts (+ shared) for caller-supplied routing ``[T, k]``."""
         x = self._check_x(x)

@@ -164,6 +164,14 @@ int ftm_moe_forward(const ftm_moe_layer* layer, const void* x, int32_t num_token
 int ftm_moe_forward_stage(const ftm_moe_layer* layer, const void* x, int32_t num_tokens, void* out,
                           int32_t stage, void* workspace, size_t ws_bytes, void* stream);
 
+/* Base name (no namespace or template arguments) of the kernel that stage
+ * `stage` of ftm_moe_forward launches for this layer at `num_tokens` tokens,
+ * as a static string; NULL when the layer is invalid, takes the generic path
+ * (which has no stages) or `stage` is out of range.  Touches no device state.
+ * No counterpart in the reference: it names what ftm_moe_forward_stage runs,
+ * for profilers and benchmarks that attribute time by kernel name. */
+const char* ftm_moe_stage_kernel(const ftm_moe_layer* layer, int32_t num_tokens, int32_t stage);
+
 /* Routed experts (+ shared expert if the layer has one) with routing supplied
  * by the caller: the grouped replacement of the per-(token, expert) loop in
  * python/freetoken/models/qwen3_5_moe/__init__.py:1732-1737 and of

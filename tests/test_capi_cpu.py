@@ -111,3 +111,38 @@ def test_copy_slots_argument_errors():
     assert lib.ftm_copy_slots(None, None, 64, ev, ev, 2, None, None) == nat.ERR_NULL
     neg = (ctypes.c_int32 * 1)(-1)
     assert lib.ftm_copy_slots(ctypes.c_void_p(16), ctypes.c_void_p(32), 64, neg, ev, 1, None, None) == nat.ERR_DIM
+
+
+def test_stage_kernel_names_follow_the_dispatch():
+    """ftm_moe_stage_kernel names the kernel each stage launches: the lean FP8
+    decode stages for the 2048x512 shape below the token crossover, the tiled
+    GEMM stages at >= 16 tokens per routed expert, the LDS-activation stages
+    up to 4 tokens and the register-fed ones above for other shapes."""
+    lib = nat.lib()
+
+    def name(L, T, st):
+        r = lib.ftm_moe_stage_kernel(ctypes.byref(L), T, st)
+        return r.decode() if r is not None else None
+
+    c3 = _layer(E=256, H=2048, I=512, k=8)
+    c3.shared_inter, c3.shared_w13, c3.shared_w2, c3.shared_gate = 512, 0xA0000, 0xB0000, 0xC0000
+    for T in (1, 4, 16, 64, 256):
+        assert name(c3, T, nat.STAGE_W13) == "k_stage_a_lean", T
+        assert name(c3, T, nat.STAGE_W2) == "k_stage_b_lean", T
+    # 512 tokens x top-8 = 16 pairs per expert on all 256 experts: GEMM stages
+    assert name(c3, 512, nat.STAGE_W13) == "k_gemm_a"
+    assert name(c3, 512, nat.STAGE_W2) == "k_gemm_b"
+    assert name(c3, 8, nat.STAGE_TOPK) == "k_topk1"
+    assert name(c3, 9, nat.STAGE_TOPK) == "k_topk"
+    assert name(c3, 16, nat.STAGE_ROUTER) == "k_router"
+    assert name(c3, 16, nat.STAGE_COMBINE) == "k_combine"
+    assert name(c3, 16, 5) is None
+    assert name(c3, 0, nat.STAGE_W13) is None
+    small = _layer(E=8, H=256, I=128, k=2)
+    assert name(small, 4, nat.STAGE_W13) == "k_stage_a_xl"
+    assert name(small, 4, nat.STAGE_W2) == "k_stage_b_xl"
+    assert name(small, 5, nat.STAGE_W13) == "k_stage_a_rows"
+    assert name(small, 5, nat.STAGE_W2) == "k_stage_b"
+    assert name(small, 64, nat.STAGE_W13) == "k_gemm_a"
+    f32 = _layer(E=8, H=256, I=128, k=2, act_dtype=nat.DT_F32)
+    assert name(f32, 4, nat.STAGE_W13) is None  # f32 activations need the bf16 router: invalid layer
