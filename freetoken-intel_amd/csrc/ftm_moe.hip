@@ -1088,6 +1088,11 @@ __device__ __forceinline__ void lean_mfma(const LeanWin<NLW>& S, const uint16_t*
       f32x4& t = part[pbase + b / 2];
       t = mfma_bf16(x0, fp8x8_to_bf16(r.x, r.y), t);
       t = mfma_bf16(x1, fp8x8_to_bf16(r.z, r.w), t);
+      // interleave: two LDS reads, then their two MFMAs.  Left alone, the
+      // scheduler issues all 2 * NLW activation reads up front (8 VGPRs each),
+      // which costs k_stage_b_lean a wave per SIMD (114 -> 102 VGPRs).
+      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
     } else {
       const u32x4 x0 = *(const u32x4*)(xl + b * kLoadK);
       part[0] = mfma_bf16(x0, r, part[0]);
