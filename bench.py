@@ -300,7 +300,7 @@ def _offload_bench(args) -> int:
     import torch
 
     from ftmoe import synthetic as S
-    from ftmoe.moe.offload_cache import OffloadMoeCache, moe_grouped_forward
+    from ftmoe.moe.offload_cache import OffloadMoeCache, moe_offload_forward
 
     dev = torch.device("cuda:0")
     cfg = S.CONFIGS["c3_fp8"]
@@ -321,11 +321,11 @@ def _offload_bench(args) -> int:
     slot_bytes = sum(cache.bank_caches[b][0].numel() * cache.bank_caches[b].element_size() for b in cache.bank_schema)
 
     def step(i):
-        cache.ensure_experts(0, torch.from_numpy(ids_all[i]))
-        misses = int(cache.num_indices.item())
-        cache.copy_missing()
-        moe_grouped_forward(xs[i % 7], ids_dev[i], w_dev[i], cache, 0, intermediate=cfg.I, shared=syn.shared)
-        return misses
+        # steps routing to more experts than slots run in chunks that fit the pool
+        before = int(cache.stat_missing)
+        moe_offload_forward(xs[i % 7], ids_dev[i], w_dev[i], cache, 0, intermediate=cfg.I, shared=syn.shared,
+                            ids_host=torch.from_numpy(ids_all[i]))
+        return int(cache.stat_missing) - before
 
     for i in range(10):  # warm the pool and the kernels
         step(steps + i)

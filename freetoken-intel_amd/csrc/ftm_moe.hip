@@ -286,7 +286,10 @@ __device__ __forceinline__ void emit_token(const LayerArgs& a, int t, int sel_e,
         atomicOr(&a.ctrl[kCtrlError], 4);
       }
     } else {
-      atomicOr(&a.ctrl[kCtrlError], 2);
+      // caller-supplied id < 0: the pair has no expert in this call (it is in
+      // no list and the combine skips its slot); >= E: an error
+      a.ids[(size_t)t * k + lane] = -1;
+      if (sel_e >= E) atomicOr(&a.ctrl[kCtrlError], 2);
     }
   }
   if (lane == 0 && a.L.shared_inter > 0) {
@@ -1316,8 +1319,11 @@ __global__ __launch_bounds__(kBlock) void k_combine(const LayerArgs a) {
   if (idx >= a.T * H4) return;
   const int t = idx / H4, n4 = idx % H4;
   const f32x4* yb = (const f32x4*)(a.ybuf + (size_t)t * KP * H) + n4;
-  f32x4 s = yb[0];
-  for (int j = 1; j < KP; ++j) s += yb[(size_t)j * H4];
+  const int32_t* ids = a.ids + (size_t)t * a.L.topk;
+  // slots in order; a routed slot without an expert (id < 0) holds nothing
+  f32x4 s = (f32x4){0.f, 0.f, 0.f, 0.f};
+  for (int j = 0; j < KP; ++j)
+    if (j >= a.L.topk || ids[j] >= 0) s += yb[(size_t)j * H4];
   if constexpr (AT == FTM_DT_F32) {
     ((f32x4*)a.out)[(size_t)t * H4 + n4] = s;
   } else {

@@ -501,5 +501,47 @@ def moe_grouped_forward(flat: torch.Tensor, top_idx: torch.Tensor, top_w: torch.
     return layer.forward_routed(flat, top_idx, top_w)
 
 
+def moe_offload_forward(flat: torch.Tensor, top_idx: torch.Tensor, top_w: torch.Tensor, cache: OffloadMoeCache,
+                        layer_id: int, *, intermediate: int, act: str = "silu", shared: Optional[dict] = None,
+                        swiglu_alpha: float = 1.702, swiglu_limit: float = 7.0,
+                        ids_host: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """The offload decode step of ``_forward_offload_core``
+    (python/freetoken/models/qwen3_5_moe/__init__.py:1609-1749) as grouped calls:
+    make the routed experts resident (:meth:`OffloadMoeCache.ensure_experts`,
+    :meth:`~OffloadMoeCache.copy_missing` on the side stream) and run
+    :func:`moe_grouped_forward` over them.
+
+    A step that routes to more experts than the pool holds (a ``decode_only``
+    pool) runs in chunks of at most ``cache_size`` experts, in ascending expert
+    id: each chunk's pairs keep their ids, the others are passed as -1 (no
+    expert), the shared expert rides with the first chunk, and the chunk
+    outputs are summed in fp32 and rounded once.  Every routed pair is
+    computed; against a single call the chunked sum differs only by the
+    rounding of each chunk's output to the activation dtype.  ``ids_host``: a
+    host copy of ``top_idx`` when the caller has one (saves the device read
+    the LRU planning needs)."""
+    ids_host = (top_idx if ids_host is None else ids_host).reshape(-1).to("cpu", torch.int64)
+    uniq = torch.unique(ids_host)
+    cap = cache.cache_size
+    if uniq.numel() <= cap:
+        cache.ensure_experts(layer_id, uniq)
+        cache.copy_missing()
+        return moe_grouped_forward(flat, top_idx, top_w, cache, layer_id, intermediate=intermediate, act=act,
+                                   shared=shared, swiglu_alpha=swiglu_alpha, swiglu_limit=swiglu_limit)
+    ids_dev = top_idx.to(torch.int32)
+    acc = None
+    for c0 in range(0, uniq.numel(), cap):
+        chunk = uniq[c0:c0 + cap]
+        cache.ensure_experts(layer_id, chunk)
+        cache.copy_missing()
+        member = torch.isin(ids_dev, chunk.to(ids_dev.device, torch.int32))
+        ids_c = torch.where(member, ids_dev, torch.full_like(ids_dev, -1))
+        out_c = moe_grouped_forward(flat, ids_c, top_w, cache, layer_id, intermediate=intermediate, act=act,
+                                    shared=shared if c0 == 0 else None, swiglu_alpha=swiglu_alpha,
+                                    swiglu_limit=swiglu_limit)
+        acc = out_c.float() if acc is None else acc + out_c.float()
+    return acc.to(flat.dtype)
+
+
 __all__ = ["OffloadMoeCache", "SlotWeightAccessor", "_BANK_SCHEMAS", "gptq_int4_bytes_per_expert_slot",
-           "moe_grouped_forward"]
+           "moe_grouped_forward", "moe_offload_forward"]

@@ -176,7 +176,10 @@ const char* ftm_moe_stage_kernel(const ftm_moe_layer* layer, int32_t num_tokens,
  * by the caller: the grouped replacement of the per-(token, expert) loop in
  * python/freetoken/models/qwen3_5_moe/__init__.py:1732-1737 and of
  * fused_moe's per-expert loop (python/freetoken/kernel/triton/fused_moe.py:129-161).
- *   topk_ids int32 [T, k] expert ids; topk_w f32 [T, k] router weights. */
+ *   topk_ids int32 [T, k] expert ids; topk_w f32 [T, k] router weights.
+ * An id < 0 marks a pair with no expert in this call: it contributes nothing
+ * and raises no error (the padding an expert-parallel shard or a slot pool
+ * smaller than the routed set uses; the reference has no such case). */
 int ftm_moe_forward_routed(const ftm_moe_layer* layer, const void* x, int32_t num_tokens,
                            const int32_t* topk_ids, const float* topk_w, void* out,
                            void* workspace, size_t ws_bytes, void* stream);

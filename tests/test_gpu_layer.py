@@ -250,3 +250,31 @@ def test_non_resident_expert_contributes_zero_and_flags(gpu, T):
     ws[12:16].zero_()
     assert err & 1, "error bit for a non-resident routed expert"
     assert_close(to_f32(out), ref["out"], what="layer output without the missing expert")
+
+
+@pytest.mark.parametrize("name,T", [("c3_fp8", 2), ("c3_fp8", 9), ("c1_int8", 5), ("c2_gptq", 7), ("c3_full", 16)])
+def test_negative_expert_ids_are_skipped(gpu, name, T):
+    """Caller-supplied routing with id -1 for some pairs: those pairs contribute
+    nothing (the combine skips their slots), no error bit is set, and the rest
+    equals the oracle with those pairs' weights at zero.  c3_full is the full C3
+    shape (the lean FP8 decode stages)."""
+    from ftmoe.layer import workspace
+
+    cfg = S.CONFIGS["c3_fp8"] if name == "c3_full" else S.SMALL[name]
+    syn = S.generate(cfg, T=T, seed=70 + T)
+    spec = oracle_spec(syn)
+    rng = np.random.RandomState(T)
+    ids = np.stack([rng.choice(syn.cfg.E, syn.cfg.k, replace=False) for _ in range(T)]).astype(np.int32)
+    w = O.round_bf16(rng.rand(T, syn.cfg.k).astype(np.float32))
+    skip = rng.rand(T, syn.cfg.k) < 0.4
+    skip[0, :] = True  # one token with no routed expert at all
+    ref = O.layer_reference(spec, np_(syn.x), ids=ids, w=np.where(skip, 0.0, w).astype(np.float32))
+    dsyn = syn.to(gpu)
+    layer = S.build_layer(dsyn)
+    ws = workspace(gpu, layer.workspace_bytes(T))
+    ws[:16].zero_()
+    ids_in = np.where(skip, -1, ids).astype(np.int32)
+    out = layer.forward_routed(dsyn.x, torch.from_numpy(ids_in).to(gpu), torch.from_numpy(w).to(gpu))
+    torch.cuda.synchronize()
+    assert int(ws[12:16].view(torch.int32).item()) == 0, "no error bit for skipped pairs"
+    assert_close(to_f32(out), ref["out"], what=f"{name} layer with skipped pairs")

@@ -6,6 +6,8 @@ layer call over resident slots).
 * a two-layer FP8 pool smaller than one layer's experts: every decode step
   (route -> ensure_experts -> copy_missing -> moe_grouped_forward) matches the
   oracle computed from the full host bank, to the layer tolerance;
+* a pool smaller than one step's routed experts (moe_offload_forward runs the
+  step in chunks that fit) still computes every routed pair;
 * SlotWeightAccessor.get is the bit-exact dequantization of the slot and
   expert_forward matches the oracle's expert."""
 import numpy as np
@@ -16,7 +18,7 @@ import ftm_oracle as O
 from ftm_helpers import assert_close, np_, oracle_proj, oracle_spec, to_f32
 
 from ftmoe import synthetic as S
-from ftmoe.moe.offload_cache import OffloadMoeCache, SlotWeightAccessor, moe_grouped_forward
+from ftmoe.moe.offload_cache import OffloadMoeCache, SlotWeightAccessor, moe_grouped_forward, moe_offload_forward
 
 pytestmark = pytest.mark.gpu
 
@@ -86,6 +88,26 @@ def test_fp8_pool_decode_steps_match_oracle(gpu):
         assert_close(to_f32(out), ref["out"], what=f"pool step {step}")
     st = c.decode_miss_stats()
     assert st["calls"] == 6 and st["missing"] > 0
+
+
+def test_steps_with_more_experts_than_slots_run_in_chunks(gpu):
+    cfg, syns, c = _fp8_pool(gpu, slots=6)  # 6 slots; T=5 x top-4 routes up to 20 experts
+    rng = np.random.RandomState(9)
+    T = 5
+    chunked = 0
+    for step in range(4):
+        layer_id = step % 2
+        syn = syns[layer_id]
+        x = syn.x[:T]
+        ids = np.stack([rng.choice(cfg.E, cfg.k, replace=False) for _ in range(T)]).astype(np.int32)
+        w = O.round_bf16(rng.rand(T, cfg.k).astype(np.float32))
+        chunked += len(np.unique(ids)) > 6
+        shared = {k: v.to(gpu) for k, v in syn.shared.items()}
+        out = moe_offload_forward(x.to(gpu), torch.from_numpy(ids).to(gpu), torch.from_numpy(w).to(gpu), c,
+                                  layer_id, intermediate=cfg.I, shared=shared)
+        ref = O.layer_reference(oracle_spec(syn), np_(x), ids=ids, w=w)
+        assert_close(to_f32(out), ref["out"], what=f"chunked pool step {step}")
+    assert chunked == 4
 
 
 def test_accessor_get_and_expert_forward(gpu):
