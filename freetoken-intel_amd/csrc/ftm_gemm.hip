@@ -283,6 +283,314 @@ __device__ __forceinline__ void gemm_tile(const ProjSlot& W, int c0, int Iu, Rsr
   __syncthreads();  // the LDS tiles are reused by the caller's next tile
 }
 
+// ---------------------------------------------------------------- LDS ring tiles (stage A)
+// The stage A tiles for FP8 / INT8 / bf16 weights, fed by a ring of up to
+// four LDS stages that direct global-to-LDS copies (global_load_lds, 16 B per
+// lane) fill three K steps ahead of the MFMAs.  Activations (bf16) and the raw
+// weight bytes both land in LDS undecoded; a wave decodes its own weight rows
+// after its LDS read.  Each 1 KiB copy writes 64 consecutive 16-byte slots, so
+// the bank-conflict swizzle is applied on the read side of the copy: the lane
+// filling slot s of row r fetches piece s ^ f(r) of that row, and a reader
+// finds piece p of row r in slot p ^ f(r).  With f below, the rows one MFMA
+// operand read touches (16 rows, one piece each) hit distinct 16-byte bank
+// groups.  The tile's quantisation-group scales are copied to LDS once, before
+// the K loop, so no scale load waits inside it.
+
+// Raw weight bytes per row per K step and rows per 1 KiB copy.
+template <int WFMT>
+struct RingW {
+  static constexpr int kRowBytes = WFMT == FTM_FMT_BF16 ? 2 * kGK : kGK;
+  static constexpr int kRowsPerCopy = 1024 / kRowBytes;
+};
+// Ring bytes per workgroup: 64 KiB (FP8/INT8: 4 stages, bf16: 2).  The
+// tile's scales follow the ring (at most kRingScaleBytes; the launch sizes the
+// dynamic LDS to what the layer needs).
+constexpr int kRingA = 64 * 1024;
+constexpr int kRingScaleBytes = 16 * 1024;
+
+template <int WFMT, int NWR, int RB>
+struct RingPlan {
+  static constexpr int kA = kGM * 2 * kGK;  // 64 token rows x 64 bf16
+  static constexpr int kW = NWR * RingW<WFMT>::kRowBytes;
+  static constexpr int kStage = kA + kW;
+  static constexpr int kStages = RB / kStage < 4 ? RB / kStage : 4;
+  static constexpr int kALoads = kA / 1024 / 4;  // 1 KiB copies per wave per stage
+  static constexpr int kWLoads = kW / 1024 / 4;
+  static constexpr int kLoads = kALoads + kWLoads;
+  static_assert(kStages >= 2 && kA % 4096 == 0 && kW % 4096 == 0, "ring shape");
+};
+
+__device__ __forceinline__ int ring_fa(int r) { return (r ^ (r >> 3)) & 7; }         // 8 pieces per row
+__device__ __forceinline__ int ring_fw(int r) { return ((r >> 1) ^ (r >> 3)) & 3; }  // 4 pieces per row
+
+// s_waitcnt vmcnt(n), other counters untouched (gfx9 encoding), n < 64.
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (0x7 << 4) | (0xf << 8));
+}
+// Wait until at most `stages` ring stages of this wave's copies are in flight.
+template <int LOADS, int MAXS>
+__device__ __forceinline__ void wait_ring(int stages) {
+  if (MAXS >= 3 && stages >= 3) wait_vm<3 * LOADS>();
+  else if (MAXS >= 2 && stages == 2) wait_vm<2 * LOADS>();
+  else if (stages == 1) wait_vm<LOADS>();
+  else wait_vm<0>();
+}
+
+// XCD-aware order: consecutive workgroups go to different XCDs (round robin),
+// so workgroup b runs item xcd * per + min(xcd, rem) + b / 8, which keeps
+// runs of consecutive items (the N tiles of one M tile) on one XCD's L2.
+__device__ __forceinline__ int xcd_item(int b, int G) {
+  const int xcd = b & 7, per = G >> 3, rem = G & 7;
+  return xcd * per + (xcd < rem ? xcd : rem) + (b >> 3);
+}
+
+// One 64-token x NWR-row tile over the whole K range (FP8, INT8 or bf16
+// weights).  Wave w owns tile rows 64 j + 16 w .. + 15 (j < NWR / 64: for
+// stage A the gate rows and the matching up rows) for all 64 tokens, so each
+// weight byte is decoded once.  LPG: K steps per quantisation group, the loop
+// unrolled so the group partial is scaled once, straight after the group's
+// last MFMAs (2: 128-wide groups); 0: no intermediate scaling (bf16, or one
+// group over K); -1: any group size (scaled with selects every step).
+//   arow[i]: activation row of this lane's slot in A copy i (always a valid row;
+//            padding rows repeat a real one and their outputs are dropped)
+//   acc[mi][j]: tokens 16 mi + 4 (lane / 16) + r, tile row 64 j + 16 w + lane % 16
+template <int WFMT, int NWR, int RB, int LPG>
+__device__ __forceinline__ void gemm_tile_ring(const ProjSlot& W, int c0, int Iu,
+                                               const char* const (&arow)[RingPlan<WFMT, NWR, RB>::kALoads],
+                                               char* lds, f32x4 (&acc)[4][NWR / 64]) {
+  using P = RingPlan<WFMT, NWR, RB>;
+  using RW = RingW<WFMT>;
+  typedef __attribute__((address_space(1))) const void* GPtr;
+  typedef __attribute__((address_space(3))) void* LPtr;
+  constexpr int NB = NWR / 64;
+  constexpr int S = P::kStages;
+  constexpr bool kPost = WFMT == FTM_FMT_FP8_BLOCK || WFMT == FTM_FMT_INT8_PACKED;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int K = W.K;
+  const int nsteps = K / kGK;
+  auto grow = [&](int r) { return NWR == 128 ? (r < 64 ? c0 + r : Iu + c0 + (r - 64)) : c0 + r; };
+  const uint32_t rb = GemmW<WFMT>::row_bytes(K);
+  float* sS = (float*)(lds + RB);
+
+  // ---- this lane's copy sources (K offset added per step)
+  const char* asrc[P::kALoads];
+#pragma unroll
+  for (int i = 0; i < P::kALoads; ++i) {
+    const int r = 8 * (wave * P::kALoads + i) + (lane >> 3);
+    asrc[i] = arow[i] + 16 * ((lane & 7) ^ ring_fa(r));
+  }
+  const char* wsrc[P::kWLoads];
+#pragma unroll
+  for (int i = 0; i < P::kWLoads; ++i) {
+    const int j = wave * P::kWLoads + i;
+    int r, piece;
+    if constexpr (WFMT == FTM_FMT_BF16) {
+      r = 8 * j + (lane >> 3);
+      piece = (lane & 7) ^ ring_fa(r);
+    } else {
+      r = 16 * j + (lane >> 2);
+      piece = (lane & 3) ^ ring_fw(r);
+    }
+    wsrc[i] = W.w + (size_t)grow(r) * rb + 16 * piece;
+  }
+  auto issue = [&](int kb, int slot) {
+    char* st = lds + slot * P::kStage;
+#pragma unroll
+    for (int i = 0; i < P::kALoads; ++i)
+      __builtin_amdgcn_global_load_lds((GPtr)(asrc[i] + kb * 2 * kGK),
+                                       (LPtr)(st + 1024 * (wave * P::kALoads + i)), 16, 0, 0);
+#pragma unroll
+    for (int i = 0; i < P::kWLoads; ++i)
+      __builtin_amdgcn_global_load_lds((GPtr)(wsrc[i] + kb * RW::kRowBytes),
+                                       (LPtr)(st + P::kA + 1024 * (wave * P::kWLoads + i)), 16, 0, 0);
+  };
+
+  // ---- group scales of the tile -> LDS as fp32 (FP8: one row per 64-row
+  // half, INT8: one row per tile row), loads issued before the ring prologue
+  const int ngroups = kPost ? (K + W.group - 1) / W.group : 0;
+  constexpr int kScaleRows = WFMT == FTM_FMT_INT8_PACKED ? NWR : NWR / 64;
+  constexpr int kScalePer = WFMT == FTM_FMT_INT8_PACKED ? (kRingScaleBytes / 4 + kBlock - 1) / kBlock : 1;
+  uint32_t sw[kScalePer];
+  uint32_t sidx[kScalePer];
+  if constexpr (kPost) {
+    const uint32_t sesz = W.s_dt == FTM_DT_F32 ? 4u : 2u;
+    const int nsc = kScaleRows * ngroups;
+    const Rsrc sres = make_rsrc(W.s, WFMT == FTM_FMT_FP8_BLOCK
+                                         ? (uint32_t)(((W.N + W.group - 1) / W.group) * ngroups) * sesz
+                                         : (uint32_t)(W.N * ngroups) * sesz);
+#pragma unroll
+    for (int q = 0; q < kScalePer; ++q) {
+      const int e = tid + kBlock * q;
+      const int sr = e / (ngroups > 0 ? ngroups : 1), g = e - sr * ngroups;
+      const int wrow = WFMT == FTM_FMT_FP8_BLOCK ? grow(64 * sr) / W.group : grow(sr);
+      sidx[q] = (uint32_t)(wrow * ngroups + g);
+      sw[q] = bload_scalar_word(sres, sidx[q], W.s_dt, e < nsc);
+    }
+  }
+  const int pro = nsteps < S - 1 ? nsteps : S - 1;
+  for (int kb = 0; kb < pro; ++kb) issue(kb, kb);
+  if constexpr (kPost) {
+    wait_ring<P::kLoads, S - 1>(pro);
+#pragma unroll
+    for (int q = 0; q < kScalePer; ++q) {
+      const int e = tid + kBlock * q;
+      if (e < kScaleRows * ngroups) sS[e] = decode_scalar_word(sw[q], sidx[q], W.s_dt);
+    }
+  }
+
+  const int g4 = lane >> 4;
+  int arr[4], wrr[NB];
+#pragma unroll
+  for (int mi = 0; mi < 4; ++mi) arr[mi] = 16 * mi + (lane & 15);
+#pragma unroll
+  for (int nj = 0; nj < NB; ++nj) wrr[nj] = 64 * nj + 16 * wave + (lane & 15);
+
+  // one K step into d: wait for its stage, refill the ring, LDS -> MFMAs
+  auto step = [&](int kb, f32x4 (&d)[4][NB]) {
+    const int ahead = nsteps - 1 - kb < S - 2 ? nsteps - 1 - kb : S - 2;
+    wait_ring<P::kLoads, S - 2>(ahead);
+    __syncthreads();  // stage kb is in LDS for every wave; every wave is done with stage kb - 1
+    if (kb + S - 1 < nsteps) issue(kb + S - 1, (kb + S - 1) % S);
+    const char* st = lds + (kb % S) * P::kStage;
+    u32x4 b0[NB], b1[NB];
+#pragma unroll
+    for (int nj = 0; nj < NB; ++nj) {
+      const char* row = st + P::kA + wrr[nj] * RW::kRowBytes;
+      if constexpr (WFMT == FTM_FMT_BF16) {
+        b0[nj] = *(const u32x4*)(row + 16 * ((2 * g4) ^ ring_fa(wrr[nj])));
+        b1[nj] = *(const u32x4*)(row + 16 * ((2 * g4 + 1) ^ ring_fa(wrr[nj])));
+      } else {
+        const u32x4 raw = *(const u32x4*)(row + 16 * (g4 ^ ring_fw(wrr[nj])));
+        if constexpr (WFMT == FTM_FMT_FP8_BLOCK) {
+          b0[nj] = fp8x8_to_bf16(raw.x, raw.y);
+          b1[nj] = fp8x8_to_bf16(raw.z, raw.w);
+        } else {
+          b0[nj] = i8x8_to_bf16(raw.x, raw.y);
+          b1[nj] = i8x8_to_bf16(raw.z, raw.w);
+        }
+      }
+    }
+#pragma unroll
+    for (int mi = 0; mi < 4; ++mi) {
+      const char* row = st + arr[mi] * (2 * kGK);
+      const u32x4 a0 = *(const u32x4*)(row + 16 * ((2 * g4) ^ ring_fa(arr[mi])));
+      const u32x4 a1 = *(const u32x4*)(row + 16 * ((2 * g4 + 1) ^ ring_fa(arr[mi])));
+#pragma unroll
+      for (int nj = 0; nj < NB; ++nj) {
+        d[mi][nj] = mfma_bf16(a0, b0[nj], d[mi][nj]);
+        d[mi][nj] = mfma_bf16(a1, b1[nj], d[mi][nj]);
+      }
+    }
+  };
+  auto scale_of = [&](int nj, int grp) {
+    return sS[(WFMT == FTM_FMT_FP8_BLOCK ? nj : wrr[nj]) * ngroups + grp];
+  };
+
+  if constexpr (!kPost) {
+    for (int kb = 0; kb < nsteps; ++kb) step(kb, acc);
+  } else {
+    f32x4 tmp[4][NB];
+#pragma unroll
+    for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+      for (int nj = 0; nj < NB; ++nj) tmp[mi][nj] = (f32x4){0.f, 0.f, 0.f, 0.f};
+    if constexpr (LPG > 0) {
+      // nsteps % LPG == 0 (checked at launch): whole groups per iteration
+      for (int kb = 0, grp = 0; kb < nsteps; kb += LPG, ++grp) {
+#pragma unroll
+        for (int q = 0; q < LPG; ++q) step(kb + q, tmp);
+#pragma unroll
+        for (int nj = 0; nj < NB; ++nj) {
+          const float sc = scale_of(nj, grp);
+#pragma unroll
+          for (int mi = 0; mi < 4; ++mi) {
+            acc[mi][nj] += tmp[mi][nj] * sc;
+            tmp[mi][nj] = (f32x4){0.f, 0.f, 0.f, 0.f};
+          }
+        }
+      }
+    } else if constexpr (LPG == 0) {
+      for (int kb = 0; kb < nsteps; ++kb) step(kb, tmp);
+#pragma unroll
+      for (int nj = 0; nj < NB; ++nj) {
+        const float sc = scale_of(nj, 0);
+#pragma unroll
+        for (int mi = 0; mi < 4; ++mi) acc[mi][nj] += tmp[mi][nj] * sc;
+      }
+    } else {
+      const int lpg = W.group / kGK;
+      for (int kb = 0; kb < nsteps; ++kb) {
+        step(kb, tmp);
+        // end of a quantisation group: acc += group partial * scale (straight-line)
+        const bool last = ((kb + 1) % lpg == 0) | (kb + 1 == nsteps);
+        const int grp = kb / lpg;
+#pragma unroll
+        for (int nj = 0; nj < NB; ++nj) {
+          const float sc = scale_of(nj, grp);
+          const float f = last ? sc : 0.0f;
+          const float keep = last ? 0.0f : 1.0f;
+#pragma unroll
+          for (int mi = 0; mi < 4; ++mi) {
+            acc[mi][nj] += tmp[mi][nj] * f;
+            tmp[mi][nj] *= keep;
+          }
+        }
+      }
+    }
+  }
+  __syncthreads();  // the ring is reused by the caller's next tile
+}
+
+// K-loop group structure of a projection: 2 (128-wide groups), 0 (one group
+// over K, or no scales), -1 (other).
+__host__ __device__ __forceinline__ int ring_lpg(int fmt, int group, int K) {
+  if (fmt != FTM_FMT_FP8_BLOCK && fmt != FTM_FMT_INT8_PACKED) return 0;
+  if (group >= K) return 0;
+  if (group == 2 * kGK && (K / kGK) % 2 == 0) return 2;
+  return -1;
+}
+
+// Stage A body on the ring tiles: item -> rows, tile, activation epilogue.
+template <int WFMT, int LPG>
+__device__ void gemm_a_ring_body(const LayerArgs& a, const ProjSlot& W, int Iu, int c0, int m0, int cnt,
+                                 const int32_t* list, int shared_col, char* lds) {
+  using P = RingPlan<WFMT, 128, kRingA>;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int H = a.L.hidden, KP = a.KP;
+  const Rsrc lres = make_rsrc(list, list ? (uint32_t)a.T * 4u : 0u);
+  const int p0 = pair_of_row(lres, list != nullptr, m0, cnt, KP, shared_col);
+  const char* ap[P::kALoads];
+#pragma unroll
+  for (int i = 0; i < P::kALoads; ++i) {
+    int p = pair_of_row(lres, list != nullptr, m0 + 8 * (wave * P::kALoads + i) + (lane >> 3), cnt, KP, shared_col);
+    p = p >= 0 ? p : p0;
+    ap[i] = (const char*)a.x + (size_t)(p / KP) * (size_t)H * 2u;
+  }
+  f32x4 acc[4][2];
+#pragma unroll
+  for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+    for (int nj = 0; nj < 2; ++nj) acc[mi][nj] = (f32x4){0.f, 0.f, 0.f, 0.f};
+  gemm_tile_ring<WFMT, 128, kRingA, LPG>(W, c0, Iu, ap, lds, acc);
+  const int ch = c0 + 16 * wave + (lane & 15);
+  const float bg = W.bias != nullptr ? load_scalar(W.bias, ch, W.bias_dt) : 0.0f;
+  const float bu = W.bias != nullptr ? load_scalar(W.bias, Iu + ch, W.bias_dt) : 0.0f;
+#pragma unroll
+  for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int pe = pair_of_row(lres, list != nullptr, m0 + 16 * mi + 4 * (lane >> 4) + r, cnt, KP, shared_col);
+      if (pe >= 0) {
+        const float h = act_fn(a.L.act, acc[mi][0][r] + bg, acc[mi][1][r] + bu, a.L.swiglu_alpha, a.L.swiglu_limit);
+        store_scalar(a.hbuf, (size_t)pe * a.Imax + ch, FTM_DT_BF16, h);
+      }
+    }
+}
+
 // ---------------------------------------------------------------- stage A (w13 + activation)
 template <int WFMT>
 __device__ void gemm_a_body(const LayerArgs& a, const ProjSlot& W, int Iu, int c0, int m0, int cnt,
@@ -335,15 +643,30 @@ __device__ void gemm_a_body(const LayerArgs& a, const ProjSlot& W, int Iu, int c
     }
 }
 
-template <int FMT>
-__global__ __launch_bounds__(kBlock) void k_gemm_a(const LayerArgs a) {
-  __shared__ __attribute__((aligned(16))) uint16_t sA[2 * kGM * kGPitch];
-  __shared__ __attribute__((aligned(16))) uint16_t sB[2 * 128 * kGPitch];
+// Stage A ring body by K-loop group structure (ring_lpg): FP8 128x128 blocks
+// take LPG 2; INT8 per-channel (one group over K) 0, 128-wide groups 2; bf16 0.
+template <int WFMT>
+__device__ __forceinline__ void ring_a(const LayerArgs& a, const ProjSlot& W, int Iu, int c0, int m0, int cnt,
+                                       const int32_t* list, int shared_col, char* lds) {
+  const int lpg = ring_lpg(WFMT, W.group, W.K);
+  if constexpr (WFMT == FTM_FMT_BF16) {
+    gemm_a_ring_body<WFMT, 0>(a, W, Iu, c0, m0, cnt, list, shared_col, lds);
+  } else if constexpr (WFMT == FTM_FMT_FP8_BLOCK) {
+    if (lpg == 2) gemm_a_ring_body<WFMT, 2>(a, W, Iu, c0, m0, cnt, list, shared_col, lds);
+    else gemm_a_ring_body<WFMT, -1>(a, W, Iu, c0, m0, cnt, list, shared_col, lds);
+  } else {
+    if (lpg == 0) gemm_a_ring_body<WFMT, 0>(a, W, Iu, c0, m0, cnt, list, shared_col, lds);
+    else if (lpg == 2) gemm_a_ring_body<WFMT, 2>(a, W, Iu, c0, m0, cnt, list, shared_col, lds);
+    else gemm_a_ring_body<WFMT, -1>(a, W, Iu, c0, m0, cnt, list, shared_col, lds);
+  }
+}
+
+template <int FMT, bool RING>
+__device__ __forceinline__ void gemm_a_item(const LayerArgs& a, int item, uint16_t* sA, uint16_t* sB) {
   const int I = a.L.inter, Is = a.L.shared_inter;
   const int nRouted = a.ctrl[kCtrlNRouted];
   const int ntn = I / 64;
   const int routed_items = gemm_routed_mtiles(a, nRouted) * ntn;
-  const int item = blockIdx.x;
   if (item < routed_items) {
     const GemmTile t = gemm_find_tile(a, item / ntn, nRouted, false);
     if (t.u < 0) return;
@@ -354,14 +677,36 @@ __global__ __launch_bounds__(kBlock) void k_gemm_a(const LayerArgs a) {
       return;
     }
     const ProjSlot W = proj_slot(a.L.w13, slot);
-    gemm_a_body<FMT>(a, W, I, (item % ntn) * 64, t.m0, t.cnt, a.lists + (size_t)e * a.T, 0, sA, sB);
+    if constexpr (RING)
+      ring_a<FMT>(a, W, I, (item % ntn) * 64, t.m0, t.cnt, a.lists + (size_t)e * a.T, 0, (char*)sA);
+    else
+      gemm_a_body<FMT>(a, W, I, (item % ntn) * 64, t.m0, t.cnt, a.lists + (size_t)e * a.T, 0, sA, sB);
   } else if (Is > 0) {
     const int sitem = item - routed_items, nts = Is / 64;
     const int m0 = (sitem / nts) * kGM;
     if (m0 >= a.T) return;
     const ProjSlot W = shared_view(a.L.shared_w13, 2 * Is, a.L.hidden);
-    gemm_a_body<FTM_FMT_BF16>(a, W, Is, (sitem % nts) * 64, m0, a.T, nullptr, a.L.topk, sA, sB);
+    if constexpr (RING)
+      ring_a<FTM_FMT_BF16>(a, W, Is, (sitem % nts) * 64, m0, a.T, nullptr, a.L.topk, (char*)sA);
+    else
+      gemm_a_body<FTM_FMT_BF16>(a, W, Is, (sitem % nts) * 64, m0, a.T, nullptr, a.L.topk, sA, sB);
   }
+}
+
+template <int FMT>
+__global__ __launch_bounds__(kBlock) void k_gemm_a(const LayerArgs a) {
+  __shared__ __attribute__((aligned(16))) uint16_t sA[2 * kGM * kGPitch];
+  __shared__ __attribute__((aligned(16))) uint16_t sB[2 * 128 * kGPitch];
+  gemm_a_item<FMT, false>(a, blockIdx.x, sA, sB);
+}
+
+extern __shared__ __attribute__((aligned(16))) uint16_t ftm_ring_lds[];
+
+// The ring tiles (dynamic LDS: ring + the layer's tile scales), items in
+// XCD-aware order.
+template <int FMT>
+__global__ __launch_bounds__(kBlock) void k_gemm_a_ring(const LayerArgs a) {
+  gemm_a_item<FMT, true>(a, xcd_item(blockIdx.x, gridDim.x), ftm_ring_lds, nullptr);
 }
 
 // ---------------------------------------------------------------- stage B (w2 -> slot buffer)
@@ -419,14 +764,11 @@ __device__ void gemm_b_body(const LayerArgs& a, const ProjSlot& W, int n0, int m
 }
 
 template <int FMT>
-__global__ __launch_bounds__(kBlock) void k_gemm_b(const LayerArgs a) {
-  __shared__ __attribute__((aligned(16))) uint16_t sA[2 * kGM * kGPitch];
-  __shared__ __attribute__((aligned(16))) uint16_t sB[2 * 64 * kGPitch];
+__device__ __forceinline__ void gemm_b_item(const LayerArgs& a, int item, uint16_t* sA, uint16_t* sB) {
   const int H = a.L.hidden, Is = a.L.shared_inter;
   const int nRouted = a.ctrl[kCtrlNRouted];
   const int ntn = H / 64;
   const int routed_items = gemm_routed_mtiles(a, nRouted) * ntn;
-  const int item = blockIdx.x;
   if (item < routed_items) {
     const GemmTile t = gemm_find_tile(a, item / ntn, nRouted, false);
     if (t.u < 0) return;
@@ -454,6 +796,13 @@ __global__ __launch_bounds__(kBlock) void k_gemm_b(const LayerArgs a) {
   }
 }
 
+template <int FMT>
+__global__ __launch_bounds__(kBlock) void k_gemm_b(const LayerArgs a) {
+  __shared__ __attribute__((aligned(16))) uint16_t sA[2 * kGM * kGPitch];
+  __shared__ __attribute__((aligned(16))) uint16_t sB[2 * 64 * kGPitch];
+  gemm_b_item<FMT>(a, blockIdx.x, sA, sB);
+}
+
 // ---------------------------------------------------------------- launch
 bool gemm_path_ok(const ftm_moe_layer& L, int T) {
   if (L.act_dtype != FTM_DT_BF16) return false;
@@ -470,6 +819,36 @@ bool gemm_path_ok(const ftm_moe_layer& L, int T) {
   return pairs >= (long)kGemmMinRows * maxU;
 }
 
+// Whether the ring tiles take this layer: FP8 / INT8 / bf16 weights whose
+// tile scales fit the LDS scale area (INT8: one fp32 per tile row and group).
+static bool ring_ok(const ftm_moe_layer& L) {
+  const int f = L.w13.fmt;
+  if (f == FTM_FMT_MXFP4) return false;
+  if (f == FTM_FMT_INT8_PACKED || f == FTM_FMT_FP8_BLOCK) {
+    const long g13 = (L.hidden + L.w13.group - 1) / L.w13.group;
+    if (f == FTM_FMT_INT8_PACKED && 128 * g13 * 4 > kRingScaleBytes) return false;
+    if (f == FTM_FMT_FP8_BLOCK && 2 * g13 > kBlock) return false;  // one scale per thread
+  }
+  return true;
+}
+
+// Dynamic LDS of the ring kernels for this layer: ring + tile scales.
+static size_t ring_lds_a(const ftm_moe_layer& L) {
+  const int f = L.w13.fmt, g = (L.hidden + L.w13.group - 1) / (L.w13.group > 0 ? L.w13.group : 1);
+  const int rows = f == FTM_FMT_FP8_BLOCK ? 2 : f == FTM_FMT_INT8_PACKED ? 128 : 0;
+  return (size_t)kRingA + (size_t)rows * g * 4;
+}
+template <int FMT>
+static void ring_lds_attr() {
+  static bool done = false;  // once per instantiation (setting it twice is harmless)
+  if (!done) {
+    // a failure here surfaces as the launch error that follows
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&k_gemm_a_ring<FMT>),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, kRingA + kRingScaleBytes);
+    done = true;
+  }
+}
+
 template <int FMT>
 static void launch_gemm_t(const LayerArgs& a, hipStream_t st, int which) {
   const ftm_moe_layer& L = a.L;
@@ -477,14 +856,24 @@ static void launch_gemm_t(const LayerArgs& a, hipStream_t st, int which) {
   const long maxU = L.num_experts < pairs ? L.num_experts : pairs;
   const long mt_routed = pairs / kGM + maxU + 1;
   const long mt_shared = L.shared_inter > 0 ? (a.T + kGM - 1) / kGM : 0;
+  const long items_a = mt_routed * (L.inter / 64) + mt_shared * (L.shared_inter > 0 ? L.shared_inter / 64 : 0);
+  const long items_b = (mt_routed + mt_shared) * (L.hidden / 64);
+  // Stage A on the ring tiles where they apply (measured on MI355X, C3 FP8:
+  // w13 285 us against 343 at T=2048, 179 against 239 at T=512; C1 INT8 T=1024:
+  // 29 against 42).  Stage B keeps the register-staged tiles: with K = I its
+  // tiles are 8 K steps long and 4 workgroups per CU beat the deeper ring
+  // (C3 T=2048 w2 259 us against 377).
+  bool ring = false;
+  if constexpr (FMT != FTM_FMT_MXFP4) ring = ring_ok(L);
   if (which & 1) {
-    const long items = mt_routed * (L.inter / 64) + mt_shared * (L.shared_inter > 0 ? L.shared_inter / 64 : 0);
-    hipLaunchKernelGGL((k_gemm_a<FMT>), dim3((unsigned)items), dim3(kBlock), 0, st, a);
+    if (ring) {
+      ring_lds_attr<FMT>();
+      hipLaunchKernelGGL((k_gemm_a_ring<FMT>), dim3((unsigned)items_a), dim3(kBlock), ring_lds_a(L), st, a);
+    } else {
+      hipLaunchKernelGGL((k_gemm_a<FMT>), dim3((unsigned)items_a), dim3(kBlock), 0, st, a);
+    }
   }
-  if (which & 2) {
-    const long items = (mt_routed + mt_shared) * (L.hidden / 64);
-    hipLaunchKernelGGL((k_gemm_b<FMT>), dim3((unsigned)items), dim3(kBlock), 0, st, a);
-  }
+  if (which & 2) hipLaunchKernelGGL((k_gemm_b<FMT>), dim3((unsigned)items_b), dim3(kBlock), 0, st, a);
 }
 
 void launch_gemm_stages(const ftm_moe_layer& L, const void* x, int T, void* out, char* ws, const WsLayout& wl,
