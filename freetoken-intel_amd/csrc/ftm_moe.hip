@@ -101,6 +101,122 @@ __global__ __launch_bounds__(kBlock) void k_router(const LayerArgs a, int row_be
   }
 }
 
+// Large T: one WG per (8 expert rows, 16 tokens), so x is read once per 8
+// rows instead of once per row.  Every (token, row) logit keeps k_router's
+// arithmetic exactly: lane l accumulates chunks c = l, l + 64, ... (8
+// elements each, in order) with one fma chain, and the wave sums the 64
+// partials with the same xor-32..1 butterfly (wave_sum).
+constexpr int kRouterRB = 8;   // expert rows per WG
+constexpr int kRouterMinT = 64;  // from here on k_router_rows (x re-reads dominate k_router)
+
+// One level of the transposing butterfly: lanes with bit M set keep values
+// [N, 2N), the others [0, N); each adds the partner's copy of what it keeps.
+template <int M, int N>
+__device__ __forceinline__ void router_halve(float (&v)[32], int lane) {
+  const bool up = (lane & M) != 0;
+#pragma unroll
+  for (int q = 0; q < N; ++q) {
+    const float mine = up ? v[q + N] : v[q];
+    const float give = up ? v[q] : v[q + N];
+    v[q] = mine + __shfl_xor(give, M);
+  }
+}
+
+__global__ __launch_bounds__(kBlock) void k_router_rows(const LayerArgs a, int row_begin, int row_end) {
+  const int E = a.L.num_experts, H = a.L.hidden, T = a.T;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int r0 = row_begin + blockIdx.x * kRouterRB;
+  const int t0 = blockIdx.y * 4 * kRouterTPW + wave * kRouterTPW;
+  Rsrc gres[kRouterRB];
+#pragma unroll
+  for (int j = 0; j < kRouterRB; ++j) {
+    const int r = r0 + j;
+    const void* grow = r < E ? (const void*)((const uint16_t*)a.L.gate_w + (size_t)r * H) : a.L.shared_gate;
+    gres[j] = make_rsrc(grow, r < row_end ? (uint32_t)H * 2u : 0u);
+  }
+  const Rsrc xres = make_rsrc(a.x, (uint32_t)T * (uint32_t)H * 2u);
+  const int nq = (H / 8 + 63) / 64;
+  float acc[kRouterTPW][kRouterRB];
+#pragma unroll
+  for (int i = 0; i < kRouterTPW; ++i)
+#pragma unroll
+    for (int j = 0; j < kRouterRB; ++j) acc[i][j] = 0.0f;
+  // chunk q in gc/xc while chunk q + 1 loads into gn/xn
+  u32x4 gc[kRouterRB], xc[kRouterTPW], gn[kRouterRB], xn[kRouterTPW];
+  auto load = [&](int q, u32x4 (&g)[kRouterRB], u32x4 (&x)[kRouterTPW]) {
+    const int c = lane + 64 * q;
+    const bool ok = q < nq && 8 * c < H;
+#pragma unroll
+    for (int j = 0; j < kRouterRB; ++j) g[j] = bload16(gres[j], ok ? 16u * (uint32_t)c : kOOB);
+#pragma unroll
+    for (int i = 0; i < kRouterTPW; ++i) {
+      const int t = t0 + i;
+      x[i] = bload16(xres, (ok && t < T) ? ((uint32_t)t * (uint32_t)H + 8u * (uint32_t)c) * 2u : kOOB);
+    }
+  };
+  load(0, gc, xc);
+  for (int q = 0; q < nq; ++q) {
+    load(q + 1, gn, xn);
+    const bool ok = 8 * (lane + 64 * q) < H;
+    float xf[kRouterTPW][8];
+#pragma unroll
+    for (int i = 0; i < kRouterTPW; ++i) {
+      const uint32_t w4[4] = {xc[i].x, xc[i].y, xc[i].z, xc[i].w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        xf[i][2 * e] = bf16_to_f32(w4[e] & 0xffffu);
+        xf[i][2 * e + 1] = bf16_to_f32(w4[e] >> 16);
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < kRouterRB; ++j) {
+      const uint32_t w4[4] = {gc[j].x, gc[j].y, gc[j].z, gc[j].w};
+      float gf[8];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        gf[2 * e] = bf16_to_f32(w4[e] & 0xffffu);
+        gf[2 * e + 1] = bf16_to_f32(w4[e] >> 16);
+      }
+#pragma unroll
+      for (int i = 0; i < kRouterTPW; ++i) {
+        float t8 = acc[i][j];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) t8 = __builtin_fmaf(xf[i][e], gf[e], t8);
+        acc[i][j] = ok ? t8 : acc[i][j];
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < kRouterRB; ++j) gc[j] = gn[j];
+#pragma unroll
+    for (int i = 0; i < kRouterTPW; ++i) xc[i] = xn[i];
+  }
+  // 32 butterfly sums at once: at xor level m a lane keeps the half of its
+  // values whose index bit matches its lane bit and adds the partner's copy
+  // (sent by the partner), so every value sees the pairs of wave_sum (xor 32,
+  // 16, 8, 4, 2, then 1) and the same bits, in 16+8+4+2+1+1 shuffles.
+  static_assert(kRouterTPW * kRouterRB == 32, "one value per lane pair after 5 halvings");
+  float v[32];
+#pragma unroll
+  for (int i = 0; i < kRouterTPW; ++i)
+#pragma unroll
+    for (int j = 0; j < kRouterRB; ++j) v[i * kRouterRB + j] = acc[i][j];
+  router_halve<32, 16>(v, lane);
+  router_halve<16, 8>(v, lane);
+  router_halve<8, 4>(v, lane);
+  router_halve<4, 2>(v, lane);
+  router_halve<2, 1>(v, lane);
+  const float tot = v[0] + __shfl_xor(v[0], 1);
+  // lane bits 5..1 name the value this lane holds: index = bit5*16 + bit4*8 + ... + bit1
+  const int idx = ((lane >> 5) & 1) * 16 + ((lane >> 4) & 1) * 8 + ((lane >> 3) & 1) * 4 + ((lane >> 2) & 1) * 2 +
+                  ((lane >> 1) & 1);
+  const int t = t0 + idx / kRouterRB, r = r0 + idx % kRouterRB;
+  if ((lane & 1) == 0 && t < T && r < row_end) {
+    float z = tot;
+    if (r < E && a.L.gate_b != nullptr) z = tot + bf16_to_f32(((const uint16_t*)a.L.gate_b)[r]);
+    a.logits[(size_t)t * (E + 1) + r] = round_to(z, a.L.act_dtype);
+  }
+}
+
 // ============================================================== top-k + grouping
 
 // Selection keys: (key desc, expert id asc) packed into one u64 that orders
@@ -1423,7 +1539,11 @@ hipError_t launch_router(const ftm_moe_layer& L, const void* x, int T, int row_b
   const LayerArgs a = make_args(L, x, nullptr, T, ws, wl);
   if (row_end - row_begin <= 0 || T <= 0) return hipSuccess;
   const int tpb = 4 * kRouterTPW;
-  hipLaunchKernelGGL(k_router, dim3(row_end - row_begin, (T + tpb - 1) / tpb), dim3(kBlock), 0, st, a, row_begin);
+  if (T >= kRouterMinT)
+    hipLaunchKernelGGL(k_router_rows, dim3((row_end - row_begin + kRouterRB - 1) / kRouterRB, (T + tpb - 1) / tpb),
+                       dim3(kBlock), 0, st, a, row_begin, row_end);
+  else
+    hipLaunchKernelGGL(k_router, dim3(row_end - row_begin, (T + tpb - 1) / tpb), dim3(kBlock), 0, st, a, row_begin);
   return hipGetLastError();
 }
 
@@ -1655,7 +1775,7 @@ static const char* expert_kernel_name_dt(const ftm_moe_layer& L, int T, int stag
 
 const char* stage_kernel_name(const ftm_moe_layer& L, int T, int stage) {
   switch (stage) {
-    case FTM_STAGE_ROUTER: return "k_router";
+    case FTM_STAGE_ROUTER: return T >= kRouterMinT ? "k_router_rows" : "k_router";
     case FTM_STAGE_TOPK: return T <= kTopk1MaxT ? "k_topk1" : "k_topk";
     case FTM_STAGE_COMBINE: return "k_combine";
     case FTM_STAGE_W13:

@@ -135,6 +135,7 @@ def test_stage_kernel_names_follow_the_dispatch():
     assert name(c3, 8, nat.STAGE_TOPK) == "k_topk1"
     assert name(c3, 9, nat.STAGE_TOPK) == "k_topk"
     assert name(c3, 16, nat.STAGE_ROUTER) == "k_router"
+    assert name(c3, 64, nat.STAGE_ROUTER) == "k_router_rows"
     assert name(c3, 16, nat.STAGE_COMBINE) == "k_combine"
     assert name(c3, 16, 5) is None
     assert name(c3, 0, nat.STAGE_W13) is None

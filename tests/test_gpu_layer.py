@@ -41,13 +41,15 @@ def test_small_layer_matches_oracle(gpu, name, T):
     _run_and_check(syn, gpu)
 
 
-@pytest.mark.parametrize("name", ["c2_gptq", "c3_fp8", "c4_mxfp4"])
-def test_small_layer_routed_matches_oracle(gpu, name):
-    syn = S.generate(S.SMALL[name], T=9, seed=5)
+@pytest.mark.parametrize("name,T", [("c2_gptq", 9), ("c3_fp8", 9), ("c4_mxfp4", 9), ("c3_fp8", 80)])
+def test_small_layer_routed_matches_oracle(gpu, name, T):
+    """Caller-supplied routing; at T=80 the shared-gate logit comes from the
+    row-blocked router over the single shared row."""
+    syn = S.generate(S.SMALL[name], T=T, seed=5)
     spec = oracle_spec(syn)
     rng = np.random.RandomState(0)
-    ids = np.stack([rng.choice(syn.cfg.E, syn.cfg.k, replace=False) for _ in range(9)]).astype(np.int32)
-    w = O.round_bf16(rng.rand(9, syn.cfg.k).astype(np.float32))
+    ids = np.stack([rng.choice(syn.cfg.E, syn.cfg.k, replace=False) for _ in range(T)]).astype(np.int32)
+    w = O.round_bf16(rng.rand(T, syn.cfg.k).astype(np.float32))
     ref = O.layer_reference(spec, np_(syn.x), ids=ids, w=w)
     dsyn = syn.to(gpu)
     layer = S.build_layer(dsyn)
