@@ -134,6 +134,8 @@ def test_stage_kernel_names_follow_the_dispatch():
     assert name(c3, 512, nat.STAGE_W2) == "k_gemm_b"
     assert name(c3, 8, nat.STAGE_TOPK) == "k_topk1"
     assert name(c3, 9, nat.STAGE_TOPK) == "k_topk"
+    assert name(c3, 255, nat.STAGE_TOPK) == "k_topk"
+    assert name(c3, 256, nat.STAGE_TOPK) == "k_topk_blk"
     assert name(c3, 16, nat.STAGE_ROUTER) == "k_router"
     assert name(c3, 64, nat.STAGE_ROUTER) == "k_router_rows"
     assert name(c3, 16, nat.STAGE_COMBINE) == "k_combine"

@@ -254,7 +254,8 @@ def test_non_resident_expert_contributes_zero_and_flags(gpu, T):
     assert_close(to_f32(out), ref["out"], what="layer output without the missing expert")
 
 
-@pytest.mark.parametrize("name,T", [("c3_fp8", 2), ("c3_fp8", 9), ("c1_int8", 5), ("c2_gptq", 7), ("c3_full", 16)])
+@pytest.mark.parametrize("name,T", [("c3_fp8", 2), ("c3_fp8", 9), ("c1_int8", 5), ("c2_gptq", 7), ("c3_full", 16),
+                                    ("c3_fp8", 300)])
 def test_negative_expert_ids_are_skipped(gpu, name, T):
     """Caller-supplied routing with id -1 for some pairs: those pairs contribute
     nothing (the combine skips their slots), no error bit is set, and the rest
@@ -280,3 +281,24 @@ def test_negative_expert_ids_are_skipped(gpu, name, T):
     torch.cuda.synchronize()
     assert int(ws[12:16].view(torch.int32).item()) == 0, "no error bit for skipped pairs"
     assert_close(to_f32(out), ref["out"], what=f"{name} layer with skipped pairs")
+
+
+@pytest.mark.parametrize("T", [9, 300])
+def test_repeated_expert_in_a_token_counts_twice(gpu, T):
+    """Caller-supplied routing that lists one expert twice for a token applies it
+    twice with both weights (the reference's per-expert loop,
+    python/freetoken/kernel/triton/fused_moe.py:129-161, selects pairs by
+    topk_ids == e).  T=9 takes the one-workgroup-per-4-tokens top-k, T=300
+    the one-token-per-wave one."""
+    syn = S.generate(S.SMALL["c3_fp8"], T=T, seed=90 + T)
+    spec = oracle_spec(syn)
+    rng = np.random.RandomState(T)
+    ids = np.stack([rng.choice(syn.cfg.E, syn.cfg.k, replace=False) for _ in range(T)]).astype(np.int32)
+    ids[1, 1] = ids[1, 0]
+    ids[T - 1, 3] = ids[T - 1, 2]
+    w = O.round_bf16(rng.rand(T, syn.cfg.k).astype(np.float32))
+    ref = O.layer_reference(spec, np_(syn.x), ids=ids, w=w)
+    dsyn = syn.to(gpu)
+    layer = S.build_layer(dsyn)
+    out = layer.forward_routed(dsyn.x, torch.from_numpy(ids).to(gpu), torch.from_numpy(w).to(gpu))
+    assert_close(to_f32(out), ref["out"], what="layer with a repeated expert")
