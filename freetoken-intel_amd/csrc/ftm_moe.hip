@@ -405,6 +405,20 @@ __device__ __forceinline__ void route_token(const LayerArgs& a, int t, const voi
   route_token_pre<MODE, NV>(a, t, logits_in, logits_dt, ids_in, w_in, logits_out, sel_e, sel_w, false, none);
 }
 
+// Zero the slot rows of token t's pairs that have no expert (caller routing
+// with id < 0: no stage writes them, and k_combine sums every slot).  Called
+// by the whole wave; skip: this lane's pair (lane < k) has no expert.
+__device__ __forceinline__ void zero_skipped_slots(const LayerArgs& a, int t, bool skip) {
+  uint64_t m = __ballot(skip);
+  const int H4 = a.L.hidden / 4, lane = threadIdx.x & 63;
+  while (m) {
+    const int j = __builtin_ctzll(m);
+    m &= m - 1;
+    f32x4* row = (f32x4*)(a.ybuf + (size_t)(t * a.KP + j) * a.L.hidden);
+    for (int i = lane; i < H4; i += 64) row[i] = (f32x4){0.f, 0.f, 0.f, 0.f};
+  }
+}
+
 // Record token t's selection: weights, ids, and one list entry per pair in
 // the expert's list (cnt: per-expert counters, in LDS or global memory).
 __device__ __forceinline__ void emit_token(const LayerArgs& a, int t, int sel_e, float sel_w, int32_t* ids_out,
@@ -427,11 +441,12 @@ __device__ __forceinline__ void emit_token(const LayerArgs& a, int t, int sel_e,
       }
     } else {
       // caller-supplied id < 0: the pair has no expert in this call (it is in
-      // no list and the combine skips its slot); >= E: an error
+      // no list and its slot is zeroed below); >= E: an error
       a.ids[(size_t)t * k + lane] = -1;
       if (sel_e >= E) atomicOr(&a.ctrl[kCtrlError], 2);
     }
   }
+  zero_skipped_slots(a, t, lane < k && !(sel_e >= 0 && sel_e < E));
   if (lane == 0 && a.L.shared_inter > 0) {
     const float sl = a.logits[(size_t)t * (E + 1) + E];
     a.wts[t * KP + k] = round_to(1.0f / (1.0f + expf(-sl)), a.L.act_dtype);
@@ -616,6 +631,7 @@ __global__ __launch_bounds__(64 * kTopkBlkWaves) void k_topk_blk(const LayerArgs
       }
       s_slot[li * k + lane] = slot;
     }
+    zero_skipped_slots(a, t, lane < k && !(sel_e >= 0 && sel_e < E));
     if (lane == 0 && a.L.shared_inter > 0) {
       const float sl = a.logits[(size_t)t * (E + 1) + E];
       a.wts[t * KP + k] = round_to(1.0f / (1.0f + expf(-sl)), a.L.act_dtype);
@@ -1568,15 +1584,9 @@ __global__ __launch_bounds__(kBlock) void k_combine(const LayerArgs a) {
   if (idx >= a.T * H4) return;
   const int t = idx / H4, n4 = idx % H4;
   const f32x4* yb = (const f32x4*)(a.ybuf + (size_t)t * KP * H) + n4;
-  const int32_t* ids = a.ids + (size_t)t * a.L.topk;
-  // slots in order; a routed slot without an expert (id < 0) holds nothing and
-  // is selected away (slot and id loads issue together, no branch between)
-  f32x4 s = (f32x4){0.f, 0.f, 0.f, 0.f};
-  for (int j = 0; j < KP; ++j) {
-    const f32x4 y = yb[(size_t)j * H4];
-    const bool ok = j >= a.L.topk || ids[j] >= 0;
-    s += ok ? y : (f32x4){0.f, 0.f, 0.f, 0.f};
-  }
+  // slots in order (a pair without an expert has a zeroed slot)
+  f32x4 s = yb[0];
+  for (int j = 1; j < KP; ++j) s += yb[(size_t)j * H4];
   if constexpr (AT == FTM_DT_F32) {
     ((f32x4*)a.out)[(size_t)t * H4 + n4] = s;
   } else {
