@@ -27,6 +27,7 @@ sys.path.insert(0, os.path.join(ROOT, "freetoken-intel_amd"))
 
 METRIC = "MoE-layer decode tokens/s + achieved HBM GB/s (% of 8 TB/s), bs 1-64"
 HBM_PEAK_GBS = 8000.0
+MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16
 
 
 def _parse():
@@ -44,6 +45,10 @@ def _parse():
                     help="run the C5 offload decode benchmark instead (64 HBM slots, 256 pinned host banks)")
     ap.add_argument("--offload-steps", type=int, default=200)
     ap.add_argument("--offload-slots", type=int, default=64)
+    ap.add_argument("--prefill-t", type=int, default=2048,
+                    help="prefill chunk measured after the decode points (tiled MFMA stages; 0 = skip)")
+    ap.add_argument("--prefill-only", action="store_true",
+                    help="measure only the prefill chunk and print its JSON (for counter runs)")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="after the bench, copy a buffer of this many MiB 3 times (a plain copy kernel of known "
                          "size, the reference point for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE)")
@@ -98,6 +103,9 @@ def main() -> int:
         syns.append(syn)
         layers.append(S.build_layer(syn))
     torch.cuda.synchronize()
+    if args.prefill_only:
+        print(json.dumps(_prefill_point(cfg, layers, max(1, args.prefill_t), max(4, min(args.steps, 20)))), flush=True)
+        return 0
     gx = torch.Generator(device=dev).manual_seed(1234)
     max_t = max([T] + [int(b) for b in args.sweep.split(",") if b])
     x_pool = [torch.randn(max_t, cfg.H, generator=gx, device=dev).to(torch.bfloat16) for _ in range(NX)]
@@ -235,6 +243,8 @@ def main() -> int:
         torch.cuda.synchronize()
         del src, dst
 
+    prefill = _prefill_point(cfg, layers, args.prefill_t, 20) if args.prefill_t > 0 else None
+
     cpu = None
     if not args.no_cpu_baseline:
         cpu = _cpu_baseline(cfg, syns[0], layers[0], xs[0], T, args.cpu_seconds)
@@ -266,11 +276,72 @@ def main() -> int:
         "unique_experts": round(U, 2),
         "bytes_per_step": int(b_alg),
         "roofline": roofline,
+        "prefill": prefill,
         "cpu_baseline": cpu,
         "sweep": sweep,
     }
     print(json.dumps(line), flush=True)
     return 0
+
+
+def _prefill_point(cfg, layers, T: int, steps: int) -> dict:
+    """One prefill chunk of T tokens through the rotated layers: layer time
+    (events around back-to-back forwards), per-stage times (each stage of the
+    rotation launched as a group, as for decode) and the expert GEMM stages'
+    rate against the dense bf16 MFMA peak (the tiles run bf16 MFMAs on weights
+    decoded exactly from their quantized form).  FLOPs count real rows only:
+    2 * pairs * (2I * H + H * I) routed + the same over T rows for the shared
+    expert; padding rows of partly filled tiles are not counted."""
+    import numpy as np
+    import torch
+
+    from ftmoe import _native as nat
+
+    dev = torch.device("cuda:0")
+    NL = len(layers)
+    g = torch.Generator(device=dev).manual_seed(4321)
+    xs = [torch.randn(T, cfg.H, generator=g, device=dev).to(torch.bfloat16) for _ in range(NL)]
+    for i in range(2 * NL):
+        layers[i % NL].forward(xs[i % NL])
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for i in range(steps):
+        layers[i % NL].forward(xs[i % NL])
+    e1.record()
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1e3 / steps
+    out = torch.empty(T, cfg.H, dtype=torch.bfloat16, device=dev)
+    stages = (nat.STAGE_ROUTER, nat.STAGE_TOPK, nat.STAGE_W13, nat.STAGE_W2, nat.STAGE_COMBINE)
+    wss = [torch.zeros(layers[l].workspace_bytes(T), dtype=torch.uint8, device=dev) for l in range(NL)]
+    for st in stages:
+        for l in range(NL):
+            layers[l].forward_stage(xs[l], out, st, ws=wss[l])
+    torch.cuda.synchronize()
+    reps = max(1, steps // NL)
+    evs = []
+    for _ in range(reps):
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(len(stages) + 1)]
+        for kq, st in enumerate(stages):
+            ev[kq].record()
+            for l in range(NL):
+                layers[l].forward_stage(xs[l], out, st, ws=wss[l])
+        ev[-1].record()
+        evs.append(ev)
+    torch.cuda.synchronize()
+    names = ("router", "topk", "w13", "w2", "combine")
+    kern = {n: float(np.mean([ev[kq].elapsed_time(ev[kq + 1]) for ev in evs])) * 1e3 / NL for kq, n in enumerate(names)}
+    pairs = T * cfg.k
+    f13 = 2.0 * pairs * 2 * cfg.I * cfg.H + (2.0 * T * 2 * cfg.shared_inter * cfg.H if cfg.shared_inter else 0.0)
+    f2 = 2.0 * pairs * cfg.H * cfg.I + (2.0 * T * cfg.H * cfg.shared_inter if cfg.shared_inter else 0.0)
+    tf = (f13 + f2) / ((kern["w13"] + kern["w2"]) * 1e-6) / 1e12
+    return {"T": T, "us_per_layer": round(us, 1), "tokens_per_s": round(T / (us * 1e-6), 1),
+            "kernels_us": {n: round(v, 1) for n, v in kern.items()},
+            "kernels": {n: layers[0].stage_kernel(T, st) for n, st in zip(names, stages)},
+            "gemm_gflop": round((f13 + f2) / 1e9, 1), "gemm_tflops": round(tf, 1),
+            "mfma_frac": round(tf / MFMA_BF16_PEAK_TFLOPS, 4), "mfma_peak_tflops": MFMA_BF16_PEAK_TFLOPS,
+            "w13_tflops": round(f13 / (kern["w13"] * 1e-6) / 1e12, 1),
+            "w2_tflops": round(f2 / (kern["w2"] * 1e-6) / 1e12, 1)}
 
 
 def _zipf_routing(rng, steps: int, T: int, E: int, k: int, s_exp: float = 1.1):

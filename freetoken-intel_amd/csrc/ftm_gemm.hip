@@ -838,6 +838,8 @@ static size_t ring_lds_a(const ftm_moe_layer& L) {
   const int rows = f == FTM_FMT_FP8_BLOCK ? 2 : f == FTM_FMT_INT8_PACKED ? 128 : 0;
   return (size_t)kRingA + (size_t)rows * g * 4;
 }
+const char* gemm_a_kernel_name(const ftm_moe_layer& L) { return ring_ok(L) ? "k_gemm_a_ring" : "k_gemm_a"; }
+
 template <int FMT>
 static void ring_lds_attr() {
   static bool done = false;  // once per instantiation (setting it twice is harmless)

@@ -74,6 +74,7 @@ hipError_t launch_experts(const ftm_moe_layer& L, const void* x, int T, void* ou
 // Prefill side of the crossover (ftm_gemm.hip): whether the tiled GEMM stages
 // take this layer at T tokens, and their launch (which: bit 0 = w13, bit 1 = w2).
 bool gemm_path_ok(const ftm_moe_layer& L, int T);
+const char* gemm_a_kernel_name(const ftm_moe_layer& L);  // the stage A tile kernel the layer takes
 void launch_gemm_stages(const ftm_moe_layer& L, const void* x, int T, void* out, char* ws, const WsLayout& wl,
                         hipStream_t st, int which);
 hipError_t launch_linear(const ftm_proj& P, int slot, const void* x, int x_dt, int M, void* out,

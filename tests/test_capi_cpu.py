@@ -130,7 +130,7 @@ def test_stage_kernel_names_follow_the_dispatch():
         assert name(c3, T, nat.STAGE_W13) == "k_stage_a_lean", T
         assert name(c3, T, nat.STAGE_W2) == "k_stage_b_lean", T
     # 512 tokens x top-8 = 16 pairs per expert on all 256 experts: GEMM stages
-    assert name(c3, 512, nat.STAGE_W13) == "k_gemm_a"
+    assert name(c3, 512, nat.STAGE_W13) == "k_gemm_a_ring"
     assert name(c3, 512, nat.STAGE_W2) == "k_gemm_b"
     assert name(c3, 8, nat.STAGE_TOPK) == "k_topk1"
     assert name(c3, 9, nat.STAGE_TOPK) == "k_topk"
@@ -146,6 +146,6 @@ def test_stage_kernel_names_follow_the_dispatch():
     assert name(small, 4, nat.STAGE_W2) == "k_stage_b_xl"
     assert name(small, 5, nat.STAGE_W13) == "k_stage_a_rows"
     assert name(small, 5, nat.STAGE_W2) == "k_stage_b"
-    assert name(small, 64, nat.STAGE_W13) == "k_gemm_a"
+    assert name(small, 64, nat.STAGE_W13) == "k_gemm_a_ring"
     f32 = _layer(E=8, H=256, I=128, k=2, act_dtype=nat.DT_F32)
     assert name(f32, 4, nat.STAGE_W13) is None  # f32 activations need the bf16 router: invalid layer
