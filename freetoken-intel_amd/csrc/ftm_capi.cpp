@@ -183,7 +183,14 @@ int ftm_moe_forward(const ftm_moe_layer* layer, const void* x, int32_t num_token
   hipStream_t st = (hipStream_t)stream;
   char* ws = (char*)workspace;
   const int rows = layer->num_experts + (layer->shared_inter > 0 ? 1 : 0);
+  // small decode batches on the lean kernels route inside stage A (no top-k launch)
+  const bool fused = fast_layer(layer, x) && lean_route_ok(*layer, num_tokens);
   hipError_t e = launch_router(*layer, x, num_tokens, 0, rows, ws, wl, st);
+  if (fused) {
+    const RouteOut ro = {topk_ids, topk_w, logits};
+    if (e == hipSuccess) e = launch_experts(*layer, x, num_tokens, out, ws, wl, st, 7, &ro);
+    return hip_rc(e);
+  }
   if (e == hipSuccess)
     e = launch_topk(*layer, num_tokens, nullptr, 0, nullptr, nullptr, topk_ids, topk_w, logits, ws, wl, st);
   if (e == hipSuccess) e = run_experts(*layer, x, num_tokens, out, ws, wl, st);
@@ -206,13 +213,16 @@ int ftm_moe_forward_stage(const ftm_moe_layer* layer, const void* x, int32_t num
   hipStream_t st = (hipStream_t)stream;
   char* ws = (char*)workspace;
   hipError_t e = hipSuccess;
+  const bool fused = lean_route_ok(*layer, num_tokens);  // routing runs in stage A
+  const RouteOut ro = {nullptr, nullptr, nullptr};
   if (stage == FTM_STAGE_ROUTER)
     e = launch_router(*layer, x, num_tokens, 0, layer->num_experts + (layer->shared_inter > 0 ? 1 : 0), ws, wl, st);
   else if (stage == FTM_STAGE_TOPK)
-    e = launch_topk(*layer, num_tokens, nullptr, 0, nullptr, nullptr, nullptr, nullptr, nullptr, ws, wl, st);
+    e = fused ? hipSuccess
+              : launch_topk(*layer, num_tokens, nullptr, 0, nullptr, nullptr, nullptr, nullptr, nullptr, ws, wl, st);
   else
     e = launch_experts(*layer, x, num_tokens, out, ws, wl, st,
-                       stage == FTM_STAGE_W13 ? 1 : stage == FTM_STAGE_W2 ? 2 : 4);
+                       stage == FTM_STAGE_W13 ? 1 : stage == FTM_STAGE_W2 ? 2 : 4, fused ? &ro : nullptr);
   return hip_rc(e);
 }
 

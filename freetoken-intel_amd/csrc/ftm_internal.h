@@ -24,6 +24,16 @@ constexpr int kRecPairs = 4;
 // Measured on MI355X (C3 layer, w13 + w2 us): T=1 15.9 vs 16.7, T=4 30.7 vs
 // 34.5, T=8 54.5 vs 54.5, T=16 92.4 vs 88.1.
 constexpr int kXlMaxT = 4;
+// Decode batches up to kLeanRouteMaxT tokens (top-k up to kLeanRouteMaxK) route
+// inside the lean stage A, which takes the top-k launch out of the layer's
+// chain of dependent launches.  Every stage-A workgroup then spends ~3 us
+// routing before its weight loads, which pays while the grid fits one round
+// of workgroups: measured on MI355X (C3), T = 1: 27.0 us per layer against
+// 29.6 with the top-k launch; T = 4: 47.8 against 42.7 (2,112 workgroups).
+// A record holds every pair of such an expert.
+constexpr int kLeanRouteMaxT = 2;
+constexpr int kLeanRouteMaxK = 16;
+static_assert(kLeanRouteMaxT <= kRecPairs, "records hold all pairs of a routed expert");
 constexpr int kCtrlArriveTopk = 0;  // arrivals of the top-k workgroups
 constexpr int kCtrlNRouted = 1;     // routed experts with >= 1 token (written per call)
 constexpr int kCtrlNU = 2;          // nRouted + shared expert
@@ -69,14 +79,44 @@ hipError_t launch_router(const ftm_moe_layer& L, const void* x, int T, int row_b
 hipError_t launch_topk(const ftm_moe_layer& L, int T, const void* logits_in, int logits_dt,
                        const int32_t* ids_in, const float* w_in, int32_t* ids_out, float* w_out,
                        float* logits_out, char* ws, const WsLayout& wl, hipStream_t st);
+// The caller's routing outputs of ftm_moe_forward (each may be null).
+struct RouteOut {
+  int32_t* ids;
+  float* w;
+  float* logits;
+};
+// ro: route inside the expert stages where lean_route_ok allows it (the caller
+// then launches no top-k); which: bit 0 = stage A, bit 1 = stage B, bit 2 = combine.
 hipError_t launch_experts(const ftm_moe_layer& L, const void* x, int T, void* out, char* ws,
-                          const WsLayout& wl, hipStream_t st, int which = 7);
+                          const WsLayout& wl, hipStream_t st, int which = 7, const RouteOut* ro = nullptr);
 // Prefill side of the crossover (ftm_gemm.hip): whether the tiled GEMM stages
 // take this layer at T tokens, and their launch (which: bit 0 = w13, bit 1 = w2).
 bool gemm_path_ok(const ftm_moe_layer& L, int T);
 const char* gemm_a_kernel_name(const ftm_moe_layer& L);  // the stage A tile kernel the layer takes
 void launch_gemm_stages(const ftm_moe_layer& L, const void* x, int T, void* out, char* ws, const WsLayout& wl,
                         hipStream_t st, int which);
+// The lean FP8 decode kernels (ftm_moe.hip) cover H = 2048 (a 512-element K
+// range per wave in stage A), I = 512 (one 8-load window per wave in stage
+// B), fp32 block-128 scales, no projection biases, bf16 activations and a
+// shared expert (if any) of the routed width, below the GEMM crossover.
+inline bool lean_ok(const ftm_moe_layer& L, int T) {
+  const ftm_proj &A = L.w13, &B = L.w2;
+  if (A.fmt != FTM_FMT_FP8_BLOCK || L.act_dtype != FTM_DT_BF16) return false;
+  if (A.group != 128 || B.group != 128 || A.s_dtype != FTM_DT_F32 || B.s_dtype != FTM_DT_F32) return false;
+  if (A.bias != nullptr || B.bias != nullptr) return false;
+  if (L.hidden != 2048 || L.inter != 512) return false;
+  if (L.shared_inter != 0 && L.shared_inter != L.inter) return false;
+  return !gemm_path_ok(L, T);
+}
+
+// Small decode batches on the lean kernels: stage A routes the T <=
+// kLeanRouteMaxT tokens in every workgroup (one wave per token) instead of
+// waiting for a top-k launch; E <= 256 (four candidates per lane) and k <=
+// kLeanRouteMaxK.
+inline bool lean_route_ok(const ftm_moe_layer& L, int T) {
+  return lean_ok(L, T) && T <= kLeanRouteMaxT && L.num_experts <= 256 && L.topk <= kLeanRouteMaxK;
+}
+
 hipError_t launch_linear(const ftm_proj& P, int slot, const void* x, int x_dt, int M, void* out,
                          int out_dt, const void* bias, int bias_dt, int final_dt, hipStream_t st);
 hipError_t launch_fill_routing(int T, int32_t slot, int32_t* slot_word, int32_t* ids, float* w, hipStream_t st);

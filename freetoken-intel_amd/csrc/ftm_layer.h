@@ -16,6 +16,10 @@ struct LayerArgs {
   void* out;
   int T, KP, Imax;
   bool lean;        // decode stages use the lean FP8 kernels (they read the work records)
+  bool route_a;     // lean stage A routes the tokens itself (no top-k launch, lean_route_ok)
+  int32_t* ids_out; // route_a: the caller's routing outputs (each may be null)
+  float* w_out;
+  float* logits_out;
   int32_t* ctrl;
   float* logits;    // [T, E+1]   (column E = shared-expert gate logit)
   float* wts;       // [T*KP]     router weight of pair p = t*KP + j (j == k: shared gate)
@@ -28,20 +32,6 @@ struct LayerArgs {
   float* ybuf;      // [T*KP, H]
 };
 
-// The lean FP8 decode kernels (ftm_moe.hip) cover H = 2048 (a 512-element K
-// range per wave in stage A), I = 512 (one 8-load window per wave in stage
-// B), fp32 block-128 scales, no projection biases, bf16 activations and a
-// shared expert (if any) of the routed width, below the GEMM crossover.
-inline bool lean_ok(const ftm_moe_layer& L, int T) {
-  const ftm_proj &A = L.w13, &B = L.w2;
-  if (A.fmt != FTM_FMT_FP8_BLOCK || L.act_dtype != FTM_DT_BF16) return false;
-  if (A.group != 128 || B.group != 128 || A.s_dtype != FTM_DT_F32 || B.s_dtype != FTM_DT_F32) return false;
-  if (A.bias != nullptr || B.bias != nullptr) return false;
-  if (L.hidden != 2048 || L.inter != 512) return false;
-  if (L.shared_inter != 0 && L.shared_inter != L.inter) return false;
-  return !gemm_path_ok(L, T);
-}
-
 inline LayerArgs make_args(const ftm_moe_layer& L, const void* x, void* out, int T, char* ws,
                            const WsLayout& wl) {
   LayerArgs a;
@@ -52,6 +42,10 @@ inline LayerArgs make_args(const ftm_moe_layer& L, const void* x, void* out, int
   a.KP = wl.KP;
   a.Imax = wl.Imax;
   a.lean = lean_ok(L, T);
+  a.route_a = false;
+  a.ids_out = nullptr;
+  a.w_out = nullptr;
+  a.logits_out = nullptr;
   a.ctrl = (int32_t*)ws;
   a.logits = (float*)(ws + wl.logits);
   a.wts = (float*)(ws + wl.wts);

@@ -1485,6 +1485,137 @@ __global__ __launch_bounds__(kBlock) void k_stage_a_lean(const LayerArgs a) {
   lean_a_item<true, KR, 1>(a, w, sc, I, (item % t8) * 8, rec.cnt, &rec, a.lists + (size_t)rec.e * a.T, 0, kp, red);
 }
 
+// ---- stage A that routes (T <= kLeanRouteMaxT): every workgroup routes the
+// call's tokens itself (route_token, one wave per token) and takes the
+// routed expert of rank u (ascending id) from an LDS expert mask; workgroup 0
+// of the routed items publishes ids, weights, records and the routed count for
+// stage B, the combine and the caller.  Replaces the top-k launch.
+
+// Rank u of the set bits of m[0..nwords) (-1 if u >= total) and the total.
+__device__ __forceinline__ int mask_rank(const uint32_t* m, int nwords, int u, int& total) {
+  int e = -1, run = 0;
+  for (int w = 0; w < nwords; ++w) {
+    uint32_t b = m[w];
+    const int c = __popc(b);
+    if (e < 0 && u < run + c) {
+      for (int q = 0; q < u - run; ++q) b &= b - 1;
+      e = 32 * w + __builtin_ctz(b);
+    }
+    run += c;
+  }
+  total = run;
+  return e;
+}
+
+// Record of expert e from the LDS selections sel[T * k]: every pair of it (T
+// <= kRecPairs), in token order (per lane: e may differ between lanes).
+__device__ __forceinline__ ExpertRec route_rec(const LayerArgs& a, const int* sel, int e) {
+  const int k = a.L.topk, n = a.T * k;
+  ExpertRec r;
+  r.e = e;
+  r.cnt = 0;
+#pragma unroll
+  for (int q = 0; q < kRecPairs; ++q) r.p[q] = -1;
+  for (int i = 0; i < n; ++i) {
+    if (sel[i] == e) {
+      const int p = (i / k) * a.KP + i % k;
+#pragma unroll
+      for (int q = 0; q < kRecPairs; ++q) r.p[q] = r.cnt == q ? p : r.p[q];
+      ++r.cnt;
+    }
+  }
+  r.slot = a.L.slot_of_expert ? a.L.slot_of_expert[e] : e;
+  return r;
+}
+
+// The same record when every lane asks for the same expert: scalar fields.
+__device__ __forceinline__ ExpertRec route_rec_uniform(const LayerArgs& a, const int* sel, int e) {
+  ExpertRec r = route_rec(a, sel, __builtin_amdgcn_readfirstlane(e));
+  r.e = __builtin_amdgcn_readfirstlane(r.e);
+  r.cnt = __builtin_amdgcn_readfirstlane(r.cnt);
+  r.slot = __builtin_amdgcn_readfirstlane(r.slot);
+#pragma unroll
+  for (int q = 0; q < kRecPairs; ++q) r.p[q] = __builtin_amdgcn_readfirstlane(r.p[q]);
+  return r;
+}
+
+template <int KR, int NWS, int MODE>
+__global__ __launch_bounds__(kBlock) void k_stage_a_lean_route(const LayerArgs a) {
+  __shared__ f32x4 red[4 * 16];
+  __shared__ int s_sel[kLeanRouteMaxT * kLeanRouteMaxK];
+  __shared__ float s_w[kLeanRouteMaxT * kLeanRouteMaxK];
+  __shared__ uint32_t s_mask[256 / 32];
+  const int kp = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  const int I = a.L.inter, t8 = I / 8, T = a.T, k = a.L.topk, E = a.L.num_experts, KP = a.KP;
+  const int nShared = a.L.shared_inter > 0 ? a.L.shared_inter / 8 : 0;
+  if ((int)blockIdx.x < nShared) {  // shared-expert items need no routing
+    lean_a_item<false, KR, NWS>(a, (const char*)a.L.shared_w13, nullptr, a.L.shared_inter, blockIdx.x * 8, T,
+                                nullptr, nullptr, k, kp, red);
+    return;
+  }
+  const int item = blockIdx.x - nShared;
+  const bool lead = item == 0;
+  if (threadIdx.x < 256 / 32) s_mask[threadIdx.x] = 0u;
+  __syncthreads();
+  if (kp < T) {
+    int sel_e;
+    float sel_w;
+    route_token<MODE, 4>(a, kp, nullptr, 0, nullptr, nullptr, lead ? a.logits_out : nullptr, sel_e, sel_w);
+    if (lane < k) {
+      s_sel[kp * k + lane] = sel_e;
+      s_w[kp * k + lane] = sel_w;
+      atomicOr(&s_mask[sel_e >> 5], 1u << (sel_e & 31));
+    }
+  }
+  __syncthreads();
+  const int nw = (E + 31) / 32;
+  int nRouted;
+  mask_rank(s_mask, nw, 0, nRouted);
+  nRouted = __builtin_amdgcn_readfirstlane(nRouted);
+  if (lead) {
+    for (int i = threadIdx.x; i < T * k; i += kBlock) {
+      const int p = (i / k) * KP + i % k;
+      a.wts[p] = s_w[i];
+      a.ids[i] = s_sel[i];
+      if (a.ids_out) a.ids_out[i] = s_sel[i];
+      if (a.w_out) a.w_out[i] = s_w[i];
+    }
+    if (a.L.shared_inter > 0) {
+      for (int t = threadIdx.x; t < T; t += kBlock) {
+        const float sl = a.logits[(size_t)t * (E + 1) + E];
+        a.wts[t * KP + k] = round_to(1.0f / (1.0f + expf(-sl)), a.L.act_dtype);
+      }
+    }
+    for (int u2 = threadIdx.x; u2 < nRouted; u2 += kBlock) {
+      int tot;
+      const ExpertRec r = route_rec(a, s_sel, mask_rank(s_mask, nw, u2, tot));
+      int32_t* dst = a.recs + (size_t)u2 * kRecWords;
+      dst[0] = r.e;
+      dst[1] = r.cnt;
+      dst[2] = r.slot;
+#pragma unroll
+      for (int q = 0; q < kRecPairs; ++q) dst[3 + q] = r.p[q];
+      dst[kRecWords - 1] = 0;
+    }
+    if (threadIdx.x == 0) {
+      a.ctrl[kCtrlNRouted] = nRouted;
+      a.ctrl[kCtrlNU] = nRouted + (a.L.shared_inter > 0 ? 1 : 0);
+    }
+  }
+  const int u = item / t8;
+  if (u >= nRouted) return;
+  int tot;
+  const ExpertRec rec = route_rec_uniform(a, s_sel, mask_rank(s_mask, nw, u, tot));
+  if (rec.slot < 0 || rec.slot >= a.L.w13.num_slots) {
+    if (threadIdx.x == 0) atomicOr(&a.ctrl[kCtrlError], 1);
+    return;
+  }
+  const char* w = (const char*)a.L.w13.w + (int64_t)rec.slot * a.L.w13.w_stride;
+  const float* sc = (const float*)((const char*)a.L.w13.s + (int64_t)rec.slot * a.L.w13.s_stride);
+  lean_a_item<true, KR, 1>(a, w, sc, I, (item % t8) * 8, rec.cnt, &rec, a.lists + (size_t)rec.e * T, 0, kp, red);
+}
+
 // Stage B item: 64 output columns of one expert, wave w owns 16 of them over
 // the full K (= I routed / Is shared); y = acc * router weight -> slot buffer.
 template <bool FP8, int KB, int NWIN>
@@ -1819,7 +1950,18 @@ static void launch_stages(const LayerArgs& a, int gridA, int gridB, hipStream_t 
     const size_t lds = 4u * (kLeanXT + 1) * (size_t)lean_pitch(512) * 2u;
     if (which & 1) {
       const int items = maxU * (a.L.inter / 8) + a.L.shared_inter / 8;
-      hipLaunchKernelGGL((k_stage_a_lean<512, 2>), dim3(items), dim3(kBlock), lds, st, a);
+      if (a.route_a) {
+        if (a.L.route_mode == FTM_ROUTE_SOFTMAX_TOPK)
+          hipLaunchKernelGGL((k_stage_a_lean_route<512, 2, FTM_ROUTE_SOFTMAX_TOPK>), dim3(items), dim3(kBlock), lds, st, a);
+        else if (a.L.route_mode == FTM_ROUTE_SOFTMAX_TOPK_LOWP)
+          hipLaunchKernelGGL((k_stage_a_lean_route<512, 2, FTM_ROUTE_SOFTMAX_TOPK_LOWP>), dim3(items), dim3(kBlock), lds,
+                             st, a);
+        else
+          hipLaunchKernelGGL((k_stage_a_lean_route<512, 2, FTM_ROUTE_TOPK_SOFTMAX>), dim3(items), dim3(kBlock), lds, st,
+                             a);
+      } else {
+        hipLaunchKernelGGL((k_stage_a_lean<512, 2>), dim3(items), dim3(kBlock), lds, st, a);
+      }
     }
     if (which & 2) {
       const int grid = (maxU + (a.L.shared_inter > 0 ? 1 : 0)) * (a.L.hidden / 64);
@@ -1878,14 +2020,20 @@ static void launch_stages_dt(const LayerArgs& a, int gridA, int gridB, hipStream
 }
 
 hipError_t launch_experts(const ftm_moe_layer& L, const void* x, int T, void* out, char* ws,
-                          const WsLayout& wl, hipStream_t st, int which) {
+                          const WsLayout& wl, hipStream_t st, int which, const RouteOut* ro) {
   if (gemm_path_ok(L, T)) {
     // above the token crossover the expert stages are tiled GEMMs
     if (which & 3) launch_gemm_stages(L, x, T, out, ws, wl, st, which & 3);
     which &= 4;
     if (which == 0) return hipGetLastError();
   }
-  const LayerArgs a = make_args(L, x, out, T, ws, wl);
+  LayerArgs a = make_args(L, x, out, T, ws, wl);
+  if (ro != nullptr && lean_route_ok(L, T)) {
+    a.route_a = true;
+    a.ids_out = ro->ids;
+    a.w_out = ro->w;
+    a.logits_out = ro->logits;
+  }
   const int maxU = L.num_experts < T * L.topk ? L.num_experts : T * L.topk;
   const int NT = L.w13.fmt == FTM_FMT_GPTQ_INT4 ? 64 : 16;
   const int has_sh = L.shared_inter > 0 ? 1 : 0;
@@ -1909,7 +2057,7 @@ template <int FMT, int AT>
 static const char* expert_kernel_name(const ftm_moe_layer& L, int T, int stage) {
   const bool lean = FMT == FTM_FMT_FP8_BLOCK && AT == FTM_DT_BF16 && lean_ok(L, T);
   if (stage == FTM_STAGE_W13) {
-    if (lean) return "k_stage_a_lean";
+    if (lean) return lean_route_ok(L, T) ? "k_stage_a_lean_route" : "k_stage_a_lean";
     if (FMT == FTM_FMT_GPTQ_INT4) return "k_stage_a";
     return xl_plan_a<FMT, AT>(L, T).ok ? "k_stage_a_xl" : "k_stage_a_rows";
   }
@@ -1927,7 +2075,9 @@ static const char* expert_kernel_name_dt(const ftm_moe_layer& L, int T, int stag
 const char* stage_kernel_name(const ftm_moe_layer& L, int T, int stage) {
   switch (stage) {
     case FTM_STAGE_ROUTER: return T >= kRouterMinT ? "k_router_rows" : "k_router";
-    case FTM_STAGE_TOPK: return T <= kTopk1MaxT ? "k_topk1" : T >= kTopkBlkMinT ? "k_topk_blk" : "k_topk";
+    case FTM_STAGE_TOPK:
+      if (lean_route_ok(L, T)) return "";  // routed inside stage A
+      return T <= kTopk1MaxT ? "k_topk1" : T >= kTopkBlkMinT ? "k_topk_blk" : "k_topk";
     case FTM_STAGE_COMBINE: return "k_combine";
     case FTM_STAGE_W13:
     case FTM_STAGE_W2: break;

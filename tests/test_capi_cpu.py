@@ -126,8 +126,12 @@ def test_stage_kernel_names_follow_the_dispatch():
 
     c3 = _layer(E=256, H=2048, I=512, k=8)
     c3.shared_inter, c3.shared_w13, c3.shared_w2, c3.shared_gate = 512, 0xA0000, 0xB0000, 0xC0000
-    for T in (1, 4, 16, 64, 256):
+    for T in (1, 2):  # small batches route inside stage A: the top-k stage launches nothing
+        assert name(c3, T, nat.STAGE_W13) == "k_stage_a_lean_route", T
+        assert name(c3, T, nat.STAGE_TOPK) == "", T
+    for T in (3, 4, 16, 64, 256):
         assert name(c3, T, nat.STAGE_W13) == "k_stage_a_lean", T
+    for T in (1, 4, 16, 64, 256):
         assert name(c3, T, nat.STAGE_W2) == "k_stage_b_lean", T
     # 512 tokens x top-8 = 16 pairs per expert on all 256 experts: GEMM stages
     assert name(c3, 512, nat.STAGE_W13) == "k_gemm_a_ring"

@@ -140,12 +140,14 @@ def test_fused_backend_bf16_serving_shape(gpu):
     assert_close(got.float().cpu().numpy(), ref, ATOL, RTOL, what="fused bf16")
 
 
-def test_stages_in_order_equal_forward(gpu):
+@pytest.mark.parametrize("full,T", [(False, 16), (True, 2)])
+def test_stages_in_order_equal_forward(gpu, full, T):
     """ftm_moe_forward_stage 0..4 launched in order is the same computation as
-    ftm_moe_forward (bitwise)."""
+    ftm_moe_forward (bitwise).  Full C3 at T=2 routes inside stage A (the
+    top-k stage launches nothing)."""
     from ftmoe import _native as nat
 
-    syn = S.generate(S.SMALL["c3_fp8"], T=16, seed=21).to(gpu)
+    syn = S.generate(S.CONFIGS["c3_fp8"] if full else S.SMALL["c3_fp8"], T=T, seed=21).to(gpu)
     layer = S.build_layer(syn)
     ref = layer.forward(syn.x)
     out = torch.empty_like(syn.x)
