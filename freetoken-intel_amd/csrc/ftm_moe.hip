@@ -1618,9 +1618,12 @@ __global__ __launch_bounds__(kBlock) void k_stage_a_lean_route(const LayerArgs a
 
 // Stage B item: 64 output columns of one expert, wave w owns 16 of them over
 // the full K (= I routed / Is shared); y = acc * router weight -> slot buffer.
+// col0: first of the wave's ncols (16 or 8) output columns; wv: the wave's LDS
+// region; s_y: null -> slot buffer rows, else LDS s_y[pair * 16 + column].
 template <bool FP8, int KB, int NWIN>
 __device__ void lean_b_item(const LayerArgs& a, const char* w, const float* sc, int cnt, const ExpertRec* rec,
-                            const int32_t* list, int shared_col, int nt, int wv) {
+                            const int32_t* list, int shared_col, int col0, int wv, float* s_y = nullptr,
+                            int ncols = 16) {
   constexpr int NLW = (FP8 ? KB / 64 : KB / 32) / NWIN;
   constexpr int NP = FP8 ? NLW / 2 : 1;
   static_assert(!FP8 || NWIN == 1, "FP8 rows: one window per wave");
@@ -1629,10 +1632,10 @@ __device__ void lean_b_item(const LayerArgs& a, const char* w, const float* sc, 
   const int H = a.L.hidden;
   const uint32_t row_bytes = (FP8 ? 1u : 2u) * (uint32_t)KB;
   const Rsrc wres = make_rsrc(w, row_bytes * (uint32_t)H);
-  const int col0 = nt * 64 + 16 * wv;
   const int brow = col0 + n;
+  const int wrow = n < ncols ? brow : -1;  // rows past ncols load nothing
   LeanWin<NLW> S;
-  lean_issue<NLW>(wres, brow, row_bytes, 0u, 0, S);
+  lean_issue<NLW>(wres, wrow, row_bytes, 0u, 0, S);
   float sv[NP];
   if constexpr (FP8) {
     const uint32_t off = (uint32_t)((col0 / 128) * (KB / 128) * 4);
@@ -1656,7 +1659,7 @@ __device__ void lean_b_item(const LayerArgs& a, const char* w, const float* sc, 
     for (int i = 0; i < NP; ++i) part[i] = (f32x4){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int wi = 0; wi < NWIN; ++wi) {
-      if (wi > 0 || (NWIN > 1 && mb > 0)) lean_issue<NLW>(wres, brow, row_bytes, 0u, wi * NLW, S);
+      if (wi > 0 || (NWIN > 1 && mb > 0)) lean_issue<NLW>(wres, wrow, row_bytes, 0u, wi * NLW, S);
       __builtin_amdgcn_s_waitcnt(0);  // weights and this wave's LDS rows have landed
       lean_mfma<FP8, NLW, NP>(S, xrow, wi * NLW * (FP8 ? 64 : 32), part, 0);
     }
@@ -1670,7 +1673,12 @@ __device__ void lean_b_item(const LayerArgs& a, const char* w, const float* sc, 
     }
 #pragma unroll
     for (int r = 0; r < kLeanXT; ++r)
-      if (lane < 16 && r < nb) a.ybuf[(size_t)pr[r] * H + brow] = acc[r] * wr[r];
+      if (lane < ncols && r < nb) {
+        if (s_y != nullptr)
+          s_y[pr[r] * 16 + n] = acc[r] * wr[r];
+        else
+          a.ybuf[(size_t)pr[r] * H + brow] = acc[r] * wr[r];
+      }
   }
 }
 
@@ -1683,7 +1691,8 @@ __global__ __launch_bounds__(kBlock) void k_stage_b_lean(const LayerArgs a) {
   const int hasSh = a.L.shared_inter > 0 ? 1 : 0;
   const int u0 = (int)blockIdx.x / tiles, nt = (int)blockIdx.x % tiles;
   if (u0 < hasSh) {
-    lean_b_item<false, KB, NWS>(a, (const char*)a.L.shared_w2, nullptr, a.T, nullptr, nullptr, a.L.topk, nt, wv);
+    lean_b_item<false, KB, NWS>(a, (const char*)a.L.shared_w2, nullptr, a.T, nullptr, nullptr, a.L.topk,
+                                nt * 64 + 16 * wv, wv);
     return;
   }
   const int u = u0 - hasSh;
@@ -1702,7 +1711,53 @@ __global__ __launch_bounds__(kBlock) void k_stage_b_lean(const LayerArgs a) {
   }
   const char* w = (const char*)a.L.w2.w + (int64_t)rec.slot * a.L.w2.w_stride;
   const float* sc = (const float*)((const char*)a.L.w2.s + (int64_t)rec.slot * a.L.w2.s_stride);
-  lean_b_item<true, KB, 1>(a, w, sc, rec.cnt, &rec, list, 0, nt, wv);
+  lean_b_item<true, KB, 1>(a, w, sc, rec.cnt, &rec, list, 0, nt * 64 + 16 * wv, wv);
+}
+
+// ---- stage B and the combine in one launch for T <= kBcMaxT (lean kernels):
+// one workgroup of kBcWaves waves per kBcCols output columns.  Wave w takes the
+// routed experts u = w, w + kBcWaves, ... and the shared expert (u =
+// nRouted); their router-weighted rows land in LDS by pair, and the workgroup
+// sums each token's slots in slot order (k_combine's order and rounding) into
+// the output.  Saves the combine launch and the slot buffer's round trip.
+constexpr int kBcWaves = 12;  // 768 threads: 170 VGPRs per lane (16 waves spill at 128)
+constexpr int kBcCols = 8;    // output columns per workgroup: H / 8 workgroups fill the CUs
+constexpr int kBcMaxT = 4;
+constexpr int kBcMaxKP = 65;  // top-k <= 64, + the shared expert
+
+template <int KB, int NWS>
+__global__ __launch_bounds__(64 * kBcWaves) void k_stage_bc_lean(const LayerArgs a) {
+  __shared__ float s_y[kBcMaxT * kBcMaxKP * 16];
+  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int H = a.L.hidden, T = a.T, KP = a.KP;
+  const int col0 = blockIdx.x * kBcCols;
+  // slots of pairs without an expert stay zero (as their slot-buffer rows would be)
+  for (int i = threadIdx.x; i < T * KP * 16; i += 64 * kBcWaves) s_y[i] = 0.0f;
+  __syncthreads();
+  const int nRouted = sload_i32(a.ctrl, kCtrlNRouted);
+  const int nU = nRouted + (a.L.shared_inter > 0 ? 1 : 0);
+  for (int u = wv; u < nU; u += kBcWaves) {
+    if (u < nRouted) {
+      const ExpertRec rec = load_rec(a, u);
+      if (rec.slot < 0 || rec.slot >= a.L.w2.num_slots) {  // non-resident: contributes zeros
+        if ((threadIdx.x & 63) == 0) atomicOr(&a.ctrl[kCtrlError], 1);
+        continue;
+      }
+      const char* w = (const char*)a.L.w2.w + (int64_t)rec.slot * a.L.w2.w_stride;
+      const float* sc = (const float*)((const char*)a.L.w2.s + (int64_t)rec.slot * a.L.w2.s_stride);
+      lean_b_item<true, KB, 1>(a, w, sc, rec.cnt, &rec, a.lists + (size_t)rec.e * T, 0, col0, wv, s_y, kBcCols);
+    } else {
+      lean_b_item<false, KB, NWS>(a, (const char*)a.L.shared_w2, nullptr, T, nullptr, nullptr, a.L.topk, col0, wv,
+                                  s_y, kBcCols);
+    }
+  }
+  __syncthreads();
+  for (int i = threadIdx.x; i < T * kBcCols; i += 64 * kBcWaves) {
+    const int t = i / kBcCols, c = i % kBcCols;
+    float sum = s_y[(t * KP) * 16 + c];
+    for (int j = 1; j < KP; ++j) sum += s_y[(t * KP + j) * 16 + c];
+    ((uint16_t*)a.out)[(size_t)t * H + col0 + c] = f32_to_bf16(sum);
+  }
 }
 
 // ============================================================== combine
@@ -1963,11 +2018,17 @@ static void launch_stages(const LayerArgs& a, int gridA, int gridB, hipStream_t 
         hipLaunchKernelGGL((k_stage_a_lean<512, 2>), dim3(items), dim3(kBlock), lds, st, a);
       }
     }
+    const bool bc = a.T <= kBcMaxT && a.KP <= kBcMaxKP;  // stage B and the combine in one launch
     if (which & 2) {
-      const int grid = (maxU + (a.L.shared_inter > 0 ? 1 : 0)) * (a.L.hidden / 64);
-      hipLaunchKernelGGL((k_stage_b_lean<512, 2>), dim3(grid), dim3(kBlock), lds, st, a);
+      if (bc) {
+        const size_t ldsb = (size_t)kBcWaves * (kLeanXT + 1) * (size_t)lean_pitch(512) * 2u;
+        hipLaunchKernelGGL((k_stage_bc_lean<512, 2>), dim3(a.L.hidden / kBcCols), dim3(64 * kBcWaves), ldsb, st, a);
+      } else {
+        const int grid = (maxU + (a.L.shared_inter > 0 ? 1 : 0)) * (a.L.hidden / 64);
+        hipLaunchKernelGGL((k_stage_b_lean<512, 2>), dim3(grid), dim3(kBlock), lds, st, a);
+      }
     }
-    which &= 4;
+    which &= bc ? 0 : 4;
   }
   if (which & 1) {
     if constexpr (FMT == FTM_FMT_GPTQ_INT4) {
@@ -2053,6 +2114,12 @@ hipError_t launch_experts(const ftm_moe_layer& L, const void* x, int T, void* ou
 // Name of the kernel launch_router / launch_topk / launch_experts start for
 // `stage` (FTM_STAGE_*) of layer L at T tokens: the same predicates as the
 // launchers above, for profilers and benchmarks that attribute time by name.
+// Stage B and the combine run as one launch (k_stage_bc_lean).
+static bool bc_fused(const ftm_moe_layer& L, int T) {
+  return lean_ok(L, T) && L.w13.fmt == FTM_FMT_FP8_BLOCK && L.act_dtype == FTM_DT_BF16 && T <= kBcMaxT &&
+         L.topk + (L.shared_inter > 0 ? 1 : 0) <= kBcMaxKP;
+}
+
 template <int FMT, int AT>
 static const char* expert_kernel_name(const ftm_moe_layer& L, int T, int stage) {
   const bool lean = FMT == FTM_FMT_FP8_BLOCK && AT == FTM_DT_BF16 && lean_ok(L, T);
@@ -2061,7 +2128,7 @@ static const char* expert_kernel_name(const ftm_moe_layer& L, int T, int stage) 
     if (FMT == FTM_FMT_GPTQ_INT4) return "k_stage_a";
     return xl_plan_a<FMT, AT>(L, T).ok ? "k_stage_a_xl" : "k_stage_a_rows";
   }
-  if (lean) return "k_stage_b_lean";
+  if (lean) return L.topk + (L.shared_inter > 0 ? 1 : 0) <= kBcMaxKP && T <= kBcMaxT ? "k_stage_bc_lean" : "k_stage_b_lean";
   if (FMT == FTM_FMT_GPTQ_INT4) return "k_stage_b";
   return xl_plan_b<FMT, AT>(L, T).ok ? "k_stage_b_xl" : "k_stage_b";
 }
@@ -2078,7 +2145,7 @@ const char* stage_kernel_name(const ftm_moe_layer& L, int T, int stage) {
     case FTM_STAGE_TOPK:
       if (lean_route_ok(L, T)) return "";  // routed inside stage A
       return T <= kTopk1MaxT ? "k_topk1" : T >= kTopkBlkMinT ? "k_topk_blk" : "k_topk";
-    case FTM_STAGE_COMBINE: return "k_combine";
+    case FTM_STAGE_COMBINE: return bc_fused(L, T) ? "" : "k_combine";  // "": done by stage B
     case FTM_STAGE_W13:
     case FTM_STAGE_W2: break;
     default: return nullptr;
