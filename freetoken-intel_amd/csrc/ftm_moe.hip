@@ -234,6 +234,20 @@ __device__ __forceinline__ float key_value(uint64_t k) {
 }
 __device__ __forceinline__ int key_expert(uint64_t k) { return (int)~(uint32_t)k; }
 
+// The same order in 32 bits for bf16-exact keys (the low 16 bits of the key
+// are zero, so the top half of its image decides): image >> 16 above ~expert
+// (16 bits, E <= 65536).
+__device__ __forceinline__ uint32_t pack_key32(float v, int e) {
+  return (uint32_t)(pack_key(v, e) >> 48) << 16 | (~(uint32_t)e & 0xffffu);
+}
+__device__ __forceinline__ float key32_value(uint32_t k) {
+  const uint32_t hi = k >> 16;
+  // the image's low half: 0 for non-negative keys, 0xffff for negative ones
+  const uint32_t b = (hi << 16) | ((hi & 0x8000u) ? 0u : 0xffffu);
+  return __uint_as_float((b & 0x80000000u) ? (b & 0x7fffffffu) : ~b);
+}
+__device__ __forceinline__ int key32_expert(uint32_t k) { return (int)(~k & 0xffffu); }
+
 template <int CTRL>
 __device__ __forceinline__ uint64_t dpp_u64(uint64_t x) {
   const uint32_t lo = (uint32_t)dpp_i<CTRL>((int)(uint32_t)x);
@@ -258,6 +272,17 @@ __device__ __forceinline__ uint64_t wave_max_u64(uint64_t x) {
   return umax64(umax64(r[0], r[1]), umax64(r[2], r[3]));
 }
 
+// Wave max of a u32 (DPP within rows, v_readlane across rows); all lanes get it.
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t x) {
+  x = max(x, (uint32_t)dpp_i<kDppXor1>((int)x));
+  x = max(x, (uint32_t)dpp_i<kDppXor2>((int)x));
+  x = max(x, (uint32_t)dpp_i<kDppHalfMirror>((int)x));
+  x = max(x, (uint32_t)dpp_i<kDppMirror>((int)x));
+  const uint32_t r0 = (uint32_t)__builtin_amdgcn_readlane((int)x, 0), r1 = (uint32_t)__builtin_amdgcn_readlane((int)x, 16);
+  const uint32_t r2 = (uint32_t)__builtin_amdgcn_readlane((int)x, 32), r3 = (uint32_t)__builtin_amdgcn_readlane((int)x, 48);
+  return max(max(r0, r1), max(r2, r3));
+}
+
 __device__ __forceinline__ void cas_desc(uint64_t& a, uint64_t& b) {
   const uint64_t hi = umax64(a, b), lo = a > b ? b : a;
   a = hi;
@@ -279,6 +304,27 @@ __device__ __forceinline__ void sort_desc(uint64_t (&k)[NV]) {
     cas_desc(k[0], k[4]); cas_desc(k[1], k[5]); cas_desc(k[2], k[6]); cas_desc(k[3], k[7]);
     cas_desc(k[2], k[4]); cas_desc(k[3], k[5]);
     cas_desc(k[1], k[2]); cas_desc(k[3], k[4]); cas_desc(k[5], k[6]);
+  }
+}
+
+__device__ __forceinline__ void cas_desc32(uint32_t& a, uint32_t& b) {
+  const uint32_t hi = max(a, b), lo = min(a, b);
+  a = hi;
+  b = lo;
+}
+template <int NV>
+__device__ __forceinline__ void sort_desc32(uint32_t (&k)[NV]) {
+  if constexpr (NV == 4) {
+    cas_desc32(k[0], k[1]); cas_desc32(k[2], k[3]);
+    cas_desc32(k[0], k[2]); cas_desc32(k[1], k[3]);
+    cas_desc32(k[1], k[2]);
+  } else {
+    cas_desc32(k[0], k[1]); cas_desc32(k[2], k[3]); cas_desc32(k[4], k[5]); cas_desc32(k[6], k[7]);
+    cas_desc32(k[0], k[2]); cas_desc32(k[1], k[3]); cas_desc32(k[4], k[6]); cas_desc32(k[5], k[7]);
+    cas_desc32(k[1], k[2]); cas_desc32(k[5], k[6]);
+    cas_desc32(k[0], k[4]); cas_desc32(k[1], k[5]); cas_desc32(k[2], k[6]); cas_desc32(k[3], k[7]);
+    cas_desc32(k[2], k[4]); cas_desc32(k[3], k[5]);
+    cas_desc32(k[1], k[2]); cas_desc32(k[3], k[4]); cas_desc32(k[5], k[6]);
   }
 }
 
@@ -360,25 +406,55 @@ __device__ __forceinline__ void route_token_pre(const LayerArgs& a, int t, const
       key[i] = v[i];
   }
   // Each lane sorts its candidates; k rounds take the wave max of the lanes'
-  // heads, and the lane holding it pops its head.
-  uint64_t lst[NV];
+  // heads, and the lane holding it pops its head.  When every key is
+  // bf16-exact (router logits and LOWP probabilities are rounded to bf16) the
+  // (key, expert) pair packs into 32 bits with the same order, and each round
+  // is a 32-bit max.
+  bool exact16 = true;
 #pragma unroll
-  for (int i = 0; i < NV; ++i) lst[i] = (lane + 64 * i < E) ? pack_key(key[i], lane + 64 * i) : 0ull;
-  sort_desc<NV>(lst);
-  uint64_t mine = 0ull, first = 0ull;
-  for (int j = 0; j < k; ++j) {
-    const uint64_t best = wave_max_u64(lst[0]);
-    first = j == 0 ? best : first;
-    mine = lane == j ? best : mine;
-    const bool pop = lst[0] == best;
+  for (int i = 0; i < NV; ++i)
+    exact16 &= (lane + 64 * i >= E) | (key[i] != key[i]) | ((__float_as_uint(key[i]) & 0xffffu) == 0u);
+  float top0;
+  if (__all(exact16)) {
+    uint32_t lst[NV];
 #pragma unroll
-    for (int i = 0; i + 1 < NV; ++i) lst[i] = pop ? lst[i + 1] : lst[i];
-    lst[NV - 1] = pop ? 0ull : lst[NV - 1];
-  }
-  const float top0 = key_value(first);
-  if (lane < k) {
-    sel_e = key_expert(mine);
-    sel_w = key_value(mine);  // the key; converted to a weight below
+    for (int i = 0; i < NV; ++i) lst[i] = (lane + 64 * i < E) ? pack_key32(key[i], lane + 64 * i) : 0u;
+    sort_desc32<NV>(lst);
+    uint32_t mine = 0u, first = 0u;
+    for (int j = 0; j < k; ++j) {
+      const uint32_t best = wave_max_u32(lst[0]);
+      first = j == 0 ? best : first;
+      mine = lane == j ? best : mine;
+      const bool pop = lst[0] == best;
+#pragma unroll
+      for (int i = 0; i + 1 < NV; ++i) lst[i] = pop ? lst[i + 1] : lst[i];
+      lst[NV - 1] = pop ? 0u : lst[NV - 1];
+    }
+    top0 = key32_value(first);
+    if (lane < k) {
+      sel_e = key32_expert(mine);
+      sel_w = key32_value(mine);  // the key; converted to a weight below
+    }
+  } else {
+    uint64_t lst[NV];
+#pragma unroll
+    for (int i = 0; i < NV; ++i) lst[i] = (lane + 64 * i < E) ? pack_key(key[i], lane + 64 * i) : 0ull;
+    sort_desc<NV>(lst);
+    uint64_t mine = 0ull, first = 0ull;
+    for (int j = 0; j < k; ++j) {
+      const uint64_t best = wave_max_u64(lst[0]);
+      first = j == 0 ? best : first;
+      mine = lane == j ? best : mine;
+      const bool pop = lst[0] == best;
+#pragma unroll
+      for (int i = 0; i + 1 < NV; ++i) lst[i] = pop ? lst[i + 1] : lst[i];
+      lst[NV - 1] = pop ? 0ull : lst[NV - 1];
+    }
+    top0 = key_value(first);
+    if (lane < k) {
+      sel_e = key_expert(mine);
+      sel_w = key_value(mine);  // the key; converted to a weight below
+    }
   }
   float p = 0.0f;
   if (lane < k) {
