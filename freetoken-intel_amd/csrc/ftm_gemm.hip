@@ -284,7 +284,7 @@ __device__ __forceinline__ void gemm_tile(const ProjSlot& W, int c0, int Iu, Rsr
 }
 
 // ---------------------------------------------------------------- LDS ring tiles (stage A)
-// The stage A tiles for FP8 / INT8 / bf16 weights, fed by a ring of up to
+// The stage A tiles for FP8 / INT8 / MXFP4 / bf16 weights, fed by a ring of up to
 // four LDS stages that direct global-to-LDS copies (global_load_lds, 16 B per
 // lane) fill three K steps ahead of the MFMAs.  Activations (bf16) and the raw
 // weight bytes both land in LDS undecoded; a wave decodes its own weight rows
@@ -299,7 +299,7 @@ __device__ __forceinline__ void gemm_tile(const ProjSlot& W, int c0, int Iu, Rsr
 // Raw weight bytes per row per K step and rows per 1 KiB copy.
 template <int WFMT>
 struct RingW {
-  static constexpr int kRowBytes = WFMT == FTM_FMT_BF16 ? 2 * kGK : kGK;
+  static constexpr int kRowBytes = WFMT == FTM_FMT_BF16 ? 2 * kGK : WFMT == FTM_FMT_MXFP4 ? kGK / 2 : kGK;
   static constexpr int kRowsPerCopy = 1024 / kRowBytes;
 };
 // Ring bytes per workgroup: 64 KiB (FP8/INT8: 4 stages, bf16: 2).  The
@@ -322,6 +322,7 @@ struct RingPlan {
 
 __device__ __forceinline__ int ring_fa(int r) { return (r ^ (r >> 3)) & 7; }         // 8 pieces per row
 __device__ __forceinline__ int ring_fw(int r) { return ((r >> 1) ^ (r >> 3)) & 3; }  // 4 pieces per row
+__device__ __forceinline__ int ring_fm(int r) { return (r >> 3) & 1; }                // 2 pieces per row (MXFP4)
 
 // s_waitcnt vmcnt(n), other counters untouched (gfx9 encoding), n < 64.
 template <int N>
@@ -390,6 +391,9 @@ __device__ __forceinline__ void gemm_tile_ring(const ProjSlot& W, int c0, int Iu
     if constexpr (WFMT == FTM_FMT_BF16) {
       r = 8 * j + (lane >> 3);
       piece = (lane & 7) ^ ring_fa(r);
+    } else if constexpr (WFMT == FTM_FMT_MXFP4) {
+      r = 32 * j + (lane >> 1);
+      piece = (lane & 1) ^ ring_fm(r);
     } else {
       r = 16 * j + (lane >> 2);
       piece = (lane & 3) ^ ring_fw(r);
@@ -412,9 +416,24 @@ __device__ __forceinline__ void gemm_tile_ring(const ProjSlot& W, int c0, int Iu
   // half, INT8: one row per tile row), loads issued before the ring prologue
   const int ngroups = kPost ? (K + W.group - 1) / W.group : 0;
   constexpr int kScaleRows = WFMT == FTM_FMT_INT8_PACKED ? NWR : NWR / 64;
-  constexpr int kScalePer = WFMT == FTM_FMT_INT8_PACKED ? (kRingScaleBytes / 4 + kBlock - 1) / kBlock : 1;
+  constexpr int kScalePer = WFMT == FTM_FMT_INT8_PACKED || WFMT == FTM_FMT_MXFP4
+                                ? (kRingScaleBytes / 4 + kBlock - 1) / kBlock : 1;
   uint32_t sw[kScalePer];
   uint32_t sidx[kScalePer];
+  // MXFP4: the e8m0 bytes [NWR rows][K / 32], copied as words; each 64-row
+  // half of the tile is one contiguous run of 64 * K / 32 bytes
+  const int kgb = K / 32;                 // scale bytes per row
+  const int mwords = 64 * kgb / 4;        // words per 64-row half
+  if constexpr (WFMT == FTM_FMT_MXFP4) {
+    const Rsrc mres = make_rsrc(W.s, (uint32_t)W.N * (uint32_t)kgb);
+#pragma unroll
+    for (int q = 0; q < kScalePer; ++q) {
+      const int e = tid + kBlock * q;
+      const int half = e / mwords, wi = e - half * mwords;
+      const bool ok = e < (NWR / 64) * mwords;
+      sw[q] = bload4(mres, ok ? (uint32_t)(grow(64 * half) * kgb + 4 * wi) : kOOB);
+    }
+  }
   if constexpr (kPost) {
     const uint32_t sesz = W.s_dt == FTM_DT_F32 ? 4u : 2u;
     const int nsc = kScaleRows * ngroups;
@@ -432,6 +451,14 @@ __device__ __forceinline__ void gemm_tile_ring(const ProjSlot& W, int c0, int Iu
   }
   const int pro = nsteps < S - 1 ? nsteps : S - 1;
   for (int kb = 0; kb < pro; ++kb) issue(kb, kb);
+  if constexpr (WFMT == FTM_FMT_MXFP4) {
+    wait_ring<P::kLoads, S - 1>(pro);
+#pragma unroll
+    for (int q = 0; q < kScalePer; ++q) {
+      const int e = tid + kBlock * q;
+      if (e < (NWR / 64) * mwords) ((uint32_t*)sS)[e] = sw[q];
+    }
+  }
   if constexpr (kPost) {
     wait_ring<P::kLoads, S - 1>(pro);
 #pragma unroll
@@ -462,6 +489,12 @@ __device__ __forceinline__ void gemm_tile_ring(const ProjSlot& W, int c0, int Iu
       if constexpr (WFMT == FTM_FMT_BF16) {
         b0[nj] = *(const u32x4*)(row + 16 * ((2 * g4) ^ ring_fa(wrr[nj])));
         b1[nj] = *(const u32x4*)(row + 16 * ((2 * g4 + 1) ^ ring_fa(wrr[nj])));
+      } else if constexpr (WFMT == FTM_FMT_MXFP4) {
+        // 16 e2m1 codes (K 16 g .. 16 g + 15), one 32-wide e8m0 group
+        const u32x2 raw = *(const u32x2*)(row + 16 * ((g4 >> 1) ^ ring_fm(wrr[nj])) + 8 * (g4 & 1));
+        const float sc = e8m0_to_f32(((const uint8_t*)sS)[wrr[nj] * kgb + 2 * kb + (g4 >> 1)]);
+        b0[nj] = fp4x8_to_bf16(raw.x, sc);
+        b1[nj] = fp4x8_to_bf16(raw.y, sc);
       } else {
         const u32x4 raw = *(const u32x4*)(row + 16 * (g4 ^ ring_fw(wrr[nj])));
         if constexpr (WFMT == FTM_FMT_FP8_BLOCK) {
@@ -649,7 +682,7 @@ template <int WFMT>
 __device__ __forceinline__ void ring_a(const LayerArgs& a, const ProjSlot& W, int Iu, int c0, int m0, int cnt,
                                        const int32_t* list, int shared_col, char* lds) {
   const int lpg = ring_lpg(WFMT, W.group, W.K);
-  if constexpr (WFMT == FTM_FMT_BF16) {
+  if constexpr (WFMT == FTM_FMT_BF16 || WFMT == FTM_FMT_MXFP4) {  // no group post-scale
     gemm_a_ring_body<WFMT, 0>(a, W, Iu, c0, m0, cnt, list, shared_col, lds);
   } else if constexpr (WFMT == FTM_FMT_FP8_BLOCK) {
     if (lpg == 2) gemm_a_ring_body<WFMT, 2>(a, W, Iu, c0, m0, cnt, list, shared_col, lds);
@@ -819,11 +852,12 @@ bool gemm_path_ok(const ftm_moe_layer& L, int T) {
   return pairs >= (long)kGemmMinRows * maxU;
 }
 
-// Whether the ring tiles take this layer: FP8 / INT8 / bf16 weights whose
-// tile scales fit the LDS scale area (INT8: one fp32 per tile row and group).
+// Whether the ring tiles take this layer: weights whose tile scales fit the
+// LDS scale area (INT8: one fp32 per tile row and group; MXFP4: one e8m0 byte
+// per tile row and 32 K).
 static bool ring_ok(const ftm_moe_layer& L) {
   const int f = L.w13.fmt;
-  if (f == FTM_FMT_MXFP4) return false;
+  if (f == FTM_FMT_MXFP4 && 128 * (L.hidden / 32) > kRingScaleBytes) return false;  // e8m0 bytes of the tile
   if (f == FTM_FMT_INT8_PACKED || f == FTM_FMT_FP8_BLOCK) {
     const long g13 = (L.hidden + L.w13.group - 1) / L.w13.group;
     if (f == FTM_FMT_INT8_PACKED && 128 * g13 * 4 > kRingScaleBytes) return false;
@@ -834,7 +868,9 @@ static bool ring_ok(const ftm_moe_layer& L) {
 
 // Dynamic LDS of the ring kernels for this layer: ring + tile scales.
 static size_t ring_lds_a(const ftm_moe_layer& L) {
-  const int f = L.w13.fmt, g = (L.hidden + L.w13.group - 1) / (L.w13.group > 0 ? L.w13.group : 1);
+  const int f = L.w13.fmt;
+  if (f == FTM_FMT_MXFP4) return (size_t)kRingA + 128u * (size_t)(L.hidden / 32);
+  const int g = (L.hidden + L.w13.group - 1) / (L.w13.group > 0 ? L.w13.group : 1);
   const int rows = f == FTM_FMT_FP8_BLOCK ? 2 : f == FTM_FMT_INT8_PACKED ? 128 : 0;
   return (size_t)kRingA + (size_t)rows * g * 4;
 }
@@ -862,11 +898,10 @@ static void launch_gemm_t(const LayerArgs& a, hipStream_t st, int which) {
   const long items_b = (mt_routed + mt_shared) * (L.hidden / 64);
   // Stage A on the ring tiles where they apply (measured on MI355X, C3 FP8:
   // w13 285 us against 343 at T=2048, 179 against 239 at T=512; C1 INT8 T=1024:
-  // 29 against 42).  Stage B keeps the register-staged tiles: with K = I its
+  // 29 against 42; C4 MXFP4 T=4096: 1045 against 1415).  Stage B keeps the register-staged tiles: with K = I its
   // tiles are 8 K steps long and 4 workgroups per CU beat the deeper ring
   // (C3 T=2048 w2 259 us against 377).
-  bool ring = false;
-  if constexpr (FMT != FTM_FMT_MXFP4) ring = ring_ok(L);
+  const bool ring = ring_ok(L);
   if (which & 1) {
     if (ring) {
       ring_lds_attr<FMT>();
