@@ -131,10 +131,10 @@ def test_stage_kernel_names_follow_the_dispatch():
         assert name(c3, T, nat.STAGE_TOPK) == "", T
     for T in (3, 4, 16, 64, 256):
         assert name(c3, T, nat.STAGE_W13) == "k_stage_a_lean", T
-    for T in (1, 4):  # stage B and the combine in one launch
+    for T in (1, 4, 16):  # stage B and the combine in one launch
         assert name(c3, T, nat.STAGE_W2) == "k_stage_bc_lean", T
         assert name(c3, T, nat.STAGE_COMBINE) == "", T
-    for T in (5, 16, 64, 256):
+    for T in (17, 64, 256):
         assert name(c3, T, nat.STAGE_W2) == "k_stage_b_lean", T
     # 512 tokens x top-8 = 16 pairs per expert on all 256 experts: GEMM stages
     assert name(c3, 512, nat.STAGE_W13) == "k_gemm_a_ring"
@@ -145,7 +145,7 @@ def test_stage_kernel_names_follow_the_dispatch():
     assert name(c3, 256, nat.STAGE_TOPK) == "k_topk_blk"
     assert name(c3, 16, nat.STAGE_ROUTER) == "k_router"
     assert name(c3, 64, nat.STAGE_ROUTER) == "k_router_rows"
-    assert name(c3, 16, nat.STAGE_COMBINE) == "k_combine"
+    assert name(c3, 17, nat.STAGE_COMBINE) == "k_combine"
     assert name(c3, 16, 5) is None
     assert name(c3, 0, nat.STAGE_W13) is None
     small = _layer(E=8, H=256, I=128, k=2)
