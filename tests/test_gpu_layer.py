@@ -304,3 +304,16 @@ def test_repeated_expert_in_a_token_counts_twice(gpu, T):
     layer = S.build_layer(dsyn)
     out = layer.forward_routed(dsyn.x, torch.from_numpy(ids).to(gpu), torch.from_numpy(w).to(gpu))
     assert_close(to_f32(out), ref["out"], what="layer with a repeated expert")
+
+
+@pytest.mark.parametrize("mode", ["softmax_topk_lowp", "topk_softmax"])
+@pytest.mark.parametrize("T", [1, 2, 3])
+def test_c3_shape_route_modes(gpu, mode, T):
+    """The C3 shape under the other two routing modes: T <= 2 routes inside
+    the lean stage A (one instantiation per mode), T = 3 through the top-k
+    kernel; routing bit-exact and outputs within tolerance either way."""
+    from dataclasses import replace
+
+    cfg = replace(S.CONFIGS["c3_fp8"], route_mode=mode)
+    syn = S.generate(cfg, T=T, seed=60 + T)
+    _run_and_check(syn, gpu)
