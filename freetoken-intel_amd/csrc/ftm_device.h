@@ -92,6 +92,15 @@ __device__ __forceinline__ f32x4 mfma_bf16(u32x4 a, u32x4 b, f32x4 c) {
                                                  __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
 }
 
+// s_waitcnt vmcnt(n), other counters untouched (gfx9 encoding), n < 64:
+// the oldest vector-memory loads of this wave have landed, up to n are still
+// in flight (they complete in issue order).
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (0x7 << 4) | (0xf << 8));
+}
+
 __device__ __forceinline__ float wave_sum(float v) {
   v += __shfl_xor(v, 32);
   v += __shfl_xor(v, 16);

@@ -324,12 +324,6 @@ __device__ __forceinline__ int ring_fa(int r) { return (r ^ (r >> 3)) & 7; }    
 __device__ __forceinline__ int ring_fw(int r) { return ((r >> 1) ^ (r >> 3)) & 3; }  // 4 pieces per row
 __device__ __forceinline__ int ring_fm(int r) { return (r >> 3) & 1; }                // 2 pieces per row (MXFP4)
 
-// s_waitcnt vmcnt(n), other counters untouched (gfx9 encoding), n < 64.
-template <int N>
-__device__ __forceinline__ void wait_vm() {
-  static_assert(N >= 0 && N < 64, "vmcnt range");
-  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (0x7 << 4) | (0xf << 8));
-}
 // Wait until at most `stages` ring stages of this wave's copies are in flight.
 template <int LOADS, int MAXS>
 __device__ __forceinline__ void wait_ring(int stages) {

@@ -865,6 +865,233 @@ __global__ __launch_bounds__(kBlock) void k_stage_a(const LayerArgs a) {
   }
 }
 
+// ---------------------------------------------------------------- stage A, GPTQ decode (activations in LDS)
+// The arithmetic of wave_gemm_gptq / stage_a_body (each nibble decoded as
+// 128 + q in bf16, per-group scale and zero-point correction from the group's
+// row sums of x) with the data path of the lean FP8 kernels: the block's token
+// rows of a wave's K range are copied to LDS once (global_load_lds), and the
+// next 128-wide group's weights, scales and zero words are in flight while the
+// current group is multiplied.  bf16 activations, group 128, a wave's K range
+// of at most kGqMaxKR; blocks of kGqXT tokens (MFMA rows past them read a zero row).
+extern __shared__ __align__(16) uint16_t ftm_xl_lds[];  // dynamic LDS of the decode stages
+
+constexpr int kGqXT = 4;
+constexpr int kGqMaxKR = 1024;
+// Larger batches keep the 16-token blocks of k_stage_a: measured on C2, this
+// kernel ties it at T=32 (64.7 against 64.5 us) and loses at T=64 (91 against 67).
+constexpr int kGqMaxT = 16;
+
+__host__ __device__ __forceinline__ constexpr int gq_pitch(int KR) { return KR + 8; }
+
+struct GqGroup {
+  u32x4 raw[4];  // 4 wave-loads of 32 K: lane (g, rl) holds k8 row 4 b + g, columns ncol .. ncol + 3
+  u32x4 scv;
+  uint32_t zw;
+};
+
+__device__ __forceinline__ void gq_issue(Rsrc wres, Rsrc sres, Rsrc zres, uint32_t ncol, int N, int grp,
+                                         uint32_t sbytes, GqGroup& G) {
+  const int g = (threadIdx.x & 63) >> 4;
+  const bool ok = ncol != kOOB;
+#pragma unroll
+  for (int b = 0; b < 4; ++b) {
+    const uint32_t prow = (uint32_t)(grp * 16 + 4 * b + g);
+    G.raw[b] = bload16(wres, ok ? (prow * (uint32_t)N + ncol) * 4u : kOOB);
+  }
+  G.scv = bload16(sres, ok ? ((uint32_t)grp * (uint32_t)N + ncol) * sbytes : kOOB);
+  G.zw = bload4(zres, ok ? ((uint32_t)grp * (uint32_t)(N / 8) + ncol / 8) * 4u : kOOB);
+}
+constexpr int kGqLoads = 6;  // vector loads per gq_issue
+
+// One group: MFMAs over its 4 wave-loads, then acc += s * (partial - (128 + z + 1) * sum x).
+__device__ __forceinline__ void gq_group(const GqGroup& G, const uint16_t* xrow, int kofs, uint32_t ncol,
+                                         uint32_t sbytes, int s_dt, f32x4 (&acc)[4]) {
+  const int lane = threadIdx.x & 63, g = lane >> 4;
+  const u32x4 zero = (u32x4){0u, 0u, 0u, 0u};
+  f32x4 tmp[4];
+#pragma unroll
+  for (int c = 0; c < 4; ++c) tmp[c] = (f32x4){0.f, 0.f, 0.f, 0.f};
+  float xs = 0.0f;
+#pragma unroll
+  for (int b = 0; b < 4; ++b) {
+    const u32x4 av = perm_gptq(*(const u32x4*)(xrow + kofs + 32 * b + 8 * g));
+    xs += sum_a8(av, zero);
+    const uint32_t wv[4] = {G.raw[b].x, G.raw[b].y, G.raw[b].z, G.raw[b].w};
+#pragma unroll
+    for (int c = 0; c < 4; ++c) tmp[c] = mfma_bf16(av, gptq_word_to_bf16(wv[c]), tmp[c]);
+  }
+  float sx = xs;
+  sx += __shfl_xor(sx, 16);
+  sx += __shfl_xor(sx, 32);
+  float sxr[4];
+#pragma unroll
+  for (int rr = 0; rr < 4; ++rr) sxr[rr] = __shfl(sx, 4 * g + rr);
+  const uint32_t sw[4] = {G.scv.x, G.scv.y, G.scv.z, G.scv.w};
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    float sc;
+    if (sbytes == 4u) {
+      sc = __uint_as_float(sw[c]);
+    } else {
+      const uint32_t h = (sw[c >> 1] >> (16 * (c & 1))) & 0xffffu;
+      sc = s_dt == FTM_DT_F16 ? f16_to_f32((uint16_t)h) : bf16_to_f32(h);
+    }
+    const float zp = (float)(((G.zw >> (4 * ((ncol + c) & 7))) & 0xfu) + 1u);
+    f32x4 corr;
+    corr.x = tmp[c].x - (128.0f + zp) * sxr[0];
+    corr.y = tmp[c].y - (128.0f + zp) * sxr[1];
+    corr.z = tmp[c].z - (128.0f + zp) * sxr[2];
+    corr.w = tmp[c].w - (128.0f + zp) * sxr[3];
+    acc[c] += corr * sc;
+  }
+}
+
+// Copy elements [k0, k0 + kr) of the rows of pairs pr[0..nb) into xw (row r at xw + r * pitch).
+__device__ __forceinline__ void gq_fill(const int (&pr)[kGqXT], int nb, const void* src, int KP, int H, int k0,
+                                        int kr, int pitch, uint16_t* xw) {
+  typedef __attribute__((address_space(1))) const void* GPtr;
+  typedef __attribute__((address_space(3))) void* LPtr;
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int r = 0; r < kGqXT; ++r) {
+    if (r < nb) {
+      const char* row = (const char*)src + ((size_t)(pr[r] / KP) * (size_t)H + (size_t)k0) * 2u;
+      for (int c = 0; c * 1024 < 2 * kr; ++c) {
+        if (c * 1024 + 16 * lane < 2 * kr)
+          __builtin_amdgcn_global_load_lds((GPtr)(row + c * 1024 + 16 * lane),
+                                           (LPtr)((char*)(xw + r * pitch) + c * 1024), 16, 0, 0);
+      }
+    }
+  }
+}
+
+// Item: 64 channels of one expert; waves 0-1 take the 64 gate columns and
+// waves 2-3 the 64 up columns, each over half of the K groups.
+template <int NT>
+__device__ void stage_a_gq(const LayerArgs& a, const ProjSlot& W, int Iu, int it, int cnt, const int32_t* list,
+                           f32x4* red) {
+  constexpr int EPI = 16 * NT / kBlock;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  const int rl = lane & 15;
+  const int H = a.L.hidden, KP = a.KP, N = W.N;
+  const int tile = wave >> 1;
+  int lo, hi;
+  wave_k_range<FTM_FMT_GPTQ_INT4>(W, wave & 1, 2, lo, hi);
+  const int k0 = lo * 128, kr = (hi - lo) * 128;
+  const uint32_t sbytes = W.s_dt == FTM_DT_F32 ? 4u : 2u;
+  const int ngroups = (W.K + 127) / 128;
+  const Rsrc wres = make_rsrc(W.w, (uint32_t)(W.K / 8) * (uint32_t)N * 4u);
+  const Rsrc zres = make_rsrc(W.z, (uint32_t)ngroups * (uint32_t)(N / 8) * 4u);
+  const Rsrc sres = make_rsrc(W.s, (uint32_t)ngroups * (uint32_t)N * sbytes);
+  const int col0 = (tile == 0 ? 0 : Iu) + it * NT;
+  const uint32_t ncol = col0 + 4 * rl < N ? (uint32_t)(col0 + 4 * rl) : kOOB;
+  const Rsrc lres = make_rsrc(list, (uint32_t)cnt * 4u);
+  constexpr int pitch = gq_pitch(kGqMaxKR);
+  uint16_t* xw = ftm_xl_lds + wave * (kGqXT + 1) * pitch;
+  for (int e = 8 * lane; e < kGqMaxKR; e += 8 * 64) *(u32x4*)(xw + kGqXT * pitch + e) = (u32x4){0u, 0u, 0u, 0u};
+  float bias_g[EPI], bias_u[EPI];
+#pragma unroll
+  for (int q = 0; q < EPI; ++q) {
+    const int j = (threadIdx.x + q * kBlock) % NT;
+    bias_g[q] = W.bias != nullptr ? load_scalar(W.bias, it * NT + j, W.bias_dt) : 0.0f;
+    bias_u[q] = W.bias != nullptr ? load_scalar(W.bias, Iu + it * NT + j, W.bias_dt) : 0.0f;
+  }
+  for (int mb = 0; mb < cnt; mb += kGqXT) {
+    const int nb = min(kGqXT, cnt - mb);
+    int pr[kGqXT];
+#pragma unroll
+    for (int i = 0; i < kGqXT; ++i) pr[i] = pair_of_row(lres, true, mb + i, cnt, KP, 0);
+    int pe[EPI];
+#pragma unroll
+    for (int q = 0; q < EPI; ++q) {
+      const int i = (threadIdx.x + q * kBlock) / NT;
+      pe[q] = i < kGqXT ? pair_of_row(lres, true, mb + i, cnt, KP, 0) : -1;
+    }
+    f32x4 acc[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) acc[c] = (f32x4){0.f, 0.f, 0.f, 0.f};
+    if (hi > lo) {
+      GqGroup GA, GB;
+      gq_issue(wres, sres, zres, ncol, N, lo, sbytes, GA);  // weights first,
+      gq_fill(pr, nb, a.x, KP, H, k0, kr, pitch, xw);       // then the token rows
+      const uint16_t* xrow = xw + (rl < nb ? rl : kGqXT) * pitch;
+      // two group buffers: the next group is in flight while this one is multiplied
+      // (a third buffer, 219 VGPRs at occupancy 2, measured no faster)
+      for (int grp = lo; grp < hi; grp += 2) {
+        const bool two = grp + 1 < hi;
+        if (two) {
+          gq_issue(wres, sres, zres, ncol, N, grp + 1, sbytes, GB);
+          wait_vm<kGqLoads>();  // group grp (and the copy) landed
+        } else {
+          __builtin_amdgcn_s_waitcnt(0);
+        }
+        gq_group(GA, xrow, (grp - lo) * 128, ncol, sbytes, W.s_dt, acc);
+        if (two) {
+          if (grp + 2 < hi) {
+            gq_issue(wres, sres, zres, ncol, N, grp + 2, sbytes, GA);
+            wait_vm<kGqLoads>();
+          } else {
+            __builtin_amdgcn_s_waitcnt(0);
+          }
+          gq_group(GB, xrow, (grp + 1 - lo) * 128, ncol, sbytes, W.s_dt, acc);
+        }
+      }
+    }
+#pragma unroll
+    for (int c = 0; c < 4; ++c) red[(wave * 4 + c) * 64 + lane] = acc[c];
+    __syncthreads();
+#pragma unroll
+    for (int q = 0; q < EPI; ++q) {
+      const int idx = threadIdx.x + q * kBlock;
+      const int i = idx / NT, j = idx % NT;
+      const int c = j & 3, jj = j >> 2;
+      const int ln = jj + 16 * (i >> 2), rr = i & 3;
+      const float g4 = red[(0 * 4 + c) * 64 + ln][rr] + red[(1 * 4 + c) * 64 + ln][rr];
+      const float u4 = red[(2 * 4 + c) * 64 + ln][rr] + red[(3 * 4 + c) * 64 + ln][rr];
+      const float gs = W.bias != nullptr ? g4 + bias_g[q] : g4;
+      const float us = W.bias != nullptr ? u4 + bias_u[q] : u4;
+      if (pe[q] >= 0) {
+        const float h = act_fn(a.L.act, gs, us, a.L.swiglu_alpha, a.L.swiglu_limit);
+        store_scalar(a.hbuf, (size_t)pe[q] * a.Imax + it * NT + j, FTM_DT_BF16, h);
+      }
+    }
+    __syncthreads();
+  }
+}
+
+// Layers the GPTQ decode stage A with activations in LDS takes.
+static bool gq_ok(const ftm_moe_layer& L, int T) {
+  const ftm_proj& A = L.w13;
+  if (A.fmt != FTM_FMT_GPTQ_INT4 || L.act_dtype != FTM_DT_BF16 || A.group != 128) return false;
+  if (L.hidden % 128 != 0 || L.inter % 64 != 0 || T > kGqMaxT) return false;
+  return (L.hidden / 128 + 1) / 2 * 128 <= kGqMaxKR;  // half of the K groups per wave
+}
+
+__global__ __launch_bounds__(kBlock) void k_stage_a_gq(const LayerArgs a) {
+  constexpr int NT = 64;
+  __shared__ f32x4 red[4 * 2 * 4 * 64];  // also the shared-expert body's reduction buffer
+  const int I = a.L.inter;
+  const int tilesR = I / NT;
+  int item = blockIdx.x;
+  const int u = min(item / tilesR, a.L.num_experts), it = item % tilesR;
+  const int e = sload_i32(a.uniq, u), cnt = sload_i32(a.ucnt, u);
+  const int nRouted = sload_i32(a.ctrl, kCtrlNRouted);
+  if (item < nRouted * tilesR) {
+    const int slot = a.L.slot_of_expert ? sload_i32(a.L.slot_of_expert, e) : e;
+    if (slot < 0 || slot >= a.L.w13.num_slots) {
+      if (threadIdx.x == 0) atomicOr(&a.ctrl[kCtrlError], 1);
+      return;
+    }
+    stage_a_gq<NT>(a, proj_slot(a.L.w13, slot), I, it, cnt, a.lists + (size_t)e * a.T, red);
+  } else {
+    item -= nRouted * tilesR;
+    const int Is = a.L.shared_inter;
+    if (Is <= 0 || item >= Is / 16) return;
+    const ProjSlot W = shared_view(a.L.shared_w13, 2 * Is, a.L.hidden);
+    stage_a_body<FTM_FMT_BF16, FTM_DT_BF16, 16>(a, W, Is, item, a.T, nullptr, a.L.topk, red);
+  }
+}
+
 // ---------------------------------------------------------------- stage A, K-major formats
 // Work item: 8 channels of one expert = 16 weight rows (the 8 gate rows and
 // their 8 up rows), K split over the 4 waves of a workgroup and reduced
@@ -2110,7 +2337,12 @@ static void launch_stages(const LayerArgs& a, int gridA, int gridB, hipStream_t 
   }
   if (which & 1) {
     if constexpr (FMT == FTM_FMT_GPTQ_INT4) {
-      hipLaunchKernelGGL((k_stage_a<FMT, AT>), dim3(gridA), dim3(kBlock), 0, st, a);
+      if (gq_ok(a.L, a.T) && AT == FTM_DT_BF16) {
+        const size_t lds = 4u * (kGqXT + 1) * (size_t)gq_pitch(kGqMaxKR) * 2u;
+        hipLaunchKernelGGL(k_stage_a_gq, dim3(gridA), dim3(kBlock), lds, st, a);
+      } else {
+        hipLaunchKernelGGL((k_stage_a<FMT, AT>), dim3(gridA), dim3(kBlock), 0, st, a);
+      }
     } else {
       // one workgroup per 8-channel item (routed upper bound + shared)
       const int maxU = a.L.num_experts < a.T * a.L.topk ? a.L.num_experts : a.T * a.L.topk;
@@ -2203,7 +2435,7 @@ static const char* expert_kernel_name(const ftm_moe_layer& L, int T, int stage) 
   const bool lean = FMT == FTM_FMT_FP8_BLOCK && AT == FTM_DT_BF16 && lean_ok(L, T);
   if (stage == FTM_STAGE_W13) {
     if (lean) return lean_route_ok(L, T) ? "k_stage_a_lean_route" : "k_stage_a_lean";
-    if (FMT == FTM_FMT_GPTQ_INT4) return "k_stage_a";
+    if (FMT == FTM_FMT_GPTQ_INT4) return AT == FTM_DT_BF16 && gq_ok(L, T) ? "k_stage_a_gq" : "k_stage_a";
     return xl_plan_a<FMT, AT>(L, T).ok ? "k_stage_a_xl" : "k_stage_a_rows";
   }
   if (lean) return L.topk + (L.shared_inter > 0 ? 1 : 0) <= kBcMaxKP && T <= kBcMaxT ? "k_stage_bc_lean" : "k_stage_b_lean";

@@ -154,5 +154,17 @@ def test_stage_kernel_names_follow_the_dispatch():
     assert name(small, 5, nat.STAGE_W13) == "k_stage_a_rows"
     assert name(small, 5, nat.STAGE_W2) == "k_stage_b"
     assert name(small, 64, nat.STAGE_W13) == "k_gemm_a_ring"
+    # GPTQ group 128: activation rows in LDS up to 16 tokens while half of the
+    # hidden size fits a wave's K range (1024), the register-fed kernel above
+    gq = _layer(E=128, H=2048, I=768, k=8)
+    gq.w13 = _proj(N=2 * 768, K=2048, num_slots=8, fmt=nat.FMT_GPTQ_INT4, z=0x3000)
+    gq.w2 = _proj(N=2048, K=768, num_slots=8, fmt=nat.FMT_GPTQ_INT4, z=0x3000)
+    for T in (1, 4, 16):
+        assert name(gq, T, nat.STAGE_W13) == "k_stage_a_gq", T
+    assert name(gq, 17, nat.STAGE_W13) == "k_stage_a"
+    assert name(gq, 16, nat.STAGE_W2) == "k_stage_b"
+    gq.hidden = 2176  # 17 groups: a wave's half would be 1152 wide
+    gq.w13.K, gq.w2.N = 2176, 2176
+    assert name(gq, 4, nat.STAGE_W13) == "k_stage_a"
     f32 = _layer(E=8, H=256, I=128, k=2, act_dtype=nat.DT_F32)
     assert name(f32, 4, nat.STAGE_W13) is None  # f32 activations need the bf16 router: invalid layer

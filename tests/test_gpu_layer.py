@@ -78,6 +78,20 @@ def test_c3_fp8_full_shape_matches_oracle(gpu, c3_full, T):
     _run_and_check(syn, gpu)
 
 
+@pytest.fixture(scope="module")
+def c2_full():
+    return S.generate(S.CONFIGS["c2_gptq"], T=64, seed=1)
+
+
+@pytest.mark.parametrize("T", [1, 16, 64])
+def test_c2_gptq_full_shape_matches_oracle(gpu, c2_full, T):
+    """GPTQ int4 g128 at the C2 shape (128 experts, top-8): the decode stage A
+    with activations in LDS (8 groups per wave) up to T = 64."""
+    base = c2_full
+    syn = S.SyntheticLayer(base.cfg, base.bank, base.gate_w, base.x[:T].contiguous(), shared=base.shared)
+    _run_and_check(syn, gpu)
+
+
 def test_c1_int8_full_shape_matches_oracle(gpu):
     syn = S.generate(S.CONFIGS["c1_int8"], T=4, seed=0)
     _run_and_check(syn, gpu)
