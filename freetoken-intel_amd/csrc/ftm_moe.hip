@@ -587,10 +587,10 @@ __device__ __forceinline__ void compact_experts(const LayerArgs& a, int32_t* cnt
 // t = w, w + 16, ...) with per-expert counters in LDS, then compacts.  No
 // cross-workgroup traffic, so no device-scope fences.  Measured on MI355X
 // (C3, 256 experts, top-8): 6.1 us at T <= 4 against 7.9-8.9 us for the
-// multi-workgroup kernel; from T = 16 on the multi-workgroup kernel wins
-// (9.2 vs 9.9 us at 16, 13.6 vs 103 us at 256), so the cut sits at 8.
+// multi-workgroup kernel, 8.1 against 9.3 at 12; from T = 16 on the
+// multi-workgroup kernel wins (9.2 vs 9.9 us at 16, 13.6 vs 103 us at 256).
 constexpr int kTopk1Waves = 16;
-constexpr int kTopk1MaxT = 8;
+constexpr int kTopk1MaxT = 12;
 
 template <int MODE, int NV>
 __global__ __launch_bounds__(64 * kTopk1Waves) void k_topk1(const LayerArgs a, const void* logits_in,
@@ -1922,11 +1922,12 @@ __global__ __launch_bounds__(kBlock) void k_stage_a_lean_route(const LayerArgs a
 // Stage B item: 64 output columns of one expert, wave w owns 16 of them over
 // the full K (= I routed / Is shared); y = acc * router weight -> slot buffer.
 // col0: first of the wave's ncols (16 or 8) output columns; wv: the wave's LDS
-// region; s_y: null -> slot buffer rows, else LDS s_y[pair * 16 + column].
+// region; s_y: null -> slot buffer rows, else LDS s_y[pair * 16 + column];
+// token blocks from mb0 (a multiple of kLeanXT) up to cnt.
 template <bool FP8, int KB, int NWIN>
 __device__ void lean_b_item(const LayerArgs& a, const char* w, const float* sc, int cnt, const ExpertRec* rec,
                             const int32_t* list, int shared_col, int col0, int wv, float* s_y = nullptr,
-                            int ncols = 16) {
+                            int ncols = 16, int mb0 = 0) {
   constexpr int NLW = (FP8 ? KB / 64 : KB / 32) / NWIN;
   constexpr int NP = FP8 ? NLW / 2 : 1;
   static_assert(!FP8 || NWIN == 1, "FP8 rows: one window per wave");
@@ -1948,7 +1949,7 @@ __device__ void lean_b_item(const LayerArgs& a, const char* w, const float* sc, 
   constexpr int pitch = lean_pitch(KB);
   uint16_t* xw = ftm_xl_lds + wv * (kLeanXT + 1) * pitch;
   for (int e = 8 * lane; e < KB; e += 8 * 64) *(u32x4*)(xw + kLeanXT * pitch + e) = (u32x4){0u, 0u, 0u, 0u};
-  for (int mb = 0; mb < cnt; mb += kLeanXT) {
+  for (int mb = mb0; mb < cnt; mb += kLeanXT) {
     const int nb = min(kLeanXT, cnt - mb);
     int pr[kLeanXT];
     lean_pairs(a, rec, list, shared_col, cnt, mb, pr);
@@ -1962,7 +1963,7 @@ __device__ void lean_b_item(const LayerArgs& a, const char* w, const float* sc, 
     for (int i = 0; i < NP; ++i) part[i] = (f32x4){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int wi = 0; wi < NWIN; ++wi) {
-      if (wi > 0 || (NWIN > 1 && mb > 0)) lean_issue<NLW>(wres, wrow, row_bytes, 0u, wi * NLW, S);
+      if (wi > 0 || (NWIN > 1 && mb > mb0)) lean_issue<NLW>(wres, wrow, row_bytes, 0u, wi * NLW, S);
       __builtin_amdgcn_s_waitcnt(0);  // weights and this wave's LDS rows have landed
       lean_mfma<FP8, NLW, NP>(S, xrow, wi * NLW * (FP8 ? 64 : 32), part, 0);
     }
@@ -2018,11 +2019,18 @@ __global__ __launch_bounds__(kBlock) void k_stage_b_lean(const LayerArgs a) {
 }
 
 // ---- stage B and the combine in one launch for T <= kBcMaxT (lean kernels):
-// one workgroup of kBcWaves waves per kBcCols output columns.  Wave w takes the
-// routed experts u = w, w + kBcWaves, ... and the shared expert (u =
-// nRouted); their router-weighted rows land in LDS by pair, and the workgroup
-// sums each token's slots in slot order (k_combine's order and rounding) into
-// the output.  Saves the combine launch and the slot buffer's round trip.
+// one workgroup of kBcWaves waves per kBcCols output columns.  Its units are
+// the shared expert's blocks of kLeanXT tokens (first: each takes every token
+// of its block, and as one unit they made the longest wave) and then the
+// routed experts; wave w takes units w, w + kBcWaves, ...  Their
+// router-weighted rows land in LDS by pair, and the workgroup sums each
+// token's slots in slot order (k_combine's order and rounding) into the
+// output.  Saves the combine launch and the slot buffer's round trip.
+// Measured on MI355X (C3), stage B + combine with the shared expert as one
+// unit against split by token block: T=8 17.2 -> 15.8 us, T=16 25.5 -> 24.0.
+// Neither a software pipeline over a wave's experts (8 waves, 198 VGPRs: the
+// compiler's vmcnt tracking across the loop still serialises the loads; 18.3
+// and 28.9 us) nor 16 waves (128 VGPRs; 18.6 and 28.1 us) was faster.
 constexpr int kBcWaves = 12;  // 768 threads: 170 VGPRs per lane (16 waves spill at 128)
 constexpr int kBcCols = 8;    // output columns per workgroup: H / 8 workgroups fill the CUs
 // Measured on MI355X (C3), stage B + combine: T=5 12.7 us against 12.2 + 4.8,
@@ -2040,10 +2048,11 @@ __global__ __launch_bounds__(64 * kBcWaves) void k_stage_bc_lean(const LayerArgs
   for (int i = threadIdx.x; i < T * KP * 16; i += 64 * kBcWaves) s_y[i] = 0.0f;
   __syncthreads();
   const int nRouted = sload_i32(a.ctrl, kCtrlNRouted);
-  const int nU = nRouted + (a.L.shared_inter > 0 ? 1 : 0);
-  for (int u = wv; u < nU; u += kBcWaves) {
-    if (u < nRouted) {
-      const ExpertRec rec = load_rec(a, u);
+  const int nSh = a.L.shared_inter > 0 ? (T + kLeanXT - 1) / kLeanXT : 0;
+  const int nU = nSh + nRouted;
+  for (int uu = wv; uu < nU; uu += kBcWaves) {
+    if (uu >= nSh) {
+      const ExpertRec rec = load_rec(a, uu - nSh);
       if (rec.slot < 0 || rec.slot >= a.L.w2.num_slots) {  // non-resident: contributes zeros
         if ((threadIdx.x & 63) == 0) atomicOr(&a.ctrl[kCtrlError], 1);
         continue;
@@ -2052,8 +2061,8 @@ __global__ __launch_bounds__(64 * kBcWaves) void k_stage_bc_lean(const LayerArgs
       const float* sc = (const float*)((const char*)a.L.w2.s + (int64_t)rec.slot * a.L.w2.s_stride);
       lean_b_item<true, KB, 1>(a, w, sc, rec.cnt, &rec, a.lists + (size_t)rec.e * T, 0, col0, wv, s_y, kBcCols);
     } else {
-      lean_b_item<false, KB, NWS>(a, (const char*)a.L.shared_w2, nullptr, T, nullptr, nullptr, a.L.topk, col0, wv,
-                                  s_y, kBcCols);
+      lean_b_item<false, KB, NWS>(a, (const char*)a.L.shared_w2, nullptr, min(T, (uu + 1) * kLeanXT), nullptr,
+                                  nullptr, a.L.topk, col0, wv, s_y, kBcCols, uu * kLeanXT);
     }
   }
   __syncthreads();
