@@ -132,7 +132,18 @@ EXPORTED = (
     "ftm_lru_ensure",
     "ftm_lru_materialize",
     "ftm_copy_slots",
+    "ftm_lru_ensure_dev",
+    "ftm_copy_slots_dev",
 )
+
+
+class FtmBankCopy(ctypes.Structure):
+    """``ftm_bank_copy`` (include/ftmoe.h)."""
+    _fields_ = [
+        ("host_bank", ctypes.c_void_p),
+        ("dev_pool", ctypes.c_void_p),
+        ("row_bytes", ctypes.c_int64),
+    ]
 
 _lib: Optional[ctypes.CDLL] = None
 
@@ -179,6 +190,11 @@ def lib() -> ctypes.CDLL:
     L.ftm_lru_materialize.argtypes = [i32, i32, i32, i32, vp, vp, vp, vp, vp, vp, vp]
     L.ftm_copy_slots.restype = ctypes.c_int
     L.ftm_copy_slots.argtypes = [vp, vp, i64, vp, vp, i32, vp, vp]
+    L.ftm_lru_ensure_dev.restype = ctypes.c_int
+    L.ftm_lru_ensure_dev.argtypes = [i32, i32, i32, i32, vp, i32, i32, i32, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp,
+                                     vp]
+    L.ftm_copy_slots_dev.restype = ctypes.c_int
+    L.ftm_copy_slots_dev.argtypes = [ctypes.POINTER(FtmBankCopy), i32, i32, i32, vp, vp, vp, i32, vp]
     _lib = L
     return L
 

@@ -78,12 +78,26 @@ class OffloadMoeCache:
         decode_only: allow ``cache_size < num_experts`` (a pool that never holds
             a whole layer, e.g. 64 slots for 256 experts); :meth:`materialize_layer`
             then refuses.  Not in the reference, whose pool always fits a layer.
+        device_lru: keep the LRU state (``slot_for_id``, ``id_of_slot``,
+            ``usage``, ``step``, the plan and the miss counters) in device memory
+            and run :meth:`ensure_experts` and :meth:`copy_missing` as GPU kernels
+            (``ftm_lru_ensure_dev``, ``ftm_copy_slots_dev``): the routed ids never
+            travel to the host, so a decode step is enqueued without a
+            synchronisation.  The state after every call equals the host LRU's.
+            Out-of-range ids cannot raise at the call; they are ignored and
+            recorded for :meth:`check_status`.  Upstream's device-side
+            ``lru_ensure`` (offload_cache.py:14-30); the reference port has none.
     """
 
     def __init__(self, num_layers: int, num_experts: int, cache_size: int, device, quant_format: str = "bf16",
-                 prefill_overlap: bool = False, *, decode_only: bool = False) -> None:
+                 prefill_overlap: bool = False, *, decode_only: bool = False, device_lru: bool = False) -> None:
         if quant_format not in _BANK_SCHEMAS:
             raise ValueError(f"unknown quant_format {quant_format!r}")
+        self.device_lru = bool(device_lru)
+        if self.device_lru and torch.device(device).type != "cuda":
+            raise ValueError("device_lru keeps the LRU in GPU memory: the slot pool must live on a GPU")
+        if self.device_lru and num_experts > 512:
+            raise ValueError(f"device_lru handles at most 512 experts per layer, got {num_experts}")
         self.decode_only = decode_only
         if cache_size < 2 or (cache_size < num_experts and not decode_only):
             raise ValueError(
@@ -99,9 +113,15 @@ class OffloadMoeCache:
         self.prefill_overlap = prefill_overlap
         self._alloc_bookkeeping(cache_size)
         self.active_mask = torch.zeros((num_experts,), dtype=torch.int32)
-        self.step = torch.zeros((), dtype=torch.int64)
-        self.stat_missing = torch.zeros((), dtype=torch.int64)
-        self.stat_calls = torch.zeros((), dtype=torch.int64)
+        sdev = self.device if self.device_lru else "cpu"
+        self.step = torch.zeros((), dtype=torch.int64, device=sdev)
+        self._stats = torch.zeros((2,), dtype=torch.int64, device=sdev)  # misses, calls
+        self.stat_missing = self._stats[0]
+        self.stat_calls = self._stats[1]
+        self._status = torch.zeros((1,), dtype=torch.int32, device=sdev)
+        self._max_staged = 0
+        self._copy_descs: dict = {}
+        self._pool_layers: dict = {}
         self.bank_sources: dict = {}
         self.bank_caches: dict = {}
         self.banks: list = []
@@ -113,14 +133,15 @@ class OffloadMoeCache:
         self._slot_dev: Optional[torch.Tensor] = None  # device mirror of slot_for_id
 
     def _alloc_bookkeeping(self, cache_size: int) -> None:
-        self.slot_for_id = torch.full((self.num_layers, self.num_experts), -1, dtype=torch.int32)
-        self.id_of_slot = torch.full((cache_size,), -1, dtype=torch.int32)
-        self.usage = torch.zeros((cache_size,), dtype=torch.int64)
+        dev = self.device if self.device_lru else "cpu"
+        self.slot_for_id = torch.full((self.num_layers, self.num_experts), -1, dtype=torch.int32, device=dev)
+        self.id_of_slot = torch.full((cache_size,), -1, dtype=torch.int32, device=dev)
+        self.usage = torch.zeros((cache_size,), dtype=torch.int64, device=dev)
         plan = max(self.num_experts, cache_size)
-        self.evict_slots = torch.zeros((plan,), dtype=torch.int32)
-        self.src_indices = torch.zeros((plan,), dtype=torch.int32)
+        self.evict_slots = torch.zeros((plan,), dtype=torch.int32, device=dev)
+        self.src_indices = torch.zeros((plan,), dtype=torch.int32, device=dev)
         self.num_indices = torch.zeros((1,), dtype=torch.int64)
-        self._staged = torch.zeros((1,), dtype=torch.int32)
+        self._staged = torch.zeros((1,), dtype=torch.int32, device=dev)
 
     # -- bank wiring ---------------------------------------------------------------
 
@@ -159,6 +180,8 @@ class OffloadMoeCache:
             self.bank_sources[bank] = hosts
             self.bank_caches[bank] = cache
             self.banks.append((hosts, cache))
+        self._copy_descs = {}
+        self._pool_layers = {}
 
     def set_extra_metadata(self, name: str, per_layer: list) -> None:
         if len(per_layer) != self.num_layers:
@@ -181,6 +204,8 @@ class OffloadMoeCache:
                 self.bank_caches[bank] = torch.zeros((cache_size, *hosts[0].shape[1:]), dtype=hosts[0].dtype,
                                                      device=self.device)
             self.banks = [(self.bank_sources[b], self.bank_caches[b]) for b in self.bank_schema]
+        self._copy_descs = {}
+        self._pool_layers = {}
         self.step.zero_()
         self.active_mask.zero_()
         self._pending_src_layer = None
@@ -222,8 +247,19 @@ class OffloadMoeCache:
         self.reset_stats()
 
     def reset_stats(self) -> None:
-        self.stat_missing.zero_()
-        self.stat_calls.zero_()
+        self._stats.zero_()
+
+    def check_status(self) -> None:
+        """``device_lru``: raise what the host LRU raises at the call for the
+        errors the kernel recorded since the last check (waits for the GPU)."""
+        if not self.device_lru:
+            return
+        st = int(self._status.item())
+        self._status.zero_()
+        if st & 1:
+            raise ValueError(f"expert ids must lie in [0, {self.num_experts})")
+        if st & 2:
+            raise RuntimeError("slot_for_id held a slot outside the pool (the expert was reloaded)")
 
     def decode_miss_stats(self) -> dict:
         return {"missing": int(self.stat_missing.item()), "calls": int(self.stat_calls.item())}
@@ -245,6 +281,22 @@ class OffloadMoeCache:
             raise ValueError(f"cache_size {self.cache_size} < num_experts {self.num_experts}: "
                              "cannot materialize a whole layer")
         self.active_mask.fill_(1)
+        if self.device_lru:  # prefill is rare: plan on the host copies, then put the state back
+            host = [t.cpu() for t in (self.slot_for_id, self.id_of_slot, self.usage, self.step, self.evict_slots,
+                                      self.src_indices, self._staged)]
+            rc = nat.lib().ftm_lru_materialize(layer_id, self.num_layers, self.num_experts, self.cache_size,
+                                               *(t.data_ptr() for t in host))
+            nat.check(rc, "ftm_lru_materialize")
+            for dst, src in zip((self.slot_for_id, self.id_of_slot, self.usage, self.step, self.evict_slots,
+                                 self.src_indices, self._staged), host):
+                dst.copy_(src)
+            staged = int(host[-1][0])
+            self._stats += torch.tensor([staged, 1], dtype=torch.int64, device=self.device)
+            self._max_staged = staged
+            self.num_indices.fill_(staged)
+            self._pending_src_layer = layer_id
+            self._pending_whole_layer = True
+            return
         rc = nat.lib().ftm_lru_materialize(layer_id, self.num_layers, self.num_experts, self.cache_size,
                                            *self._lru_args())
         nat.check(rc, "ftm_lru_materialize")
@@ -262,6 +314,9 @@ class OffloadMoeCache:
                 f"cache_size {self.cache_size} < 2: the pool cannot hold a routed expert plus "
                 "a victim to evict; raise moe_cache_size"
             )
+        if self.device_lru:
+            self.ensure_experts_chunk(layer_id, expert_ids, 0, self.num_experts)
+            return
         ids = expert_ids.reshape(-1).to("cpu", torch.int64).contiguous()
         if ids.numel() and (int(ids.min()) < 0 or int(ids.max()) >= self.num_experts):
             raise ValueError(f"expert ids must lie in [0, {self.num_experts})")
@@ -273,6 +328,38 @@ class OffloadMoeCache:
                                       *self._lru_args())
         nat.check(rc, "ftm_lru_ensure")
         self._after_plan(layer_id, int(self._staged[0]), whole=False)
+
+    def ensure_experts_chunk(self, layer_id: int, expert_ids: torch.Tensor, chunk: int, chunk_cap: int,
+                             want_ids: bool = False) -> Optional[torch.Tensor]:
+        """``device_lru``: :meth:`ensure_experts` for the routed experts of ranks
+        ``[chunk * chunk_cap, (chunk + 1) * chunk_cap)`` in ascending id (chunk 0
+        is always an LRU step; a later chunk past the last routed expert changes
+        nothing), on the current stream.  ``want_ids``: also return
+        ``expert_ids`` with every pair outside the chunk set to -1 (int32, same
+        shape).  Ids < 0 are pairs without an expert."""
+        if not self.device_lru:
+            raise RuntimeError("ensure_experts_chunk runs the device LRU (device_lru=True)")
+        if not (0 <= layer_id < self.num_layers):
+            raise ValueError(f"Invalid layer id {layer_id}")
+        if self.banks and self.cache_size < 2:
+            raise RuntimeError(
+                f"cache_size {self.cache_size} < 2: the pool cannot hold a routed expert plus "
+                "a victim to evict; raise moe_cache_size"
+            )
+        ids = expert_ids.to(self.device, torch.int32).contiguous()
+        n = ids.numel()
+        ids_c = torch.empty_like(ids) if want_ids else None
+        rc = nat.lib().ftm_lru_ensure_dev(
+            layer_id, self.num_layers, self.num_experts, self.cache_size, ids.data_ptr() if n else None, n,
+            int(chunk), int(chunk_cap), self.slot_for_id.data_ptr(), self.id_of_slot.data_ptr(),
+            self.usage.data_ptr(), self.step.data_ptr(), self.evict_slots.data_ptr(), self.src_indices.data_ptr(),
+            self._staged.data_ptr(), ids_c.data_ptr() if ids_c is not None else None, self._stats.data_ptr(),
+            self._status.data_ptr(), torch.cuda.current_stream(self.device).cuda_stream)
+        nat.check(rc, "ftm_lru_ensure_dev")
+        self._max_staged = min(self.num_experts, int(chunk_cap), n)
+        self._pending_src_layer = layer_id
+        self._pending_whole_layer = False
+        return ids_c
 
     def _after_plan(self, layer_id: int, staged: int, whole: bool) -> None:
         self.num_indices.fill_(staged)
@@ -296,6 +383,24 @@ class OffloadMoeCache:
             return
         if not self.is_gpu:
             raise RuntimeError("copy_missing streams into a GPU slot pool; this cache lives on the CPU")
+        if self.device_lru:
+            # the plan stays in device memory: one kernel reads it and pulls the rows of every bank
+            descs = self._copy_descs.get(layer_id)
+            if descs is None:
+                descs = (nat.FtmBankCopy * len(self.banks))()
+                for j, (hosts, cache) in enumerate(self.banks):
+                    host = hosts[layer_id]
+                    descs[j] = nat.FtmBankCopy(host.data_ptr(), cache.data_ptr(), host[0].numel() * host.element_size())
+                self._copy_descs[layer_id] = descs
+            if self._max_staged:
+                rc = nat.lib().ftm_copy_slots_dev(descs, len(self.banks), self.num_experts, self.cache_size,
+                                                  self.evict_slots.data_ptr(), self.src_indices.data_ptr(),
+                                                  self._staged.data_ptr(), self._max_staged,
+                                                  torch.cuda.current_stream(self.device).cuda_stream)
+                nat.check(rc, "ftm_copy_slots_dev")
+            self._pending_src_layer = None
+            self._pending_whole_layer = False
+            return
         n = int(self.num_indices.item())
         if n:
             cur = torch.cuda.current_stream(self.device)
@@ -321,6 +426,8 @@ class OffloadMoeCache:
     def slot_of_expert(self, layer_id: int) -> torch.Tensor:
         """Device ``int32 [E]``: the slot holding each expert of ``layer_id``, -1 if
         not resident (what the layer kernels read)."""
+        if self.device_lru:
+            return self.slot_for_id[layer_id]
         if self._slot_dev is None:
             src = self.slot_for_id.pin_memory() if self.is_gpu else self.slot_for_id
             self._slot_dev = src.to(self.device, non_blocking=True)
@@ -329,7 +436,7 @@ class OffloadMoeCache:
     def resident_slots(self, layer_id: int) -> list:
         E = self.num_experts
         base = layer_id * E
-        ids = self.id_of_slot
+        ids = self.id_of_slot.cpu()
         return [s for s in range(self.cache_size) if base <= int(ids[s]) < base + E]
 
 
@@ -490,8 +597,11 @@ def moe_grouped_forward(flat: torch.Tensor, top_idx: torch.Tensor, top_w: torch.
     been made resident with :meth:`OffloadMoeCache.ensure_experts` and
     :meth:`~OffloadMoeCache.copy_missing` (a routed expert that is not resident
     contributes zeros and sets the workspace error bit)."""
-    acc = SlotWeightAccessor(cache, intermediate, flat.dtype)
-    pool = acc.pool_layer()
+    key = (int(intermediate), flat.dtype)
+    pool = cache._pool_layers.get(key)
+    if pool is None:  # the pool's projections, built once per bank registration
+        pool = SlotWeightAccessor(cache, intermediate, flat.dtype).pool_layer()
+        cache._pool_layers[key] = pool
     from ..layer import MoeLayer
 
     layer = MoeLayer(w13=pool.w13, w2=pool.w2, num_experts=cache.num_experts, hidden=pool.hidden,
@@ -519,7 +629,31 @@ def moe_offload_forward(flat: torch.Tensor, top_idx: torch.Tensor, top_w: torch.
     computed; against a single call the chunked sum differs only by the
     rounding of each chunk's output to the activation dtype.  ``ids_host``: a
     host copy of ``top_idx`` when the caller has one (saves the device read
-    the LRU planning needs)."""
+    the LRU planning needs).
+
+    With ``cache.device_lru`` the planning runs on the GPU and nothing is read
+    back: the number of distinct experts is not known on the host, so the step
+    runs ``ceil(min(T*k, E) / cache_size)`` chunk calls (ranks ``[c * S,
+    (c + 1) * S)``; a chunk past the last distinct expert changes nothing and
+    adds zeros).  The result and the LRU state equal the host path's."""
+    if cache.device_lru:
+        cap = cache.cache_size
+        ids32 = top_idx.to(torch.int32)
+        nchunks = max(1, -(-min(ids32.numel(), cache.num_experts) // cap))
+        if nchunks == 1:
+            cache.ensure_experts_chunk(layer_id, ids32, 0, cap)
+            cache.copy_missing()
+            return moe_grouped_forward(flat, top_idx, top_w, cache, layer_id, intermediate=intermediate, act=act,
+                                       shared=shared, swiglu_alpha=swiglu_alpha, swiglu_limit=swiglu_limit)
+        acc = None
+        for c in range(nchunks):
+            ids_c = cache.ensure_experts_chunk(layer_id, ids32, c, cap, want_ids=True)
+            cache.copy_missing()
+            out_c = moe_grouped_forward(flat, ids_c, top_w, cache, layer_id, intermediate=intermediate, act=act,
+                                        shared=shared if c == 0 else None, swiglu_alpha=swiglu_alpha,
+                                        swiglu_limit=swiglu_limit)
+            acc = out_c.float() if acc is None else acc + out_c.float()
+        return acc.to(flat.dtype)
     ids_host = (top_idx if ids_host is None else ids_host).reshape(-1).to("cpu", torch.int64)
     uniq = torch.unique(ids_host)
     cap = cache.cache_size

@@ -254,6 +254,51 @@ int ftm_copy_slots(void* dev_pool, const void* host_bank, int64_t row_bytes,
                    const int32_t* evict_slots, const int32_t* src_rows, int32_t n,
                    void* stream, void* done_event);
 
+/* ---- the same LRU and copy engine on the GPU (no host round trip) ----
+ * Upstream's device-side lru_ensure (described at offload_cache.py:14-30) and
+ * the batched copy its port leaves as stubs (python/freetoken/kernel/sycl/
+ * batch_memcpy.py:11-12, python/freetoken/kernel/sycl/index.py:11-12). */
+
+/* ensure_experts (offload_cache.py:560-647) as one kernel on `stream` over
+ * device-resident state: slot_for_id [L*E] int32, id_of_slot [S] int32,
+ * usage [S] int64, step [1] int64, the plan evict_slots / src_rows [>= E]
+ * int32 and num_staged [1] int32 (all device memory, updated in place; the
+ * same values ftm_lru_ensure computes).  expert_ids [n] int32 device: the
+ * routed ids of the step (ids < 0 are pairs without an expert; ids >= E set
+ * status bit 1 and are ignored).  The call takes the routed experts of ranks
+ * [chunk * chunk_cap, (chunk + 1) * chunk_cap) in ascending id; chunk 0
+ * is always an LRU step (as a call with no routed expert is), a later chunk
+ * past the last routed expert changes nothing (num_staged = 0).  ids_chunk [n] int32 (device, may
+ * be NULL): each pair's id if its expert is in the chunk, else -1.  stats
+ * [2] int64 (device, may be NULL): += misses, += 1 call.  status [1] int32
+ * (device, may be NULL): error bits OR-ed in.  num_experts <= 512,
+ * cache_size <= 2^21. */
+int ftm_lru_ensure_dev(int32_t layer_id, int32_t num_layers, int32_t num_experts,
+                       int32_t cache_size, const int32_t* expert_ids, int32_t n,
+                       int32_t chunk, int32_t chunk_cap, int32_t* slot_for_id,
+                       int32_t* id_of_slot, int64_t* usage, int64_t* step,
+                       int32_t* evict_slots, int32_t* src_rows, int32_t* num_staged,
+                       int32_t* ids_chunk, int64_t* stats, int32_t* status, void* stream);
+
+/* One bank of a layer for ftm_copy_slots_dev: host_bank (pinned host memory,
+ * rows of row_bytes) -> dev_pool (slot rows of row_bytes). */
+typedef struct ftm_bank_copy {
+  const void* host_bank;
+  void* dev_pool;
+  int64_t row_bytes;
+} ftm_bank_copy;
+
+/* copy_missing (offload_cache.py:651-674) as one kernel on `stream`: for i <
+ * min(*num_staged, max_rows) (device values, as ftm_lru_ensure_dev leaves
+ * them), row src_rows[i] of every bank -> slot evict_slots[i], read from the
+ * pinned host banks by the kernel.  Plan entries outside [0, host_rows) /
+ * [0, pool_slots) are skipped.  Up to 8 banks; a host bank that is not
+ * pinned, mapped host memory returns FTM_ERR_HIP before anything is
+ * launched. */
+int ftm_copy_slots_dev(const ftm_bank_copy* banks, int32_t num_banks, int32_t host_rows,
+                       int32_t pool_slots, const int32_t* evict_slots, const int32_t* src_rows,
+                       const int32_t* num_staged, int32_t max_rows, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -436,3 +436,80 @@ def ref_cpu_moe_forward_fast(x: np.ndarray, ids: np.ndarray, w: np.ndarray, gate
     if rc != 0:
         raise RuntimeError(f"freetoken_cpu_moe_forward_fast rc={rc}")
     return out
+
+
+# ----------------------------------------------------------------- slot-pool LRU (pure Python)
+@dataclass
+class LruState:
+    """OffloadMoeCache's bookkeeping (python/freetoken/moe/offload_cache.py:218-694):
+    flat id = layer * E + expert."""
+    L: int
+    E: int
+    S: int
+    slot_for_id: list
+    id_of_slot: list
+    usage: list
+    step: int = 0
+    missing: int = 0
+    calls: int = 0
+
+
+def lru_new(L: int, E: int, S: int) -> LruState:
+    return LruState(L, E, S, [-1] * (L * E), [-1] * S, [0] * S)
+
+
+def lru_resync(st: LruState) -> None:
+    """_resync_slot_for_id (offload_cache.py:401-435): slot_for_id rebuilt from id_of_slot."""
+    st.slot_for_id = [-1] * (st.L * st.E)
+    for s, i in enumerate(st.id_of_slot):
+        if 0 <= i < st.L * st.E:
+            st.slot_for_id[i] = s
+
+
+def lru_ensure(st: LruState, layer_id: int, expert_ids) -> tuple:
+    """ensure_experts (offload_cache.py:560-647), statement by statement: the
+    routed experts in first-appearance order; step += 1; phase 1 stamps the
+    slot of every resident one; phase 2 takes the missing ones in ascending id,
+    each evicting ``min(range(S), key=(usage[s], s))`` and stamping it; then the
+    resync.  Returns the plan ``(evict_slots, src_rows)``."""
+    E, S, base = st.E, st.S, layer_id * st.E
+    seen = []
+    for e in expert_ids:
+        e = int(e)
+        if e not in seen:
+            seen.append(e)
+    step = st.step + 1
+    st.step = step
+    for e in seen:
+        s = st.slot_for_id[base + e]
+        if s != -1:
+            st.usage[s] = step
+    missing = sorted(e for e in seen if st.slot_for_id[base + e] == -1)
+    st.missing += len(missing)
+    st.calls += 1
+    evict, src = [], []
+    for e in missing:
+        victim = min(range(S), key=lambda s: (st.usage[s], s))
+        old = st.id_of_slot[victim]
+        if old >= 0:
+            st.slot_for_id[old] = -1
+        st.id_of_slot[victim] = base + e
+        st.slot_for_id[base + e] = victim
+        st.usage[victim] = step
+        evict.append(victim)
+        src.append(e)
+    lru_resync(st)
+    return evict, src
+
+
+def lru_ensure_chunk(st: LruState, layer_id: int, expert_ids, chunk: int, cap: int) -> tuple:
+    """The chunked decode step of this build's moe_offload_forward (not in the
+    reference): the distinct routed experts (ids >= 0) in ascending id, ranks
+    [chunk * cap, (chunk + 1) * cap) through :func:`lru_ensure`; chunk 0 is
+    always a call (an empty one still steps, as the reference's does), a later
+    empty chunk leaves the state alone.  Returns ``(plan or None, members)``."""
+    uniq = sorted({int(e) for e in expert_ids if int(e) >= 0})
+    members = uniq[chunk * cap:(chunk + 1) * cap]
+    if not members and chunk > 0:
+        return None, members
+    return lru_ensure(st, layer_id, members), members

@@ -113,6 +113,42 @@ def test_copy_slots_argument_errors():
     assert lib.ftm_copy_slots(ctypes.c_void_p(16), ctypes.c_void_p(32), 64, neg, ev, 1, None, None) == nat.ERR_DIM
 
 
+def test_device_lru_and_copy_argument_errors():
+    lib = nat.lib()
+    p = ctypes.c_void_p(0x1000)
+
+    def ens(L=2, E=8, S=4, layer=0, n=3, chunk=0, cap=8, ids=p, sfi=p):
+        return lib.ftm_lru_ensure_dev(layer, L, E, S, ids, n, chunk, cap, sfi, p, p, p, p, p, p, None, None, None,
+                                      None)
+
+    assert ens(E=0) == nat.ERR_DIM
+    assert ens(E=513) == nat.ERR_DIM  # one expert per thread of the workgroup
+    assert ens(S=0) == nat.ERR_DIM
+    assert ens(S=(1 << 21) + 1) == nat.ERR_DIM  # slot index packed in 21 bits
+    assert ens(layer=2) == nat.ERR_DIM
+    assert ens(n=-1) == nat.ERR_DIM
+    assert ens(chunk=-1) == nat.ERR_DIM
+    assert ens(cap=0) == nat.ERR_DIM
+    assert ens(ids=None) == nat.ERR_NULL
+    assert ens(sfi=None) == nat.ERR_NULL
+    B = nat.FtmBankCopy
+    one = (B * 1)(B(0x1000, 0x2000, 64))
+
+    def cp(banks=one, nb=1, rows=4, slots=4, ev=p, mx=2):
+        return lib.ftm_copy_slots_dev(banks, nb, rows, slots, ev, p, p, mx, None)
+
+    assert cp(nb=0) == nat.ERR_DIM
+    assert cp(nb=9) == nat.ERR_DIM
+    assert cp(rows=0) == nat.ERR_DIM
+    assert cp(slots=0) == nat.ERR_DIM
+    assert cp(mx=-1) == nat.ERR_DIM
+    assert cp(banks=None) == nat.ERR_NULL
+    assert cp(ev=None) == nat.ERR_NULL
+    assert cp(banks=(B * 1)(B(0x1000, 0x2000, 0))) == nat.ERR_DIM
+    assert cp(banks=(B * 1)(B(None, 0x2000, 64))) == nat.ERR_NULL
+    assert cp(mx=0) == nat.OK  # nothing to copy: no launch
+
+
 def test_stage_kernel_names_follow_the_dispatch():
     """ftm_moe_stage_kernel names the kernel each stage launches: the lean FP8
     decode stages for the 2048x512 shape below the token crossover, the tiled

@@ -225,3 +225,58 @@ def test_accessor_refuses_to_guess():
     with pytest.raises(ValueError, match="get_gptq_packed is gptq_int4-only"):
         acc.get_gptq_packed(0)
     assert acc.get_fp8_packed(1)[4] == 128
+
+
+# ---- the oracle's restatement of the LRU, and the native LRU against it
+
+def test_oracle_lru_known_answers():
+    """The reference's own cases (tests/test_moe_offload_cache.py:66-292, as
+    restated above for the product) through the oracle's literal restatement."""
+    import ftm_oracle as O
+
+    st = O.lru_new(L, E, E)
+    st.id_of_slot = list(range(E))
+    O.lru_resync(st)
+    st.usage, st.step = [10, 9, 8, 7], 10
+    evict, src = O.lru_ensure(st, 1, [3, 1, 1, 2])
+    assert src == [1, 2, 3] and evict == [3, 2, 1]
+    assert st.missing == 3 and st.calls == 1
+    st = O.lru_new(L, E, E)
+    st.id_of_slot = list(range(E))
+    O.lru_resync(st)
+    st.usage, st.step = [1, 2, 3, 4], 5
+    assert O.lru_ensure(st, 1, [0]) == ([0], [0])
+    assert st.slot_for_id[E + 0] == 0 and st.slot_for_id[0] == -1 and st.slot_for_id[1] == 1
+    # more misses than slots: once every slot carries this step, each further
+    # miss takes min (step, slot) = slot 0, and the last one keeps it
+    st = O.lru_new(1, 8, 3)
+    evict, src = O.lru_ensure(st, 0, [5, 1, 7, 2, 6])
+    assert src == [1, 2, 5, 6, 7] and evict == [0, 1, 2, 0, 0]
+    assert st.id_of_slot == [7, 2, 5]
+
+
+def _random_ids(rng, E, n):
+    return rng.randint(0, E, size=n).tolist()
+
+
+@pytest.mark.parametrize("Ln,En,Sn", [(3, 16, 5), (3, 16, 12), (2, 16, 40), (4, 8, 8)])
+def test_native_lru_matches_oracle_on_random_sequences(Ln, En, Sn):
+    import numpy as np
+
+    import ftm_oracle as O
+
+    rng = np.random.RandomState(Ln * 100 + En + Sn)
+    c = OffloadMoeCache(Ln, En, Sn, "cpu", decode_only=Sn < En)
+    st = O.lru_new(Ln, En, Sn)
+    for call in range(60):
+        layer = int(rng.randint(Ln))
+        ids = _random_ids(rng, En, int(rng.randint(1, 2 * En)))
+        c.ensure_experts(layer, torch.tensor(ids, dtype=torch.int64))
+        evict, src = O.lru_ensure(st, layer, ids)
+        n = int(c.num_indices.item())
+        assert n == len(evict), call
+        assert c.evict_slots[:n].tolist() == evict and c.src_indices[:n].tolist() == src, call
+        assert c.slot_for_id.reshape(-1).tolist() == st.slot_for_id, call
+        assert c.id_of_slot.tolist() == st.id_of_slot, call
+        assert c.usage.tolist() == st.usage and int(c.step) == st.step, call
+    assert c.decode_miss_stats() == {"missing": st.missing, "calls": st.calls}
