@@ -946,16 +946,17 @@ __device__ __forceinline__ void gq_group(const GqGroup& G, const uint16_t* xrow,
   }
 }
 
-// Copy elements [k0, k0 + kr) of the rows of pairs pr[0..nb) into xw (row r at xw + r * pitch).
-__device__ __forceinline__ void gq_fill(const int (&pr)[kGqXT], int nb, const void* src, int KP, int H, int k0,
-                                        int kr, int pitch, uint16_t* xw) {
+// Copy elements [k0, k0 + kr) of the rows of pairs pr[0..nb) into xw (row r
+// at xw + r * pitch); the row of pair p starts at src + (p / div) * row_elems.
+__device__ __forceinline__ void gq_fill(const int (&pr)[kGqXT], int nb, const void* src, int div, int row_elems,
+                                        int k0, int kr, int pitch, uint16_t* xw) {
   typedef __attribute__((address_space(1))) const void* GPtr;
   typedef __attribute__((address_space(3))) void* LPtr;
   const int lane = threadIdx.x & 63;
 #pragma unroll
   for (int r = 0; r < kGqXT; ++r) {
     if (r < nb) {
-      const char* row = (const char*)src + ((size_t)(pr[r] / KP) * (size_t)H + (size_t)k0) * 2u;
+      const char* row = (const char*)src + ((size_t)(pr[r] / div) * (size_t)row_elems + (size_t)k0) * 2u;
       for (int c = 0; c * 1024 < 2 * kr; ++c) {
         if (c * 1024 + 16 * lane < 2 * kr)
           __builtin_amdgcn_global_load_lds((GPtr)(row + c * 1024 + 16 * lane),
@@ -1089,6 +1090,150 @@ __global__ __launch_bounds__(kBlock) void k_stage_a_gq(const LayerArgs a) {
     if (Is <= 0 || item >= Is / 16) return;
     const ProjSlot W = shared_view(a.L.shared_w13, 2 * Is, a.L.hidden);
     stage_a_body<FTM_FMT_BF16, FTM_DT_BF16, 16>(a, W, Is, item, a.T, nullptr, a.L.topk, red);
+  }
+}
+
+// ---------------------------------------------------------------- stage B, GPTQ decode (h rows in LDS)
+// The data path of k_stage_a_gq for w2: an item is 128 output columns of one
+// expert; waves 0-1 take columns [0, 64) of it and waves 2-3 [64, 128), each
+// over half of the K groups (K = I), the next group's weights, scales and zero
+// word in flight while the current one is multiplied; the two halves are
+// summed through LDS, router-weighted, and written to the slot buffer rows
+// (k_combine sums them).
+constexpr int kGqNB = 128;  // output columns per stage-B item
+// Measured on C2 (w2, against the register-fed k_stage_b): T=4 18.6 -> 11.6
+// us, T=16 39.5 -> 29.3, T=24 46.3 -> 36.0, T=32 49.6 -> 41.0; T=64 55.3 ->
+// 56.5, so it stops at 32 tokens.
+constexpr int kGqBMaxT = 32;
+
+__device__ void stage_b_gq(const LayerArgs& a, const ProjSlot& W, int it, int cnt, const int32_t* list,
+                           f32x4* red) {
+  constexpr int EPI = kGqXT * kGqNB / kBlock;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  const int rl = lane & 15;
+  const int H = a.L.hidden, KP = a.KP, N = W.N;
+  const int tile = wave >> 1;
+  int lo, hi;
+  wave_k_range<FTM_FMT_GPTQ_INT4>(W, wave & 1, 2, lo, hi);
+  const int k0 = lo * 128, kr = (hi - lo) * 128;
+  const uint32_t sbytes = W.s_dt == FTM_DT_F32 ? 4u : 2u;
+  const int ngroups = (W.K + 127) / 128;
+  const Rsrc wres = make_rsrc(W.w, (uint32_t)(W.K / 8) * (uint32_t)N * 4u);
+  const Rsrc zres = make_rsrc(W.z, (uint32_t)ngroups * (uint32_t)(N / 8) * 4u);
+  const Rsrc sres = make_rsrc(W.s, (uint32_t)ngroups * (uint32_t)N * sbytes);
+  const int col0 = it * kGqNB + 64 * tile;
+  const uint32_t ncol = col0 + 4 * rl < N ? (uint32_t)(col0 + 4 * rl) : kOOB;
+  const Rsrc lres = make_rsrc(list, (uint32_t)cnt * 4u);
+  const Rsrc wtres = make_rsrc(a.wts, (uint32_t)a.T * (uint32_t)KP * 4u);
+  constexpr int pitch = gq_pitch(kGqMaxKR);
+  uint16_t* xw = ftm_xl_lds + wave * (kGqXT + 1) * pitch;
+  for (int e = 8 * lane; e < kGqMaxKR; e += 8 * 64) *(u32x4*)(xw + kGqXT * pitch + e) = (u32x4){0u, 0u, 0u, 0u};
+  float bias_n[EPI];
+#pragma unroll
+  for (int q = 0; q < EPI; ++q) {
+    const int n = it * kGqNB + (threadIdx.x + q * kBlock) % kGqNB;
+    bias_n[q] = (W.bias != nullptr && n < H) ? load_scalar(W.bias, n, W.bias_dt) : 0.0f;
+  }
+  for (int mb = 0; mb < cnt; mb += kGqXT) {
+    const int nb = min(kGqXT, cnt - mb);
+    int pr[kGqXT];
+#pragma unroll
+    for (int i = 0; i < kGqXT; ++i) pr[i] = pair_of_row(lres, true, mb + i, cnt, KP, 0);
+    int pe[EPI];
+    float we[EPI];
+#pragma unroll
+    for (int q = 0; q < EPI; ++q) {
+      const int i = (threadIdx.x + q * kBlock) / kGqNB;
+      pe[q] = pair_of_row(lres, true, mb + i, cnt, KP, 0);
+      we[q] = __uint_as_float(bload4(wtres, pe[q] >= 0 ? 4u * (uint32_t)pe[q] : kOOB));
+    }
+    f32x4 acc[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) acc[c] = (f32x4){0.f, 0.f, 0.f, 0.f};
+    if (hi > lo) {
+      GqGroup GA, GB;
+      gq_issue(wres, sres, zres, ncol, N, lo, sbytes, GA);       // weights first,
+      gq_fill(pr, nb, a.hbuf, 1, a.Imax, k0, kr, pitch, xw);     // then the h rows
+      const uint16_t* xrow = xw + (rl < nb ? rl : kGqXT) * pitch;
+      for (int grp = lo; grp < hi; grp += 2) {
+        const bool two = grp + 1 < hi;
+        if (two) {
+          gq_issue(wres, sres, zres, ncol, N, grp + 1, sbytes, GB);
+          wait_vm<kGqLoads>();
+        } else {
+          __builtin_amdgcn_s_waitcnt(0);
+        }
+        gq_group(GA, xrow, (grp - lo) * 128, ncol, sbytes, W.s_dt, acc);
+        if (two) {
+          if (grp + 2 < hi) {
+            gq_issue(wres, sres, zres, ncol, N, grp + 2, sbytes, GA);
+            wait_vm<kGqLoads>();
+          } else {
+            __builtin_amdgcn_s_waitcnt(0);
+          }
+          gq_group(GB, xrow, (grp + 1 - lo) * 128, ncol, sbytes, W.s_dt, acc);
+        }
+      }
+    }
+#pragma unroll
+    for (int c = 0; c < 4; ++c) red[(wave * 4 + c) * 64 + lane] = acc[c];
+    __syncthreads();
+#pragma unroll
+    for (int q = 0; q < EPI; ++q) {
+      const int idx = threadIdx.x + q * kBlock;
+      const int i = idx / kGqNB, j = idx % kGqNB;
+      const int t = j >> 6, jl = j & 63;
+      const int c = jl & 3, ln = (jl >> 2) + 16 * (i >> 2), rr = i & 3;
+      const int n = it * kGqNB + j;
+      float y = red[((2 * t) * 4 + c) * 64 + ln][rr] + red[((2 * t + 1) * 4 + c) * 64 + ln][rr];
+      if (pe[q] >= 0 && n < H) {
+        if (W.bias != nullptr) y += bias_n[q];
+        a.ybuf[(size_t)pe[q] * H + n] = y * we[q];
+      }
+    }
+    __syncthreads();
+  }
+}
+
+// Layers the GPTQ decode stage B with h rows in LDS takes.
+static bool gq_b_ok(const ftm_moe_layer& L, int T) {
+  const ftm_proj& B = L.w2;
+  if (B.fmt != FTM_FMT_GPTQ_INT4 || L.act_dtype != FTM_DT_BF16 || B.group != 128) return false;
+  if (L.hidden % kGqNB != 0 || L.inter % 128 != 0 || T > kGqBMaxT) return false;
+  return (L.inter / 128 + 1) / 2 * 128 <= kGqMaxKR;
+}
+
+template <int EFMT, int AT>
+__device__ void stage_b_body(const LayerArgs& a, const ProjSlot& W, int cnt, const int32_t* list, int shared_col,
+                             int nt, f32x4* red);
+
+// Routed items (expert, 128 columns) first, then the shared expert's 64-column tiles.
+__global__ __launch_bounds__(kBlock) void k_stage_b_gq(const LayerArgs a) {
+  __shared__ f32x4 red[4 * 4 * 64];
+  const int H = a.L.hidden;
+  const int tilesR = H / kGqNB;
+  int item = blockIdx.x;
+  const int nRouted = sload_i32(a.ctrl, kCtrlNRouted);
+  if (item < nRouted * tilesR) {
+    const int u = item / tilesR, it = item % tilesR;
+    const int e = sload_i32(a.uniq, u), cnt = sload_i32(a.ucnt, u);
+    const int32_t* list = a.lists + (size_t)e * a.T;
+    const int slot = a.L.slot_of_expert ? sload_i32(a.L.slot_of_expert, e) : e;
+    if (slot < 0 || slot >= a.L.w2.num_slots) {
+      // non-resident expert: contribute zeros, flag the error
+      for (int idx = threadIdx.x; idx < cnt * kGqNB; idx += kBlock) {
+        const int m = idx / kGqNB, n = it * kGqNB + idx % kGqNB;
+        a.ybuf[(size_t)list[m] * H + n] = 0.0f;
+      }
+      if (threadIdx.x == 0) atomicOr(&a.ctrl[kCtrlError], 1);
+      return;
+    }
+    stage_b_gq(a, proj_slot(a.L.w2, slot), it, cnt, list, red);
+  } else {
+    item -= nRouted * tilesR;
+    if (a.L.shared_inter <= 0 || item >= H / 64) return;
+    const ProjSlot W = shared_view(a.L.shared_w2, H, a.L.shared_inter);
+    stage_b_body<FTM_FMT_BF16, FTM_DT_BF16>(a, W, a.T, nullptr, a.L.topk, item, red);
   }
 }
 
@@ -2372,7 +2517,13 @@ static void launch_stages(const LayerArgs& a, int gridA, int gridB, hipStream_t 
   if (which & 2) {
     const XlPlan pb = xl_plan_b<FMT, AT>(a.L, a.T);
     if constexpr (FMT == FTM_FMT_GPTQ_INT4) {
-      hipLaunchKernelGGL((k_stage_b<FMT, AT>), dim3(gridB), dim3(kBlock), 0, st, a);
+      if (gq_b_ok(a.L, a.T) && AT == FTM_DT_BF16) {
+        // routed items of 128 columns + the shared expert's 64-column tiles: within gridB
+        const size_t lds = 4u * (kGqXT + 1) * (size_t)gq_pitch(kGqMaxKR) * 2u;
+        hipLaunchKernelGGL(k_stage_b_gq, dim3(gridB), dim3(kBlock), lds, st, a);
+      } else {
+        hipLaunchKernelGGL((k_stage_b<FMT, AT>), dim3(gridB), dim3(kBlock), 0, st, a);
+      }
     } else if (pb.ok) {
       const size_t lds = 4u * kXT * (size_t)xl_pitch(a.Imax, 1) * 2u;
       const int nt = pb.nt;
@@ -2448,7 +2599,7 @@ static const char* expert_kernel_name(const ftm_moe_layer& L, int T, int stage) 
     return xl_plan_a<FMT, AT>(L, T).ok ? "k_stage_a_xl" : "k_stage_a_rows";
   }
   if (lean) return L.topk + (L.shared_inter > 0 ? 1 : 0) <= kBcMaxKP && T <= kBcMaxT ? "k_stage_bc_lean" : "k_stage_b_lean";
-  if (FMT == FTM_FMT_GPTQ_INT4) return "k_stage_b";
+  if (FMT == FTM_FMT_GPTQ_INT4) return AT == FTM_DT_BF16 && gq_b_ok(L, T) ? "k_stage_b_gq" : "k_stage_b";
   return xl_plan_b<FMT, AT>(L, T).ok ? "k_stage_b_xl" : "k_stage_b";
 }
 

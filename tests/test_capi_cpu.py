@@ -197,8 +197,10 @@ def test_stage_kernel_names_follow_the_dispatch():
     gq.w2 = _proj(N=2048, K=768, num_slots=8, fmt=nat.FMT_GPTQ_INT4, z=0x3000)
     for T in (1, 4, 16):
         assert name(gq, T, nat.STAGE_W13) == "k_stage_a_gq", T
+        assert name(gq, T, nat.STAGE_W2) == "k_stage_b_gq", T
     assert name(gq, 17, nat.STAGE_W13) == "k_stage_a"
-    assert name(gq, 16, nat.STAGE_W2) == "k_stage_b"
+    assert name(gq, 32, nat.STAGE_W2) == "k_stage_b_gq"  # stage B keeps LDS rows up to 32 tokens
+    assert name(gq, 33, nat.STAGE_W2) == "k_stage_b"
     gq.hidden = 2176  # 17 groups: a wave's half would be 1152 wide
     gq.w13.K, gq.w2.N = 2176, 2176
     assert name(gq, 4, nat.STAGE_W13) == "k_stage_a"

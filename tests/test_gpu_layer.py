@@ -41,6 +41,17 @@ def test_small_layer_matches_oracle(gpu, name, T):
     _run_and_check(syn, gpu)
 
 
+@pytest.mark.parametrize("T", [1, 6, 16, 20, 40])
+def test_gptq_layer_with_shared_expert_matches_oracle(gpu, T):
+    """GPTQ routed experts beside a dense shared expert: the GPTQ decode
+    stages (stage A up to 16 tokens, stage B up to 32) run the shared
+    expert's items on their bf16 path, the register-fed ones above."""
+    from dataclasses import replace
+
+    syn = S.generate(replace(S.SMALL["c2_gptq"], shared_inter=128), T=T, seed=40 + T)
+    _run_and_check(syn, gpu)
+
+
 @pytest.mark.parametrize("name,T", [("c2_gptq", 9), ("c3_fp8", 9), ("c4_mxfp4", 9), ("c3_fp8", 80)])
 def test_small_layer_routed_matches_oracle(gpu, name, T):
     """Caller-supplied routing; at T=80 the shared-gate logit comes from the
@@ -83,10 +94,11 @@ def c2_full():
     return S.generate(S.CONFIGS["c2_gptq"], T=64, seed=1)
 
 
-@pytest.mark.parametrize("T", [1, 16, 64])
+@pytest.mark.parametrize("T", [1, 16, 32, 64])
 def test_c2_gptq_full_shape_matches_oracle(gpu, c2_full, T):
-    """GPTQ int4 g128 at the C2 shape (128 experts, top-8): the decode stage A
-    with activations in LDS (8 groups per wave) up to T = 64."""
+    """GPTQ int4 g128 at the C2 shape (128 experts, top-8): the decode stages
+    with rows in LDS (stage A: 8 groups per wave up to 16 tokens; stage B: 3
+    groups per wave up to 32) and the register-fed stages at 64."""
     base = c2_full
     syn = S.SyntheticLayer(base.cfg, base.bank, base.gate_w, base.x[:T].contiguous(), shared=base.shared)
     _run_and_check(syn, gpu)
