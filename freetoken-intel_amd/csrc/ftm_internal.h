@@ -21,9 +21,14 @@ constexpr int kRecPairs = 4;
 // Batches up to kXlMaxT tokens run the decode stages with activations in LDS
 // and per-expert work records (latency-bound there); larger batches keep the
 // register-fed chunked kernels, which sustain more bytes in flight per CU.
-// Measured on MI355X (C3 layer, w13 + w2 us): T=1 15.9 vs 16.7, T=4 30.7 vs
-// 34.5, T=8 54.5 vs 54.5, T=16 92.4 vs 88.1.
+// Measured on MI355X (C3 layer before its lean kernels, w13 + w2 us): T=1 15.9
+// vs 16.7, T=4 30.7 vs 34.5, T=8 54.5 vs 54.5, T=16 92.4 vs 88.1.  MXFP4
+// stage A (C4, w13 us) keeps the LDS path up to kXlMaxTMx: T=8 67.4 -> 54.8,
+// T=16 90.9 -> 76.7, T=32 114.1 against 112.0 (its stage B: no change).
 constexpr int kXlMaxT = 4;
+constexpr int kXlMaxTMx = 16;
+// the top-k compaction writes work records up to this many tokens
+constexpr int kRecMaxT = kXlMaxTMx;
 // Decode batches up to kLeanRouteMaxT tokens (top-k up to kLeanRouteMaxK) route
 // inside the lean stage A, which takes the top-k launch out of the layer's
 // chain of dependent launches.  Every stage-A workgroup then spends ~3 us

@@ -557,7 +557,7 @@ __device__ __forceinline__ void compact_experts(const LayerArgs& a, int32_t* cnt
       a.uniq[u] = e;
       a.ucnt[u] = c;
     }
-    if (f && (a.T <= kXlMaxT || a.lean)) {
+    if (f && (a.T <= kRecMaxT || a.lean)) {
       // work record for the LDS-activation stages: the list of expert e is
       // complete here
       const int u = running + wpre + pre;
@@ -2426,7 +2426,7 @@ static XlPlan xl_plan_a(const ftm_moe_layer& L, int T) {
   if constexpr (FMT == FTM_FMT_GPTQ_INT4 || AT != FTM_DT_BF16) {
     return p;
   } else {
-    if (T > kXlMaxT) return p;
+    if (T > (FMT == FTM_FMT_MXFP4 ? kXlMaxTMx : kXlMaxT)) return p;
     // routed rows: one window per wave (the bf16 shared rows may take several)
     if (!pf_window_fits<FMT>(L.hidden, 4)) return p;
     if (L.hidden % 8 != 0) return p;

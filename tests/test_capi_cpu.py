@@ -204,5 +204,14 @@ def test_stage_kernel_names_follow_the_dispatch():
     gq.hidden = 2176  # 17 groups: a wave's half would be 1152 wide
     gq.w13.K, gq.w2.N = 2176, 2176
     assert name(gq, 4, nat.STAGE_W13) == "k_stage_a"
+    # MXFP4 (C4 shape): stage A keeps activations in LDS up to 16 tokens; stage
+    # B is register-fed (w2's 2880-wide K is more than one wave window)
+    mx = _layer(E=32, H=2880, I=2880, k=4)
+    mx.w13 = _proj(N=2 * 2880, K=2880, num_slots=8, fmt=nat.FMT_MXFP4, group=32)
+    mx.w2 = _proj(N=2880, K=2880, num_slots=8, fmt=nat.FMT_MXFP4, group=32)
+    for T in (1, 8, 16):
+        assert name(mx, T, nat.STAGE_W13) == "k_stage_a_xl", T
+    assert name(mx, 17, nat.STAGE_W13) == "k_stage_a_rows"
+    assert name(mx, 4, nat.STAGE_W2) == "k_stage_b"
     f32 = _layer(E=8, H=256, I=128, k=2, act_dtype=nat.DT_F32)
     assert name(f32, 4, nat.STAGE_W13) is None  # f32 activations need the bf16 router: invalid layer

@@ -104,6 +104,22 @@ def test_c2_gptq_full_shape_matches_oracle(gpu, c2_full, T):
     _run_and_check(syn, gpu)
 
 
+@pytest.fixture(scope="module")
+def c4_full(gpu):
+    # drawn and quantized on the GPU (423 MB of MXFP4 banks: about a minute on the host)
+    return S.generate(S.CONFIGS["c4_mxfp4"], T=32, seed=2, device=gpu)
+
+
+@pytest.mark.parametrize("T", [1, 16, 32])
+def test_c4_mxfp4_full_shape_matches_oracle(gpu, c4_full, T):
+    """MXFP4 at the C4 shape (H = I = 2880, 32 experts, top-4 on biased logits,
+    clamped SwiGLU with biases): stage A with activations in LDS up to 16
+    tokens, register-fed above."""
+    from dataclasses import replace
+
+    _run_and_check(replace(c4_full, x=c4_full.x[:T].contiguous()), gpu)
+
+
 def test_c1_int8_full_shape_matches_oracle(gpu):
     syn = S.generate(S.CONFIGS["c1_int8"], T=4, seed=0)
     _run_and_check(syn, gpu)
