@@ -27,8 +27,9 @@ constexpr int kRecPairs = 4;
 // T=16 90.9 -> 76.7, T=32 114.1 against 112.0 (its stage B: no change).
 constexpr int kXlMaxT = 4;
 constexpr int kXlMaxTMx = 16;
-// the top-k compaction writes work records up to this many tokens
-constexpr int kRecMaxT = kXlMaxTMx;
+// the top-k compaction writes work records up to this many tokens (the xl
+// stage A and the K-split stage B read them)
+constexpr int kRecMaxT = 32;
 // Decode batches up to kLeanRouteMaxT tokens (top-k up to kLeanRouteMaxK) route
 // inside the lean stage A, which takes the top-k launch out of the layer's
 // chain of dependent launches.  Every stage-A workgroup then spends ~3 us

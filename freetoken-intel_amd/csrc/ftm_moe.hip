@@ -1639,6 +1639,89 @@ __global__ __launch_bounds__(kBlock) void k_stage_a_xl(const LayerArgs a) {
   }
 }
 
+// Stage B item with K split: 16 output columns (w2 rows c0 .. c0 + 15) of one
+// expert, K split over the 4 waves and reduced through LDS (the stage-A xl
+// data path with plain rows).  For small batches whose 64-column items would
+// leave CUs idle and whose rows are too long for one window per wave.
+template <int EFMT, int LPG>
+__device__ void stage_b_ks_body(const LayerArgs& a, const ProjSlot& W, int c0, int cnt, const ExpertRec* rec,
+                                const int32_t* list, int shared_col, int kp, f32x4* red) {
+  using F = KMajor<EFMT>;
+  constexpr int KS = 4;
+  const int lane = threadIdx.x & 63;
+  const int n = lane & 15;
+  const int H = a.L.hidden;
+  const int nL = fmt_loads<EFMT>(W.K);
+  const int L_lo = kp * nL / KS, L_hi = (kp + 1) * nL / KS;
+  const bool multi = L_hi - L_lo > kRowsNLW;
+  RowGeom<EFMT> G[1];
+  RowStream<EFMT, kRowsNLW> S[1];
+  G[0] = RowGeom<EFMT>(W, c0 + n, W.group > 0 ? c0 / W.group : 0, W.group > 0 ? (c0 + 8) / W.group : 0);
+  rows_issue<EFMT, kRowsNLW, true>(W, G[0], L_lo, L_hi, S[0]);
+  const int pitch = xl_pitch(a.Imax, KS);
+  uint16_t* xw = ftm_xl_lds + kp * kXT * pitch;
+  const int k0 = L_lo * F::kLoadK, k1 = min(L_hi * F::kLoadK, W.K);
+  const float bn = (W.bias != nullptr && kp == 0) ? load_scalar(W.bias, c0 + n, W.bias_dt) : 0.0f;
+  for (int mb = 0; mb < cnt; mb += kXT) {
+    const int nb = min(kXT, cnt - mb);
+    int pr[kXT];
+    block_pairs(a, rec, list, shared_col, cnt, mb, pr);
+    xl_fill_wave(pr, a.hbuf, 1, a.Imax, k0, k1, xw, pitch);
+    f32x4 acc[1] = {(f32x4){0.f, 0.f, 0.f, 0.f}};
+    for (int Lw = L_lo; Lw < L_hi; Lw += kRowsNLW) {
+      if (Lw != L_lo || (mb > 0 && multi)) rows_issue<EFMT, kRowsNLW, true>(W, G[0], Lw, L_hi, S[0]);
+      __builtin_amdgcn_s_waitcnt(0);  // weights and this wave's LDS copy have landed
+      rows_consume_lds<EFMT, kRowsNLW, 1, LPG, true>(W, G, Lw, L_hi, S, xw, k0, pitch, nb, acc);
+    }
+    // MFMA rows 0..kXT-1 (the block's tokens) live in lanes 0..15, lane n = column c0 + n
+    if (lane < 16) red[kp * 16 + lane] = acc[0];
+    __syncthreads();
+    if (kp == 0 && lane < 16) {
+      f32x4 v = red[n];
+#pragma unroll
+      for (int j = 1; j < KS; ++j) v += red[j * 16 + n];
+#pragma unroll
+      for (int r = 0; r < kXT; ++r)
+        if (r < nb) {
+          const float wr = __uint_as_float(sload4(a.wts, 4u * (uint32_t)pr[r]));  // router weight or shared gate
+          a.ybuf[(size_t)pr[r] * H + c0 + n] = (v[r] + bn) * wr;
+        }
+    }
+    __syncthreads();
+  }
+}
+
+// 16 output columns per workgroup: routed items first, then the shared expert's.
+template <int FMT, int LPG>
+__global__ __launch_bounds__(kBlock) void k_stage_b_ks(const LayerArgs a) {
+  __shared__ f32x4 red[4 * 16];
+  const int kp = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int H = a.L.hidden;
+  const int tn = H / 16;
+  const int item = blockIdx.x;
+  const int u = min(item / tn, a.L.num_experts);
+  const ExpertRec rec = load_rec(a, u);
+  const int nRouted = sload_i32(a.ctrl, kCtrlNRouted);
+  if (item < nRouted * tn) {
+    const int c0 = (item % tn) * 16;
+    const int32_t* list = a.lists + (size_t)rec.e * a.T;
+    if (rec.slot < 0 || rec.slot >= a.L.w2.num_slots) {
+      // non-resident expert: contribute zeros, flag the error
+      for (int idx = threadIdx.x; idx < rec.cnt * 16; idx += kBlock)
+        a.ybuf[(size_t)list[idx / 16] * H + c0 + idx % 16] = 0.0f;
+      if (threadIdx.x == 0) atomicOr(&a.ctrl[kCtrlError], 1);
+      return;
+    }
+    stage_b_ks_body<FMT, LPG>(a, proj_slot(a.L.w2, rec.slot), c0, rec.cnt, &rec, list, 0, kp, red);
+  } else {
+    const int sitem = item - nRouted * tn;
+    const int Is = a.L.shared_inter;
+    if (Is <= 0 || sitem >= tn) return;
+    const ProjSlot W = shared_view(a.L.shared_w2, H, Is);
+    stage_b_ks_body<FTM_FMT_BF16, kRowsNLW>(a, W, sitem * 16, a.T, nullptr, nullptr, a.L.topk, kp, red);
+  }
+}
+
 // Stage B item body: NT x 64 output columns of one expert; in each 64-column
 // tile wave w owns columns 16w .. 16w + 15, over the full K (no cross-wave
 // reduction).
@@ -2455,6 +2538,28 @@ static XlPlan xl_plan_b(const ftm_moe_layer& L, int T) {
   }
 }
 
+// Stage B with K split over the waves (k_stage_b_ks): small batches whose w2
+// rows do not fit one window per wave (the full-K xl kernel's condition).
+// Measured on MI355X (C4 w2, against the register-fed k_stage_b): T=1 13.9 ->
+// 9.7 us, T=4 29.5 -> 20.9, T=8 38.0 -> 28.6, T=16 48.3 -> 38.3, T=24 56.2 ->
+// 46.3, T=32 60.3 -> 52.2.
+constexpr int kBksMaxT = 32;
+template <int FMT, int AT>
+static XlPlan ks_plan_b(const ftm_moe_layer& L, int T) {
+  XlPlan p{false, 1, kRowsNLW};
+  if constexpr (FMT == FTM_FMT_GPTQ_INT4 || AT != FTM_DT_BF16) {
+    return p;
+  } else {
+    if (T > kBksMaxT || T > kRecMaxT || L.hidden % 16 != 0) return p;
+    if (!pf_window_fits<FMT>(L.inter, 4) || L.inter % 8 != 0) return p;
+    if (L.shared_inter > 0 && (!pf_window_fits<FTM_FMT_BF16>(L.shared_inter, 4) || L.shared_inter % 8 != 0))
+      return p;
+    p.lpg = xl_lpg<FMT>(L.w2, 4);
+    p.ok = p.lpg != 0;
+    return p;
+  }
+}
+
 // which: bit 0 = stage A (w13 + act), bit 1 = stage B (w2), bit 2 = combine
 template <int FMT, int AT>
 static void launch_stages(const LayerArgs& a, int gridA, int gridB, hipStream_t st, int which) {
@@ -2532,6 +2637,14 @@ static void launch_stages(const LayerArgs& a, int gridA, int gridB, hipStream_t 
 #define FTM_XLB(NT, LPG) hipLaunchKernelGGL((k_stage_b_xl<FMT, NT, LPG>), dim3(gridx), dim3(kBlock), lds, st, a)
       if (pb.lpg == 2) FTM_XLB(1, 2); else FTM_XLB(1, kRowsNLW);
 #undef FTM_XLB
+    } else if (const XlPlan pk = ks_plan_b<FMT, AT>(a.L, a.T); pk.ok) {
+      const int maxU = a.L.num_experts < a.T * a.L.topk ? a.L.num_experts : a.T * a.L.topk;
+      const size_t lds = 4u * kXT * (size_t)xl_pitch(a.Imax, 4) * 2u;  // the regions stage_b_ks_body lays out
+      const int gridk = (maxU + (a.L.shared_inter > 0 ? 1 : 0)) * (a.L.hidden / 16);
+      if (pk.lpg == 2)
+        hipLaunchKernelGGL((k_stage_b_ks<FMT, 2>), dim3(gridk), dim3(kBlock), lds, st, a);
+      else
+        hipLaunchKernelGGL((k_stage_b_ks<FMT, kRowsNLW>), dim3(gridk), dim3(kBlock), lds, st, a);
     } else {
       hipLaunchKernelGGL((k_stage_b<FMT, AT>), dim3(gridB), dim3(kBlock), 0, st, a);
     }
@@ -2600,7 +2713,8 @@ static const char* expert_kernel_name(const ftm_moe_layer& L, int T, int stage) 
   }
   if (lean) return L.topk + (L.shared_inter > 0 ? 1 : 0) <= kBcMaxKP && T <= kBcMaxT ? "k_stage_bc_lean" : "k_stage_b_lean";
   if (FMT == FTM_FMT_GPTQ_INT4) return AT == FTM_DT_BF16 && gq_b_ok(L, T) ? "k_stage_b_gq" : "k_stage_b";
-  return xl_plan_b<FMT, AT>(L, T).ok ? "k_stage_b_xl" : "k_stage_b";
+  if (xl_plan_b<FMT, AT>(L, T).ok) return "k_stage_b_xl";
+  return ks_plan_b<FMT, AT>(L, T).ok ? "k_stage_b_ks" : "k_stage_b";
 }
 
 template <int FMT>

@@ -188,7 +188,8 @@ def test_stage_kernel_names_follow_the_dispatch():
     assert name(small, 4, nat.STAGE_W13) == "k_stage_a_xl"
     assert name(small, 4, nat.STAGE_W2) == "k_stage_b_xl"
     assert name(small, 5, nat.STAGE_W13) == "k_stage_a_rows"
-    assert name(small, 5, nat.STAGE_W2) == "k_stage_b"
+    assert name(small, 5, nat.STAGE_W2) == "k_stage_b_ks"  # K split over the waves up to 32 tokens
+    assert name(small, 33, nat.STAGE_W2) == "k_stage_b"
     assert name(small, 64, nat.STAGE_W13) == "k_gemm_a_ring"
     # GPTQ group 128: activation rows in LDS up to 16 tokens while half of the
     # hidden size fits a wave's K range (1024), the register-fed kernel above
@@ -205,13 +206,15 @@ def test_stage_kernel_names_follow_the_dispatch():
     gq.w13.K, gq.w2.N = 2176, 2176
     assert name(gq, 4, nat.STAGE_W13) == "k_stage_a"
     # MXFP4 (C4 shape): stage A keeps activations in LDS up to 16 tokens; stage
-    # B is register-fed (w2's 2880-wide K is more than one wave window)
+    # B splits w2's 2880-wide K over the waves up to 32 (more than one window)
     mx = _layer(E=32, H=2880, I=2880, k=4)
     mx.w13 = _proj(N=2 * 2880, K=2880, num_slots=8, fmt=nat.FMT_MXFP4, group=32)
     mx.w2 = _proj(N=2880, K=2880, num_slots=8, fmt=nat.FMT_MXFP4, group=32)
     for T in (1, 8, 16):
         assert name(mx, T, nat.STAGE_W13) == "k_stage_a_xl", T
     assert name(mx, 17, nat.STAGE_W13) == "k_stage_a_rows"
-    assert name(mx, 4, nat.STAGE_W2) == "k_stage_b"
+    for T in (1, 4, 32):
+        assert name(mx, T, nat.STAGE_W2) == "k_stage_b_ks", T
+    assert name(mx, 33, nat.STAGE_W2) == "k_stage_b"
     f32 = _layer(E=8, H=256, I=128, k=2, act_dtype=nat.DT_F32)
     assert name(f32, 4, nat.STAGE_W13) is None  # f32 activations need the bf16 router: invalid layer

@@ -35,7 +35,7 @@ def _run_and_check(syn, gpu, *, check_routing=True):
 
 
 @pytest.mark.parametrize("name", ["c1_int8", "c2_gptq", "c3_fp8", "c4_mxfp4"])
-@pytest.mark.parametrize("T", [1, 5, 16])
+@pytest.mark.parametrize("T", [1, 5, 16, 24])
 def test_small_layer_matches_oracle(gpu, name, T):
     syn = S.generate(S.SMALL[name], T=T, seed=11 + T)
     _run_and_check(syn, gpu)
