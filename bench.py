@@ -151,13 +151,17 @@ def main() -> int:
             layers[j % NL].forward(xs[j % NX])
         torch.cuda.synchronize()
         wall_ms = (time.perf_counter() - w0) * 1e3 / steps
-        # device time: a sleep kernel queued first lets the host enqueue ahead,
-        # so the events see the forwards back to back on the GPU (at T <= 2 a
-        # forward's host enqueue, ~20 us of Python and ctypes, is as long as
-        # its kernels and would otherwise leave gaps between them)
+        # device time: a short sleep kernel queued first lets the host enqueue
+        # ahead, so the events see the forwards back to back on the GPU (at
+        # T <= 2 a forward's host enqueue, ~20 us of Python and ctypes, is as
+        # long as its kernels and would otherwise leave gaps between them); a
+        # few untimed forwards after it bring the clocks back up (a 40 ms sleep
+        # cost 3-7 % at T >= 16)
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         if hasattr(torch.cuda, "_sleep"):
-            torch.cuda._sleep(100_000_000)
+            torch.cuda._sleep(2_000_000)
+        for i in range(3):
+            layers[i % NL].forward(xs[i % NX])
         e0.record()
         for i in range(steps):
             j = warmup + i
