@@ -496,9 +496,10 @@ __device__ __forceinline__ void zero_skipped_slots(const LayerArgs& a, int t, bo
 }
 
 // Record token t's selection: weights, ids, and one list entry per pair in
-// the expert's list (cnt: per-expert counters, in LDS or global memory).
+// the expert's list (cnt: per-expert counters, in LDS or global memory;
+// s_first: null, or an LDS copy of each list's first kRecPairs entries).
 __device__ __forceinline__ void emit_token(const LayerArgs& a, int t, int sel_e, float sel_w, int32_t* ids_out,
-                                           float* w_out, int32_t* cnt) {
+                                           float* w_out, int32_t* cnt, int32_t* s_first = nullptr) {
   const int E = a.L.num_experts, k = a.L.topk, T = a.T, KP = a.KP;
   const int lane = threadIdx.x & 63;
   if (lane < k) {
@@ -511,6 +512,7 @@ __device__ __forceinline__ void emit_token(const LayerArgs& a, int t, int sel_e,
       const int pos = atomicAdd(&cnt[sel_e], 1);
       if (pos < T) {
         a.lists[(size_t)sel_e * T + pos] = p;
+        if (s_first != nullptr && pos < kRecPairs) s_first[sel_e * kRecPairs + pos] = p;
       } else {  // a token listed the same expert twice (caller-supplied routing)
         atomicSub(&cnt[sel_e], 1);
         atomicOr(&a.ctrl[kCtrlError], 4);
@@ -531,8 +533,11 @@ __device__ __forceinline__ void emit_token(const LayerArgs& a, int t, int sel_e,
 
 // Compaction of the routed experts (ascending id) by one workgroup of NW
 // waves from the per-expert counters; counters are cleared when global.
+// s_first: null (records read the lists' heads from global memory), or the
+// LDS copy emit_token kept.
 template <int NW>
-__device__ __forceinline__ void compact_experts(const LayerArgs& a, int32_t* cnt, bool global_cnt, int* s_wsum) {
+__device__ __forceinline__ void compact_experts(const LayerArgs& a, int32_t* cnt, bool global_cnt, int* s_wsum,
+                                                const int32_t* s_first = nullptr) {
   const int E = a.L.num_experts;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   int running = 0;
@@ -567,7 +572,8 @@ __device__ __forceinline__ void compact_experts(const LayerArgs& a, int32_t* cnt
       rec[1] = c;
       rec[2] = a.L.slot_of_expert ? a.L.slot_of_expert[e] : e;
 #pragma unroll
-      for (int i = 0; i < kRecPairs; ++i) rec[3 + i] = i < c ? list[i] : -1;
+      for (int i = 0; i < kRecPairs; ++i)
+        rec[3 + i] = i < c ? (s_first != nullptr ? s_first[e * kRecPairs + i] : list[i]) : -1;
       rec[kRecWords - 1] = 0;
       int32_t* dst = a.recs + (size_t)u * kRecWords;
 #pragma unroll
@@ -598,6 +604,7 @@ __global__ __launch_bounds__(64 * kTopk1Waves) void k_topk1(const LayerArgs a, c
                                                             const float* w_in, int32_t* ids_out, float* w_out,
                                                             float* logits_out) {
   __shared__ int32_t s_cnt[kMaxExperts];
+  __shared__ int32_t s_first[kMaxExperts * kRecPairs];  // each list's first pairs, for the records
   __shared__ int s_wsum[kTopk1Waves];
   const int E = a.L.num_experts, T = a.T;
   for (int e = threadIdx.x; e < E; e += 64 * kTopk1Waves) s_cnt[e] = 0;
@@ -606,10 +613,10 @@ __global__ __launch_bounds__(64 * kTopk1Waves) void k_topk1(const LayerArgs a, c
     int sel_e;
     float sel_w;
     route_token<MODE, NV>(a, t, logits_in, logits_dt, ids_in, w_in, logits_out, sel_e, sel_w);
-    emit_token(a, t, sel_e, sel_w, ids_out, w_out, s_cnt);
+    emit_token(a, t, sel_e, sel_w, ids_out, w_out, s_cnt, s_first);
   }
   __syncthreads();
-  compact_experts<kTopk1Waves>(a, s_cnt, false, s_wsum);
+  compact_experts<kTopk1Waves>(a, s_cnt, false, s_wsum, s_first);
 }
 
 // Large batches: one wave per token, 4 per workgroup; the last-arriving
