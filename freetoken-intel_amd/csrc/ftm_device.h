@@ -468,10 +468,34 @@ __device__ __forceinline__ void wave_gemm_kmajor(const ProjSlot& W, const int (&
 #pragma unroll
       for (int r = 0; r < NR; ++r) {
         raw[r][b] = bload16(wres, kok ? woff[r] + F::elem_off(kk) : kOOB);
-        if constexpr (FMT == FTM_FMT_MXFP4) {
-          sc[r][b] = e8m0_to_f32(bload1(sres, kok ? soff[r] + (uint32_t)(kk / 32) : kOOB));
-        } else if constexpr (F::kPostScale) {
+        if constexpr (F::kPostScale) {
           scw[r][b] = bload_scalar_word(sres, soff[r] + (uint32_t)grp_b[b], W.s_dt, L < L_hi && soff[r] != kOOB);
+        }
+      }
+    }
+    if constexpr (FMT == FTM_FMT_MXFP4) {
+      // row r's e8m0 bytes of wave-loads b = 0 .. CH-1 sit 4 bytes apart
+      // (group 4 (Lc + b) + g): byte sh / 8 of CH consecutive dwords, fetched
+      // by ceil(CH / 4) 16-byte loads rather than one byte load per wave-load;
+      // wave-loads outside the range take scale byte 0 (their weights are 0)
+#pragma unroll
+      for (int r = 0; r < NR; ++r) {
+        const uint32_t b0 = soff[r] != kOOB ? soff[r] + 4u * (uint32_t)Lc + (uint32_t)g : kOOB;
+        const uint32_t sh = b0 != kOOB ? 8u * (b0 & 3u) : 0u;
+        uint32_t dw[(CH + 3) / 4 * 4];
+#pragma unroll
+        for (int q = 0; q < (CH + 3) / 4; ++q) {
+          const u32x4 v = bload16(sres, b0 != kOOB ? (b0 & ~3u) + 16u * (uint32_t)q : kOOB);
+          dw[4 * q] = v.x;
+          dw[4 * q + 1] = v.y;
+          dw[4 * q + 2] = v.z;
+          dw[4 * q + 3] = v.w;
+        }
+#pragma unroll
+        for (int b = 0; b < CH; ++b) {
+          const int L = Lc + b;
+          const bool kok = (L < L_hi) && (L * F::kLoadK + F::kLaneK * g < K);
+          sc[r][b] = e8m0_to_f32(kok ? (dw[b] >> sh) & 0xffu : 0u);
         }
       }
     }
@@ -682,7 +706,9 @@ __device__ __forceinline__ void wave_rows_kmajor(const ProjSlot& W, int lrow, in
 template <int FMT, int NLW>
 struct RowStream {
   u32x4 raw[NLW];
-  uint32_t sw[NLW];  // FP8 / INT8: scale word of the wave-load's group; MXFP4: e8m0 byte
+  uint32_t sw[NLW];  // FP8 / INT8: scale word of the wave-load's group; MXFP4: the dword holding its e8m0 byte
+  uint32_t sh;       // MXFP4: bit position of the byte in those dwords
+  uint32_t vmask;    // MXFP4: wave-loads inside the lane's K range (the others decode with scale byte 0)
 };
 
 template <int FMT>
@@ -731,6 +757,7 @@ __device__ __forceinline__ void rows_issue(const ProjSlot& W, const RowGeom<FMT>
   const int K = W.K;
   int gcur = Lw / G.lpg;
   int gpos = Lw - gcur * G.lpg;
+  if constexpr (FMT == FTM_FMT_MXFP4) S.vmask = 0u;
 #pragma unroll
   for (int b = 0; b < NLW; ++b) {
     const int L = Lw + b;
@@ -738,7 +765,7 @@ __device__ __forceinline__ void rows_issue(const ProjSlot& W, const RowGeom<FMT>
     const bool kok = (L < L_hi) && (kk < K);
     S.raw[b] = bload16(G.wres, kok ? G.woff + F::elem_off(kk) : kOOB);
     if constexpr (FMT == FTM_FMT_MXFP4) {
-      S.sw[b] = bload1(G.sres, kok ? G.soff + (uint32_t)(kk / 32) : kOOB);
+      S.vmask |= kok ? 1u << b : 0u;
     } else if constexpr (FMT == FTM_FMT_FP8_BLOCK) {
       // each lane reads its own row block's word with the weights (a vector
       // load: nothing waits for it until the MFMAs)
@@ -752,6 +779,22 @@ __device__ __forceinline__ void rows_issue(const ProjSlot& W, const RowGeom<FMT>
       const bool wrap = gpos == G.lpg - 1;
       gpos = wrap ? 0 : gpos + 1;
       gcur += wrap ? 1 : 0;
+    }
+  }
+  if constexpr (FMT == FTM_FMT_MXFP4) {
+    // the lane's e8m0 bytes of wave-loads b = 0 .. NLW-1 sit 4 bytes apart in
+    // its scale row (group 4 (Lw + b) + g), so they are byte sh / 8 of NLW
+    // consecutive dwords: ceil(NLW / 4) 16-byte loads instead of one byte
+    // load per wave-load (half the vector-memory instructions of the stream)
+    const uint32_t b0 = G.soff != kOOB ? G.soff + 4u * (uint32_t)Lw + (uint32_t)g : kOOB;
+    S.sh = b0 != kOOB ? 8u * (b0 & 3u) : 0u;
+#pragma unroll
+    for (int q = 0; q < (NLW + 3) / 4; ++q) {
+      const u32x4 v = bload16(G.sres, b0 != kOOB ? (b0 & ~3u) + 16u * (uint32_t)q : kOOB);
+      if (4 * q + 0 < NLW) S.sw[4 * q + 0] = v.x;
+      if (4 * q + 1 < NLW) S.sw[4 * q + 1] = v.y;
+      if (4 * q + 2 < NLW) S.sw[4 * q + 2] = v.z;
+      if (4 * q + 3 < NLW) S.sw[4 * q + 3] = v.w;
     }
   }
 }
@@ -803,7 +846,8 @@ __device__ __forceinline__ void rows_consume_lds(const ProjSlot& W, const RowGeo
           bq = q == 0 ? i8x8_to_bf16(r.x, r.y) : i8x8_to_bf16(r.z, r.w);
         } else if constexpr (FMT == FTM_FMT_MXFP4) {
           const uint32_t wq = q == 0 ? r.x : q == 1 ? r.y : q == 2 ? r.z : r.w;
-          bq = fp4x8_to_bf16(wq, e8m0_to_f32(S[t].sw[b]));
+          const uint32_t e8 = ((S[t].vmask >> b) & 1u) ? (S[t].sw[b] >> S[t].sh) & 0xffu : 0u;
+          bq = fp4x8_to_bf16(wq, e8m0_to_f32(e8));
         } else {
           bq = r;
         }

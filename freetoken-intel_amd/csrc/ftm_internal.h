@@ -24,9 +24,10 @@ constexpr int kRecPairs = 4;
 // Measured on MI355X (C3 layer before its lean kernels, w13 + w2 us): T=1 15.9
 // vs 16.7, T=4 30.7 vs 34.5, T=8 54.5 vs 54.5, T=16 92.4 vs 88.1.  MXFP4
 // stage A (C4, w13 us) keeps the LDS path up to kXlMaxTMx: T=8 67.4 -> 54.8,
-// T=16 90.9 -> 76.7, T=32 114.1 against 112.0 (its stage B: no change).
+// T=16 90.9 -> 76.7, and with its scale bytes fetched 16 at a time T=24
+// 106.6 -> 89.3, T=32 115.6 -> 100.1.
 constexpr int kXlMaxT = 4;
-constexpr int kXlMaxTMx = 16;
+constexpr int kXlMaxTMx = 32;
 // the top-k compaction writes work records up to this many tokens (the xl
 // stage A and the K-split stage B read them)
 constexpr int kRecMaxT = 32;

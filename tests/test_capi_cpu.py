@@ -205,14 +205,14 @@ def test_stage_kernel_names_follow_the_dispatch():
     gq.hidden = 2176  # 17 groups: a wave's half would be 1152 wide
     gq.w13.K, gq.w2.N = 2176, 2176
     assert name(gq, 4, nat.STAGE_W13) == "k_stage_a"
-    # MXFP4 (C4 shape): stage A keeps activations in LDS up to 16 tokens; stage
+    # MXFP4 (C4 shape): stage A keeps activations in LDS up to 32 tokens; stage
     # B splits w2's 2880-wide K over the waves up to 32 (more than one window)
     mx = _layer(E=32, H=2880, I=2880, k=4)
     mx.w13 = _proj(N=2 * 2880, K=2880, num_slots=8, fmt=nat.FMT_MXFP4, group=32)
     mx.w2 = _proj(N=2880, K=2880, num_slots=8, fmt=nat.FMT_MXFP4, group=32)
-    for T in (1, 8, 16):
+    for T in (1, 8, 32):
         assert name(mx, T, nat.STAGE_W13) == "k_stage_a_xl", T
-    assert name(mx, 17, nat.STAGE_W13) == "k_stage_a_rows"
+    assert name(mx, 33, nat.STAGE_W13) == "k_stage_a_rows"
     for T in (1, 4, 32):
         assert name(mx, T, nat.STAGE_W2) == "k_stage_b_ks", T
     assert name(mx, 33, nat.STAGE_W2) == "k_stage_b"

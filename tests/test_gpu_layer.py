@@ -113,8 +113,8 @@ def c4_full(gpu):
 @pytest.mark.parametrize("T", [1, 16, 32])
 def test_c4_mxfp4_full_shape_matches_oracle(gpu, c4_full, T):
     """MXFP4 at the C4 shape (H = I = 2880, 32 experts, top-4 on biased logits,
-    clamped SwiGLU with biases): stage A with activations in LDS up to 16
-    tokens, register-fed above."""
+    clamped SwiGLU with biases): stage A with activations in LDS and stage B
+    with K split over the waves up to 32 tokens."""
     from dataclasses import replace
 
     _run_and_check(replace(c4_full, x=c4_full.x[:T].contiguous()), gpu)
