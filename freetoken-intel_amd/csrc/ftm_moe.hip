@@ -593,10 +593,11 @@ __device__ __forceinline__ void compact_experts(const LayerArgs& a, int32_t* cnt
 // t = w, w + 16, ...) with per-expert counters in LDS, then compacts.  No
 // cross-workgroup traffic, so no device-scope fences.  Measured on MI355X
 // (C3, 256 experts, top-8): 6.1 us at T <= 4 against 7.9-8.9 us for the
-// multi-workgroup kernel, 8.1 against 9.3 at 12; from T = 16 on the
-// multi-workgroup kernel wins (9.2 vs 9.9 us at 16, 13.6 vs 103 us at 256).
+// multi-workgroup kernel, 8.1 against 9.3 at 12, 8.9 against 9.2 at 16;
+// they tie at 20 and from 24 on the multi-workgroup kernel wins (9.8 vs 13.3
+// us at 32, 10.0 vs 17.3 at 48).
 constexpr int kTopk1Waves = 16;
-constexpr int kTopk1MaxT = 12;
+constexpr int kTopk1MaxT = 16;
 
 template <int MODE, int NV>
 __global__ __launch_bounds__(64 * kTopk1Waves) void k_topk1(const LayerArgs a, const void* logits_in,
@@ -2319,9 +2320,18 @@ __global__ __launch_bounds__(kBlock) void k_combine(const LayerArgs a) {
   if (idx >= a.T * H4) return;
   const int t = idx / H4, n4 = idx % H4;
   const f32x4* yb = (const f32x4*)(a.ybuf + (size_t)t * KP * H) + n4;
-  // slots in order (a pair without an expert has a zeroed slot)
+  // slots in order (a pair without an expert has a zeroed slot); the loads
+  // of 8 slots issue together before their adds, which keep slot order
   f32x4 s = yb[0];
-  for (int j = 1; j < KP; ++j) s += yb[(size_t)j * H4];
+  int j = 1;
+  for (; j + 8 <= KP; j += 8) {
+    f32x4 v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) v[u] = yb[(size_t)(j + u) * H4];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) s += v[u];
+  }
+  for (; j < KP; ++j) s += yb[(size_t)j * H4];
   if constexpr (AT == FTM_DT_F32) {
     ((f32x4*)a.out)[(size_t)t * H4 + n4] = s;
   } else {

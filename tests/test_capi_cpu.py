@@ -175,8 +175,8 @@ def test_stage_kernel_names_follow_the_dispatch():
     # 512 tokens x top-8 = 16 pairs per expert on all 256 experts: GEMM stages
     assert name(c3, 512, nat.STAGE_W13) == "k_gemm_a_ring"
     assert name(c3, 512, nat.STAGE_W2) == "k_gemm_b"
-    assert name(c3, 12, nat.STAGE_TOPK) == "k_topk1"
-    assert name(c3, 13, nat.STAGE_TOPK) == "k_topk"
+    assert name(c3, 16, nat.STAGE_TOPK) == "k_topk1"
+    assert name(c3, 17, nat.STAGE_TOPK) == "k_topk"
     assert name(c3, 255, nat.STAGE_TOPK) == "k_topk"
     assert name(c3, 256, nat.STAGE_TOPK) == "k_topk_blk"
     assert name(c3, 16, nat.STAGE_ROUTER) == "k_router"
