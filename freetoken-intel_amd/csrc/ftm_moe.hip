@@ -1923,9 +1923,21 @@ __device__ __forceinline__ void lean_pairs(const LayerArgs& a, const ExpertRec* 
 // split over the 4 waves (KR = H / 4 each).  FP8: one window of KR / 64
 // wave-loads, fp32 scale words sc_lo (gate rows' block) / sc_hi (up rows').
 // BF16 (shared expert): NWIN windows of KR / (32 NWIN) wave-loads.
+// The shared expert's tokens split into blocks of kLeanAShXT for stage A,
+// one workgroup per (block, 8 channels), so its workgroups take no longer
+// than a routed expert's.  Measured on MI355X (C3, stage A): T=64 92.4 ->
+// 87.7 us against one workgroup per 8 channels taking every token (4: 88.4,
+// 16: 88.9); no change up to T=32.
+constexpr int kLeanAShXT = 8;
+static_assert(kLeanRouteMaxT <= kLeanAShXT, "the routing stage A takes the shared expert as one block");
+__host__ __device__ __forceinline__ int lean_a_sh_blocks(const ftm_moe_layer& L, int T) {
+  return L.shared_inter > 0 ? (T + kLeanAShXT - 1) / kLeanAShXT : 0;
+}
+
 template <bool FP8, int KR, int NWIN>
 __device__ void lean_a_item(const LayerArgs& a, const char* w, const float* sc, int Iu, int c0, int cnt,
-                            const ExpertRec* rec, const int32_t* list, int shared_col, int kp, f32x4* red) {
+                            const ExpertRec* rec, const int32_t* list, int shared_col, int kp, f32x4* red,
+                            int mb0 = 0) {
   constexpr int NLW = (FP8 ? KR / 64 : KR / 32) / NWIN;
   constexpr int NP = FP8 ? NLW / 2 : 1;
   static_assert(!FP8 || NWIN == 1, "FP8 rows: one window per wave");
@@ -1955,7 +1967,7 @@ __device__ void lean_a_item(const LayerArgs& a, const char* w, const float* sc, 
   uint16_t* xw = ftm_xl_lds + kp * (kLeanXT + 1) * pitch;
   // zero row for MFMA rows without a token (this wave's region only)
   for (int e = 8 * lane; e < KR; e += 8 * 64) *(u32x4*)(xw + kLeanXT * pitch + e) = (u32x4){0u, 0u, 0u, 0u};
-  for (int mb = 0; mb < cnt; mb += kLeanXT) {
+  for (int mb = mb0; mb < cnt; mb += kLeanXT) {
     const int nb = min(kLeanXT, cnt - mb);
     int pr[kLeanXT];
     lean_pairs(a, rec, list, shared_col, cnt, mb, pr);
@@ -1966,7 +1978,7 @@ __device__ void lean_a_item(const LayerArgs& a, const char* w, const float* sc, 
     for (int i = 0; i < NP; ++i) part[i] = (f32x4){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int wi = 0; wi < NWIN; ++wi) {
-      if (wi > 0 || (NWIN > 1 && mb > 0)) lean_issue<NLW>(wres, lrow, row_bytes, kbase, wi * NLW, S);
+      if (wi > 0 || (NWIN > 1 && mb > mb0)) lean_issue<NLW>(wres, lrow, row_bytes, kbase, wi * NLW, S);
       __builtin_amdgcn_s_waitcnt(0);  // weights and this wave's LDS rows have landed
       lean_mfma<FP8, NLW, NP>(S, xrow, wi * NLW * (FP8 ? 64 : 32), part, 0);
     }
@@ -2003,12 +2015,15 @@ __global__ __launch_bounds__(kBlock) void k_stage_a_lean(const LayerArgs a) {
   const int kp = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int I = a.L.inter;
   const int t8 = I / 8;
-  // shared-expert items first: each takes every token, so they start early
-  // instead of trailing the grid
-  const int nShared = a.L.shared_inter > 0 ? a.L.shared_inter / 8 : 0;
+  // the shared expert's (token block, 8-channel) items first, so they start
+  // early instead of trailing the grid
+  const int ts = a.L.shared_inter / 8;
+  const int nShared = ts * lean_a_sh_blocks(a.L, a.T);
   if ((int)blockIdx.x < nShared) {
-    lean_a_item<false, KR, NWS>(a, (const char*)a.L.shared_w13, nullptr, a.L.shared_inter, blockIdx.x * 8, a.T,
-                                nullptr, nullptr, a.L.topk, kp, red);
+    const int b = (int)blockIdx.x / ts, c = (int)blockIdx.x % ts;
+    lean_a_item<false, KR, NWS>(a, (const char*)a.L.shared_w13, nullptr, a.L.shared_inter, c * 8,
+                                min(a.T, (b + 1) * kLeanAShXT), nullptr, nullptr, a.L.topk, kp, red,
+                                b * kLeanAShXT);
     return;
   }
   const int item = blockIdx.x - nShared;
@@ -2222,17 +2237,27 @@ __device__ void lean_b_item(const LayerArgs& a, const char* w, const float* sc, 
   }
 }
 
+// The shared expert's tokens split into blocks of kLeanBShXT, one workgroup
+// per (block, column tile), so its workgroups take no longer than a routed
+// expert's.  Measured on MI355X (C3, stage B): T=32 37.3 -> 33.7 us, T=48
+// 50.3 -> 41.7, T=64 60.9 -> 48.6 against one workgroup per tile taking every
+// token (blocks of 4: 34.5 at T=32; 16: as 8).
+constexpr int kLeanBShXT = 8;
+__host__ __device__ __forceinline__ int lean_b_sh_blocks(const ftm_moe_layer& L, int T) {
+  return L.shared_inter > 0 ? (T + kLeanBShXT - 1) / kLeanBShXT : 0;
+}
+
 template <int KB, int NWS>
 __global__ __launch_bounds__(kBlock) void k_stage_b_lean(const LayerArgs a) {
   const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int H = a.L.hidden;
   const int tiles = H / 64;
-  // the shared expert's column tiles first (see k_stage_a_lean)
-  const int hasSh = a.L.shared_inter > 0 ? 1 : 0;
+  // the shared expert's (token block, column tile) units first
+  const int hasSh = lean_b_sh_blocks(a.L, a.T);
   const int u0 = (int)blockIdx.x / tiles, nt = (int)blockIdx.x % tiles;
   if (u0 < hasSh) {
-    lean_b_item<false, KB, NWS>(a, (const char*)a.L.shared_w2, nullptr, a.T, nullptr, nullptr, a.L.topk,
-                                nt * 64 + 16 * wv, wv);
+    lean_b_item<false, KB, NWS>(a, (const char*)a.L.shared_w2, nullptr, min(a.T, (u0 + 1) * kLeanBShXT), nullptr,
+                                nullptr, a.L.topk, nt * 64 + 16 * wv, wv, nullptr, 16, u0 * kLeanBShXT);
     return;
   }
   const int u = u0 - hasSh;
@@ -2585,7 +2610,7 @@ static void launch_stages(const LayerArgs& a, int gridA, int gridB, hipStream_t 
     const int maxU = a.L.num_experts < a.T * a.L.topk ? a.L.num_experts : a.T * a.L.topk;
     const size_t lds = 4u * (kLeanXT + 1) * (size_t)lean_pitch(512) * 2u;
     if (which & 1) {
-      const int items = maxU * (a.L.inter / 8) + a.L.shared_inter / 8;
+      const int items = maxU * (a.L.inter / 8) + (a.L.shared_inter / 8) * lean_a_sh_blocks(a.L, a.T);
       if (a.route_a) {
         if (a.L.route_mode == FTM_ROUTE_SOFTMAX_TOPK)
           hipLaunchKernelGGL((k_stage_a_lean_route<512, 2, FTM_ROUTE_SOFTMAX_TOPK>), dim3(items), dim3(kBlock), lds, st, a);
@@ -2605,7 +2630,7 @@ static void launch_stages(const LayerArgs& a, int gridA, int gridB, hipStream_t 
         const size_t ldsb = (size_t)kBcWaves * (kLeanXT + 1) * (size_t)lean_pitch(512) * 2u;
         hipLaunchKernelGGL((k_stage_bc_lean<512, 2>), dim3(a.L.hidden / kBcCols), dim3(64 * kBcWaves), ldsb, st, a);
       } else {
-        const int grid = (maxU + (a.L.shared_inter > 0 ? 1 : 0)) * (a.L.hidden / 64);
+        const int grid = (maxU + lean_b_sh_blocks(a.L, a.T)) * (a.L.hidden / 64);
         hipLaunchKernelGGL((k_stage_b_lean<512, 2>), dim3(grid), dim3(kBlock), lds, st, a);
       }
     }

@@ -35,7 +35,7 @@ def _run_and_check(syn, gpu, *, check_routing=True):
 
 
 @pytest.mark.parametrize("name", ["c1_int8", "c2_gptq", "c3_fp8", "c4_mxfp4"])
-@pytest.mark.parametrize("T", [1, 5, 16, 24])
+@pytest.mark.parametrize("T", [1, 5, 16, 21, 24])
 def test_small_layer_matches_oracle(gpu, name, T):
     syn = S.generate(S.SMALL[name], T=T, seed=11 + T)
     _run_and_check(syn, gpu)
@@ -82,7 +82,7 @@ def c3_full():
     return S.generate(S.CONFIGS["c3_fp8"], T=64, seed=0)
 
 
-@pytest.mark.parametrize("T", [1, 4, 16, 64])
+@pytest.mark.parametrize("T", [1, 4, 16, 37, 64])
 def test_c3_fp8_full_shape_matches_oracle(gpu, c3_full, T):
     base = c3_full
     syn = S.SyntheticLayer(base.cfg, base.bank, base.gate_w, base.x[:T].contiguous(), shared=base.shared)
