@@ -1204,47 +1204,11 @@ __device__ void stage_b_gq(const LayerArgs& a, const ProjSlot& W, int it, int cn
 }
 
 // Layers the GPTQ decode stage B with h rows in LDS takes.
-static bool gq_b_ok(const ftm_moe_layer& L, int T) {
-  const ftm_proj& B = L.w2;
-  if (B.fmt != FTM_FMT_GPTQ_INT4 || L.act_dtype != FTM_DT_BF16 || B.group != 128) return false;
-  if (L.hidden % kGqNB != 0 || L.inter % 128 != 0 || T > kGqBMaxT) return false;
-  return (L.inter / 128 + 1) / 2 * 128 <= kGqMaxKR;
-}
-
 template <int EFMT, int AT>
 __device__ void stage_b_body(const LayerArgs& a, const ProjSlot& W, int cnt, const int32_t* list, int shared_col,
                              int nt, f32x4* red);
 
 // Routed items (expert, 128 columns) first, then the shared expert's 64-column tiles.
-__global__ __launch_bounds__(kBlock) void k_stage_b_gq(const LayerArgs a) {
-  __shared__ f32x4 red[4 * 4 * 64];
-  const int H = a.L.hidden;
-  const int tilesR = H / kGqNB;
-  int item = blockIdx.x;
-  const int nRouted = sload_i32(a.ctrl, kCtrlNRouted);
-  if (item < nRouted * tilesR) {
-    const int u = item / tilesR, it = item % tilesR;
-    const int e = sload_i32(a.uniq, u), cnt = sload_i32(a.ucnt, u);
-    const int32_t* list = a.lists + (size_t)e * a.T;
-    const int slot = a.L.slot_of_expert ? sload_i32(a.L.slot_of_expert, e) : e;
-    if (slot < 0 || slot >= a.L.w2.num_slots) {
-      // non-resident expert: contribute zeros, flag the error
-      for (int idx = threadIdx.x; idx < cnt * kGqNB; idx += kBlock) {
-        const int m = idx / kGqNB, n = it * kGqNB + idx % kGqNB;
-        a.ybuf[(size_t)list[m] * H + n] = 0.0f;
-      }
-      if (threadIdx.x == 0) atomicOr(&a.ctrl[kCtrlError], 1);
-      return;
-    }
-    stage_b_gq(a, proj_slot(a.L.w2, slot), it, cnt, list, red);
-  } else {
-    item -= nRouted * tilesR;
-    if (a.L.shared_inter <= 0 || item >= H / 64) return;
-    const ProjSlot W = shared_view(a.L.shared_w2, H, a.L.shared_inter);
-    stage_b_body<FTM_FMT_BF16, FTM_DT_BF16>(a, W, a.T, nullptr, a.L.topk, item, red);
-  }
-}
-
 // ---------------------------------------------------------------- stage A, K-major formats
 // Work item: 8 channels of one expert = 16 weight rows (the 8 gate rows and
 // their 8 up rows), K split over the 4 waves of a workgroup and reduced
@@ -1653,7 +1617,7 @@ __global__ __launch_bounds__(kBlock) void k_stage_a_xl(const LayerArgs a) {
 // leave CUs idle and whose rows are too long for one window per wave.
 template <int EFMT, int LPG>
 __device__ void stage_b_ks_body(const LayerArgs& a, const ProjSlot& W, int c0, int cnt, const ExpertRec* rec,
-                                const int32_t* list, int shared_col, int kp, f32x4* red) {
+                                const int32_t* list, int shared_col, int kp, f32x4* red, int mb0 = 0) {
   using F = KMajor<EFMT>;
   constexpr int KS = 4;
   const int lane = threadIdx.x & 63;
@@ -1670,14 +1634,14 @@ __device__ void stage_b_ks_body(const LayerArgs& a, const ProjSlot& W, int c0, i
   uint16_t* xw = ftm_xl_lds + kp * kXT * pitch;
   const int k0 = L_lo * F::kLoadK, k1 = min(L_hi * F::kLoadK, W.K);
   const float bn = (W.bias != nullptr && kp == 0) ? load_scalar(W.bias, c0 + n, W.bias_dt) : 0.0f;
-  for (int mb = 0; mb < cnt; mb += kXT) {
+  for (int mb = mb0; mb < cnt; mb += kXT) {
     const int nb = min(kXT, cnt - mb);
     int pr[kXT];
     block_pairs(a, rec, list, shared_col, cnt, mb, pr);
     xl_fill_wave(pr, a.hbuf, 1, a.Imax, k0, k1, xw, pitch);
     f32x4 acc[1] = {(f32x4){0.f, 0.f, 0.f, 0.f}};
     for (int Lw = L_lo; Lw < L_hi; Lw += kRowsNLW) {
-      if (Lw != L_lo || (mb > 0 && multi)) rows_issue<EFMT, kRowsNLW, true>(W, G[0], Lw, L_hi, S[0]);
+      if (Lw != L_lo || (mb > mb0 && multi)) rows_issue<EFMT, kRowsNLW, true>(W, G[0], Lw, L_hi, S[0]);
       __builtin_amdgcn_s_waitcnt(0);  // weights and this wave's LDS copy have landed
       rows_consume_lds<EFMT, kRowsNLW, 1, LPG, true>(W, G, Lw, L_hi, S, xw, k0, pitch, nb, acc);
     }
@@ -1728,6 +1692,66 @@ __global__ __launch_bounds__(kBlock) void k_stage_b_ks(const LayerArgs a) {
     const ProjSlot W = shared_view(a.L.shared_w2, H, Is);
     stage_b_ks_body<FTM_FMT_BF16, kRowsNLW>(a, W, sitem * 16, a.T, nullptr, nullptr, a.L.topk, kp, red);
   }
+}
+
+// GPTQ stage B: the shared expert's items first, 16 output columns each with
+// K split over the 4 waves (stage_b_ks_body) and its tokens in blocks of
+// kGqBShXT, one workgroup per (block, 16 columns); then the routed experts'
+// 128-column items (stage_b_gq).  Measured on MI355X with a Qwen1.5-MoE-A2.7B
+// shaped layer (60 GPTQ experts of 1408, top-4, a bf16 shared expert of
+// 5632): stage B T=1 35.4 -> 15.2 us, T=16 60.8 -> 34.8, T=32 101 -> 61
+// against 64-column shared items over every token (H / 64 = 32 workgroups of
+// 720 KB each); blocks of 4 or 16 tokens: within 1 us of 8 up to T=16.
+constexpr int kGqBShXT = 8;
+__host__ __device__ __forceinline__ int gq_b_sh_items(const ftm_moe_layer& L, int T) {
+  return L.shared_inter > 0 ? (L.hidden / 16) * ((T + kGqBShXT - 1) / kGqBShXT) : 0;
+}
+
+// Layers the GPTQ decode stage B takes: the routed items' K halves within
+// kGqMaxKR, the shared expert's LDS regions (4 waves x kXT rows of a quarter
+// of K) within 64 KiB.
+static bool gq_b_ok(const ftm_moe_layer& L, int T) {
+  const ftm_proj& B = L.w2;
+  if (B.fmt != FTM_FMT_GPTQ_INT4 || L.act_dtype != FTM_DT_BF16 || B.group != 128) return false;
+  if (L.hidden % kGqNB != 0 || L.inter % 128 != 0 || T > kGqBMaxT) return false;
+  if (L.shared_inter > 0) {
+    const int imax = L.inter > L.shared_inter ? L.inter : L.shared_inter;
+    if (L.shared_inter % 8 != 0 || 4 * kXT * xl_pitch(imax, 4) * 2 > 65536) return false;
+  }
+  return (L.inter / 128 + 1) / 2 * 128 <= kGqMaxKR;
+}
+
+__global__ __launch_bounds__(kBlock) void k_stage_b_gq(const LayerArgs a) {
+  __shared__ f32x4 red[4 * 4 * 64];
+  const int H = a.L.hidden;
+  const int tilesR = H / kGqNB;
+  const int nSh = gq_b_sh_items(a.L, a.T);
+  const int item = (int)blockIdx.x;
+  if (item < nSh) {
+    const int tn = H / 16, b = item / tn, c0 = (item % tn) * 16;
+    const int kp = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const ProjSlot W = shared_view(a.L.shared_w2, H, a.L.shared_inter);
+    stage_b_ks_body<FTM_FMT_BF16, kRowsNLW>(a, W, c0, min(a.T, (b + 1) * kGqBShXT), nullptr, nullptr, a.L.topk, kp,
+                                            red, b * kGqBShXT);
+    return;
+  }
+  const int ritem = item - nSh;
+  const int nRouted = sload_i32(a.ctrl, kCtrlNRouted);
+  if (ritem >= nRouted * tilesR) return;
+  const int u = ritem / tilesR, it = ritem % tilesR;
+  const int e = sload_i32(a.uniq, u), cnt = sload_i32(a.ucnt, u);
+  const int32_t* list = a.lists + (size_t)e * a.T;
+  const int slot = a.L.slot_of_expert ? sload_i32(a.L.slot_of_expert, e) : e;
+  if (slot < 0 || slot >= a.L.w2.num_slots) {
+    // non-resident expert: contribute zeros, flag the error
+    for (int idx = threadIdx.x; idx < cnt * kGqNB; idx += kBlock) {
+      const int m = idx / kGqNB, n = it * kGqNB + idx % kGqNB;
+      a.ybuf[(size_t)list[m] * H + n] = 0.0f;
+    }
+    if (threadIdx.x == 0) atomicOr(&a.ctrl[kCtrlError], 1);
+    return;
+  }
+  stage_b_gq(a, proj_slot(a.L.w2, slot), it, cnt, list, red);
 }
 
 // Stage B item body: NT x 64 output columns of one expert; in each 64-column
@@ -2665,9 +2689,12 @@ static void launch_stages(const LayerArgs& a, int gridA, int gridB, hipStream_t 
     const XlPlan pb = xl_plan_b<FMT, AT>(a.L, a.T);
     if constexpr (FMT == FTM_FMT_GPTQ_INT4) {
       if (gq_b_ok(a.L, a.T) && AT == FTM_DT_BF16) {
-        // routed items of 128 columns + the shared expert's 64-column tiles: within gridB
-        const size_t lds = 4u * (kGqXT + 1) * (size_t)gq_pitch(kGqMaxKR) * 2u;
-        hipLaunchKernelGGL(k_stage_b_gq, dim3(gridB), dim3(kBlock), lds, st, a);
+        // the shared expert's (token block, 16 columns) items + routed items of 128 columns
+        const size_t lds_r = 4u * (kGqXT + 1) * (size_t)gq_pitch(kGqMaxKR) * 2u;
+        const size_t lds_s = a.L.shared_inter > 0 ? 4u * kXT * (size_t)xl_pitch(a.Imax, 4) * 2u : 0u;
+        const int maxU = a.L.num_experts < a.T * a.L.topk ? a.L.num_experts : a.T * a.L.topk;
+        const int grid = gq_b_sh_items(a.L, a.T) + maxU * (a.L.hidden / kGqNB);
+        hipLaunchKernelGGL(k_stage_b_gq, dim3(grid), dim3(kBlock), lds_r > lds_s ? lds_r : lds_s, st, a);
       } else {
         hipLaunchKernelGGL((k_stage_b<FMT, AT>), dim3(gridB), dim3(kBlock), 0, st, a);
       }

@@ -41,14 +41,17 @@ def test_small_layer_matches_oracle(gpu, name, T):
     _run_and_check(syn, gpu)
 
 
-@pytest.mark.parametrize("T", [1, 6, 16, 20, 40])
-def test_gptq_layer_with_shared_expert_matches_oracle(gpu, T):
+@pytest.mark.parametrize("Is,T", [(128, 1), (128, 6), (128, 16), (128, 20), (128, 40), (1408, 1), (1408, 9),
+                                  (1408, 20)])
+def test_gptq_layer_with_shared_expert_matches_oracle(gpu, Is, T):
     """GPTQ routed experts beside a dense shared expert: the GPTQ decode
     stages (stage A up to 16 tokens, stage B up to 32) run the shared
-    expert's items on their bf16 path, the register-fed ones above."""
+    expert's items on their bf16 path (stage B: 16 columns, K split over 4
+    waves, tokens in blocks of 8; at 1408 a wave's K quarter takes several
+    prefetch windows), the register-fed ones above."""
     from dataclasses import replace
 
-    syn = S.generate(replace(S.SMALL["c2_gptq"], shared_inter=128), T=T, seed=40 + T)
+    syn = S.generate(replace(S.SMALL["c2_gptq"], shared_inter=Is), T=T, seed=40 + T + Is)
     _run_and_check(syn, gpu)
 
 
