@@ -66,6 +66,7 @@ int check_proj_dequant(const ftm_proj* P) {
     case FTM_FMT_FP32:
       return FTM_OK;
     case FTM_FMT_FP8_BLOCK:
+    case FTM_FMT_FP8_E5M2_BLOCK:
       if (P->s == nullptr) return FTM_ERR_NULL;
       if (!dt_ok(P->s_dtype)) return FTM_ERR_FORMAT;
       return P->group > 0 ? FTM_OK : FTM_ERR_DIM;
@@ -94,6 +95,8 @@ int check_layer(const ftm_moe_layer* L, bool need_router) {
   const int E = L->num_experts, H = L->hidden, I = L->inter, k = L->topk;
   if (E <= 0 || E > kMaxExperts || H <= 0 || I <= 0 || k <= 0 || k > E || k > 64) return FTM_ERR_DIM;
   if (L->act_dtype != FTM_DT_BF16 && L->act_dtype != FTM_DT_F32) return FTM_ERR_FORMAT;
+  // bf16 activations hold h in bf16: only the no-op roundings fit them
+  if (!dt_ok(L->h_dtype) || (L->act_dtype == FTM_DT_BF16 && L->h_dtype == FTM_DT_F16)) return FTM_ERR_FORMAT;
   if (L->route_mode < FTM_ROUTE_SOFTMAX_TOPK || L->route_mode > FTM_ROUTE_TOPK_SOFTMAX) return FTM_ERR_FORMAT;
   if (L->act < FTM_ACT_SILU || L->act > FTM_ACT_SWIGLU_OAI) return FTM_ERR_FORMAT;
   int rc = check_proj_dequant(&L->w13);

@@ -3,6 +3,8 @@
 // Each element is the reference's fp32 product rounded once to the output
 // dtype (round-to-nearest-even):
 //   FP8   w = fp32(e4m3) * s[n/B][k/B]                 fp8_block_linear.py:48-91
+//         (e5m2 bytes: the same product; an e5m2 byte is the high byte of the
+//         fp16 with the same value, so its decode is exact)
 //   GPTQ  w = s[g][n] * (q[k][n] - (z[g][n] + 1))      gptq_linear.py:55-124 (output [K, N])
 //   INT8  w = (byte - 128) * s[n][k/gs]                int8_packed_linear.py:74-125
 //   MXFP4 w = LUT[nibble] * 2^(e8m0 - 127)             mxfp4_linear.py:38-76
@@ -18,6 +20,15 @@ namespace ftm {
 __constant__ float kE2M1[16] = {0.0f,  0.5f,  1.0f,  1.5f,  2.0f,  3.0f,  4.0f,  6.0f,
                                 -0.0f, -0.5f, -1.0f, -1.5f, -2.0f, -3.0f, -4.0f, -6.0f};
 
+// e5m2 (sign, 5 exponent bits with bias 15, 2 mantissa bits: the high byte of
+// an IEEE fp16) -> its exact fp32 value, infinities and NaN included.
+__device__ __forceinline__ float e5m2_to_f32(uint32_t b) {
+  const uint32_t sign = (b & 0x80u) << 24, e = (b >> 2) & 31u, m = b & 3u;
+  if (e == 31u) return __uint_as_float(sign | 0x7f800000u | (m << 21));
+  if (e == 0u) return __uint_as_float(sign | __float_as_uint((float)m * 0x1p-16f));
+  return __uint_as_float(sign | ((e + 112u) << 23) | (m << 21));
+}
+
 __device__ __forceinline__ float dequant_elem(const ProjSlot& W, int n, int k) {
   const int N = W.N, K = W.K;
   switch (W.fmt) {
@@ -27,6 +38,12 @@ __device__ __forceinline__ float dequant_elem(const ProjSlot& W, int n, int k) {
       const int nkb = (K + W.group - 1) / W.group;
       const float s = load_scalar(W.s, (int64_t)(n / W.group) * nkb + k / W.group, W.s_dt);
       return f.x * s;
+    }
+    case FTM_FMT_FP8_E5M2_BLOCK: {
+      const float f = e5m2_to_f32((uint8_t)W.w[(int64_t)n * K + k]);
+      const int nkb = (K + W.group - 1) / W.group;
+      const float s = load_scalar(W.s, (int64_t)(n / W.group) * nkb + k / W.group, W.s_dt);
+      return f * s;
     }
     case FTM_FMT_GPTQ_INT4: {
       const uint32_t word = ((const uint32_t*)W.w)[(int64_t)(k / 8) * N + n];
@@ -165,7 +182,8 @@ __global__ __launch_bounds__(kBlock) void k_gen_stage_a(const GenArgs a) {
       g += load_scalar(W.bias, i, W.bias_dt);
       u += load_scalar(W.bias, Iu + i, W.bias_dt);
     }
-    store_scalar(a.hbuf, (int64_t)p * a.Imax + i, dt, gen_act(a.L.act, g, u, a.L.swiglu_alpha, a.L.swiglu_limit));
+    store_scalar(a.hbuf, (int64_t)p * a.Imax + i, dt,
+                 round_to(gen_act(a.L.act, g, u, a.L.swiglu_alpha, a.L.swiglu_limit), a.L.h_dtype));
   }
 }
 

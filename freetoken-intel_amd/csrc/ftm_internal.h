@@ -44,7 +44,8 @@ static_assert(kLeanRouteMaxT <= kRecPairs, "records hold all pairs of a routed e
 constexpr int kCtrlArriveTopk = 0;  // arrivals of the top-k workgroups
 constexpr int kCtrlNRouted = 1;     // routed experts with >= 1 token (written per call)
 constexpr int kCtrlNU = 2;          // nRouted + shared expert
-constexpr int kCtrlError = 3;       // sticky error bits (bit 0: routed to a non-resident slot)
+constexpr int kCtrlError = 3;       // sticky error bits (FTM_WS_ERR_*), read and cleared by the caller
+static_assert(kCtrlError * 4 == FTM_WS_ERROR_OFFSET, "error word offset of the C ABI");
 constexpr int kCtrlExpertCnt = 16;  // [E] per-expert pair counters (E <= kMaxExperts)
 constexpr int kMaxExperts = 512;
 constexpr int kCtrlTileCnt = kCtrlExpertCnt + kMaxExperts;  // [H/64] combine arrivals

@@ -344,6 +344,32 @@ __device__ __forceinline__ void route_load(const LayerArgs& a, int t, uint32_t (
   }
 }
 
+// Caller routing may list one expert more than once for a token; the
+// reference's per-pair loop (python/freetoken/models/qwen3_5_moe/__init__.py:
+// 1732-1737) then applies the expert once per listing.  The repeats' weights
+// are added, in listing order, to the expert's first listing and the repeats
+// become pairs without an expert: y * ((w1 + w2) + ...) for y * w1 + y * w2 +
+// ..., and no expert's list can hold more than T pairs.  Whole wave; lanes >= k
+// hold sel_e = -1.
+__device__ __forceinline__ void fold_repeats(int& sel_e, float& sel_w, int E, int k) {
+  const int lane = threadIdx.x & 63;
+  const bool valid = lane < k && sel_e >= 0 && sel_e < E;
+  bool repeat = false;
+  float tot = sel_w;
+  for (int j = 0; j < k; ++j) {
+    const int ej = __shfl(sel_e, j);
+    const float wj = __shfl(sel_w, j);
+    if (valid && ej == sel_e) {
+      repeat = repeat || j < lane;
+      tot = j > lane ? tot + wj : tot;
+    }
+  }
+  if (valid) {
+    sel_e = repeat ? -1 : sel_e;
+    sel_w = repeat ? 0.0f : tot;
+  }
+}
+
 // use_pre: take the router logits of t from pre (route_load, router path only).
 template <int MODE, int NV>
 __device__ __forceinline__ void route_token_pre(const LayerArgs& a, int t, const void* logits_in, int logits_dt,
@@ -360,6 +386,7 @@ __device__ __forceinline__ void route_token_pre(const LayerArgs& a, int t, const
       sel_e = ids_in[(size_t)t * k + lane];
       sel_w = w_in[(size_t)t * k + lane];
     }
+    fold_repeats(sel_e, sel_w, E, k);
     return;
   }
   const int pdt = logits_in ? logits_dt : act_dt;  // dtype the probabilities live in (LOWP)
@@ -486,12 +513,16 @@ __device__ __forceinline__ void route_token(const LayerArgs& a, int t, const voi
 // by the whole wave; skip: this lane's pair (lane < k) has no expert.
 __device__ __forceinline__ void zero_skipped_slots(const LayerArgs& a, int t, bool skip) {
   uint64_t m = __ballot(skip);
-  const int H4 = a.L.hidden / 4, lane = threadIdx.x & 63;
+  const int H = a.L.hidden, lane = threadIdx.x & 63;
   while (m) {
     const int j = __builtin_ctzll(m);
     m &= m - 1;
-    f32x4* row = (f32x4*)(a.ybuf + (size_t)(t * a.KP + j) * a.L.hidden);
-    for (int i = lane; i < H4; i += 64) row[i] = (f32x4){0.f, 0.f, 0.f, 0.f};
+    float* row = a.ybuf + (size_t)(t * a.KP + j) * H;
+    if (H % 4 == 0) {
+      for (int i = lane; i < H / 4; i += 64) ((f32x4*)row)[i] = (f32x4){0.f, 0.f, 0.f, 0.f};
+    } else {
+      for (int i = lane; i < H; i += 64) row[i] = 0.0f;
+    }
   }
 }
 
@@ -502,6 +533,7 @@ __device__ __forceinline__ void emit_token(const LayerArgs& a, int t, int sel_e,
                                            float* w_out, int32_t* cnt, int32_t* s_first = nullptr) {
   const int E = a.L.num_experts, k = a.L.topk, T = a.T, KP = a.KP;
   const int lane = threadIdx.x & 63;
+  bool listed = false;
   if (lane < k) {
     const int p = t * KP + lane;
     if (sel_e >= 0 && sel_e < E) {
@@ -513,9 +545,11 @@ __device__ __forceinline__ void emit_token(const LayerArgs& a, int t, int sel_e,
       if (pos < T) {
         a.lists[(size_t)sel_e * T + pos] = p;
         if (s_first != nullptr && pos < kRecPairs) s_first[sel_e * kRecPairs + pos] = p;
-      } else {  // a token listed the same expert twice (caller-supplied routing)
+        listed = true;
+      } else {  // more than T pairs for one expert (fold_repeats rules it out): dropped, flagged
         atomicSub(&cnt[sel_e], 1);
         atomicOr(&a.ctrl[kCtrlError], 4);
+        a.ids[(size_t)t * k + lane] = -1;
       }
     } else {
       // caller-supplied id < 0: the pair has no expert in this call (it is in
@@ -524,7 +558,8 @@ __device__ __forceinline__ void emit_token(const LayerArgs& a, int t, int sel_e,
       if (sel_e >= E) atomicOr(&a.ctrl[kCtrlError], 2);
     }
   }
-  zero_skipped_slots(a, t, lane < k && !(sel_e >= 0 && sel_e < E));
+  // every slot no stage writes is zeroed (k_combine sums all of a token's slots)
+  zero_skipped_slots(a, t, lane < k && !listed);
   if (lane == 0 && a.L.shared_inter > 0) {
     const float sl = a.logits[(size_t)t * (E + 1) + E];
     a.wts[t * KP + k] = round_to(1.0f / (1.0f + expf(-sl)), a.L.act_dtype);
@@ -734,10 +769,13 @@ __global__ __launch_bounds__(64 * kTopkBlkWaves) void k_topk_blk(const LayerArgs
       const int slot = s_slot[li * k + lane];
       if (slot >= 0) {
         const int e = slot & 511, pos = s_cnt[e] + (slot >> 9);
-        if (pos < T)
+        if (pos < T) {
           a.lists[(size_t)e * T + pos] = t * KP + lane;
-        else  // more than T pairs for one expert: a token listed it twice (caller routing)
+        } else {  // more than T pairs for one expert (fold_repeats rules it out): dropped, flagged, slot zeroed
           atomicOr(&a.ctrl[kCtrlError], 4);
+          float* row = a.ybuf + (size_t)(t * KP + lane) * a.L.hidden;
+          for (int i = 0; i < a.L.hidden; ++i) row[i] = 0.0f;
+        }
       }
     }
   }
@@ -835,7 +873,7 @@ __device__ void stage_a_body(const LayerArgs& a, const ProjSlot& W, int Iu, int 
       const float gs = W.bias != nullptr ? g4 + bias_g[q] : g4;
       const float us = W.bias != nullptr ? u4 + bias_u[q] : u4;
       if (pe[q] >= 0) {
-        const float h = act_fn(a.L.act, gs, us, a.L.swiglu_alpha, a.L.swiglu_limit);
+        const float h = round_to(act_fn(a.L.act, gs, us, a.L.swiglu_alpha, a.L.swiglu_limit), a.L.h_dtype);
         store_scalar(a.hbuf, (size_t)pe[q] * a.Imax + it * NT + j, AT, h);
       }
     }
@@ -1260,7 +1298,7 @@ __device__ void stage_a_rows(const LayerArgs& a, const ProjSlot& W, int Iu, int 
         const float gs = acc[r] + bg;
         const float us = dpp_f<kDppRowShl8>(acc[r]) + bu;
         if (n < 8 && pe[r] >= 0) {
-          const float h = act_fn(a.L.act, gs, us, a.L.swiglu_alpha, a.L.swiglu_limit);
+          const float h = round_to(act_fn(a.L.act, gs, us, a.L.swiglu_alpha, a.L.swiglu_limit), a.L.h_dtype);
           store_scalar(a.hbuf, (size_t)pe[r] * a.Imax + c0 + n, AT, h);
         }
       }
@@ -1437,6 +1475,8 @@ __global__ __launch_bounds__(kBlock) void k_stage_b(const LayerArgs a) {
 // where they are used.  Tokens are taken kXT at a time (MFMA rows kXT..15
 // read zero).
 constexpr int kXT = 4;
+// Dynamic LDS a launch may ask for without raising the kernel's attribute.
+constexpr int kDynLdsMax = 65536;
 extern __shared__ __align__(16) uint16_t ftm_xl_lds[];
 
 // LDS elements per token row of one wave's region: its K range plus 8 (shifts
@@ -1716,7 +1756,7 @@ static bool gq_b_ok(const ftm_moe_layer& L, int T) {
   if (L.hidden % kGqNB != 0 || L.inter % 128 != 0 || T > kGqBMaxT) return false;
   if (L.shared_inter > 0) {
     const int imax = L.inter > L.shared_inter ? L.inter : L.shared_inter;
-    if (L.shared_inter % 8 != 0 || 4 * kXT * xl_pitch(imax, 4) * 2 > 65536) return false;
+    if (L.shared_inter % 8 != 0 || 4 * kXT * xl_pitch(imax, 4) * 2 > kDynLdsMax) return false;
   }
   return (L.inter / 128 + 1) / 2 * 128 <= kGqMaxKR;
 }
@@ -2579,6 +2619,7 @@ static XlPlan xl_plan_a(const ftm_moe_layer& L, int T) {
     // routed rows: one window per wave (the bf16 shared rows may take several)
     if (!pf_window_fits<FMT>(L.hidden, 4)) return p;
     if (L.hidden % 8 != 0) return p;
+    if (4 * kXT * xl_pitch(L.hidden, 4) * 2 > kDynLdsMax) return p;
     p.lpg = xl_lpg<FMT>(L.w13, 4);
     if (p.lpg == 0) return p;
     p.nt = 1;
@@ -2596,6 +2637,9 @@ static XlPlan xl_plan_b(const ftm_moe_layer& L, int T) {
     if (T > kXlMaxT) return p;
     if (!pf_window_fits<FMT>(L.inter, 1)) return p;
     if (L.inter % 8 != 0 || (L.shared_inter > 0 && L.shared_inter % 8 != 0)) return p;
+    // the LDS regions are sized for the wider of the routed and shared rows
+    const int imax = L.inter > L.shared_inter ? L.inter : L.shared_inter;
+    if (4 * kXT * xl_pitch(imax, 1) * 2 > kDynLdsMax) return p;
     p.lpg = xl_lpg<FMT>(L.w2, 1);
     if (p.lpg == 0) return p;
     p.nt = 1;
@@ -2620,6 +2664,8 @@ static XlPlan ks_plan_b(const ftm_moe_layer& L, int T) {
     if (!pf_window_fits<FMT>(L.inter, 4) || L.inter % 8 != 0) return p;
     if (L.shared_inter > 0 && (!pf_window_fits<FTM_FMT_BF16>(L.shared_inter, 4) || L.shared_inter % 8 != 0))
       return p;
+    const int imax = L.inter > L.shared_inter ? L.inter : L.shared_inter;
+    if (4 * kXT * xl_pitch(imax, 4) * 2 > kDynLdsMax) return p;
     p.lpg = xl_lpg<FMT>(L.w2, 4);
     p.ok = p.lpg != 0;
     return p;

@@ -274,14 +274,21 @@ struct CopyArgs {
   const int32_t* num;
 };
 
-// Workgroup (row i, piece c): piece c of row i's banks in bank order.
+// Workgroup (row i, piece c): piece c of row i's banks in bank order.  The
+// plan is applied as copy_missing applies it, in order: a row whose slot a
+// later row of the plan also takes is skipped, so the last one lands (when
+// every slot is stamped, ensure_experts passes the remaining misses through
+// slot 0 and only the last stays).
 __global__ __launch_bounds__(kCopyThreads) void k_copy_slots(const CopyArgs g) {
   const int i = (int)blockIdx.x / g.per_row;
   int c = (int)blockIdx.x % g.per_row;
-  const int n = g.num[0];
-  if (i >= n || i >= g.max_rows) return;
+  const int n = min(g.num[0], g.max_rows);
+  if (i >= n) return;
   const int row = g.src[i], slot = g.evict[i];
   if (row < 0 || row >= g.host_rows || slot < 0 || slot >= g.pool_slots) return;  // never outside the banks
+  bool later = false;
+  for (int j = i + 1 + (int)threadIdx.x; j < n; j += kCopyThreads) later = later || g.evict[j] == slot;
+  if (__syncthreads_or(later)) return;
   int b = 0;
   while (b + 1 < g.nb && c >= g.b[b].pieces) c -= g.b[b++].pieces;
   const CopyBank B = g.b[b];

@@ -33,6 +33,7 @@ FMT_GPTQ_INT4 = 2
 FMT_INT8_PACKED = 3
 FMT_MXFP4 = 4
 FMT_FP32 = 5
+FMT_FP8_E5M2_BLOCK = 6
 
 DT_F32 = 0
 DT_F16 = 1
@@ -48,6 +49,10 @@ ACT_RELU = 2
 ACT_SWIGLU_OAI = 3
 
 WS_CTRL_BYTES = 4096
+WS_ERROR_OFFSET = 12
+WS_ERR_SLOT = 1
+WS_ERR_ID = 2
+WS_ERR_LIST = 4
 
 STAGE_ROUTER = 0
 STAGE_TOPK = 1
@@ -113,6 +118,7 @@ class FtmMoeLayer(ctypes.Structure):
         ("swiglu_limit", ctypes.c_float),
         ("apply_router_weight_on_input", ctypes.c_int32),
         ("act_dtype", ctypes.c_int32),
+        ("h_dtype", ctypes.c_int32),
     ]
 
 

@@ -29,6 +29,7 @@ FORMATS = {
     "int8_channel": nat.FMT_INT8_PACKED,
     "mxfp4": nat.FMT_MXFP4,
     "fp32": nat.FMT_FP32,
+    "fp8_e5m2_block": nat.FMT_FP8_E5M2_BLOCK,
 }
 
 

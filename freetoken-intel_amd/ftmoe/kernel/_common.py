@@ -40,13 +40,21 @@ def run_linear(proj: Proj, x: torch.Tensor, *, out_dtype: Optional[torch.dtype],
 def run_expert(gate_up: Proj, down: Proj, x: torch.Tensor, *, intermediate: int,
                out_dtype: Optional[torch.dtype]) -> torch.Tensor:
     """``down(silu(gate(x)) * up(x))`` for one packed expert, w13 + activation +
-    w2 fused in the HIP layer kernels (h rounded to the activation dtype)."""
+    w2 fused in the HIP layer kernels: ``gu`` in fp32, ``h`` rounded to
+    ``out_dtype`` (default ``x.dtype``), fp32 down projection rounded to
+    ``out_dtype`` -- the reference's two fused calls
+    (python/freetoken/kernel/triton/fused_fp8_linear.py:172-175).  bf16 in and
+    out runs the bf16 layer kernels; any other pair runs them on fp32
+    activations (``x`` widened exactly) with ``h`` rounded to ``out_dtype``."""
     nat.require_gpu(x, "x")
     out_dtype = out_dtype if out_dtype is not None else x.dtype
-    act_dtype = torch.bfloat16 if x.dtype == torch.bfloat16 else torch.float32
+    if x.dtype == torch.bfloat16 and out_dtype == torch.bfloat16:
+        act_dtype, h_dtype = torch.bfloat16, None
+    else:
+        act_dtype, h_dtype = torch.float32, out_dtype
     xa = x.to(act_dtype).contiguous()
     layer = MoeLayer(w13=gate_up, w2=down, num_experts=1, hidden=gate_up.K, inter=intermediate, topk=1,
-                     act="silu", act_dtype=act_dtype)
+                     act="silu", act_dtype=act_dtype, h_dtype=h_dtype)
     y = layer.expert_forward(0, xa)
     return y if y.dtype == out_dtype else y.to(out_dtype)
 

@@ -26,9 +26,10 @@ def dequantize_block_fp8(weight_fp8: torch.Tensor, weight_scale_inv: torch.Tenso
             f"weight_scale_inv shape {tuple(weight_scale_inv.shape)} does not match "
             f"the expected {expected} for weight_fp8 shape {(N, K)} at block={block}"
         )
-    if weight_fp8.dtype != torch.float8_e4m3fn:
-        raise TypeError(f"weight_fp8 must be float8_e4m3fn, got {weight_fp8.dtype}")
-    return dequant(single_proj("fp8_block", weight_fp8, N, K, s=weight_scale_inv, group=block), out_dtype=out_dtype)
+    if weight_fp8.dtype not in (torch.float8_e4m3fn, torch.float8_e5m2):
+        raise TypeError(f"weight_fp8 must be float8_e4m3fn or float8_e5m2, got {weight_fp8.dtype}")
+    fmt = "fp8_e5m2_block" if weight_fp8.dtype == torch.float8_e5m2 else "fp8_block"
+    return dequant(single_proj(fmt, weight_fp8, N, K, s=weight_scale_inv, group=block), out_dtype=out_dtype)
 
 
 def fp8_block_linear(x: torch.Tensor, weight_fp8: torch.Tensor, weight_scale_inv: torch.Tensor, *,

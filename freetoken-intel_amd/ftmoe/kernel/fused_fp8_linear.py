@@ -5,7 +5,9 @@ gfx950: e4m3 bytes are converted in registers to their exact bf16 values
 (``v_cvt_scalef32_pk_bf16_fp8``, scale 1.0), multiplied on the bf16 matrix
 core, and each 128x128 block's fp32 scale is applied to the block's partial
 sum.  Activations in fp32/fp16 are split into bf16 hi + lo halves so the
-product keeps ~16 significant bits (the reference's tl.dot runs in fp32)."""
+product keeps ~16 significant bits (the reference's tl.dot runs in fp32).
+e5m2 weights (accepted by the reference, fused_fp8_linear.py:123) run on the
+generic GPU kernels with the same fp32 arithmetic."""
 from __future__ import annotations
 
 import torch
@@ -17,7 +19,8 @@ _QBLOCK = 128
 
 def _proj(weight_fp8: torch.Tensor, weight_scale_inv: torch.Tensor, block: int):
     n, k = weight_fp8.shape
-    return single_proj("fp8_block", weight_fp8, n, k, s=weight_scale_inv, group=block)
+    fmt = "fp8_e5m2_block" if weight_fp8.dtype == torch.float8_e5m2 else "fp8_block"
+    return single_proj(fmt, weight_fp8, n, k, s=weight_scale_inv, group=block)
 
 
 def fused_fp8_linear(
@@ -38,9 +41,7 @@ def fused_fp8_linear(
     but not used (the gfx950 tiling is fixed)."""
     if block % block_n != 0:
         raise ValueError(f"block_n {block_n} must divide block {block} evenly")
-    if weight_fp8.dtype != torch.float8_e4m3fn:
-        if weight_fp8.dtype == torch.float8_e5m2:
-            raise TypeError("weight_fp8 float8_e5m2 is not supported by the gfx950 kernels (e4m3fn only)")
+    if weight_fp8.dtype not in (torch.float8_e4m3fn, torch.float8_e5m2):
         raise TypeError(f"weight_fp8 must be an fp8 dtype, got {weight_fp8.dtype}")
     m, k = x.shape
     n, k2 = weight_fp8.shape
@@ -68,7 +69,7 @@ def fused_fp8_expert_forward(
 ) -> torch.Tensor:
     """One expert's SwiGLU forward against packed block-FP8 banks
     (fused_fp8_linear.py:154-175): gu in fp32, h = silu(gate) * up rounded to
-    the activation dtype, then the down projection."""
+    ``out_dtype`` (default ``x.dtype``), then the down projection."""
     return run_expert(_proj(weight_fp8_gate_up, weight_scale_inv_gate_up, block),
                       _proj(weight_fp8_down, weight_scale_inv_down, block), x,
                       intermediate=intermediate, out_dtype=out_dtype)

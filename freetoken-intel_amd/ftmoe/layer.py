@@ -39,18 +39,81 @@ ACTIVATIONS = {
 
 # One growing workspace per (device, stream): the layer kernels run in stream
 # order, so every MoE layer on a stream can share it.  Its control words are
-# zero at allocation and every call leaves its counters zero again.
+# zero at allocation and every call leaves its counters zero again (the sticky
+# error word excepted: check_status reads and clears it).
 _WS: dict = {}
+# Workspaces a larger call replaced on the same stream.  They stay allocated: a
+# HIP graph captured before the growth still holds their addresses.
+_WS_RETIRED: dict = {}
+
+
+def _ws_key(device: torch.device) -> tuple:
+    return (device.index, torch.cuda.current_stream(device).cuda_stream)
 
 
 def workspace(device: torch.device, nbytes: int) -> torch.Tensor:
-    stream = torch.cuda.current_stream(device).cuda_stream
-    key = (device.index, stream)
+    """This stream's layer workspace, grown to at least ``nbytes``.  Growing
+    allocates, which a HIP graph capture cannot record: size it before the
+    capture (run the largest batch once on the capture stream, or call
+    :func:`reserve_workspace`)."""
+    key = _ws_key(device)
     ws = _WS.get(key)
     if ws is None or ws.numel() < nbytes:
+        if torch.cuda.is_current_stream_capturing():
+            raise RuntimeError(
+                f"the MoE layer workspace of this stream would grow to {nbytes} bytes inside a HIP graph capture; "
+                "run the largest batch once on the capture stream before capturing, or call "
+                "ftmoe.layer.reserve_workspace(device, nbytes)")
+        if ws is not None:
+            _WS_RETIRED.setdefault(key, []).append(ws)
         ws = torch.zeros(max(nbytes, nat.WS_CTRL_BYTES), dtype=torch.uint8, device=device)
         _WS[key] = ws
     return ws
+
+
+def reserve_workspace(device: torch.device, nbytes: int) -> torch.Tensor:
+    """Grow the current stream's workspace to ``nbytes`` now (before a capture)."""
+    return workspace(torch.device(device), int(nbytes))
+
+
+_STATUS_TEXT = {
+    nat.WS_ERR_SLOT: "a routed expert had no resident slot: stale slot map (ensure_experts desync); "
+                     "its pairs contributed zeros",
+    nat.WS_ERR_ID: "an expert id was >= num_experts; its pairs contributed zeros",
+    nat.WS_ERR_LIST: "more pairs than tokens were routed to one expert; the extra pairs were dropped",
+}
+
+
+def read_status(device: Optional[torch.device] = None, *, clear: bool = True) -> int:
+    """The error bits (``ftmoe._native.WS_ERR_*``) the layer kernels recorded in
+    the current stream's workspaces since the last clear (waits for the stream)."""
+    device = torch.device("cuda", torch.cuda.current_device()) if device is None else torch.device(device)
+    key = _ws_key(device)
+    bits = 0
+    for ws in [_WS.get(key)] + _WS_RETIRED.get(key, []):
+        if ws is None:
+            continue
+        word = ws[nat.WS_ERROR_OFFSET:nat.WS_ERROR_OFFSET + 4].view(torch.int32)
+        bits |= int(word.item())
+        if clear:
+            word.zero_()
+    return bits
+
+
+def check_status(device: Optional[torch.device] = None, *, layer_id: Optional[int] = None) -> None:
+    """Raise for the errors :func:`read_status` reports, and clear them: a
+    routed expert without a resident slot raises ``IndexError`` as the
+    reference's stale-slot tripwire does
+    (python/freetoken/models/qwen3_5_moe/__init__.py:1676-1685); an id >= E
+    raises ``ValueError``; a list overflow ``RuntimeError``."""
+    bits = read_status(device)
+    where = f"layer {layer_id}: " if layer_id is not None else ""
+    if bits & nat.WS_ERR_SLOT:
+        raise IndexError(where + _STATUS_TEXT[nat.WS_ERR_SLOT])
+    if bits & nat.WS_ERR_ID:
+        raise ValueError(where + _STATUS_TEXT[nat.WS_ERR_ID])
+    if bits & nat.WS_ERR_LIST:
+        raise RuntimeError(where + _STATUS_TEXT[nat.WS_ERR_LIST])
 
 
 class MoeLayer:
@@ -65,6 +128,9 @@ class MoeLayer:
             (softmax in the logits dtype, Qwen3 / ``fused_moe``), ``"topk_softmax"`` (gpt-oss).
         act: ``"silu"`` / ``"gelu"`` / ``"relu"`` / ``"swiglu_oai"``.
         slot_of_expert: optional int32 device tensor ``[E]`` mapping expert -> bank slot.
+        act_dtype: dtype of ``x``, ``h`` and the output (bf16 or fp32).
+        h_dtype: dtype ``h`` is rounded to before the down projection (None: the
+            activation dtype's own); fp16 needs fp32 activations.
     """
 
     def __init__(self, *, w13: Proj, w2: Proj, num_experts: int, hidden: int, inter: int, topk: int,
@@ -72,7 +138,7 @@ class MoeLayer:
                  shared: Optional[dict] = None, route_mode: str = "softmax_topk", renormalize: bool = True,
                  act: str = "silu", swiglu_alpha: float = 1.702, swiglu_limit: float = 7.0,
                  apply_router_weight_on_input: bool = False, slot_of_expert: Optional[torch.Tensor] = None,
-                 act_dtype: torch.dtype = torch.bfloat16) -> None:
+                 act_dtype: torch.dtype = torch.bfloat16, h_dtype: Optional[torch.dtype] = None) -> None:
         if route_mode not in ROUTE_MODES:
             raise ValueError(f"unknown route_mode {route_mode!r}")
         if act not in ACTIVATIONS:
@@ -87,6 +153,7 @@ class MoeLayer:
         self.apply_router_weight_on_input = apply_router_weight_on_input
         self.slot_of_expert = slot_of_expert
         self.act_dtype = act_dtype
+        self.h_dtype = h_dtype
         self.device = w13.device
         for name, t in (("w13", w13.w), ("w2", w2.w), ("gate_w", self.gate_w), ("slot_of_expert", slot_of_expert)):
             nat.require_gpu(t, name)
@@ -120,6 +187,7 @@ class MoeLayer:
             L.swiglu_limit = float(self.swiglu_limit)
             L.apply_router_weight_on_input = 1 if self.apply_router_weight_on_input else 0
             L.act_dtype = nat.dtype_code(self.act_dtype)
+            L.h_dtype = nat.dtype_code(self.h_dtype) if self.h_dtype is not None else nat.DT_F32
             self._c = L
         return self._c
 
@@ -176,8 +244,12 @@ class MoeLayer:
         name = nat.lib().ftm_moe_stage_kernel(ctypes.byref(self.c()), int(num_tokens), int(stage))
         return name.decode() if name is not None else None
 
-    def forward_routed(self, x: torch.Tensor, topk_ids: torch.Tensor, topk_w: torch.Tensor) -> torch.Tensor:
-        """Routed experts (+ shared) for caller-supplied routing ``[T, k]``."""
+    def forward_routed(self, x: torch.Tensor, topk_ids: torch.Tensor, topk_w: torch.Tensor, *,
+                       check: bool = False) -> torch.Tensor:
+        """Routed experts (+ shared) for caller-supplied routing ``[T, k]``.  An id
+        < 0 marks a pair without an expert; an expert listed twice for one token
+        is applied with the sum of its weights.  ``check``: wait for the call and
+        raise (:func:`check_status`) if a routed expert had no resident slot."""
         x = self._check_x(x)
         T = x.shape[0]
         if tuple(topk_ids.shape) != (T, self.topk) or tuple(topk_w.shape) != (T, self.topk):
@@ -191,6 +263,8 @@ class MoeLayer:
         rc = nat.lib().ftm_moe_forward_routed(ctypes.byref(self.c()), x.data_ptr(), T, ids.data_ptr(), w.data_ptr(),
                                               out.data_ptr(), ws.data_ptr(), ws.numel(), nat.stream_of(x))
         nat.check(rc, "ftm_moe_forward_routed")
+        if check:
+            check_status(x.device)
         return out
 
     def route(self, x: Optional[torch.Tensor] = None, logits: Optional[torch.Tensor] = None):

@@ -130,7 +130,10 @@ class OffloadMoeCache:
         self._pending_whole_layer = False
         self._side_stream = None
         self._copy_done = None
-        self._slot_dev: Optional[torch.Tensor] = None  # device mirror of slot_for_id
+        # device mirror of slot_for_id (host LRU): one buffer for the cache's
+        # lifetime, so layer descriptors that hold its address stay valid
+        self._slot_dev: Optional[torch.Tensor] = None
+        self._slot_dirty = True
 
     def _alloc_bookkeeping(self, cache_size: int) -> None:
         dev = self.device if self.device_lru else "cpu"
@@ -210,7 +213,7 @@ class OffloadMoeCache:
         self.active_mask.zero_()
         self._pending_src_layer = None
         self._pending_whole_layer = False
-        self._slot_dev = None
+        self._slot_dirty = True
 
     def bank_views(self, n: Optional[int] = None) -> tuple:
         """Per-bank device pools in schema order: all ``S`` slots, or the first ``n``."""
@@ -230,7 +233,7 @@ class OffloadMoeCache:
         slots = (ids >= 0).nonzero(as_tuple=True)[0]
         valid = ids[slots]
         self.slot_for_id[valid // E, valid % E] = slots.to(torch.int32)
-        self._slot_dev = None
+        self._slot_dirty = True
 
     def reset(self) -> None:
         self.slot_for_id.fill_(-1)
@@ -241,7 +244,7 @@ class OffloadMoeCache:
         self.num_indices.zero_()
         self._pending_src_layer = None
         self._pending_whole_layer = False
-        self._slot_dev = None
+        self._slot_dirty = True
         for cache in self.bank_caches.values():
             cache.zero_()
         self.reset_stats()
@@ -250,16 +253,23 @@ class OffloadMoeCache:
         self._stats.zero_()
 
     def check_status(self) -> None:
-        """``device_lru``: raise what the host LRU raises at the call for the
-        errors the kernel recorded since the last check (waits for the GPU)."""
-        if not self.device_lru:
-            return
-        st = int(self._status.item())
-        self._status.zero_()
-        if st & 1:
-            raise ValueError(f"expert ids must lie in [0, {self.num_experts})")
-        if st & 2:
-            raise RuntimeError("slot_for_id held a slot outside the pool (the expert was reloaded)")
+        """Raise for the errors recorded on the GPU since the last check (waits
+        for the GPU): with ``device_lru``, what the host LRU raises at the call;
+        then the layer kernels' error word of the current stream
+        (:func:`ftmoe.layer.check_status`: a routed expert without a resident
+        slot raises ``IndexError``, the reference's stale-slot tripwire,
+        python/freetoken/models/qwen3_5_moe/__init__.py:1676-1685)."""
+        if self.device_lru:
+            st = int(self._status.item())
+            self._status.zero_()
+            if st & 1:
+                raise ValueError(f"expert ids must lie in [0, {self.num_experts})")
+            if st & 2:
+                raise RuntimeError("slot_for_id held a slot outside the pool (the expert was reloaded)")
+        if self.is_gpu:
+            from ..layer import check_status
+
+            check_status(self.device)
 
     def decode_miss_stats(self) -> dict:
         return {"missing": int(self.stat_missing.item()), "calls": int(self.stat_calls.item())}
@@ -367,7 +377,7 @@ class OffloadMoeCache:
         self.stat_calls += 1
         self._pending_src_layer = layer_id
         self._pending_whole_layer = whole
-        self._slot_dev = None
+        self._slot_dirty = True
 
     # -- copy engine -----------------------------------------------------------------
 
@@ -429,9 +439,32 @@ class OffloadMoeCache:
         if self.device_lru:
             return self.slot_for_id[layer_id]
         if self._slot_dev is None:
+            self._slot_dev = torch.full_like(self.slot_for_id, -1, device=self.device)
+            self._slot_dirty = True
+        if self._slot_dirty:
+            # a pinned snapshot: the host map changes again before the copy runs
             src = self.slot_for_id.pin_memory() if self.is_gpu else self.slot_for_id
-            self._slot_dev = src.to(self.device, non_blocking=True)
+            self._slot_dev.copy_(src, non_blocking=True)
+            self._slot_dirty = False
         return self._slot_dev[layer_id]
+
+    def require_resident(self, layer_id: int, expert_ids: torch.Tensor) -> None:
+        """Host LRU: raise ``IndexError`` when a routed expert of ``layer_id`` has
+        no slot in ``[0, cache_size)`` -- the reference's loud stale-slot guard
+        (python/freetoken/models/qwen3_5_moe/__init__.py:1676-1685), here also
+        for a slot of -1 (the reference would skip such a pair silently)."""
+        if self.device_lru:
+            raise RuntimeError("require_resident reads the host LRU; with device_lru use check_status()")
+        ids = expert_ids.reshape(-1).to("cpu", torch.int64)
+        ids = ids[ids >= 0]
+        if ids.numel() == 0:
+            return
+        slots = self.slot_for_id[layer_id].to(torch.int64)[ids]
+        bad = (slots < 0) | (slots >= self.cache_size)
+        if bool(bad.any()):
+            stale = int(slots[bad][0])
+            raise IndexError(f"layer {layer_id}: offload routed slot id {stale} outside cache_size "
+                             f"{self.cache_size}: stale slot map (ensure_experts desync)")
 
     def resident_slots(self, layer_id: int) -> list:
         E = self.num_experts
@@ -552,21 +585,15 @@ class SlotWeightAccessor:
         return self._layer
 
     def expert_forward(self, s_i: int, x: torch.Tensor) -> torch.Tensor:
-        """``down(silu(gate(x)) * up(x))`` for slot ``s_i``: the fused expert kernel
-        (fp32 accumulation, ``h`` rounded to the activation dtype) when the
-        format's ``prefer_fused_over_dequant(rows)`` holds, else the dense
-        weights of :meth:`get` through torch matmuls on the GPU."""
+        """``down(silu(gate(x)) * up(x))`` for slot ``s_i`` (offload_cache.py:926-996)
+        on the gfx950 expert kernels for every row count: up to the format's
+        ``prefer_fused_over_dequant`` crossover the decode stages, above it the
+        MFMA-tiled stages the layer switches to (weights decoded exactly in
+        registers), where the reference dequantizes the slot with :meth:`get`
+        and runs dense matmuls.  fp32 accumulation, ``h`` rounded to the
+        accessor's dtype."""
         nat.require_gpu(x, "x")
-        from ..kernel import fused_fp8_linear, fused_int8_linear, fused_mxfp4_linear, gptq_fused_linear
-
-        prefer = {"fp8_block": fused_fp8_linear.prefer_fused_over_dequant,
-                  "int8_channel": fused_int8_linear.prefer_fused_over_dequant,
-                  "mxfp4": fused_mxfp4_linear.prefer_fused_over_dequant,
-                  "gptq_int4": gptq_fused_linear.prefer_fused_over_dequant}.get(self.quant_format)
-        if self.quant_format == "bf16" or (prefer is not None and prefer(x.shape[0])):
-            return self.pool_layer().expert_forward(int(s_i), x.to(self._dtype))
-        gate_w, up_w, down_w = self.get(s_i)
-        return (torch.nn.functional.silu(x @ gate_w.t()) * (x @ up_w.t())) @ down_w.t()
+        return self.pool_layer().expert_forward(int(s_i), x.to(self._dtype))
 
     def get(self, s_i: int):
         """``(gate_w [I, H], up_w [I, H], down_w [H, I])`` of slot ``s_i`` in the
@@ -587,28 +614,49 @@ class SlotWeightAccessor:
         return result
 
 
+def grouped_layer(cache: OffloadMoeCache, layer_id: int, *, intermediate: int, topk: int, dtype: torch.dtype,
+                  act: str = "silu", shared: Optional[dict] = None, swiglu_alpha: float = 1.702,
+                  swiglu_limit: float = 7.0):
+    """The :class:`~ftmoe.layer.MoeLayer` over the slot pool for ``layer_id``
+    (expert ``e`` read from slot ``slot_of_expert(layer_id)[e]``), built once per
+    (layer, shape, activation, shared expert) and bank registration, so a
+    decode step pays no descriptor construction."""
+    skey = None if not shared else tuple(sorted((k, v.data_ptr(), tuple(v.shape)) for k, v in shared.items()))
+    key = ("grouped", int(layer_id), int(intermediate), dtype, int(topk), act, skey, float(swiglu_alpha),
+           float(swiglu_limit))
+    layer = cache._pool_layers.get(key)
+    if layer is None:
+        pkey = (int(intermediate), dtype)
+        pool = cache._pool_layers.get(pkey)
+        if pool is None:  # the pool's projections, built once per bank registration
+            pool = SlotWeightAccessor(cache, intermediate, dtype).pool_layer()
+            cache._pool_layers[pkey] = pool
+        from ..layer import MoeLayer
+
+        layer = MoeLayer(w13=pool.w13, w2=pool.w2, num_experts=cache.num_experts, hidden=pool.hidden,
+                         inter=intermediate, topk=int(topk), shared=shared, act=act, swiglu_alpha=swiglu_alpha,
+                         swiglu_limit=swiglu_limit, slot_of_expert=cache.slot_of_expert(layer_id), act_dtype=dtype)
+        cache._pool_layers[key] = layer
+    else:
+        cache.slot_of_expert(layer_id)  # refresh the device map if the host LRU moved
+    return layer
+
+
 def moe_grouped_forward(flat: torch.Tensor, top_idx: torch.Tensor, top_w: torch.Tensor, cache: OffloadMoeCache,
                         layer_id: int, *, intermediate: int, act: str = "silu", shared: Optional[dict] = None,
-                        swiglu_alpha: float = 1.702, swiglu_limit: float = 7.0) -> torch.Tensor:
+                        swiglu_alpha: float = 1.702, swiglu_limit: float = 7.0, check: bool = False) -> torch.Tensor:
     """One grouped call for a layer whose experts sit in the slot pool: replaces
     the per-(token, expert) loop of ``_forward_offload_core``
     (python/freetoken/models/qwen3_5_moe/__init__.py:1706-1737).  ``top_idx`` /
     ``top_w`` ``[T, k]`` are expert ids and router weights; the layer must have
     been made resident with :meth:`OffloadMoeCache.ensure_experts` and
-    :meth:`~OffloadMoeCache.copy_missing` (a routed expert that is not resident
-    contributes zeros and sets the workspace error bit)."""
-    key = (int(intermediate), flat.dtype)
-    pool = cache._pool_layers.get(key)
-    if pool is None:  # the pool's projections, built once per bank registration
-        pool = SlotWeightAccessor(cache, intermediate, flat.dtype).pool_layer()
-        cache._pool_layers[key] = pool
-    from ..layer import MoeLayer
-
-    layer = MoeLayer(w13=pool.w13, w2=pool.w2, num_experts=cache.num_experts, hidden=pool.hidden,
-                     inter=intermediate, topk=int(top_idx.shape[1]), shared=shared, act=act,
-                     swiglu_alpha=swiglu_alpha, swiglu_limit=swiglu_limit,
-                     slot_of_expert=cache.slot_of_expert(layer_id), act_dtype=flat.dtype)
-    return layer.forward_routed(flat, top_idx, top_w)
+    :meth:`~OffloadMoeCache.copy_missing`.  A routed expert that is not
+    resident contributes zeros and sets the workspace error bit, which
+    ``check=True`` (a synchronisation) or a later :meth:`OffloadMoeCache.check_status`
+    turns into ``IndexError``."""
+    layer = grouped_layer(cache, layer_id, intermediate=intermediate, topk=int(top_idx.shape[1]), dtype=flat.dtype,
+                          act=act, shared=shared, swiglu_alpha=swiglu_alpha, swiglu_limit=swiglu_limit)
+    return layer.forward_routed(flat, top_idx, top_w, check=check)
 
 
 def moe_offload_forward(flat: torch.Tensor, top_idx: torch.Tensor, top_w: torch.Tensor, cache: OffloadMoeCache,
@@ -659,6 +707,7 @@ def moe_offload_forward(flat: torch.Tensor, top_idx: torch.Tensor, top_w: torch.
     cap = cache.cache_size
     if uniq.numel() <= cap:
         cache.ensure_experts(layer_id, uniq)
+        cache.require_resident(layer_id, uniq)
         cache.copy_missing()
         return moe_grouped_forward(flat, top_idx, top_w, cache, layer_id, intermediate=intermediate, act=act,
                                    shared=shared, swiglu_alpha=swiglu_alpha, swiglu_limit=swiglu_limit)
@@ -667,6 +716,7 @@ def moe_offload_forward(flat: torch.Tensor, top_idx: torch.Tensor, top_w: torch.
     for c0 in range(0, uniq.numel(), cap):
         chunk = uniq[c0:c0 + cap]
         cache.ensure_experts(layer_id, chunk)
+        cache.require_resident(layer_id, chunk)
         cache.copy_missing()
         member = torch.isin(ids_dev, chunk.to(ids_dev.device, torch.int32))
         ids_c = torch.where(member, ids_dev, torch.full_like(ids_dev, -1))
@@ -678,4 +728,4 @@ def moe_offload_forward(flat: torch.Tensor, top_idx: torch.Tensor, top_w: torch.
 
 
 __all__ = ["OffloadMoeCache", "SlotWeightAccessor", "_BANK_SCHEMAS", "gptq_int4_bytes_per_expert_slot",
-           "moe_grouped_forward", "moe_offload_forward"]
+           "grouped_layer", "moe_grouped_forward", "moe_offload_forward"]

@@ -16,6 +16,8 @@
  *   FTM_FMT_FP32        w: f32  [N, K]
  *   FTM_FMT_FP8_BLOCK   w: e4m3fn bytes [N, K]; s: [ceil(N/B), ceil(K/B)] (B = group)
  *                       python/freetoken/kernel/triton/fp8_block_linear.py:48-91
+ *   FTM_FMT_FP8_E5M2_BLOCK  the same with e5m2 bytes (fused_fp8_linear.py:123 accepts
+ *                       torch.float8_e5m2 weights); runs on the generic GPU kernels
  *   FTM_FMT_GPTQ_INT4   w: int32 qweight [K/8, N] (8 nibbles along K, LSB first);
  *                       z: int32 qzeros [K/group, N/8]; s: scales [K/group, N]
  *                       python/freetoken/kernel/triton/gptq_linear.py:39-124
@@ -55,6 +57,7 @@ extern "C" {
 #define FTM_FMT_INT8_PACKED 3
 #define FTM_FMT_MXFP4 4
 #define FTM_FMT_FP32 5
+#define FTM_FMT_FP8_E5M2_BLOCK 6
 
 /* ---- scalar dtypes (activations, scales, outputs, biases) ---- */
 #define FTM_DT_F32 0
@@ -124,6 +127,11 @@ typedef struct ftm_moe_layer {
   float swiglu_limit;           /* FTM_ACT_SWIGLU_OAI clamp limit (7.0) */
   int32_t apply_router_weight_on_input; /* scale x by the router weight instead of y */
   int32_t act_dtype;            /* FTM_DT_BF16 or FTM_DT_F32: x, h and out dtype */
+  int32_t h_dtype;              /* FTM_DT_*: h is rounded to it before w2 (then held in
+                                   act_dtype); FTM_DT_F32 = no extra rounding;
+                                   FTM_DT_F16 needs act_dtype FTM_DT_F32.  The
+                                   reference rounds h to out_dtype
+                                   (python/freetoken/kernel/triton/fused_fp8_linear.py:172-175) */
 } ftm_moe_layer;
 
 /* ABI version (FTM_ABI_VERSION). Never fails. */
@@ -132,9 +140,19 @@ int ftm_version(void);
 /* Device workspace bytes ftm_moe_forward / ftm_moe_forward_routed / ftm_route
  * need for `num_tokens` tokens.  The first FTM_WS_CTRL_BYTES of a workspace
  * must be zero before its first use (ftm_workspace_init does that); every call
- * leaves them zero again.  Replaces the per-call host buffers of
+ * leaves them zero again, except the sticky error word (int32 at byte
+ * FTM_WS_ERROR_OFFSET), whose bits the kernels OR in and the caller reads and
+ * clears: FTM_WS_ERR_SLOT a routed expert had no resident slot (it contributed
+ * zeros: the reference raises IndexError on such a stale slot,
+ * python/freetoken/models/qwen3_5_moe/__init__.py:1676-1685), FTM_WS_ERR_ID an
+ * expert id >= E (the pair contributed zeros), FTM_WS_ERR_LIST more than T pairs
+ * for one expert (the pair was dropped).  Replaces the per-call host buffers of
  * python/freetoken/moe/offload_cache.py:560-674 and fused_moe.py:106-161. */
 #define FTM_WS_CTRL_BYTES 4096
+#define FTM_WS_ERROR_OFFSET 12
+#define FTM_WS_ERR_SLOT 1
+#define FTM_WS_ERR_ID 2
+#define FTM_WS_ERR_LIST 4
 size_t ftm_moe_workspace_bytes(const ftm_moe_layer* layer, int32_t num_tokens);
 int ftm_workspace_init(void* workspace, size_t ws_bytes, void* stream);
 

@@ -74,6 +74,8 @@ def lib():
         L.orc_e8m0_to_f32.argtypes = [ctypes.c_uint8]
         L.orc_f32_to_bf16.restype = ctypes.c_uint16
         L.orc_f32_to_bf16.argtypes = [ctypes.c_float]
+        L.orc_act.restype = ctypes.c_double
+        L.orc_act.argtypes = [i32, ctypes.c_double, ctypes.c_double, ctypes.c_double, ctypes.c_double]
         _lib = L
     return _lib
 
@@ -278,6 +280,17 @@ def route(logits: np.ndarray, k: int, mode: str = "softmax_topk", renormalize: b
 
 
 # ----------------------------------------------------------------- C-backed pieces
+def act(name: str, g, u, alpha: float = 1.702, limit: float = 7.0) -> np.ndarray:
+    """The expert activation h = act(g, u) of the C oracle (oracle_core.c act_d)
+    in double precision, elementwise (fused_moe.py:53-61, gpt_oss/__init__.py:306-310)."""
+    g = np.asarray(g, np.float64)
+    u = np.broadcast_to(np.asarray(u, np.float64), g.shape)
+    f, code = lib().orc_act, ACTS[name]
+    return np.array([f(code, float(a), float(b), float(alpha), float(limit)) for a, b in zip(g.ravel(), u.ravel())],
+                    np.float64).reshape(g.shape)
+
+
+
 def _dt_code(arr: np.ndarray) -> int:
     if arr.dtype == np.float32:
         return D_F32

@@ -201,6 +201,9 @@ static double act_d(int act, double g, double u, double alpha, double limit) {
   }
 }
 
+/* The activation alone, for the tests that pin it against library routines. */
+double orc_act(int act, double g, double u, double alpha, double limit) { return act_d(act, g, u, alpha, limit); }
+
 static float bias_val(const orc_proj* P, int slot, int n) {
   if (P->bias == NULL) return 0.0f;
   const char* b = (const char*)P->bias + (int64_t)slot * P->bias_stride;

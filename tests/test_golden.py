@@ -71,3 +71,18 @@ def test_router_ties_select_the_same_scores_as_torch_topk():
         if np.sum(logits[t] == kth) == np.sum(logits[t][d["top_idx"][t]] == kth):
             # no tie across the boundary: the same experts
             assert set(ids[t].tolist()) == set(d["top_idx"][t].tolist()), t
+
+
+def test_int8_quantizer_matches_reference_vectors():
+    """Per-channel symmetric INT8 (int8_linear.py:34-43): scale = max(amax,
+    1e-12) / 127, codes round half to even and clamp to +-127 -- on .5 ties,
+    a zero row, a subnormal row and huge magnitudes."""
+    d = _load("int8_quant.npz")
+    q, s = O.quantize_int8_channel(d["w"])
+    np.testing.assert_array_equal(q, d["q"])
+    np.testing.assert_array_equal(s, d["scale"])
+    pq, ps = quant.quantize_int8_channel(torch.from_numpy(d["w"]))
+    np.testing.assert_array_equal(pq.numpy(), d["q"])
+    np.testing.assert_array_equal(ps.numpy(), d["scale"])
+    # the ties of row 0 (scale 1) round to even: -15.5 -> -16, -14.5 -> -14
+    assert d["scale"][0] == 1.0 and d["q"][0, 0] == -16 and d["q"][0, 1] == -14

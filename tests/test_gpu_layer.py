@@ -110,17 +110,36 @@ def test_c2_gptq_full_shape_matches_oracle(gpu, c2_full, T):
 @pytest.fixture(scope="module")
 def c4_full(gpu):
     # drawn and quantized on the GPU (423 MB of MXFP4 banks: about a minute on the host)
-    return S.generate(S.CONFIGS["c4_mxfp4"], T=32, seed=2, device=gpu)
+    return S.generate(S.CONFIGS["c4_mxfp4"], T=128, seed=2, device=gpu)
 
 
-@pytest.mark.parametrize("T", [1, 16, 32])
+@pytest.mark.parametrize("T", [1, 16, 32, 128])
 def test_c4_mxfp4_full_shape_matches_oracle(gpu, c4_full, T):
     """MXFP4 at the C4 shape (H = I = 2880, 32 experts, top-4 on biased logits,
     clamped SwiGLU with biases): stage A with activations in LDS and stage B
-    with K split over the waves up to 32 tokens."""
+    with K split over the waves up to 32 tokens; at 128 (every expert hit,
+    16 tokens per expert) the tiled stages."""
     from dataclasses import replace
 
     _run_and_check(replace(c4_full, x=c4_full.x[:T].contiguous()), gpu)
+
+
+def test_c4_mxfp4_prefill_token_subset(gpu, c4_full):
+    """C4 at its prefill size (T=4096 through the MXFP4 GEMM tiles): a token's
+    output depends only on its own row, so 40 sampled tokens are checked
+    against the oracle run on just those rows; routing bit-exact."""
+    from dataclasses import replace
+
+    g = torch.Generator(device=gpu).manual_seed(4096)
+    x = torch.randn(4096, c4_full.cfg.H, generator=g, device=gpu).to(torch.bfloat16)
+    syn = replace(c4_full, x=x)
+    layer = S.build_layer(syn)
+    out, ids, _, _ = layer.forward(x, return_routing=True)
+    torch.cuda.synchronize()
+    rows = np.sort(np.random.RandomState(1).choice(4096, 40, replace=False))
+    ref = O.layer_reference(oracle_spec(syn), np_(x)[rows])
+    np.testing.assert_array_equal(ids.cpu().numpy()[rows], ref["ids"])
+    assert_close(to_f32(out)[rows], ref["out"], what="C4 prefill rows")
 
 
 def test_c1_int8_full_shape_matches_oracle(gpu):
@@ -330,25 +349,101 @@ def test_negative_expert_ids_are_skipped(gpu, name, T):
     assert_close(to_f32(out), ref["out"], what=f"{name} layer with skipped pairs")
 
 
-@pytest.mark.parametrize("T", [9, 300])
-def test_repeated_expert_in_a_token_counts_twice(gpu, T):
+@pytest.mark.parametrize("name,T", [("c3_fp8", 1), ("c3_fp8", 2), ("c3_fp8", 9), ("c3_fp8", 300), ("c3_full", 1),
+                                    ("c3_full", 2), ("c2_gptq", 2)])
+def test_repeated_expert_in_a_token_counts_twice(gpu, name, T):
     """Caller-supplied routing that lists one expert twice for a token applies it
     twice with both weights (the reference's per-expert loop,
     python/freetoken/kernel/triton/fused_moe.py:129-161, selects pairs by
-    topk_ids == e).  T=9 takes the one-workgroup-per-4-tokens top-k, T=300
-    the one-token-per-wave one."""
-    syn = S.generate(S.SMALL["c3_fp8"], T=T, seed=90 + T)
+    topk_ids == e).  At T = 1 and 2 the expert gets more pairs than there are
+    tokens (T = 2: token 0 lists it twice, token 1 once), which the lists hold
+    because a repeat's weight is folded into its first listing; no error bit.
+    T=9 takes the one-workgroup-per-4-tokens top-k, T=300 the
+    one-token-per-wave one; c3_full the lean decode stages."""
+    from ftmoe.layer import read_status
+
+    cfg = S.CONFIGS["c3_fp8"] if name == "c3_full" else S.SMALL[name]
+    syn = S.generate(cfg, T=T, seed=90 + T)
     spec = oracle_spec(syn)
     rng = np.random.RandomState(T)
     ids = np.stack([rng.choice(syn.cfg.E, syn.cfg.k, replace=False) for _ in range(T)]).astype(np.int32)
-    ids[1, 1] = ids[1, 0]
-    ids[T - 1, 3] = ids[T - 1, 2]
+    e = int(ids[0, 0])
+    ids[0, 1] = e
+    if T >= 2:
+        if e in ids[1]:  # token 1 lists e once, in column 2
+            ids[1, ids[1].tolist().index(e)] = next(c for c in range(syn.cfg.E) if c != e and c not in ids[1])
+        ids[1, 2] = e
+        ids[T - 1, 3] = ids[T - 1, 2]
     w = O.round_bf16(rng.rand(T, syn.cfg.k).astype(np.float32))
     ref = O.layer_reference(spec, np_(syn.x), ids=ids, w=w)
     dsyn = syn.to(gpu)
     layer = S.build_layer(dsyn)
+    read_status(gpu)
     out = layer.forward_routed(dsyn.x, torch.from_numpy(ids).to(gpu), torch.from_numpy(w).to(gpu))
+    assert read_status(gpu) == 0, "no error bit: every pair was applied"
     assert_close(to_f32(out), ref["out"], what="layer with a repeated expert")
+
+
+def test_workspace_growth_keeps_captured_graphs_valid(gpu):
+    """A HIP graph captured at T=8 keeps its workspace when a larger batch later
+    grows the stream's workspace: replays after the growth still equal the
+    eager result.  Growing inside a capture raises instead of allocating."""
+    from ftmoe.layer import workspace
+
+    syn = S.generate(S.SMALL["c3_fp8"], T=40, seed=31).to(gpu)
+    layer = S.build_layer(syn)
+    x8 = syn.x[:8].contiguous()
+    ref8 = layer.forward(x8)
+    ref40 = layer.forward(syn.x)
+    s = torch.cuda.Stream(device=gpu)
+    s.wait_stream(torch.cuda.current_stream(gpu))
+    with torch.cuda.stream(s):
+        layer.forward(x8)
+        small = workspace(gpu, 0).data_ptr()
+    torch.cuda.current_stream(gpu).wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        out8 = layer.forward(x8)
+    with torch.cuda.stream(s):
+        out40 = layer.forward(syn.x)  # grows this stream's workspace
+        assert workspace(gpu, 0).data_ptr() != small
+    torch.cuda.current_stream(gpu).wait_stream(s)
+    for _ in range(3):
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out8, ref8)
+        layer.forward(syn.x)
+        torch.cuda.synchronize()
+    assert torch.equal(out40, ref40)
+    # a capture that would have to grow the workspace refuses
+    s2 = torch.cuda.Stream(device=gpu)
+    g2 = torch.cuda.CUDAGraph()
+    with pytest.raises(RuntimeError, match="inside a HIP graph capture"):
+        with torch.cuda.graph(g2, stream=s2):
+            layer.forward(x8)
+
+
+def test_non_resident_expert_raises_when_checked(gpu):
+    """forward_routed(check=True) turns the non-resident-slot error bit into
+    IndexError (the reference's stale-slot tripwire,
+    python/freetoken/models/qwen3_5_moe/__init__.py:1676-1685), and clears it."""
+    from ftmoe.layer import check_status, read_status
+
+    syn = S.generate(S.SMALL["c3_fp8"], T=3, seed=33)
+    dsyn = syn.to(gpu)
+    slots = torch.arange(syn.cfg.E, dtype=torch.int32, device=gpu)
+    ids = torch.tensor([[0, 1, 2, 3]] * 3, dtype=torch.int32, device=gpu)[:, :syn.cfg.k]
+    w = torch.full(ids.shape, 0.25, dtype=torch.float32, device=gpu)
+    slots[1] = -1
+    layer = S.build_layer(dsyn, slot_of_expert=slots)
+    read_status(gpu)
+    with pytest.raises(IndexError, match="stale slot map"):
+        layer.forward_routed(dsyn.x, ids, w, check=True)
+    assert read_status(gpu) == 0
+    slots[1] = 1
+    layer.forward_routed(dsyn.x, ids, w, check=True)
+    check_status(gpu)
 
 
 @pytest.mark.parametrize("mode", ["softmax_topk_lowp", "topk_softmax"])

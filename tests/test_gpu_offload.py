@@ -117,6 +117,8 @@ def test_accessor_get_and_expert_forward(gpu):
     acc = SlotWeightAccessor(c, cfg.I, torch.bfloat16)
     spec13 = oracle_proj(cfg.fmt, syns[0].bank, "gate_up", 2 * cfg.I, cfg.H, cfg.group)
     spec2 = oracle_proj(cfg.fmt, syns[0].bank, "down", cfg.H, cfg.I, cfg.group)
+    g = torch.Generator().manual_seed(7)
+    x_many = torch.randn(40, cfg.H, generator=g).to(torch.bfloat16)
     for slot in (0, 5, 31):
         e = int(c.id_of_slot[slot]) % cfg.E
         gate, up, down = acc.get(slot)
@@ -124,9 +126,53 @@ def test_accessor_get_and_expert_forward(gpu):
         np.testing.assert_array_equal(to_f32(gate), gu_ref[:cfg.I])
         np.testing.assert_array_equal(to_f32(up), gu_ref[cfg.I:])
         np.testing.assert_array_equal(to_f32(down), O.round_bf16(O.dequant(spec2, e)))
-        x = syns[0].x[:3].to(gpu)
-        got = acc.expert_forward(slot, x)
-        ref = O.expert_forward(spec13, spec2, e, O.bf16_bits_to_f32(np_(x)))
-        assert_close(to_f32(got), ref, what=f"expert slot {slot}")
+        # 3 rows: below the FP8 crossover (8); 40 rows: above it, where the
+        # reference dequantizes and the expert runs on the tiled HIP stages
+        for x in (syns[0].x[:3], x_many):
+            got = acc.expert_forward(slot, x.to(gpu))
+            ref = O.expert_forward(spec13, spec2, e, O.bf16_bits_to_f32(np_(x)))
+            assert_close(to_f32(got), ref, what=f"expert slot {slot}, {x.shape[0]} rows")
     fp8 = acc.get_fp8_packed(0)
     assert fp8[0].shape == (2 * cfg.I, cfg.H) and fp8[4] == 128
+
+
+def _zipf_steps(E, T, k, steps, seed):
+    """C5 routing: per token k distinct experts drawn Zipf(1.1) over ranks mapped
+    through a seeded permutation; weights the softmax of N(0, 1) logits, bf16."""
+    rng = np.random.RandomState(seed)
+    perm = rng.permutation(E)
+    p = 1.0 / np.arange(1, E + 1) ** 1.1
+    p /= p.sum()
+    ids = np.stack([np.stack([perm[rng.choice(E, k, replace=False, p=p)] for _ in range(T)])
+                    for _ in range(steps)]).astype(np.int32)
+    z = rng.randn(steps, T, k)
+    w = np.exp(z - z.max(-1, keepdims=True))
+    return ids, O.round_bf16((w / w.sum(-1, keepdims=True)).astype(np.float32))
+
+
+@pytest.mark.parametrize("device_lru", [True, False])
+def test_c5_offload_full_shape_matches_oracle(gpu, device_lru):
+    """C5 at its own shape: the C3 FP8 layer (256 experts, H=2048, I=512, top-8,
+    shared expert) with 64 HBM slots fed from pinned host banks, 16-token
+    decode steps with Zipf routing.  Steps 0 and 2 route to more than 64
+    experts (67 and 65) and run in chunks.  Every step's output matches the
+    oracle on the full bank."""
+    cfg = S.CONFIGS["c3_fp8"]
+    syn = S.generate(cfg, T=16, seed=5, device=gpu)
+    host = syn.to("cpu")
+    ids_all, w_all = _zipf_steps(cfg.E, 16, cfg.k, 4, seed=3)
+    distinct = [len(np.unique(s)) for s in ids_all]
+    assert max(distinct) > 64 and min(distinct) <= 64, distinct
+    c = OffloadMoeCache(1, cfg.E, 64, gpu, quant_format="fp8_block", decode_only=True, device_lru=device_lru)
+    c.set_bank_sources({b: [host.bank[b]] for b in c.bank_schema})
+    spec = oracle_spec(host)
+    g = torch.Generator().manual_seed(55)
+    for step in range(4):
+        x = torch.randn(16, cfg.H, generator=g).to(torch.bfloat16)
+        print(f"c5 full shape device_lru={device_lru} step {step} distinct={distinct[step]}", flush=True)
+        out = moe_offload_forward(x.to(gpu), torch.from_numpy(ids_all[step]).to(gpu),
+                                  torch.from_numpy(w_all[step]).to(gpu), c, 0, intermediate=cfg.I, shared=syn.shared)
+        ref = O.layer_reference(spec, np_(x), ids=ids_all[step], w=w_all[step])
+        assert_close(to_f32(out), ref["out"], what=f"C5 step {step} ({distinct[step]} experts)")
+    c.check_status()
+    assert c.decode_miss_stats()["missing"] > 0

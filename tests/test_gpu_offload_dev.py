@@ -188,3 +188,43 @@ def test_device_offload_forward_matches_host_path(gpu, slots):
         assert cd.usage.cpu().tolist() == ch.usage.tolist() and int(cd.step) == int(ch.step), step
     assert cd.decode_miss_stats() == ch.decode_miss_stats()
     cd.check_status()
+
+
+def test_copy_kernel_applies_repeated_slots_in_plan_order(gpu):
+    """A plan that names one slot more than once (ensure_experts passes every
+    miss beyond the unstamped slots through slot 0) lands the last such row,
+    as copy_missing's in-order copies do (offload_cache.py:651-674)."""
+    rows, slots = 6, 4
+    bank = _pinned(torch.arange(rows, dtype=torch.uint8)[:, None].repeat(1, 70_000) + 1)  # row r holds r + 1
+    pool = torch.zeros((slots, 70_000), dtype=torch.uint8, device=gpu)
+    evict = torch.tensor([3, 0, 0, 0], dtype=torch.int32, device=gpu)
+    src = torch.tensor([5, 1, 2, 4], dtype=torch.int32, device=gpu)
+    num = torch.tensor([4], dtype=torch.int32, device=gpu)
+    descs = (nat.FtmBankCopy * 1)(nat.FtmBankCopy(bank.data_ptr(), pool.data_ptr(), 70_000))
+    assert nat.lib().ftm_copy_slots_dev(descs, 1, rows, slots, evict.data_ptr(), src.data_ptr(), num.data_ptr(), 4,
+                                        torch.cuda.current_stream(gpu).cuda_stream) == nat.OK
+    torch.cuda.synchronize()
+    assert torch.equal(pool[3].cpu(), bank[5]) and torch.equal(pool[0].cpu(), bank[4])
+    assert int(pool[1].sum()) == 0 and int(pool[2].sum()) == 0
+
+
+def test_device_pool_smaller_than_the_step_keeps_the_last_miss(gpu):
+    """ensure_experts on a pool smaller than the step's distinct experts (the
+    misses beyond the pool pass through slot 0, the last one stays): after
+    copy_missing every slot holds exactly the bank row its id_of_slot names,
+    on the device path as on the host path."""
+    Ln, En, Sn = 1, 8, 3
+    srcs = {"gate_up": [torch.stack([_bank_values(0, e)[0] for e in range(En)])],
+            "down": [torch.stack([_bank_values(0, e)[1] for e in range(En)])]}
+    for dev_lru in (True, False):
+        c = OffloadMoeCache(Ln, En, Sn, gpu, decode_only=True, device_lru=dev_lru)
+        c.set_bank_sources(srcs)
+        for ids in ([0, 1, 2, 3, 4, 5], [6, 7, 1], [2, 3, 4, 5, 6, 7, 0]):
+            c.ensure_experts(0, torch.tensor(ids, device=gpu))
+            c.copy_missing()
+            torch.cuda.synchronize()
+            for s, fid in enumerate(c.id_of_slot.tolist()):
+                assert fid >= 0
+                gu, dn = _bank_values(0, fid % En)
+                assert torch.equal(c.bank_caches["gate_up"][s].cpu(), gu), (dev_lru, ids, s, fid)
+                assert torch.equal(c.bank_caches["down"][s].cpu(), dn), (dev_lru, ids, s, fid)

@@ -224,6 +224,84 @@ def test_route_matches_torch_softmax_topk():
     np.testing.assert_allclose(np.sort(w[ok], 1), np.sort(tw.numpy()[ok], 1), rtol=2 ** -7)
 
 
+def _tie_free_rows(keys: np.ndarray, k: int) -> np.ndarray:
+    """Rows whose k largest keys are distinct and strictly above the (k+1)-th."""
+    srt = np.sort(keys, axis=1)[:, ::-1]
+    ok = srt[:, k - 1] > srt[:, k]
+    for j in range(k - 1):
+        ok &= srt[:, j] > srt[:, j + 1]
+    return ok
+
+
+@pytest.mark.parametrize("E,k", [(128, 8), (256, 8), (32, 4)])
+def test_route_lowp_matches_torch_bf16_softmax_topk_renorm(E, k):
+    """softmax_topk_lowp against the reference's own sequence in bf16
+    (fused_moe.py:92-96, qwen3_moe/__init__.py:473-475): F.softmax on bf16
+    logits -> torch.topk -> bf16 renorm, on rows without ties in the bf16
+    probabilities (torch's tie order is unspecified).  Ids must be equal and
+    the weights equal bit for bit."""
+    g = torch.Generator().manual_seed(E + k)
+    logits = (torch.randn(512, E, generator=g) * 2.0).to(torch.bfloat16)
+    p = torch.nn.functional.softmax(logits, dim=-1)
+    assert p.dtype == torch.bfloat16
+    tw, ti = torch.topk(p, k, dim=-1)
+    tw = tw / tw.sum(dim=-1, keepdim=True)
+    ids, w = O.route(logits.float().numpy(), k, "softmax_topk_lowp", True, weight_dt="bf16", prob_dt="bf16")
+    ok = _tie_free_rows(p.float().numpy(), k)
+    assert ok.sum() > 100
+    np.testing.assert_array_equal(ids[ok], ti.numpy()[ok])
+    np.testing.assert_array_equal(w[ok], tw.float().numpy()[ok])
+    # the comparison separates the plausible mistakes: fp32 probabilities (the
+    # softmax_topk mode) and a renorm whose sum is not rounded to bf16
+    _, w32 = O.route(logits.float().numpy(), k, "softmax_topk", True)
+    assert not np.array_equal(w32[ok], tw.float().numpy()[ok])
+    top = torch.topk(p, k, dim=-1)[0].float()
+    w_sum32 = (top / top.sum(dim=-1, keepdim=True)).to(torch.bfloat16).float().numpy()
+    assert not np.array_equal(w_sum32[ok], tw.float().numpy()[ok])
+
+
+# ------------------------------------------------------------------ activations
+_GRID = np.concatenate([np.linspace(-12.0, 12.0, 481), [-80.0, -30.0, -1e-6, 0.0, 1e-6, 30.0, 80.0]])
+
+
+@pytest.mark.parametrize("name,fn", [("silu", torch.nn.functional.silu), ("gelu", torch.nn.functional.gelu),
+                                     ("relu", torch.nn.functional.relu)])
+def test_activation_matches_torch(name, fn):
+    """The oracle's gate activations against torch's (fused_moe.py:53-61 calls
+    F.silu / F.gelu (erf form) / F.relu), float64, times a varying up value."""
+    u = np.linspace(-3.0, 3.0, _GRID.size)
+    got = O.act(name, _GRID, u)
+    want = (fn(torch.from_numpy(_GRID)) * torch.from_numpy(u)).numpy()
+    np.testing.assert_allclose(got, want, rtol=1e-12, atol=1e-300)
+
+
+def test_clamped_glu_reduces_to_silu_without_limit():
+    """gpt-oss's clamped GLU (gpt_oss/__init__.py:306-310) with no clamp is
+    (u + 1) * g * sigmoid(alpha g) = (u + 1) * silu(alpha g) / alpha."""
+    u = np.linspace(-4.0, 4.0, _GRID.size)
+    for alpha in (1.0, 1.702):
+        got = O.act("swiglu_oai", _GRID, u, alpha=alpha, limit=np.inf)
+        silu = torch.nn.functional.silu(torch.from_numpy(_GRID * alpha)).numpy() / alpha
+        np.testing.assert_allclose(got, (u + 1.0) * silu, rtol=1e-12, atol=1e-300)
+
+
+def test_clamped_glu_at_and_beyond_the_limit():
+    """gate clamped from above only, up from both sides: past +-limit the value
+    equals the value at the limit; below -limit the gate is not clamped."""
+    L, a = 7.0, 1.702
+    at = O.act("swiglu_oai", [L], [L], alpha=a, limit=L)[0]
+    for g, u in ((7.5, 7.0), (7.0, 9.0), (1e6, 1e6)):
+        assert O.act("swiglu_oai", [g], [u], alpha=a, limit=L)[0] == at
+    lo = O.act("swiglu_oai", [1.5], [-L], alpha=a, limit=L)[0]
+    assert O.act("swiglu_oai", [1.5], [-20.0], alpha=a, limit=L)[0] == lo  # u clamped to -7: (u + 1) = -6
+    assert lo == pytest.approx(-6.0 * torch.nn.functional.silu(torch.tensor(1.5 * a, dtype=torch.float64)).item() / a,
+                               rel=1e-12)
+    # the gate has no lower clamp: g = -20 keeps its (tiny, negative) value
+    g = -20.0
+    want = (0.5 + 1.0) * torch.nn.functional.silu(torch.tensor(g * a, dtype=torch.float64)).item() / a
+    assert O.act("swiglu_oai", [g], [0.5], alpha=a, limit=L)[0] == pytest.approx(want, rel=1e-12)
+
+
 # ------------------------------------------------------------------ layer
 def _brute_layer(spec, x_bits, ids, w):
     """Independent float64 restatement: dense numpy dequant + per-token loops."""
