@@ -7,11 +7,48 @@
 #include <hip/hip_runtime.h>
 #include <string.h>
 
+#include <mutex>
+
 #include "ftm_internal.h"
 
 using namespace ftm;
 
+// ---- scratch of ftm_moe_forward_noalloc: the layer workspace as a file-scope
+// device array, FTM_NOALLOC_SCRATCH_BYTES per GPU, held until the process
+// ends.  In host code `scratch` is only a stand-in for the symbol: the device
+// address of each GPU's copy comes from hipGetSymbolAddress, once per device,
+// and only that address is handed to kernels.
+static __device__ __align__(256) char scratch[FTM_NOALLOC_SCRATCH_BYTES];
+
 namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+bool g_scratch_clear[kMaxDevices] = {};  // the control region has been cleared on this device
+
+// This device's scratch address, looked up once; sets `first` when the caller
+// must clear the control region (the first call on the device).
+int scratch_of_current_device(void** ptr, bool* first) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+    (void)hipGetLastError();
+    return FTM_ERR_HIP;
+  }
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || p == nullptr) {
+      (void)hipGetLastError();
+      return FTM_ERR_HIP;
+    }
+    g_scratch_ptr[dev] = p;
+  }
+  *ptr = g_scratch_ptr[dev];
+  *first = !g_scratch_clear[dev];
+  g_scratch_clear[dev] = true;
+  return FTM_OK;
+}
 
 bool dt_ok(int dt) { return dt == FTM_DT_F32 || dt == FTM_DT_F16 || dt == FTM_DT_BF16; }
 
@@ -198,6 +235,25 @@ int ftm_moe_forward(const ftm_moe_layer* layer, const void* x, int32_t num_token
     e = launch_topk(*layer, num_tokens, nullptr, 0, nullptr, nullptr, topk_ids, topk_w, logits, ws, wl, st);
   if (e == hipSuccess) e = run_experts(*layer, x, num_tokens, out, ws, wl, st);
   return hip_rc(e);
+}
+
+int ftm_moe_forward_noalloc(const ftm_moe_layer* layer, const void* x, int32_t num_tokens, void* out,
+                            int32_t* topk_ids, float* topk_w, float* logits, void* stream) {
+  int rc = check_layer(layer, true);
+  if (rc != FTM_OK) return rc;
+  if (num_tokens < 0) return FTM_ERR_DIM;
+  if (num_tokens == 0) return FTM_OK;
+  if (x == nullptr || out == nullptr) return FTM_ERR_NULL;
+  if (!aligned16(x)) return FTM_ERR_ALIGN;
+  const size_t need = ws_layout(*layer, num_tokens).total;
+  if (need > (size_t)FTM_NOALLOC_SCRATCH_BYTES) return FTM_ERR_WORKSPACE;
+  void* ws = nullptr;
+  bool first = false;
+  rc = scratch_of_current_device(&ws, &first);
+  if (rc != FTM_OK) return rc;
+  // every call leaves the control region zero; it starts zeroed by a fill kernel
+  if (first && launch_ws_init(ws, (hipStream_t)stream) != hipSuccess) return FTM_ERR_HIP;
+  return ftm_moe_forward(layer, x, num_tokens, out, topk_ids, topk_w, logits, ws, need, stream);
 }
 
 int ftm_moe_forward_stage(const ftm_moe_layer* layer, const void* x, int32_t num_tokens, void* out, int32_t stage,

@@ -49,6 +49,7 @@ ACT_RELU = 2
 ACT_SWIGLU_OAI = 3
 
 WS_CTRL_BYTES = 4096
+NOALLOC_SCRATCH_BYTES = 16 << 20
 WS_ERROR_OFFSET = 12
 WS_ERR_SLOT = 1
 WS_ERR_ID = 2
@@ -128,6 +129,7 @@ EXPORTED = (
     "ftm_moe_workspace_bytes",
     "ftm_workspace_init",
     "ftm_moe_forward",
+    "ftm_moe_forward_noalloc",
     "ftm_moe_forward_stage",
     "ftm_moe_stage_kernel",
     "ftm_moe_forward_routed",
@@ -176,6 +178,8 @@ def lib() -> ctypes.CDLL:
     L.ftm_workspace_init.argtypes = [vp, sz, vp]
     L.ftm_moe_forward.restype = ctypes.c_int
     L.ftm_moe_forward.argtypes = [P_layer, vp, i32, vp, vp, vp, vp, vp, sz, vp]
+    L.ftm_moe_forward_noalloc.restype = ctypes.c_int
+    L.ftm_moe_forward_noalloc.argtypes = [P_layer, vp, i32, vp, vp, vp, vp, vp]
     L.ftm_moe_forward_stage.restype = ctypes.c_int
     L.ftm_moe_forward_stage.argtypes = [P_layer, vp, i32, vp, i32, vp, sz, vp]
     L.ftm_moe_stage_kernel.restype = ctypes.c_char_p

@@ -169,6 +169,21 @@ int ftm_moe_forward(const ftm_moe_layer* layer, const void* x, int32_t num_token
                     void* out, int32_t* topk_ids, float* topk_w, float* logits,
                     void* workspace, size_t ws_bytes, void* stream);
 
+/* ftm_moe_forward without a workspace argument, for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  No counterpart in the reference.  The
+ * workspace is a static device array of FTM_NOALLOC_SCRATCH_BYTES per GPU (the
+ * library's own, held until the process ends; FTM_ERR_WORKSPACE when the layer
+ * needs more at num_tokens: ftm_moe_workspace_bytes tells); the call allocates
+ * nothing.  Every call on one GPU shares that array: calls that overlap on one
+ * GPU (several streams or host threads) race.  Its sticky error word is not
+ * readable here: use ftm_moe_forward with a workspace to check it.  Same
+ * kernels and result as ftm_moe_forward. */
+#define FTM_NOALLOC_SCRATCH_BYTES (16u << 20)
+int ftm_moe_forward_noalloc(const ftm_moe_layer* layer, const void* x, int32_t num_tokens,
+                            void* out, int32_t* topk_ids, float* topk_w, float* logits,
+                            void* stream);
+
 /* One stage of ftm_moe_forward, for per-kernel timing with events on `stream`:
  *   0 = router GEMV, 1 = softmax/top-k/grouping, 2 = w13 + activation,
  *   3 = w2 (router-weighted slots), 4 = combine of the slots into `out`.
