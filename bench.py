@@ -2,23 +2,42 @@
 """Benchmark of the fused quantized MoE layer on one MI355X.
 
 Metric: MoE-layer decode tokens/s + achieved HBM GB/s (% of
-8 TB/s).  A step is one full layer forward (router GEMV -> top-k -> grouped
-w13 + SiLU-gate -> w2 + weighted combine, + the shared expert) over one batch
-of synthetic tokens already resident in HBM.  To keep the weights streaming
-from HBM rather than the 256 MB last-level cache, ``--layers`` independent
-random-init layers (4 x 805 MB for C3) are cycled, one per step, each with a
-fresh activation batch -- the pattern a real decode step has across layers.
+8 TB/s), bs 1-64.  A step is one full layer forward (router GEMV -> top-k ->
+grouped w13 + gate activation -> w2 + weighted combine, + the shared expert)
+over one batch of synthetic tokens already resident in HBM.  The weights
+stream from HBM, not the 256 MB last-level cache: ``--layers`` independent
+random-init layers of each config are cycled, one per step (4 x 805 MB for
+C3), each step with a fresh activation batch, as a real decode step has
+across layers.
 
-Prints ONE JSON line.  ``roofline`` covers the dominant kernel (the w13 stage),
-timed with HIP events on the launch stream; ``cpu_baseline`` times the
-reference's own CPU MoE kernel (python/freetoken/kernel/csrc/cpu_moe/cpu_moe.cpp,
-built unmodified into oracle/_ref) on the same routing.
+Every BASELINE config is measured in the one JSON line the driver reads:
+
+* ``value`` / ``ms_per_step``: the headline, C3 FP8 (256 experts, top-8 +
+  shared expert) decode at T=16 -- ``configs[2]`` of BASELINE.json;
+* ``configs``: C1 INT8 T=4; C2 GPTQ T=1/4/16/64; C3 T=1..64 and the
+  2048-token prefill chunk; C4 MXFP4 T=1/32/128 and the 4096-token prefill;
+  C5 offload (64 HBM slots, 256 pinned host banks, 200 Zipf steps).  Each
+  decode point: tokens/s, GB/s and fraction of 8 TB/s from the median over
+  batches of 10 back-to-back forwards, ``--steps`` forwards in all (mean
+  beside it);
+  each config's w13 and w2 kernels against the HBM roofline (stage events on
+  the launch stream); prefill: the GEMM stages against the dense bf16 MFMA
+  peak;
+* ``cpu_baseline``: the reference's own CPU MoE kernel
+  (python/freetoken/kernel/csrc/cpu_moe/cpu_moe.cpp, built unmodified into
+  oracle/_ref) on the same routing, on the host cores of the GPU box, for
+  every config: all cores clamped to E (the kernel's own rule,
+  cpu_moe.cpp:485-490), one thread, and "reference-equivalent" with the
+  per-call full-bank fp32 conversion of python/freetoken/kernel/cpu_moe.py:460-461.
+
+Prints ONE JSON line.
 """
 from __future__ import annotations
 
 import argparse
 import json
 import os
+import subprocess
 import sys
 import time
 
@@ -28,40 +47,43 @@ sys.path.insert(0, os.path.join(ROOT, "freetoken-intel_amd"))
 METRIC = "MoE-layer decode tokens/s + achieved HBM GB/s (% of 8 TB/s), bs 1-64"
 HBM_PEAK_GBS = 8000.0
 MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16
+HEADLINE = ("c3_fp8", 16)
+# decode batches and the dominant-kernel point of each config
+DECODE_T = {"c1_int8": (4,), "c2_gptq": (1, 4, 16, 64), "c3_fp8": (1, 2, 4, 8, 16, 32, 64),
+            "c4_mxfp4": (1, 32, 128)}
+KERNEL_T = {"c1_int8": 4, "c2_gptq": 16, "c3_fp8": 16, "c4_mxfp4": 32}
 
 
 def _parse():
     ap = argparse.ArgumentParser(description=__doc__)
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--steps", type=int, default=200, help="timed forwards per decode point")
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--config", default="c3_fp8")
-    ap.add_argument("--batch", type=int, default=16)
+    ap.add_argument("--configs", default="c1_int8,c2_gptq,c3_fp8,c4_mxfp4,c5",
+                    help="comma list of configs to measure (c5 = the offload decode)")
+    ap.add_argument("--point", default="",
+                    help="measure only one decode point, CONFIG:T (for profiler runs; no CPU baseline)")
     ap.add_argument("--layers", type=int, default=4)
-    ap.add_argument("--sweep", default="1,4,16,64", help="extra decode batch sizes to report ('' = none)")
-    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--cpu-seconds", type=float, default=3.0, help="CPU work per baseline row")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--offload", action="store_true",
-                    help="run the C5 offload decode benchmark instead (64 HBM slots, 256 pinned host banks)")
+    ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--prefill-only", default="", help="measure only this config's prefill chunk (counter runs)")
     ap.add_argument("--offload-steps", type=int, default=200)
     ap.add_argument("--offload-slots", type=int, default=64)
     ap.add_argument("--offload-lru", choices=("device", "host"), default="device",
                     help="C5: LRU planning and copies as GPU kernels (device) or host LRU + per-row memcpy (host)")
-    ap.add_argument("--prefill-t", type=int, default=2048,
-                    help="prefill chunk measured after the decode points (tiled MFMA stages; 0 = skip)")
-    ap.add_argument("--prefill-only", action="store_true",
-                    help="measure only the prefill chunk and print its JSON (for counter runs)")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="after the bench, copy a buffer of this many MiB 3 times (a plain copy kernel of known "
                          "size, the reference point for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE)")
     return ap.parse_args()
 
 
+# ------------------------------------------------------------------ helpers
 def _pmc_traffic(kernel: str, config: str, T: int):
-    """HBM bytes per launch of the w13 kernel from the committed rocprofv3 PMC
-    summary (FETCH_SIZE + WRITE_SIZE per dispatch, scaled by the factor the
-    same counters read for a copy kernel of known size), if one exists for
-    this kernel and workload."""
+    """HBM bytes per launch of a kernel from the committed rocprofv3 PMC summary
+    (FETCH_SIZE + WRITE_SIZE per dispatch, scaled by the factor the same
+    counters read for a copy kernel of known size), if one exists for this
+    kernel and workload."""
     path = os.path.join(ROOT, "profiles", f"{kernel}__{config}_T{T}__pmc.md")
     try:
         with open(path) as f:
@@ -73,295 +95,382 @@ def _pmc_traffic(kernel: str, config: str, T: int):
     return None
 
 
-def _w13_bytes_per_expert(syn) -> int:
-    return sum(t[0].numel() * t.element_size() for k, t in syn.bank.items() if k.endswith("gate_up")) + (
-        syn.bias13[0].numel() * 2 if syn.bias13 is not None else 0)
+def _proj_bytes(syn, which: str) -> int:
+    """Bytes of one routed expert's projection ``which`` (gate_up / down) incl. its bias."""
+    n = sum(t[0].numel() * t.element_size() for k, t in syn.bank.items() if k.endswith(which))
+    bias = syn.bias13 if which == "gate_up" else syn.bias2
+    return n + (bias[0].numel() * 2 if bias is not None else 0)
 
 
-def main() -> int:
-    args = _parse()
-    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
-        print("bench.py measures one MI355X only: this build has no multi-GPU path "
-              "(expert-parallel sharding is a design note), so --gpus must be 1.", file=sys.stderr)
-        return 2
+def _cpu_info() -> dict:
+    info = {}
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        for line in out.splitlines():
+            key, _, val = line.partition(":")
+            key, val = key.strip(), val.strip()
+            if key in ("Model name", "Socket(s)", "Core(s) per socket", "Thread(s) per core", "CPU(s)", "CPU family",
+                       "Model", "Hypervisor vendor", "L3 cache"):
+                info[key] = val
+    except (OSError, subprocess.SubprocessError):
+        pass
+    try:
+        info["cpus_available_to_process"] = len(os.sched_getaffinity(0))
+    except OSError:
+        pass
+    return info
 
+
+def _median(v):
     import numpy as np
-    import torch
 
-    from ftmoe import _native as nat
-    from ftmoe import synthetic as S
+    return float(np.median(np.asarray(v, np.float64)))
 
-    if args.offload:
-        return _offload_bench(args)
 
-    dev = torch.device("cuda:0")
-    cfg = S.CONFIGS[args.config]
-    T = args.batch
-    NL = max(1, args.layers)
-    NX = 7
-    layers, syns = [], []
-    for s in range(NL):
-        syn = S.generate(cfg, T=T, seed=s, device=dev)
-        syns.append(syn)
-        layers.append(S.build_layer(syn))
-    torch.cuda.synchronize()
-    if args.prefill_only:
-        print(json.dumps(_prefill_point(cfg, layers, max(1, args.prefill_t), max(4, min(args.steps, 20)))), flush=True)
-        return 0
-    gx = torch.Generator(device=dev).manual_seed(1234)
-    max_t = max([T] + [int(b) for b in args.sweep.split(",") if b])
-    x_pool = [torch.randn(max_t, cfg.H, generator=gx, device=dev).to(torch.bfloat16) for _ in range(NX)]
+# ------------------------------------------------------------------ decode
+class ConfigBench:
+    """NL rotated random-init layers of one config on the GPU."""
 
-    cap_stream = torch.cuda.Stream(device=dev)
+    def __init__(self, cfg, NL: int, max_t: int):
+        import torch
 
-    def graphs_for(xs):
-        """One HIP graph per (layer, batch) pair of the rotation: a serving loop
-        replays a captured layer forward instead of paying Python launch cost."""
+        from ftmoe import synthetic as S
+
+        self.cfg = cfg
+        self.dev = torch.device("cuda:0")
+        self.syns, self.layers = [], []
+        for s in range(NL):
+            syn = S.generate(cfg, T=1, seed=s, device=self.dev)
+            self.syns.append(syn)
+            self.layers.append(S.build_layer(syn))
+        gx = torch.Generator(device=self.dev).manual_seed(1234)
+        self.NX = 7
+        self.x_pool = [torch.randn(max_t, cfg.H, generator=gx, device=self.dev).to(torch.bfloat16)
+                       for _ in range(self.NX)]
+        torch.cuda.synchronize()
+
+    def xs(self, T):
+        return [x[:T].contiguous() for x in self.x_pool]
+
+    def decode_point(self, T: int, steps: int, warmup: int, graphs: bool = False, batch: int = 10) -> dict:
+        """Layer time over ``steps`` forwards of T tokens: the median over
+        batches of ``batch`` back-to-back forwards, each batch between two HIP
+        events on the launch stream (queued behind a short sleep kernel so the
+        host runs ahead and the events see GPU time only), and the mean over
+        all of them; the rotation's realised unique experts and B_alg.  An
+        event marker serialises the kernels on either side of it (about 2.7 us
+        at C3 T=16), so markers go between batches, not between forwards."""
+        import numpy as np
+        import torch
+
+        from ftmoe import synthetic as S
+
+        NL, NX = len(self.layers), self.NX
+        xs = self.xs(T)
+        for i in range(warmup):
+            self.layers[i % NL].forward(xs[i % NX])
+        torch.cuda.synchronize()
+        # host wall clock: enqueue + execution
+        w0 = time.perf_counter()
+        for i in range(steps):
+            self.layers[(warmup + i) % NL].forward(xs[(warmup + i) % NX])
+        torch.cuda.synchronize()
+        wall_us = (time.perf_counter() - w0) * 1e6 / steps
+        # device time: events every `batch` forwards
+        nb = max(1, steps // batch)
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(nb + 1)]
+        if hasattr(torch.cuda, "_sleep"):
+            torch.cuda._sleep(2_000_000)
+        for i in range(3):  # clocks back up after the sleep
+            self.layers[i % NL].forward(xs[i % NX])
+        for b in range(nb):
+            ev[b].record()
+            for i in range(batch):
+                j = warmup + b * batch + i
+                self.layers[j % NL].forward(xs[j % NX])
+        ev[nb].record()
+        torch.cuda.synchronize()
+        per = [ev[b].elapsed_time(ev[b + 1]) * 1e3 / batch for b in range(nb)]
+        uniq = []
+        for i in range(min(steps, 4 * NL * NX)):
+            j = warmup + i
+            _, ids, _, _ = self.layers[j % NL].forward(xs[j % NX], return_routing=True)
+            uniq.append(int(torch.unique(ids).numel()))
+        b_alg = float(np.mean([S.algorithmic_bytes(self.cfg, u, T) for u in uniq]))
+        med = _median(per)
+        res = {"T": T, "us_per_layer": round(med, 2), "us_mean": round(float(np.mean(per)), 2),
+               "timed_forwards": nb * batch, "wall_us_per_layer": round(wall_us, 2),
+               "tokens_per_s": round(T / (med * 1e-6), 1), "unique_experts": round(float(np.mean(uniq)), 2),
+               "bytes": int(b_alg), "GBps": round(b_alg / (med * 1e-6) / 1e9, 1),
+               "hbm_frac": round(b_alg / (med * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+        if graphs:
+            res["graph_us_per_layer"], res["graph_bitwise_equal"] = self._graph_point(xs, steps, warmup)
+        return res
+
+    def _graph_point(self, xs, steps, warmup):
+        """The same steps as HIP-graph replays (one captured forward per
+        (layer, batch) pair), checked bitwise against eager forwards."""
+        import torch
+
+        NL, NX = len(self.layers), self.NX
+        cap = torch.cuda.Stream(device=self.dev)
         pairs = [(l, j) for l in range(NL) for j in range(NX)]
-        cap_stream.wait_stream(torch.cuda.current_stream(dev))
-        with torch.cuda.stream(cap_stream):
-            for l, j in pairs:  # allocates this stream's workspace outside capture
-                layers[l].forward(xs[j])
-        torch.cuda.current_stream(dev).wait_stream(cap_stream)
+        cap.wait_stream(torch.cuda.current_stream(self.dev))
+        with torch.cuda.stream(cap):
+            for l, j in pairs:  # sizes this stream's workspace outside capture
+                self.layers[l].forward(xs[j])
+        torch.cuda.current_stream(self.dev).wait_stream(cap)
         torch.cuda.synchronize()
         gs = {}
         for l, j in pairs:
             g = torch.cuda.CUDAGraph()
-            with torch.cuda.graph(g, stream=cap_stream):
-                o = layers[l].forward(xs[j])
+            with torch.cuda.graph(g, stream=cap):
+                o = self.layers[l].forward(xs[j])
             gs[(l, j)] = (g, o)
-        # replays must equal the eager forward bit for bit (deterministic kernels)
         ok = True
         for (l, j), (g, o) in list(gs.items())[:3]:
             g.replay()
-            ref = layers[l].forward(xs[j])
+            ref = self.layers[l].forward(xs[j])
             torch.cuda.synchronize()
             ok = ok and bool(torch.equal(o, ref))
-        return gs, ok
-
-    def run_point(Tb: int, steps: int, warmup: int):
-        xs = [x[:Tb].contiguous() for x in x_pool]
-        for i in range(warmup):
-            layers[i % NL].forward(xs[i % NX])
-        torch.cuda.synchronize()
-        # host wall clock: enqueue + execution, the GPU idle at the start
-        w0 = time.perf_counter()
-        for i in range(steps):
-            j = warmup + i
-            layers[j % NL].forward(xs[j % NX])
-        torch.cuda.synchronize()
-        wall_ms = (time.perf_counter() - w0) * 1e3 / steps
-        # device time: a short sleep kernel queued first lets the host enqueue
-        # ahead, so the events see the forwards back to back on the GPU (at
-        # T <= 2 a forward's host enqueue, ~20 us of Python and ctypes, is as
-        # long as its kernels and would otherwise leave gaps between them); a
-        # few untimed forwards after it bring the clocks back up (a 40 ms sleep
-        # cost 3-7 % at T >= 16)
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        if hasattr(torch.cuda, "_sleep"):
-            torch.cuda._sleep(2_000_000)
-        for i in range(3):
-            layers[i % NL].forward(xs[i % NX])
-        e0.record()
-        for i in range(steps):
-            j = warmup + i
-            layers[j % NL].forward(xs[j % NX])
-        e1.record()
-        torch.cuda.synchronize()
-        ms = e0.elapsed_time(e1) / steps
-        # the same steps as HIP-graph replays (one captured forward per pair)
-        gs, graph_ok = graphs_for(xs)
         for i in range(warmup):
             gs[(i % NL, i % NX)][0].replay()
         torch.cuda.synchronize()
         f0, f1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         f0.record()
         for i in range(steps):
-            j = warmup + i
-            gs[(j % NL, j % NX)][0].replay()
+            gs[((warmup + i) % NL, (warmup + i) % NX)][0].replay()
         f1.record()
         torch.cuda.synchronize()
-        graph_ms = f0.elapsed_time(f1) / steps
-        del gs
-        # routing of the same (layer, batch) pairs, untimed: realised unique experts
-        uniq = []
-        for i in range(steps):
-            j = warmup + i
-            _, ids, _, _ = layers[j % NL].forward(xs[j % NX], return_routing=True)
-            uniq.append(int(torch.unique(ids).numel()))
-        b_alg = float(np.mean([S.algorithmic_bytes(cfg, u, Tb) for u in uniq]))
-        return ms, wall_ms, float(np.mean(uniq)), b_alg, xs, graph_ms, graph_ok
+        return round(f0.elapsed_time(f1) * 1e3 / steps, 2), ok
 
-    ms, wall_ms, U, b_alg, xs, graph_ms, graph_ok = run_point(T, args.steps, args.warmup)
-    gbs = b_alg / (ms * 1e-3) / 1e9
+    def stage_times(self, T: int, reps: int = 15) -> dict:
+        """Average duration of each of the five stage launches at T tokens: each
+        stage is launched as a group of NL consecutive launches, one per rotated
+        layer (each layer with its own workspace, so the groups keep every
+        layer's stage order), between two events on the launch stream; a sleep
+        kernel queued first lets the host run ahead."""
+        import numpy as np
+        import torch
 
-    # ---- per-kernel durations.  Each of the five launches of a forward is
-    # timed as a group of NL consecutive launches, one per rotated layer (each
-    # layer with its own workspace, so the groups keep every layer's stage
-    # order), between two events on the launch stream; a sleep kernel queued
-    # first lets the host run ahead, so no host gap falls inside a group.
-    out = torch.empty(T, cfg.H, dtype=torch.bfloat16, device=dev)
-    nsteps = max(1, min(args.steps, 60) // NL)
-    stages = (nat.STAGE_ROUTER, nat.STAGE_TOPK, nat.STAGE_W13, nat.STAGE_W2, nat.STAGE_COMBINE)
-    wss = [torch.zeros(layers[l].workspace_bytes(T), dtype=torch.uint8, device=dev) for l in range(NL)]
-    for st in stages:
-        for l in range(NL):
-            layers[l].forward_stage(xs[l % NX], out, st, ws=wss[l])
-    torch.cuda.synchronize()
-    if hasattr(torch.cuda, "_sleep"):
-        torch.cuda._sleep(100_000_000)
-    evs = []
-    for i in range(nsteps):
-        ev = [torch.cuda.Event(enable_timing=True) for _ in range(len(stages) + 1)]
-        for k, st in enumerate(stages):
-            ev[k].record()
+        from ftmoe import _native as nat
+
+        NL, NX = len(self.layers), self.NX
+        xs = self.xs(T)
+        out = torch.empty(T, self.cfg.H, dtype=torch.bfloat16, device=self.dev)
+        stages = (nat.STAGE_ROUTER, nat.STAGE_TOPK, nat.STAGE_W13, nat.STAGE_W2, nat.STAGE_COMBINE)
+        wss = [torch.zeros(self.layers[l].workspace_bytes(T), dtype=torch.uint8, device=self.dev) for l in range(NL)]
+        for st in stages:
             for l in range(NL):
-                layers[l].forward_stage(xs[(i + l) % NX], out, st, ws=wss[l])
-        ev[-1].record()
-        evs.append((ev, i))
-    torch.cuda.synchronize()
-    kern_us = {name: float(np.mean([ev[k].elapsed_time(ev[k + 1]) for ev, _ in evs])) * 1e3 / NL
-               for k, name in enumerate(("router", "topk", "w13", "w2", "combine"))}
-    w13_unit = _w13_bytes_per_expert(syns[0])
-    sh_w13 = 2 * cfg.shared_inter * cfg.H * 2 if cfg.shared_inter else 0
-    bytes_a = []
-    for _, i in evs:
-        for l in range(NL):
-            _, ids, _, _ = layers[l].forward(xs[(i + l) % NX], return_routing=True)
-            u = int(torch.unique(ids).numel())
-            bytes_a.append(u * w13_unit + sh_w13 + T * cfg.H * 2)
-    ach = float(np.mean(bytes_a)) / (kern_us["w13"] * 1e-6) / 1e9
-    w13_kernel = layers[0].stage_kernel(T, nat.STAGE_W13)
-    traffic = _pmc_traffic(w13_kernel, cfg.name, T)
-    roofline = {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": traffic["bytes"] if traffic else None,
-                "kernel": f"{w13_kernel} ({cfg.fmt} w13 + activation)",
-                "kernel_avg_us": round(kern_us["w13"], 2),
-                "bytes_per_launch": int(np.mean(bytes_a)),
-                "unit_bytes": w13_unit, "units_per_launch": round((np.mean(bytes_a) - sh_w13 - T * cfg.H * 2) / w13_unit, 2),
-                "traffic_source": traffic["source"] if traffic else None,
-                "kernels_us": {k: round(v, 2) for k, v in kern_us.items()}}
-
-    # ---- extra decode batch sizes (same layers)
-    sweep = []
-    for tb in [int(b) for b in args.sweep.split(",") if b]:
-        ms_b, wall_b, U_b, balg_b, _, graph_b, _ = run_point(tb, 50, 10)
-        g_b = balg_b / (ms_b * 1e-3) / 1e9
-        sweep.append({"T": tb, "tokens_per_s": round(tb / (ms_b * 1e-3), 1), "us_per_layer": round(ms_b * 1e3, 2),
-                      "wall_us_per_layer": round(wall_b * 1e3, 2), "graph_us_per_layer": round(graph_b * 1e3, 2),
-                      "unique_experts": round(U_b, 1), "GBps": round(g_b, 1), "hbm_frac": round(g_b / HBM_PEAK_GBS, 4)})
-
-    if args.copy_probe_mib > 0:
-        n = args.copy_probe_mib * (1 << 20) // 4
-        src = torch.ones(n, dtype=torch.float32, device=dev)
-        dst = torch.empty_like(src)
-        for _ in range(3):
-            dst.copy_(src)
+                self.layers[l].forward_stage(xs[l % NX], out, st, ws=wss[l])
         torch.cuda.synchronize()
-        del src, dst
+        if hasattr(torch.cuda, "_sleep"):
+            torch.cuda._sleep(100_000_000)
+        evs = []
+        for i in range(reps):
+            ev = [torch.cuda.Event(enable_timing=True) for _ in range(len(stages) + 1)]
+            for k, st in enumerate(stages):
+                ev[k].record()
+                for l in range(NL):
+                    self.layers[l].forward_stage(xs[(i + l) % NX], out, st, ws=wss[l])
+            ev[-1].record()
+            evs.append((ev, i))
+        torch.cuda.synchronize()
+        us = {name: float(np.mean([ev[k].elapsed_time(ev[k + 1]) for ev, _ in evs])) * 1e3 / NL
+              for k, name in enumerate(("router", "topk", "w13", "w2", "combine"))}
+        # realised unique experts of the same (layer, batch) pairs
+        uniq = []
+        for _, i in evs:
+            for l in range(NL):
+                _, ids, _, _ = self.layers[l].forward(xs[(i + l) % NX], return_routing=True)
+                uniq.append(int(torch.unique(ids).numel()))
+        return {"us": us, "unique": float(np.mean(uniq)), "xs": xs}
 
-    prefill = _prefill_point(cfg, layers, args.prefill_t, 20) if args.prefill_t > 0 else None
+    def rooflines(self, T: int) -> dict:
+        """The w13 and w2 kernels at T tokens against the HBM roofline:
+        algorithmic bytes per launch (realised unique experts x the projection's
+        bytes per expert + the shared expert's projection + activations) over
+        the kernel's average launch duration."""
+        from ftmoe import _native as nat
 
-    cpu = None
-    if not args.no_cpu_baseline:
-        cpu = _cpu_baseline(cfg, syns[0], layers[0], xs[0], T, args.cpu_seconds)
+        st = self.stage_times(T)
+        cfg, syn, U = self.cfg, self.syns[0], st["unique"]
+        us = st["us"]
+        Is = cfg.shared_inter
+        out = {"kernels_us": {k: round(v, 2) for k, v in us.items()}, "unique_experts": round(U, 2)}
+        for stage, which, name, sh_bytes, act_bytes in (
+                ("w13", "gate_up", nat.STAGE_W13, 2 * Is * cfg.H * 2, T * cfg.H * 2),
+                ("w2", "down", nat.STAGE_W2, cfg.H * Is * 2, T * (cfg.k + (1 if Is else 0)) * cfg.I * 2)):
+            unit = _proj_bytes(syn, which)
+            b = U * unit + sh_bytes + act_bytes
+            kern = self.layers[0].stage_kernel(T, name)
+            ach = b / (us[stage] * 1e-6) / 1e9
+            traffic = _pmc_traffic(kern, cfg.name, T)
+            out[stage] = {"bound": "hbm", "kernel": kern, "achieved": round(ach, 1), "peak": HBM_PEAK_GBS,
+                          "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBS, 4),
+                          "traffic": traffic["bytes"] if traffic else None,
+                          "traffic_source": traffic["source"] if traffic else None,
+                          "kernel_avg_us": round(us[stage], 2), "bytes_per_launch": int(b), "unit_bytes": unit,
+                          "units_per_launch": round(U, 2)}
+        return out
 
-    line = {
-        "metric": METRIC,
-        "value": round(T / (ms * 1e-3), 1),
-        "unit": "tokens/s",
-        "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
-        "ms_per_step": round(ms, 5),
-        "wall_ms_per_step": round(wall_ms, 5),
-        "graph_ms_per_step": round(graph_ms, 5),
-        "timing": "events around K layer forwards launched back to back from Python (one ctypes call each), "
-                  "queued behind a sleep kernel so the host runs ahead; wall = host clock around the same K "
-                  "forwards without the head start; graph = the same steps as HIP-graph replays (checked "
-                  "bitwise against eager: %s)" % ("ok" if graph_ok else "MISMATCH"),
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": "bf16",
-        "weights": cfg.fmt,
-        "data": "synthetic (seeded random-init weights at the real layer shape, N(0,1) bf16 tokens)",
-        "config": {"workload": f"{cfg.name} decode T={T}: {cfg.fmt} H={cfg.H} I={cfg.I} E={cfg.E} top-{cfg.k}"
-                               + (f" + shared bf16 I={cfg.shared_inter}" if cfg.shared_inter else ""),
-                   "global_batch": T, "seq_len": 1, "parallelism": "none (1 GPU)", "layers_rotated": NL},
-        "GBps": round(gbs, 1),
-        "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
-        "unique_experts": round(U, 2),
-        "bytes_per_step": int(b_alg),
-        "roofline": roofline,
-        "prefill": prefill,
-        "cpu_baseline": cpu,
-        "sweep": sweep,
-    }
-    print(json.dumps(line), flush=True)
-    return 0
+    def prefill_point(self, T: int, steps: int = 12) -> dict:
+        """One prefill chunk of T tokens through the rotated layers: layer time
+        (events around back-to-back forwards), per-stage times and the expert
+        GEMM stages' rate against the dense bf16 MFMA peak (the tiles run bf16
+        MFMAs on weights decoded exactly from their quantized form).  FLOPs
+        count real rows only: 2 * pairs * (2I * H + H * I) routed + the same
+        over T rows for the shared expert; padding rows of partly filled tiles
+        are not counted."""
+        import numpy as np
+        import torch
+
+        from ftmoe import _native as nat
+
+        cfg, dev = self.cfg, self.dev
+        NL = len(self.layers)
+        g = torch.Generator(device=dev).manual_seed(4321)
+        xs = [torch.randn(T, cfg.H, generator=g, device=dev).to(torch.bfloat16) for _ in range(NL)]
+        for i in range(2 * NL):
+            self.layers[i % NL].forward(xs[i % NL])
+        torch.cuda.synchronize()
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
+        for i in range(steps):
+            ev[i].record()
+            self.layers[i % NL].forward(xs[i % NL])
+        ev[steps].record()
+        torch.cuda.synchronize()
+        us = _median([ev[i].elapsed_time(ev[i + 1]) * 1e3 for i in range(steps)])
+        out = torch.empty(T, cfg.H, dtype=torch.bfloat16, device=dev)
+        stages = (nat.STAGE_ROUTER, nat.STAGE_TOPK, nat.STAGE_W13, nat.STAGE_W2, nat.STAGE_COMBINE)
+        wss = [torch.zeros(self.layers[l].workspace_bytes(T), dtype=torch.uint8, device=dev) for l in range(NL)]
+        for st in stages:
+            for l in range(NL):
+                self.layers[l].forward_stage(xs[l], out, st, ws=wss[l])
+        torch.cuda.synchronize()
+        evs = []
+        for _ in range(max(1, steps // NL)):
+            e = [torch.cuda.Event(enable_timing=True) for _ in range(len(stages) + 1)]
+            for kq, st in enumerate(stages):
+                e[kq].record()
+                for l in range(NL):
+                    self.layers[l].forward_stage(xs[l], out, st, ws=wss[l])
+            e[-1].record()
+            evs.append(e)
+        torch.cuda.synchronize()
+        names = ("router", "topk", "w13", "w2", "combine")
+        kern = {n: float(np.mean([e[kq].elapsed_time(e[kq + 1]) for e in evs])) * 1e3 / NL
+                for kq, n in enumerate(names)}
+        pairs = T * cfg.k
+        Is = cfg.shared_inter
+        f13 = 2.0 * pairs * 2 * cfg.I * cfg.H + 2.0 * T * 2 * Is * cfg.H
+        f2 = 2.0 * pairs * cfg.H * cfg.I + 2.0 * T * cfg.H * Is
+        tf = (f13 + f2) / ((kern["w13"] + kern["w2"]) * 1e-6) / 1e12
+        syn = self.syns[0]
+        w_bytes = cfg.E * (_proj_bytes(syn, "gate_up") + _proj_bytes(syn, "down")) + cfg.E * cfg.H * 2 + 3 * cfg.H * Is * 2
+        b_alg = w_bytes + 2 * T * cfg.H * 2
+        return {"T": T, "us_per_layer": round(us, 1), "tokens_per_s": round(T / (us * 1e-6), 1),
+                "GBps": round(b_alg / (us * 1e-6) / 1e9, 1),
+                "hbm_frac": round(b_alg / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                "kernels_us": {n: round(v, 1) for n, v in kern.items()},
+                "kernels": {n: self.layers[0].stage_kernel(T, st) for n, st in zip(names, stages)},
+                "gemm_gflop": round((f13 + f2) / 1e9, 1), "gemm_tflops": round(tf, 1),
+                "mfma_frac": round(tf / MFMA_BF16_PEAK_TFLOPS, 4), "mfma_peak_tflops": MFMA_BF16_PEAK_TFLOPS,
+                "w13_tflops": round(f13 / (kern["w13"] * 1e-6) / 1e12, 1),
+                "w2_tflops": round(f2 / (kern["w2"] * 1e-6) / 1e12, 1)}
 
 
-def _prefill_point(cfg, layers, T: int, steps: int) -> dict:
-    """One prefill chunk of T tokens through the rotated layers: layer time
-    (events around back-to-back forwards), per-stage times (each stage of the
-    rotation launched as a group, as for decode) and the expert GEMM stages'
-    rate against the dense bf16 MFMA peak (the tiles run bf16 MFMAs on weights
-    decoded exactly from their quantized form).  FLOPs count real rows only:
-    2 * pairs * (2I * H + H * I) routed + the same over T rows for the shared
-    expert; padding rows of partly filled tiles are not counted."""
+# ------------------------------------------------------------------ CPU baseline
+def _cpu_baselines(cb: ConfigBench, T: int, seconds: float) -> dict:
+    """The reference's CPU MoE (cpu_moe.cpp freetoken_cpu_moe_forward_fast) on
+    the config's layer and the GPU run's routing at T tokens, three rows:
+
+    * ``all_cores``: threads = 0, the kernel's own rule (hardware concurrency
+      clamped to E, cpu_moe.cpp:485-490), fp32 banks dequantized once outside
+      the timer (by the GPU dequant kernel);
+    * ``one_thread``: the same, threads = 1;
+    * ``reference_equivalent``: what python/freetoken/kernel/cpu_moe.py:460-461
+      does per call: the dense bf16 banks converted to fp32 (whole [E,2I,H] and
+      [E,H,I]) inside the timer, then the all-cores call.
+
+    The shared expert (C3) rides as one more always-routed expert weighted by
+    its sigmoid gate; the router GEMV is not timed.  Each row runs calls for
+    about ``seconds`` (at least one)."""
     import numpy as np
     import torch
 
-    from ftmoe import _native as nat
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import ftm_oracle as O
+    from ftmoe.kernel._dequant import dequant
 
-    dev = torch.device("cuda:0")
-    NL = len(layers)
-    g = torch.Generator(device=dev).manual_seed(4321)
-    xs = [torch.randn(T, cfg.H, generator=g, device=dev).to(torch.bfloat16) for _ in range(NL)]
-    for i in range(2 * NL):
-        layers[i % NL].forward(xs[i % NL])
-    torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record()
-    for i in range(steps):
-        layers[i % NL].forward(xs[i % NL])
-    e1.record()
-    torch.cuda.synchronize()
-    us = e0.elapsed_time(e1) * 1e3 / steps
-    out = torch.empty(T, cfg.H, dtype=torch.bfloat16, device=dev)
-    stages = (nat.STAGE_ROUTER, nat.STAGE_TOPK, nat.STAGE_W13, nat.STAGE_W2, nat.STAGE_COMBINE)
-    wss = [torch.zeros(layers[l].workspace_bytes(T), dtype=torch.uint8, device=dev) for l in range(NL)]
-    for st in stages:
-        for l in range(NL):
-            layers[l].forward_stage(xs[l], out, st, ws=wss[l])
-    torch.cuda.synchronize()
-    reps = max(1, steps // NL)
-    evs = []
-    for _ in range(reps):
-        ev = [torch.cuda.Event(enable_timing=True) for _ in range(len(stages) + 1)]
-        for kq, st in enumerate(stages):
-            ev[kq].record()
-            for l in range(NL):
-                layers[l].forward_stage(xs[l], out, st, ws=wss[l])
-        ev[-1].record()
-        evs.append(ev)
-    torch.cuda.synchronize()
-    names = ("router", "topk", "w13", "w2", "combine")
-    kern = {n: float(np.mean([ev[kq].elapsed_time(ev[kq + 1]) for ev in evs])) * 1e3 / NL for kq, n in enumerate(names)}
-    pairs = T * cfg.k
-    f13 = 2.0 * pairs * 2 * cfg.I * cfg.H + (2.0 * T * 2 * cfg.shared_inter * cfg.H if cfg.shared_inter else 0.0)
-    f2 = 2.0 * pairs * cfg.H * cfg.I + (2.0 * T * cfg.H * cfg.shared_inter if cfg.shared_inter else 0.0)
-    tf = (f13 + f2) / ((kern["w13"] + kern["w2"]) * 1e-6) / 1e12
-    return {"T": T, "us_per_layer": round(us, 1), "tokens_per_s": round(T / (us * 1e-6), 1),
-            "kernels_us": {n: round(v, 1) for n, v in kern.items()},
-            "kernels": {n: layers[0].stage_kernel(T, st) for n, st in zip(names, stages)},
-            "gemm_gflop": round((f13 + f2) / 1e9, 1), "gemm_tflops": round(tf, 1),
-            "mfma_frac": round(tf / MFMA_BF16_PEAK_TFLOPS, 4), "mfma_peak_tflops": MFMA_BF16_PEAK_TFLOPS,
-            "w13_tflops": round(f13 / (kern["w13"] * 1e-6) / 1e12, 1),
-            "w2_tflops": round(f2 / (kern["w2"] * 1e-6) / 1e12, 1)}
+    if not O.ref_cpu_moe_available():
+        return {"rows": [], "note": "oracle/_ref/libcpu_moe_ref.so not built"}
+    cfg, layer, syn = cb.cfg, cb.layers[0], cb.syns[0]
+    x = cb.x_pool[0][:T].contiguous()
+    _, ids, w, _ = layer.forward(x, return_routing=True)
+    ids, w = ids.cpu().numpy(), w.cpu().numpy()
+    E_tot = cfg.E + (1 if cfg.shared_inter else 0)
+    Imax = max(cfg.I, cfg.shared_inter)
+    assert not cfg.shared_inter or cfg.shared_inter == cfg.I
+    gu_bf = torch.empty(E_tot, 2 * cfg.I, cfg.H, dtype=torch.bfloat16)
+    dn_bf = torch.empty(E_tot, cfg.H, Imax, dtype=torch.bfloat16)
+    gu = torch.empty(E_tot, 2 * cfg.I, cfg.H, dtype=torch.float32)
+    dn = torch.empty(E_tot, cfg.H, Imax, dtype=torch.float32)
+    for e in range(cfg.E):
+        a = dequant(layer.w13, out_dtype=torch.float32, slot=e)
+        b = dequant(layer.w2, out_dtype=torch.float32, slot=e)
+        gu[e], dn[e] = a.cpu(), b.cpu()
+        gu_bf[e], dn_bf[e] = a.to(torch.bfloat16).cpu(), b.to(torch.bfloat16).cpu()
+    if cfg.shared_inter:
+        gu[cfg.E], dn[cfg.E] = syn.shared["w13"].float().cpu(), syn.shared["w2"].float().cpu()
+        gu_bf[cfg.E], dn_bf[cfg.E] = syn.shared["w13"].cpu(), syn.shared["w2"].cpu()
+        sl = (x.float() @ syn.shared["gate"].float().T).cpu().numpy()[:, 0]
+        sw = O.round_bf16((1.0 / (1.0 + np.exp(-sl))).astype(np.float32))
+        ids = np.concatenate([ids, np.full((T, 1), cfg.E, np.int32)], axis=1)
+        w = np.concatenate([w, sw[:, None]], axis=1)
+    gu_np, dn_np = gu.numpy(), dn.numpy()
+    xf = x.float().cpu().numpy()
+
+    def timed(fn):
+        fn()  # warm (page-in, thread start-up)
+        n, t0 = 0, time.perf_counter()
+        while True:
+            fn()
+            n += 1
+            el = time.perf_counter() - t0
+            if el >= seconds:
+                return n, el
+
+    def ref_equiv():
+        a, b = gu_bf.to(torch.float32).contiguous(), dn_bf.to(torch.float32).contiguous()
+        return O.ref_cpu_moe_forward_fast(xf, ids, w, a.numpy(), b.numpy(), threads=0)
+
+    rows = []
+    hw = os.cpu_count() or 1
+    for name, fn, threads in (("all_cores", lambda: O.ref_cpu_moe_forward_fast(xf, ids, w, gu_np, dn_np, threads=0),
+                               min(hw, E_tot)),
+                              ("one_thread", lambda: O.ref_cpu_moe_forward_fast(xf, ids, w, gu_np, dn_np, threads=1), 1),
+                              ("reference_equivalent", ref_equiv, min(hw, E_tot))):
+        n, el = timed(fn)
+        tps = T * n / el
+        b_alg = _alg_bytes_fp32(cfg, ids, T)
+        rows.append({"row": name, "tokens_per_s": round(tps, 2), "ms_per_call": round(el * 1e3 / n, 3),
+                     "threads": threads, "calls": n, "seconds": round(el, 2),
+                     "GBps_fp32_banks": round(b_alg * n / el / 1e9, 2)})
+    return {"T": T, "rows": rows}
 
 
+def _alg_bytes_fp32(cfg, ids, T):
+    """Bytes the CPU kernel streams per call: the fp32 rows of every expert it
+    touches (realised unique experts incl. the shared one) + x and out."""
+    import numpy as np
+
+    u = len(np.unique(ids))
+    Imax = max(cfg.I, cfg.shared_inter)
+    return u * (2 * cfg.I * cfg.H + cfg.H * Imax) * 4 + 2 * T * cfg.H * 4
+
+
+# ------------------------------------------------------------------ C5 offload
 def _zipf_routing(rng, steps: int, T: int, E: int, k: int, s_exp: float = 1.1):
     """Per token k distinct experts drawn Zipf(s) over ranks mapped through a
     seeded permutation; router weights = softmax of N(0, 1) logits over the k."""
@@ -379,15 +488,15 @@ def _zipf_routing(rng, steps: int, T: int, E: int, k: int, s_exp: float = 1.1):
     return ids, (w / w.sum(-1, keepdims=True)).astype(np.float32)
 
 
-def _offload_bench(args) -> int:
+def _offload_bench(args) -> dict:
     """C5: the C3 FP8 layer with only ``--offload-slots`` expert slots in HBM and
-    all 256 banks in pinned host memory.  Each step: LRU -> copies of the misses
-    -> grouped layer call over the slot pool (+ shared expert).  ``device``: the
-    LRU and the copies are GPU kernels reading the routing and the pinned banks
-    directly (no host synchronisation inside the timed loop); ``host``: the
-    host LRU and per-row copies on a side stream.  Reports tokens/s, the hit
-    rate over unique expert requests and the achieved H2D GB/s next to a pinned
-    256 MiB host-to-device copy."""
+    all 256 banks in pinned host memory.  Each step: LRU -> copies of the
+    misses -> grouped layer call over the slot pool (+ shared expert).
+    ``device``: the LRU and the copies are GPU kernels reading the routing and
+    the pinned banks directly (no host synchronisation inside the timed loop);
+    ``host``: the host LRU and per-row copies on a side stream.  Reports
+    tokens/s, the hit rate over unique expert requests and the achieved H2D
+    GB/s next to a pinned 256 MiB host-to-device copy."""
     import numpy as np
     import torch
 
@@ -396,7 +505,7 @@ def _offload_bench(args) -> int:
 
     dev = torch.device("cuda:0")
     cfg = S.CONFIGS["c3_fp8"]
-    T, steps, slots = args.batch, args.offload_steps, args.offload_slots
+    T, steps, slots = 16, args.offload_steps, args.offload_slots
     syn = S.generate(cfg, T=T, seed=0, device=dev)
     bank_host = {k: v.cpu() for k, v in syn.bank.items()}
     del syn.bank
@@ -447,93 +556,156 @@ def _offload_bench(args) -> int:
     e1.record()
     torch.cuda.synchronize()
     peak = 5 * (256 << 20) / (e0.elapsed_time(e1) * 1e-3) / 1e9
-
-    line = {
-        "metric": "offload decode tokens/s (C5: C3 FP8 layer, 64 HBM slots, 256 pinned host banks)",
-        "value": round(steps * T / el, 1), "unit": "tokens/s", "n_gpus": 1, "steps": steps, "warmup": 10,
-        "ms_per_step": round(el * 1e3 / steps, 4), "higher_is_better": True, "scaling": "weak",
-        "vs_baseline": None, "dtype": "bf16", "weights": cfg.fmt,
-        "data": "synthetic (seeded random-init FP8 banks at the C3 shape; Zipf(1.1) routing over a seeded "
-                "expert permutation, softmax weights of N(0,1) logits)",
-        "config": {"workload": f"c5 offload: {cfg.name} T={T}, slots={slots} of E={cfg.E}, one layer",
-                   "global_batch": T, "seq_len": 1, "parallelism": "none (1 GPU)"},
+    del cache
+    torch.cuda.empty_cache()
+    return {
+        "workload": f"c5 offload: c3_fp8 T={T}, slots={slots} of E={cfg.E}, one layer, {steps} Zipf(1.1) steps",
+        "tokens_per_s": round(steps * T / el, 1), "ms_per_step": round(el * 1e3 / steps, 4),
         "hit_rate": round(1.0 - misses / req, 4), "misses_per_step": round(misses / steps, 2),
         "unique_experts_per_step": round(float(np.mean(uniq)), 2), "steps_with_more_experts_than_slots": over,
         "h2d_bytes_per_slot": slot_bytes, "h2d_GBps": round(h2d / el / 1e9, 2),
         "h2d_pinned_copy_peak_GBps": round(peak, 2),
-        "h2d_frac_of_copy_peak": round(h2d / el / 1e9 / peak, 4),
+        "roofline": {"bound": "pcie_h2d", "achieved": round(h2d / el / 1e9, 2), "peak": round(peak, 2),
+                     "unit": "GB/s", "frac": round(h2d / el / 1e9 / peak, 4),
+                     "peak_source": "5 x 256 MiB pinned host-to-device copies on this box"},
         "lru": args.offload_lru,
         "timing": ("wall clock around the steps (LRU + copy kernels + layer kernels, enqueued without a host "
                    "synchronisation), synchronised at both ends" if dev_lru else
-                   "wall clock around the steps (host LRU + side-stream copies + kernels), synchronised at both ends"),
+                   "wall clock around the steps (host LRU + side-stream copies + kernels), synchronised at both "
+                   "ends"),
+    }
+
+
+# ------------------------------------------------------------------ main
+def _config_line(cb: ConfigBench, args, T_list, with_cpu: bool) -> dict:
+    import torch
+
+    cfg = cb.cfg
+    res = {"name": cfg.name, "workload": f"{cfg.fmt} H={cfg.H} I={cfg.I} E={cfg.E} top-{cfg.k}"
+                                        + (f" + shared bf16 I={cfg.shared_inter}" if cfg.shared_inter else ""),
+           "decode": []}
+    for T in T_list:
+        res["decode"].append(cb.decode_point(T, args.steps, args.warmup, graphs=(cfg.name, T) == HEADLINE))
+        torch.cuda.synchronize()
+    kt = KERNEL_T[cfg.name]
+    if kt in T_list:
+        res["kernel_T"] = kt
+        res["rooflines"] = cb.rooflines(kt)
+    if cfg.prefill and not args.no_prefill:
+        res["prefill"] = cb.prefill_point(cfg.prefill)
+    if with_cpu:
+        res["cpu_baseline"] = _cpu_baselines(cb, kt, args.cpu_seconds)
+    return res
+
+
+def main() -> int:
+    args = _parse()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one MI355X only: this build has no multi-GPU path "
+              "(expert-parallel sharding is a design note), so --gpus must be 1.", file=sys.stderr)
+        return 2
+
+    import torch
+
+    from ftmoe import synthetic as S
+
+    if args.prefill_only:
+        cfg = S.CONFIGS[args.prefill_only]
+        cb = ConfigBench(cfg, max(1, args.layers), 1)
+        print(json.dumps(cb.prefill_point(cfg.prefill)), flush=True)
+        return 0
+    if args.point:
+        name, T = args.point.split(":")
+        cfg = S.CONFIGS[name]
+        cb = ConfigBench(cfg, max(1, args.layers), int(T))
+        line = {"point": args.point, "decode": cb.decode_point(int(T), args.steps, args.warmup),
+                "rooflines": cb.rooflines(int(T))}
+        if args.copy_probe_mib > 0:
+            _copy_probe(args.copy_probe_mib)
+        print(json.dumps(line), flush=True)
+        return 0
+
+    want = [c.strip() for c in args.configs.split(",") if c.strip()]
+    configs = {}
+    t_start = time.perf_counter()
+    for name in ("c1_int8", "c2_gptq", "c3_fp8", "c4_mxfp4"):
+        if name not in want:
+            continue
+        cfg = S.CONFIGS[name]
+        T_list = DECODE_T[name]
+        cb = ConfigBench(cfg, max(1, args.layers), max(T_list))
+        configs[name] = _config_line(cb, args, T_list, with_cpu=not args.no_cpu_baseline)
+        del cb
+        torch.cuda.synchronize()
+        torch.cuda.empty_cache()
+    if "c5" in want:
+        configs["c5_offload"] = _offload_bench(args)
+    if args.copy_probe_mib > 0:
+        _copy_probe(args.copy_probe_mib)
+
+    c3 = configs.get(HEADLINE[0])
+    head = next((d for d in c3["decode"] if d["T"] == HEADLINE[1]), None) if c3 else None
+    cpu_info = _cpu_info()
+    cpu = None
+    if c3 and "cpu_baseline" in c3 and c3["cpu_baseline"].get("rows"):
+        r = next(r for r in c3["cpu_baseline"]["rows"] if r["row"] == "all_cores")
+        cpu = {"value": r["tokens_per_s"], "unit": "tokens/s", "cores": r["threads"], "kind": "reference",
+               "sample": f"{r['calls']} calls x {HEADLINE[1]} tokens of c3_fp8 in {r['seconds']} s: "
+                         "freetoken_cpu_moe_forward_fast (python/freetoken/kernel/csrc/cpu_moe/cpu_moe.cpp, "
+                         "built unmodified), threads=0 (all cores clamped to E), fp32 banks dequantized once "
+                         "outside the timer, routing from the GPU run, shared expert as an always-routed "
+                         "expert, router GEMV not timed; one-thread and reference-equivalent rows per config "
+                         "under configs.*.cpu_baseline",
+               "host": cpu_info}
+    roof = None
+    if c3 and "rooflines" in c3:
+        r13 = c3["rooflines"]["w13"]
+        roof = dict(r13)
+        roof["kernel"] = f"{r13['kernel']} (fp8_block w13 + activation, C3 T={HEADLINE[1]})"
+        roof["kernels_us"] = c3["rooflines"]["kernels_us"]
+    line = {
+        "metric": METRIC,
+        "value": head["tokens_per_s"] if head else None,
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(head["us_per_layer"] * 1e-3, 5) if head else None,
+        "ms_per_step_mean": round(head["us_mean"] * 1e-3, 5) if head else None,
+        "timing": f"median over {args.steps // 10} batches of 10 back-to-back layer forwards ({args.steps} timed), "
+                  "HIP events on the launch stream between batches, forwards queued behind a sleep kernel so the "
+                  "host runs ahead; mean, host wall clock and HIP-graph replay beside it; weights rotated over "
+                  f"{args.layers} random-init layers per config so they stream from HBM",
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "weights": "fp8_block",
+        "data": "synthetic (seeded random-init weights at the real layer shapes, N(0,1) bf16 tokens)",
+        "config": {"workload": f"c3_fp8 decode T={HEADLINE[1]}: fp8_block H=2048 I=512 E=256 top-8 + shared bf16 "
+                               "I=512 (BASELINE.json configs[2]); every other config under 'configs'",
+                   "global_batch": HEADLINE[1], "seq_len": 1, "parallelism": "none (1 GPU)",
+                   "layers_rotated": args.layers},
+        "GBps": head["GBps"] if head else None,
+        "hbm_frac": head["hbm_frac"] if head else None,
+        "roofline": roof,
+        "cpu_baseline": cpu,
+        "configs": configs,
+        "bench_seconds": round(time.perf_counter() - t_start, 1),
     }
     print(json.dumps(line), flush=True)
     return 0
 
 
-def _cpu_baseline(cfg, syn, layer, x, T, seconds):
-    """The reference's CPU MoE (cpu_moe.cpp freetoken_cpu_moe_forward_fast) on the
-    same layer: banks dequantized to fp32 once outside the timer (by the GPU dequant
-    kernel), routing taken from the GPU run, the shared expert as one more
-    always-routed expert weighted by its sigmoid gate."""
-    import numpy as np
+def _copy_probe(mib: int) -> None:
     import torch
 
-    sys.path.insert(0, os.path.join(ROOT, "oracle"))
-    import ftm_oracle as O
-    from ftmoe.kernel._dequant import dequant
-
-    out, ids, w, _ = layer.forward(x, return_routing=True)
-    ids = ids.cpu().numpy()
-    w = w.cpu().numpy()
-    gu = torch.empty(cfg.E + 1, 2 * cfg.I, cfg.H, dtype=torch.float32)
-    dn = torch.empty(cfg.E + 1, cfg.H, cfg.I, dtype=torch.float32)
-    for e in range(cfg.E):
-        gu[e] = dequant(layer.w13, out_dtype=torch.float32, slot=e).cpu()
-        dn[e] = dequant(layer.w2, out_dtype=torch.float32, slot=e).cpu()
-    E_tot = cfg.E
-    if cfg.shared_inter:
-        assert cfg.shared_inter == cfg.I
-        gu[cfg.E] = syn.shared["w13"].float().cpu()
-        dn[cfg.E] = syn.shared["w2"].float().cpu()
-        sl = (x.float() @ syn.shared["gate"].float().T).cpu().numpy()[:, 0]
-        sw = O.round_bf16(1.0 / (1.0 + np.exp(-sl)).astype(np.float32))
-        ids = np.concatenate([ids, np.full((T, 1), cfg.E, np.int32)], axis=1)
-        w = np.concatenate([w, sw[:, None]], axis=1)
-        E_tot += 1
-    gu_np = gu[:E_tot].numpy()
-    dn_np = dn[:E_tot].numpy()
-    xf = x.float().cpu().numpy()
-    threads = min(16, os.cpu_count() or 1)
-    kind = "reference" if O.ref_cpu_moe_available() else "port"
-
-    def call():
-        if kind == "reference":
-            return O.ref_cpu_moe_forward_fast(xf, ids, w, gu_np, dn_np, threads=threads)
-        spec_w13 = O.OracleProj("fp32", gu_np, 2 * cfg.I, cfg.H)
-        spec_w2 = O.OracleProj("fp32", dn_np, cfg.H, cfg.I)
-        return O.moe_experts(spec_w13, spec_w2, xf, ids, w, E=E_tot, h_bf16=False)
-
-    call()
-    n, t0 = 0, time.perf_counter()
-    while True:
-        call()
-        n += 1
-        el = time.perf_counter() - t0
-        if el >= seconds:
-            break
-    model = ""
-    try:
-        with open("/proc/cpuinfo") as f:
-            model = next((l.split(":", 1)[1].strip() for l in f if l.startswith("model name")), "")
-    except OSError:
-        pass
-    return {"value": round(T * n / el, 2), "unit": "tokens/s", "cores": threads if kind == "reference" else 1,
-            "kind": kind,
-            "sample": f"{n} calls x {T} tokens of {cfg.name} in {el:.1f} s on {model or 'host CPU'}: "
-                      "freetoken_cpu_moe_forward_fast (python/freetoken/kernel/csrc/cpu_moe/cpu_moe.cpp, built "
-                      "unmodified), fp32 banks dequantized once outside the timer, routing from the GPU run, "
-                      "shared expert as an always-routed expert; router GEMV not timed"}
+    n = mib * (1 << 20) // 4
+    src = torch.ones(n, dtype=torch.float32, device="cuda:0")
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
 
 
 if __name__ == "__main__":
