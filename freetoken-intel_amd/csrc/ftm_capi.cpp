@@ -225,6 +225,11 @@ int ftm_moe_forward(const ftm_moe_layer* layer, const void* x, int32_t num_token
   const int rows = layer->num_experts + (layer->shared_inter > 0 ? 1 : 0);
   // small decode batches on the lean kernels route inside stage A (no top-k launch)
   const bool fused = fast_layer(layer, x) && lean_route_ok(*layer, num_tokens);
+  if (!fused && route_topk_fused(*layer, num_tokens)) {  // router + top-k in one launch
+    hipError_t e = launch_route_topk(*layer, x, num_tokens, topk_ids, topk_w, logits, ws, wl, st);
+    if (e == hipSuccess) e = run_experts(*layer, x, num_tokens, out, ws, wl, st);
+    return hip_rc(e);
+  }
   hipError_t e = launch_router(*layer, x, num_tokens, 0, rows, ws, wl, st);
   if (fused) {
     const RouteOut ro = {topk_ids, topk_w, logits};
@@ -273,12 +278,16 @@ int ftm_moe_forward_stage(const ftm_moe_layer* layer, const void* x, int32_t num
   char* ws = (char*)workspace;
   hipError_t e = hipSuccess;
   const bool fused = lean_route_ok(*layer, num_tokens);  // routing runs in stage A
+  const bool rt = !fused && route_topk_fused(*layer, num_tokens);  // the router launch also routes
   const RouteOut ro = {nullptr, nullptr, nullptr};
   if (stage == FTM_STAGE_ROUTER)
-    e = launch_router(*layer, x, num_tokens, 0, layer->num_experts + (layer->shared_inter > 0 ? 1 : 0), ws, wl, st);
+    e = rt ? launch_route_topk(*layer, x, num_tokens, nullptr, nullptr, nullptr, ws, wl, st)
+           : launch_router(*layer, x, num_tokens, 0, layer->num_experts + (layer->shared_inter > 0 ? 1 : 0), ws, wl,
+                           st);
   else if (stage == FTM_STAGE_TOPK)
-    e = fused ? hipSuccess
-              : launch_topk(*layer, num_tokens, nullptr, 0, nullptr, nullptr, nullptr, nullptr, nullptr, ws, wl, st);
+    e = fused || rt
+            ? hipSuccess
+            : launch_topk(*layer, num_tokens, nullptr, 0, nullptr, nullptr, nullptr, nullptr, nullptr, ws, wl, st);
   else
     e = launch_experts(*layer, x, num_tokens, out, ws, wl, st,
                        stage == FTM_STAGE_W13 ? 1 : stage == FTM_STAGE_W2 ? 2 : 4, fused ? &ro : nullptr);

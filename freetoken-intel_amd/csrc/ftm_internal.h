@@ -125,6 +125,12 @@ inline bool lean_route_ok(const ftm_moe_layer& L, int T) {
   return lean_ok(L, T) && T <= kLeanRouteMaxT && L.num_experts <= 256 && L.topk <= kLeanRouteMaxK;
 }
 
+// Router and top-k as one launch (k_route_topk1) for small batches that do
+// not route inside stage A: bf16 activations, a router matrix, T <= 16.
+bool route_topk_fused(const ftm_moe_layer& L, int T);
+hipError_t launch_route_topk(const ftm_moe_layer& L, const void* x, int T, int32_t* ids_out, float* w_out,
+                             float* logits_out, char* ws, const WsLayout& wl, hipStream_t st);
+
 hipError_t launch_linear(const ftm_proj& P, int slot, const void* x, int x_dt, int M, void* out,
                          int out_dt, const void* bias, int bias_dt, int final_dt, hipStream_t st);
 hipError_t launch_fill_routing(int T, int32_t slot, int32_t* slot_word, int32_t* ids, float* w, hipStream_t st);

@@ -46,12 +46,11 @@ namespace ftm {
 constexpr int kRouterTPW = 4;  // tokens per wave
 constexpr int kRouterSteps = 4;  // 512-element chunk steps per load group
 
-__global__ __launch_bounds__(kBlock) void k_router(const LayerArgs a, int row_begin) {
-  const int r = row_begin + blockIdx.x;
+// Logits of row r for tokens tb + 4 i (i < kRouterTPW), by one wave.
+__device__ __forceinline__ void router_row_tile(const LayerArgs& a, int r, int tb) {
   const int E = a.L.num_experts, H = a.L.hidden, T = a.T;
   const void* grow = (r < E) ? (const void*)((const uint16_t*)a.L.gate_w + (size_t)r * H) : a.L.shared_gate;
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int tb = blockIdx.y * 4 * kRouterTPW + wave;
+  const int lane = threadIdx.x & 63;
   const Rsrc gres = make_rsrc(grow, (uint32_t)H * 2u);
   const Rsrc xres = make_rsrc(a.x, (uint32_t)T * (uint32_t)H * 2u);
   const int nsteps = (H + 511) / 512;
@@ -101,6 +100,11 @@ __global__ __launch_bounds__(kBlock) void k_router(const LayerArgs a, int row_be
   }
 }
 
+__global__ __launch_bounds__(kBlock) void k_router(const LayerArgs a, int row_begin) {
+  const int wave = threadIdx.x >> 6;
+  router_row_tile(a, row_begin + blockIdx.x, blockIdx.y * 4 * kRouterTPW + wave);
+}
+
 // Large T: one WG per (8 expert rows, 16 tokens), so x is read once per 8
 // rows instead of once per row.  Every (token, row) logit keeps k_router's
 // arithmetic exactly: lane l accumulates chunks c = l, l + 64, ... (8
@@ -122,11 +126,11 @@ __device__ __forceinline__ void router_halve(float (&v)[32], int lane) {
   }
 }
 
-__global__ __launch_bounds__(kBlock) void k_router_rows(const LayerArgs a, int row_begin, int row_end) {
+// Logits of rows [r0, r0 + kRouterRB) (below row_end) for tokens [t0, t0 +
+// kRouterTPW), by one wave.
+__device__ __forceinline__ void router_rows_tile(const LayerArgs& a, int r0, int row_end, int t0) {
   const int E = a.L.num_experts, H = a.L.hidden, T = a.T;
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int r0 = row_begin + blockIdx.x * kRouterRB;
-  const int t0 = blockIdx.y * 4 * kRouterTPW + wave * kRouterTPW;
+  const int lane = threadIdx.x & 63;
   Rsrc gres[kRouterRB];
 #pragma unroll
   for (int j = 0; j < kRouterRB; ++j) {
@@ -215,6 +219,11 @@ __global__ __launch_bounds__(kBlock) void k_router_rows(const LayerArgs a, int r
     if (r < E && a.L.gate_b != nullptr) z = tot + bf16_to_f32(((const uint16_t*)a.L.gate_b)[r]);
     a.logits[(size_t)t * (E + 1) + r] = round_to(z, a.L.act_dtype);
   }
+}
+
+__global__ __launch_bounds__(kBlock) void k_router_rows(const LayerArgs a, int row_begin, int row_end) {
+  const int wave = threadIdx.x >> 6;
+  router_rows_tile(a, row_begin + blockIdx.x * kRouterRB, row_end, blockIdx.y * 4 * kRouterTPW + wave * kRouterTPW);
 }
 
 // ============================================================== top-k + grouping
@@ -653,6 +662,48 @@ __global__ __launch_bounds__(64 * kTopk1Waves) void k_topk1(const LayerArgs a, c
   }
   __syncthreads();
   compact_experts<kTopk1Waves>(a, s_cnt, false, s_wsum, s_first);
+}
+
+// Router and top-k in one launch for T <= kTopk1MaxT: workgroup g computes
+// the logits of rows [4 g, 4 g + 4) for every token, each of its 16 waves
+// one (row, token quad) exactly as a k_router wave does (router_row_tile: all
+// of a step group's loads in flight, the same fp32 order), and the last
+// workgroup to arrive runs k_topk1's body -- one wave per token, per-expert
+// counters in LDS, compaction and work records.  Takes the top-k launch and
+// its ramp out of the chain router -> top-k -> stage A.
+constexpr int kRouteRows = 4;  // router rows per k_route_topk1 workgroup
+template <int MODE, int NV>
+__global__ __launch_bounds__(64 * kTopk1Waves) void k_route_topk1(const LayerArgs a, int row_end, int32_t* ids_out,
+                                                                  float* w_out, float* logits_out) {
+  __shared__ int32_t s_cnt[kMaxExperts];
+  __shared__ int32_t s_first[kMaxExperts * kRecPairs];
+  __shared__ int s_wsum[kTopk1Waves];
+  __shared__ int s_last;
+  const int wave = threadIdx.x >> 6;
+  static_assert(kRouteRows * 4 == kTopk1Waves && 4 * kRouterTPW >= kTopk1MaxT, "16 waves: 4 rows x 16 tokens");
+  const int r = (int)blockIdx.x * kRouteRows + (wave & 3);
+  if (r < row_end) router_row_tile(a, r, wave >> 2);
+  // publish this workgroup's logits; the last arrival sees every workgroup's
+  __syncthreads();
+  if (threadIdx.x < 64) {
+    __threadfence();
+    if (threadIdx.x == 0) s_last = (atomicAdd(&a.ctrl[kCtrlArriveTopk], 1) == (int)gridDim.x - 1);
+    __threadfence();
+  }
+  __syncthreads();
+  if (!s_last) return;
+  const int E = a.L.num_experts, T = a.T;
+  for (int e = threadIdx.x; e < E; e += 64 * kTopk1Waves) s_cnt[e] = 0;
+  __syncthreads();
+  for (int t = wave; t < T; t += kTopk1Waves) {
+    int sel_e;
+    float sel_w;
+    route_token<MODE, NV>(a, t, nullptr, 0, nullptr, nullptr, logits_out, sel_e, sel_w);
+    emit_token(a, t, sel_e, sel_w, ids_out, w_out, s_cnt, s_first);
+  }
+  __syncthreads();
+  compact_experts<kTopk1Waves>(a, s_cnt, false, s_wsum, s_first);
+  if (threadIdx.x == 0) a.ctrl[kCtrlArriveTopk] = 0;
 }
 
 // Large batches: one wave per token, 4 per workgroup; the last-arriving
@@ -2528,6 +2579,30 @@ hipError_t launch_router(const ftm_moe_layer& L, const void* x, int T, int row_b
   return hipGetLastError();
 }
 
+bool route_topk_fused(const ftm_moe_layer& L, int T) {
+  return T >= 1 && T <= kTopk1MaxT && L.gate_w != nullptr && L.act_dtype == FTM_DT_BF16 && L.hidden % 8 == 0 &&
+         !lean_route_ok(L, T);
+}
+
+hipError_t launch_route_topk(const ftm_moe_layer& L, const void* x, int T, int32_t* ids_out, float* w_out,
+                             float* logits_out, char* ws, const WsLayout& wl, hipStream_t st) {
+  const LayerArgs a = make_args(L, x, nullptr, T, ws, wl);
+  const int rows = L.num_experts + (L.shared_inter > 0 ? 1 : 0);
+  const dim3 grid((rows + kRouteRows - 1) / kRouteRows), block(64 * kTopk1Waves);
+#define FTM_RT_NV(M)                                                                                         \
+  if (L.num_experts <= 256)                                                                                  \
+    hipLaunchKernelGGL((k_route_topk1<M, 4>), grid, block, 0, st, a, rows, ids_out, w_out, logits_out);     \
+  else                                                                                                       \
+    hipLaunchKernelGGL((k_route_topk1<M, 8>), grid, block, 0, st, a, rows, ids_out, w_out, logits_out);
+  switch (L.route_mode) {
+    case FTM_ROUTE_SOFTMAX_TOPK: FTM_RT_NV(FTM_ROUTE_SOFTMAX_TOPK) break;
+    case FTM_ROUTE_SOFTMAX_TOPK_LOWP: FTM_RT_NV(FTM_ROUTE_SOFTMAX_TOPK_LOWP) break;
+    default: FTM_RT_NV(FTM_ROUTE_TOPK_SOFTMAX) break;
+  }
+#undef FTM_RT_NV
+  return hipGetLastError();
+}
+
 hipError_t launch_topk(const ftm_moe_layer& L, int T, const void* logits_in, int logits_dt,
                        const int32_t* ids_in, const float* w_in, int32_t* ids_out, float* w_out,
                        float* logits_out, char* ws, const WsLayout& wl, hipStream_t st) {
@@ -2840,9 +2915,11 @@ static const char* expert_kernel_name_dt(const ftm_moe_layer& L, int T, int stag
 
 const char* stage_kernel_name(const ftm_moe_layer& L, int T, int stage) {
   switch (stage) {
-    case FTM_STAGE_ROUTER: return T >= kRouterMinT ? "k_router_rows" : "k_router";
+    case FTM_STAGE_ROUTER:
+      if (route_topk_fused(L, T)) return "k_route_topk1";
+      return T >= kRouterMinT ? "k_router_rows" : "k_router";
     case FTM_STAGE_TOPK:
-      if (lean_route_ok(L, T)) return "";  // routed inside stage A
+      if (lean_route_ok(L, T) || route_topk_fused(L, T)) return "";  // routed inside stage A / the router
       return T <= kTopk1MaxT ? "k_topk1" : T >= kTopkBlkMinT ? "k_topk_blk" : "k_topk";
     case FTM_STAGE_COMBINE: return bc_fused(L, T) ? "" : "k_combine";  // "": done by stage B
     case FTM_STAGE_W13:

@@ -175,11 +175,14 @@ def test_stage_kernel_names_follow_the_dispatch():
     # 512 tokens x top-8 = 16 pairs per expert on all 256 experts: GEMM stages
     assert name(c3, 512, nat.STAGE_W13) == "k_gemm_a_ring"
     assert name(c3, 512, nat.STAGE_W2) == "k_gemm_b"
-    assert name(c3, 16, nat.STAGE_TOPK) == "k_topk1"
+    # 3..16 tokens: router and top-k in one launch (the top-k stage launches nothing)
+    for T in (3, 16):
+        assert name(c3, T, nat.STAGE_ROUTER) == "k_route_topk1", T
+        assert name(c3, T, nat.STAGE_TOPK) == "", T
     assert name(c3, 17, nat.STAGE_TOPK) == "k_topk"
     assert name(c3, 255, nat.STAGE_TOPK) == "k_topk"
     assert name(c3, 256, nat.STAGE_TOPK) == "k_topk_blk"
-    assert name(c3, 16, nat.STAGE_ROUTER) == "k_router"
+    assert name(c3, 17, nat.STAGE_ROUTER) == "k_router"
     assert name(c3, 64, nat.STAGE_ROUTER) == "k_router_rows"
     assert name(c3, 17, nat.STAGE_COMBINE) == "k_combine"
     assert name(c3, 16, 5) is None
