@@ -142,6 +142,10 @@ EXPORTED = (
     "ftm_copy_slots",
     "ftm_lru_ensure_dev",
     "ftm_copy_slots_dev",
+    "ftm_cpu_moe_forward",
+    "ftm_cpu_moe_submit",
+    "ftm_cpu_moe_wait",
+    "ftm_cpu_avx512",
 )
 
 
@@ -205,6 +209,14 @@ def lib() -> ctypes.CDLL:
                                      vp]
     L.ftm_copy_slots_dev.restype = ctypes.c_int
     L.ftm_copy_slots_dev.argtypes = [ctypes.POINTER(FtmBankCopy), i32, i32, i32, vp, vp, vp, i32, vp]
+    L.ftm_cpu_moe_forward.restype = ctypes.c_int
+    L.ftm_cpu_moe_forward.argtypes = [P_layer, vp, i32, vp, vp, vp, i32, i32, vp]
+    L.ftm_cpu_moe_submit.restype = ctypes.c_int64
+    L.ftm_cpu_moe_submit.argtypes = [P_layer, vp, i32, vp, vp, vp, i32, vp]
+    L.ftm_cpu_moe_wait.restype = ctypes.c_int
+    L.ftm_cpu_moe_wait.argtypes = [i64]
+    L.ftm_cpu_avx512.restype = ctypes.c_int
+    L.ftm_cpu_avx512.argtypes = []
     _lib = L
     return L
 

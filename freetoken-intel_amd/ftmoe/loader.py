@@ -531,8 +531,12 @@ def bank_sources(gate_up_banks: list, down_banks: list) -> dict:
                 "scale_gate_up": [b.weight_scale_inv for b in gate_up_banks],
                 "weight_down": [b.weight for b in down_banks], "scale_down": [b.weight_scale_inv for b in down_banks]}
     if fmt == "mxfp4":
-        return {"blocks_gate_up": [b.blocks for b in gate_up_banks], "scales_gate_up": [b.scales for b in gate_up_banks],
-                "blocks_down": [b.blocks for b in down_banks], "scales_down": [b.scales for b in down_banks]}
+        src = {"blocks_gate_up": [b.blocks for b in gate_up_banks], "scales_gate_up": [b.scales for b in gate_up_banks],
+               "blocks_down": [b.blocks for b in down_banks], "scales_down": [b.scales for b in down_banks]}
+        if gate_up_banks[0].bias is not None:  # gpt-oss: per-expert biases ride in the slot like the weights
+            src["bias_gate_up"] = [b.bias for b in gate_up_banks]
+            src["bias_down"] = [b.bias for b in down_banks]
+        return src
     if fmt == "int8_channel":
         return {"weight_packed_gate_up": [b.weight_packed for b in gate_up_banks],
                 "weight_scale_gate_up": [b.weight_scale for b in gate_up_banks],
@@ -549,7 +553,7 @@ def attach_offload_cache(gate_up_banks: list, down_banks: list, *, num_experts: 
     attributes :class:`~ftmoe.moe.offload_cache.SlotWeightAccessor` refuses to
     guess (``gptq_group_size`` from the checkpoint, ``int8_k_gate_up`` /
     ``int8_k_down`` from the banks, checked equal across layers), MXFP4
-    biases as ``extra_metadata`` (``bias_gate_up`` / ``bias_down``)."""
+    biases as two more per-slot banks (``bias_gate_up`` / ``bias_down``)."""
     from .moe.offload_cache import OffloadMoeCache
 
     L = len(gate_up_banks)
@@ -575,9 +579,6 @@ def attach_offload_cache(gate_up_banks: list, down_banks: list, *, num_experts: 
         cache.int8_k_gate_up, cache.int8_k_down = ku.pop(), kd.pop()
     elif fmt == "fp8_block":
         cache.fp8_block_size = int(fp8_block)
-    elif fmt == "mxfp4" and gate_up_banks[0].bias is not None:
-        cache.set_extra_metadata("bias_gate_up", [b.bias for b in gate_up_banks])
-        cache.set_extra_metadata("bias_down", [b.bias for b in down_banks])
     return cache
 
 

@@ -42,6 +42,11 @@ _BANK_SCHEMAS: dict = {
     "gguf_kquant": ("raw_gate", "raw_up", "raw_down"),
 }
 
+# Banks a format may carry beyond its schema: the per-expert projection biases
+# of gpt-oss MXFP4 experts, one row per slot like the weights.  Not in the
+# reference, whose pool has no bias component (gpt_oss/__init__.py:46-61).
+_OPTIONAL_BANKS: dict = {"mxfp4": ("bias_gate_up", "bias_down")}
+
 # Formats whose expert math the gfx950 kernels implement.
 _COMPUTE_FORMATS = ("bf16", "gptq_int4", "fp8_block", "mxfp4", "int8_channel")
 
@@ -162,9 +167,12 @@ class OffloadMoeCache:
         """Attach the host banks (``{bank: [num_layers x [E, ...] host tensor]}``)
         and allocate one ``[cache_size, ...]`` device pool per bank.  Host banks
         are kept in pinned memory (copied there if they are not already)."""
-        if set(sources) != set(self.bank_schema):
-            raise ValueError(
-                f"banks {sorted(sources)} do not match the {self.quant_format!r} schema {self.bank_schema}")
+        base, opt = _BANK_SCHEMAS[self.quant_format], _OPTIONAL_BANKS.get(self.quant_format, ())
+        extra = set(sources) - set(base)
+        if not set(base) <= set(sources) or extra not in (set(), set(opt)):
+            raise ValueError(f"banks {sorted(sources)} do not match the {self.quant_format!r} schema {base}"
+                             + (f" (optionally with {opt})" if opt else ""))
+        self.bank_schema = base + (opt if extra else ())
         self.banks = []
         for bank in self.bank_schema:
             per_layer = sources[bank]
@@ -578,8 +586,9 @@ class SlotWeightAccessor:
             group = {"gptq_int4": getattr(self, "_group_size", None), "fp8_block": getattr(self, "_fp8_block", None),
                      "mxfp4": 32}.get(fmt)
             kd = self._int8_k_down if fmt == "int8_channel" else I
-            w13 = proj_from_bank(fmt, self._banks, which="gate_up", N=2 * I, K=H, group=group)
-            w2 = proj_from_bank(fmt, self._banks, which="down", N=H, K=kd, group=group)
+            b13, b2 = self._banks.get("bias_gate_up"), self._banks.get("bias_down")  # per slot, MXFP4 only
+            w13 = proj_from_bank(fmt, self._banks, which="gate_up", N=2 * I, K=H, group=group, bias=b13)
+            w2 = proj_from_bank(fmt, self._banks, which="down", N=H, K=kd, group=group, bias=b2)
             self._layer = MoeLayer(w13=w13, w2=w2, num_experts=w13.num_slots, hidden=H, inter=I, topk=1,
                                    act_dtype=self._dtype)
         return self._layer
@@ -704,6 +713,7 @@ def moe_offload_forward(flat: torch.Tensor, top_idx: torch.Tensor, top_w: torch.
         return acc.to(flat.dtype)
     ids_host = (top_idx if ids_host is None else ids_host).reshape(-1).to("cpu", torch.int64)
     uniq = torch.unique(ids_host)
+    uniq = uniq[uniq >= 0]  # ids < 0: pairs without an expert
     cap = cache.cache_size
     if uniq.numel() <= cap:
         cache.ensure_experts(layer_id, uniq)

@@ -332,6 +332,36 @@ int ftm_copy_slots_dev(const ftm_bank_copy* banks, int32_t num_banks, int32_t ho
                        int32_t pool_slots, const int32_t* evict_slots, const int32_t* src_rows,
                        const int32_t* num_staged, int32_t max_rows, void* stream);
 
+/* ---- the host-CPU half of the hybrid CPU || GPU split ----
+ * Routed experts of `layer` computed on the host cores from packed HOST banks
+ * (every format the GPU kernels take, decoded per element as the reference
+ * dequantizes: fp32 product, one rounding): fp32 gu, fp32 h = act(gate) * up
+ * (+ the projection biases), fp32 down projection, out[t] += w[t, j] * y, for
+ * the pairs whose expert has expert_mask[e] != 0 (expert_mask NULL = all).
+ * x [T, H] f32, topk_ids [T, k] int32, topk_w [T, k] f32, out [T, H] f32
+ * (overwritten).  Experts split into contiguous ranges over `threads` host
+ * threads (0 = hardware concurrency clamped to E) with private partial sums.
+ * The shared expert is not included.  Replaces freetoken_cpu_moe_forward_fast
+ * (python/freetoken/kernel/csrc/cpu_moe/cpu_moe.cpp:470-528, 763-786), which
+ * takes only dense fp32 / bf16 banks.  force_scalar: skip the AVX-512 path. */
+int ftm_cpu_moe_forward(const ftm_moe_layer* layer, const float* x, int32_t num_tokens,
+                        const int32_t* topk_ids, const float* topk_w, const uint8_t* expert_mask,
+                        int32_t threads, int32_t force_scalar, float* out);
+
+/* The same call on the library's persistent worker thread, one job at a time
+ * (submit waits for the previous job to be collected): returns a handle > 0
+ * (or a negative error code before anything runs); every pointer must stay
+ * valid until ftm_cpu_moe_wait(handle) returns the call's code
+ * (FTM_ERR_HANDLE for an unknown handle).  Replaces freetoken_cpu_moe_submit /
+ * _wait (cpu_moe.cpp:596-706, 820-853). */
+int64_t ftm_cpu_moe_submit(const ftm_moe_layer* layer, const float* x, int32_t num_tokens,
+                           const int32_t* topk_ids, const float* topk_w, const uint8_t* expert_mask,
+                           int32_t threads, float* out);
+int ftm_cpu_moe_wait(int64_t handle);
+
+/* 1 when the host CPU runs the AVX-512 path (freetoken_cpu_moe_avx512_available). */
+int ftm_cpu_avx512(void);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,109 @@
+"""The host-CPU expert kernel of the hybrid split (ftm_cpu_moe_forward,
+csrc/ftm_cpu.cpp) on the CPU: every bank format against the oracle (fp32 h,
+as the reference CPU backend computes it), the AVX-512 and scalar paths, one
+and several threads, expert masks, the async submit/wait worker and its
+errors, and the split rule of the reference's hybrid forward."""
+from dataclasses import replace
+
+import numpy as np
+import pytest
+import torch
+
+import ftm_oracle as O
+from ftm_helpers import np_, oracle_spec
+
+from ftmoe import _native as nat
+from ftmoe import synthetic as S
+from ftmoe.moe import hybrid as HY
+
+NAMES = ["c1_int8", "c2_gptq", "c3_fp8", "c4_mxfp4"]
+
+
+def _host(syn):
+    c = syn.cfg
+    int8_k = (c.H, c.I) if c.fmt == "int8_channel" else None
+    return HY.host_layer_from_bank(c.fmt, syn.bank, num_experts=c.E, intermediate=c.I, topk=c.k, group=c.group,
+                                   int8_k=int8_k, bias13=syn.bias13, bias2=syn.bias2, act=c.act)
+
+
+def _routing(syn, T, seed):
+    rng = np.random.RandomState(seed)
+    ids = np.stack([rng.choice(syn.cfg.E, syn.cfg.k, replace=False) for _ in range(T)]).astype(np.int32)
+    return ids, rng.rand(T, syn.cfg.k).astype(np.float32)
+
+
+def _ref(syn, x, ids, w, mask=None):
+    spec = oracle_spec(syn)
+    if mask is not None:
+        w = np.where(mask[ids] != 0, w, 0.0).astype(np.float32)
+    return O.moe_experts(spec["w13"], spec["w2"], x, ids, w, E=syn.cfg.E, act=syn.cfg.act, alpha=syn.cfg.swiglu_alpha,
+                         limit=syn.cfg.swiglu_limit, h_bf16=False, x_bf16=False)
+
+
+@pytest.mark.parametrize("name", NAMES)
+@pytest.mark.parametrize("force_scalar", [False, True])
+def test_cpu_half_matches_oracle(name, force_scalar):
+    cfg = replace(S.SMALL[name], E=6)
+    syn = S.generate(cfg, T=5, seed=500)
+    L, keep = _host(syn)
+    x = syn.x.float()
+    ids, w = _routing(syn, 5, 1)
+    got = HY.cpu_moe_forward(L, x, torch.from_numpy(ids), torch.from_numpy(w), force_scalar=force_scalar)
+    ref = _ref(syn, x.numpy(), ids, w)
+    np.testing.assert_allclose(got.numpy(), ref, rtol=2e-4, atol=2e-5 * np.abs(ref).max())
+
+
+def test_avx512_path_equals_scalar_path_closely_and_threads_agree():
+    syn = S.generate(replace(S.SMALL["c3_fp8"], E=8), T=9, seed=501)
+    L, keep = _host(syn)
+    x = syn.x.float()
+    ids, w = _routing(syn, 9, 2)
+    ids_t, w_t = torch.from_numpy(ids), torch.from_numpy(w)
+    a = HY.cpu_moe_forward(L, x, ids_t, w_t, threads=1)
+    b = HY.cpu_moe_forward(L, x, ids_t, w_t, threads=1, force_scalar=True)
+    c = HY.cpu_moe_forward(L, x, ids_t, w_t, threads=3)
+    np.testing.assert_allclose(a.numpy(), b.numpy(), rtol=1e-4, atol=1e-5)
+    np.testing.assert_allclose(a.numpy(), c.numpy(), rtol=1e-5, atol=1e-6)
+    assert torch.equal(c, HY.cpu_moe_forward(L, x, ids_t, w_t, threads=3))  # deterministic per thread count
+
+
+def test_expert_mask_and_async_worker():
+    syn = S.generate(replace(S.SMALL["c2_gptq"], E=8), T=6, seed=502)
+    L, keep = _host(syn)
+    x = syn.x.float().contiguous()
+    ids, w = _routing(syn, 6, 3)
+    mask = np.zeros(8, np.uint8)
+    mask[[1, 4, 5]] = 1
+    got = HY.cpu_moe_forward(L, x, torch.from_numpy(ids), torch.from_numpy(w), torch.from_numpy(mask))
+    ref = _ref(syn, x.numpy(), ids, w, mask)
+    np.testing.assert_allclose(got.numpy(), ref, rtol=2e-4, atol=2e-5 * np.abs(ref).max())
+    out = torch.empty_like(x)
+    job = HY.CpuJob(L, x, torch.from_numpy(ids), torch.from_numpy(w), torch.from_numpy(mask), out, keep)
+    assert torch.equal(job.result(), got)
+    with pytest.raises(RuntimeError, match="twice"):
+        job.result()
+    assert nat.lib().ftm_cpu_moe_wait(12345) == nat.ERR_HANDLE
+
+
+def test_cpu_half_argument_errors():
+    syn = S.generate(replace(S.SMALL["c3_fp8"], E=4), T=2, seed=503)
+    L, keep = _host(syn)
+    x = torch.zeros(2, syn.cfg.H)
+    ids = torch.tensor([[0, 9, 1, 2], [0, 1, 2, 3]], dtype=torch.int32)[:, :syn.cfg.k]
+    w = torch.ones(2, syn.cfg.k)
+    with pytest.raises(nat.FtmError, match="code -2"):
+        HY.cpu_moe_forward(L, x, ids, w)  # an id >= E
+    assert nat.lib().ftm_cpu_moe_forward(None, None, 0, None, None, None, 0, 0, None) == nat.ERR_NULL
+
+
+def test_split_rule_matches_the_reference():
+    """qwen3_moe/__init__.py:733-752: n distinct experts, n_fetch = round(n f)
+    clamped to [1, n - 1] and max_fetch, the CPU takes the lowest ids."""
+    ids = torch.tensor([[7, 3, 9], [3, 1, 12]])
+    assert HY.split_experts(ids, 0.5) == {1, 3, 7}       # n = 5: round(2.5) = 2 fetched (half to even), 3 on the CPU
+    assert HY.split_experts(ids, 0.3) == {1, 3, 7}       # round(1.5) = 2 fetched
+    assert HY.split_experts(ids, 0.99) == {1}            # n_fetch clamped to n - 1
+    assert HY.split_experts(ids, 0.01) == {1, 3, 7, 9}   # at least one fetched
+    assert HY.split_experts(ids, 0.8, max_fetch=1) == {1, 3, 7, 9}
+    assert HY.split_experts(ids, 1.0) is None and HY.split_experts(ids, 0.0) is None
+    assert HY.split_experts(torch.tensor([[4, -1]]), 0.5) is None  # one expert: nothing to split

@@ -40,7 +40,10 @@ def test_checkpoint_banks_round_trip(tmp_path, name):
     assert len(gu) == len(dn) == 2
     for layer, syn in enumerate(syns):
         src = LD.bank_sources([gu[layer]], [dn[layer]])
-        assert set(src) == set(syn.bank)
+        bias = {"bias_gate_up": syn.bias13, "bias_down": syn.bias2} if fmt == "mxfp4" else {}
+        assert set(src) == set(syn.bank) | set(bias)
+        for k, v in bias.items():
+            assert torch.equal(src.pop(k)[0], v)
         for k, v in src.items():
             assert v[0].dtype == syn.bank[k].dtype and torch.equal(v[0].view(torch.uint8), syn.bank[k].view(torch.uint8)), k
         if fmt == "mxfp4":
@@ -171,13 +174,14 @@ def test_attach_offload_cache_wires_the_slot_api(tmp_path, name):
     gs = LD.checkpoint_gptq_group_size(str(tmp_path)) if fmt == "gptq_int4" else None
     c = LD.attach_offload_cache(gu, dn, num_experts=4, device="cpu", gptq_group_size=gs)
     assert c.quant_format == fmt and c.cache_size == 4 + 2
-    assert set(c.bank_schema) == set(syns[0].bank)
+    assert set(c.bank_schema) == set(syns[0].bank) | ({"bias_gate_up", "bias_down"} if fmt == "mxfp4" else set())
     if fmt == "gptq_int4":
         assert c.gptq_group_size == 128 and len(c.get_extra_metadata("g_idx_down", 1)) == syns[0].cfg.I
     if fmt == "int8_channel":
         assert (c.int8_k_gate_up, c.int8_k_down) == (syns[0].cfg.H, syns[0].cfg.I)
     if fmt == "mxfp4":
-        assert torch.equal(c.get_extra_metadata("bias_gate_up", 1), syns[1].bias13)
+        assert torch.equal(c.bank_sources["bias_gate_up"][1], syns[1].bias13)
+        assert c.bank_caches["bias_down"].shape == (c.cache_size, syns[0].cfg.H)
     if fmt == "gptq_int4":
         with pytest.raises(ValueError, match="group_size"):
             LD.attach_offload_cache(gu, dn, num_experts=4, device="cpu")
