@@ -88,8 +88,14 @@ float e4m3_f(uint32_t b) {
 }
 float e5m2_f(uint32_t b) { return f16_f((uint16_t)(b << 8)); }
 const float kE2M1[16] = {0.f, .5f, 1.f, 1.5f, 2.f, 3.f, 4.f, 6.f, -0.f, -.5f, -1.f, -1.5f, -2.f, -3.f, -4.f, -6.f};
-// e8m0 as the reference decodes it (torch.exp2(e - 127)): 255 -> inf
-float e8m0_f(uint32_t e) { return ldexpf(1.0f, (int)e - 127); }
+// e8m0 as the reference decodes it (torch.exp2(e - 127)): the fp32 with
+// exponent field e; 0 -> 2^-127 (subnormal), 255 -> inf
+inline float e8m0_f(uint32_t e) {
+  const uint32_t u = e == 0 ? 0x00400000u : e == 255 ? 0x7f800000u : e << 23;
+  float f;
+  memcpy(&f, &u, 4);
+  return f;
+}
 
 struct Slot {  // one slot of a projection bank, host pointers
   const char *w, *s, *z, *bias;
@@ -166,132 +172,212 @@ void proj_scalar(const Slot& W, const float* x, int ldx, int M, float* y, int ld
   }
 }
 
-__attribute__((target("avx512f,avx512bw,avx512vl,avx512dq"))) __m512 e4m3x16(__m128i v8, bool e5m2) {
-  const __m512i v = _mm512_cvtepu8_epi32(v8);
-  if (e5m2) {  // the high byte of an fp16: convert through the fp16 path
-    const __m256i h = _mm512_cvtepi32_epi16(_mm512_slli_epi32(v, 8));
-    return _mm512_cvtph_ps(h);
-  }
-  const __m512i sign = _mm512_slli_epi32(_mm512_and_si512(v, _mm512_set1_epi32(0x80)), 24);
-  const __m512i e = _mm512_and_si512(_mm512_srli_epi32(v, 3), _mm512_set1_epi32(15));
-  const __m512i m = _mm512_and_si512(v, _mm512_set1_epi32(7));
-  __m512i bits = _mm512_or_si512(_mm512_slli_epi32(_mm512_add_epi32(e, _mm512_set1_epi32(120)), 23),
-                                 _mm512_slli_epi32(m, 20));
-  const __mmask16 sub = _mm512_cmpeq_epi32_mask(e, _mm512_setzero_si512());
-  const __m512 subf = _mm512_mul_ps(_mm512_cvtepi32_ps(m), _mm512_set1_ps(0x1p-9f));
-  bits = _mm512_mask_mov_epi32(bits, sub, _mm512_castps_si512(subf));
-  const __mmask16 nan = _mm512_cmpeq_epi32_mask(_mm512_and_si512(v, _mm512_set1_epi32(0x7f)), _mm512_set1_epi32(0x7f));
-  bits = _mm512_mask_mov_epi32(bits, nan, _mm512_set1_epi32(0x7fc00000));
-  return _mm512_castsi512_ps(_mm512_or_si512(bits, sign));
-}
+#define FTM_AVX512 __attribute__((target("avx512f,avx512bw,avx512vl,avx512dq")))
 
-// 16 weights [k0, k0 + 16) of K-major row n, dequantized (k0 % 16 == 0, k0 + 16 <= K).
-__attribute__((target("avx512f,avx512bw,avx512vl,avx512dq"))) __m512 row16(const Slot& W, int n, int k0) {
-  const int K = W.K;
-  switch (W.fmt) {
-    case FTM_FMT_FP8_BLOCK:
-    case FTM_FMT_FP8_E5M2_BLOCK: {
-      const __m128i b = _mm_loadu_si128((const __m128i*)(W.w + (int64_t)n * K + k0));
-      const int nkb = (K + W.group - 1) / W.group;
-      const float s = load_dt(W.s, (int64_t)(n / W.group) * nkb + k0 / W.group, W.s_dt);
-      return _mm512_mul_ps(e4m3x16(b, W.fmt == FTM_FMT_FP8_E5M2_BLOCK), _mm512_set1_ps(s));
-    }
-    case FTM_FMT_INT8_PACKED: {
-      const __m128i b = _mm_loadu_si128((const __m128i*)(W.w + (int64_t)n * K + k0));
-      const __m512i v = _mm512_sub_epi32(_mm512_cvtepu8_epi32(b), _mm512_set1_epi32(128));
-      const float s = load_dt(W.s, (int64_t)n * (K / W.group) + k0 / W.group, W.s_dt);
-      return _mm512_mul_ps(_mm512_cvtepi32_ps(v), _mm512_set1_ps(s));
-    }
-    case FTM_FMT_MXFP4: {
-      // 8 bytes hold elements k0 .. k0 + 15, low nibble first
-      uint64_t b8;
-      memcpy(&b8, W.w + (int64_t)n * (K / 2) + k0 / 2, 8);
-      const __m512i bytes = _mm512_cvtepu8_epi32(_mm_set_epi64x(0, (long long)b8));  // byte j in lane j (j < 8)
-      const __m512i idx = _mm512_set_epi32(7, 7, 6, 6, 5, 5, 4, 4, 3, 3, 2, 2, 1, 1, 0, 0);
-      const __m512i pair = _mm512_permutexvar_epi32(idx, bytes);
-      const __m512i shift = _mm512_set_epi32(4, 0, 4, 0, 4, 0, 4, 0, 4, 0, 4, 0, 4, 0, 4, 0);
-      const __m512i nib = _mm512_and_si512(_mm512_srlv_epi32(pair, shift), _mm512_set1_epi32(15));
-      const __m512 lut = _mm512_loadu_ps(kE2M1);
-      const float s = e8m0_f((uint8_t)W.s[(int64_t)n * (K / 32) + k0 / 32]);
-      return _mm512_mul_ps(_mm512_permutexvar_ps(nib, lut), _mm512_set1_ps(s));
-    }
-    case FTM_FMT_FP32:
-      return _mm512_loadu_ps((const float*)W.w + (int64_t)n * K + k0);
-    default: {  // bf16
-      const __m256i h = _mm256_loadu_si256((const __m256i*)((const uint16_t*)W.w + (int64_t)n * K + k0));
-      return _mm512_castsi512_ps(_mm512_slli_epi32(_mm512_cvtepu16_epi32(h), 16));
-    }
+// K-major formats of the vector path
+enum KFmt { kE4M3, kE5M2, kI8, kFP4, kF32, kBF16 };
+
+// 16 weights [k, k + 16) of one K-major row, before the group scale.  E4M3
+// comes out as value * 2^-8: its byte, widened to 16 bits as s.eeee.mmm <<
+// 7, is the fp16 of value * 2^-8 (normals and subnormals alike), and the
+// scale factor carries the 2^8; 0x7f / 0xff (NaN) are patched.  E5M2 is the
+// high byte of an fp16.  INT8 offset-binary: b ^ 0x80 is b - 128 as int8.
+template <int F>
+FTM_AVX512 inline __m512 dec16(const char* row, int k) {
+  if constexpr (F == kE4M3) {
+    const __m256i b = _mm256_cvtepu8_epi16(_mm_loadu_si128((const __m128i*)(row + k)));
+    const __m256i mag = _mm256_and_si256(b, _mm256_set1_epi16(0x7f));
+    const __m256i h = _mm256_or_si256(_mm256_slli_epi16(_mm256_and_si256(b, _mm256_set1_epi16(0x80)), 8),
+                                      _mm256_slli_epi16(mag, 7));
+    const __mmask16 nan = _mm256_cmpeq_epi16_mask(mag, _mm256_set1_epi16(0x7f));
+    return _mm512_mask_mov_ps(_mm512_cvtph_ps(h), nan, _mm512_set1_ps(__builtin_nanf("")));
+  } else if constexpr (F == kE5M2) {
+    const __m256i b = _mm256_cvtepu8_epi16(_mm_loadu_si128((const __m128i*)(row + k)));
+    return _mm512_cvtph_ps(_mm256_slli_epi16(b, 8));
+  } else if constexpr (F == kI8) {
+    const __m128i b = _mm_xor_si128(_mm_loadu_si128((const __m128i*)(row + k)), _mm_set1_epi8((char)0x80));
+    return _mm512_cvtepi32_ps(_mm512_cvtepi8_epi32(b));
+  } else if constexpr (F == kFP4) {
+    // 8 bytes hold elements k .. k + 15, low nibble first
+    uint64_t b8;
+    memcpy(&b8, row + k / 2, 8);
+    const __m512i bytes = _mm512_cvtepu8_epi32(_mm_set_epi64x(0, (long long)b8));
+    const __m512i pair = _mm512_permutexvar_epi32(_mm512_set_epi32(7, 7, 6, 6, 5, 5, 4, 4, 3, 3, 2, 2, 1, 1, 0, 0), bytes);
+    const __m512i nib = _mm512_and_si512(
+        _mm512_srlv_epi32(pair, _mm512_set_epi32(4, 0, 4, 0, 4, 0, 4, 0, 4, 0, 4, 0, 4, 0, 4, 0)), _mm512_set1_epi32(15));
+    return _mm512_permutexvar_ps(nib, _mm512_loadu_ps(kE2M1));
+  } else if constexpr (F == kF32) {
+    return _mm512_loadu_ps((const float*)row + k);
+  } else {
+    const __m256i h = _mm256_loadu_si256((const __m256i*)((const uint16_t*)row + k));
+    return _mm512_castsi512_ps(_mm512_slli_epi32(_mm512_cvtepu16_epi32(h), 16));
   }
 }
 
-// K-major projection, AVX-512: tokens in blocks of up to 8 share each decoded vector.
-__attribute__((target("avx512f,avx512bw,avx512vl,avx512dq"))) void proj_kmajor_avx512(const Slot& W, const float* x,
-                                                                                     int ldx, int M, float* y,
-                                                                                     int ldy) {
+template <int F>
+constexpr int row_bytes(int K) {
+  return F == kFP4 ? K / 2 : F == kF32 ? 4 * K : F == kBF16 ? 2 * K : K;
+}
+
+// The group scale of row n at column k (1 for the unscaled formats).
+template <int F>
+inline float group_scale(const Slot& W, int n, int k) {
+  if constexpr (F == kE4M3 || F == kE5M2) {
+    const int nkb = (W.K + W.group - 1) / W.group;
+    return load_dt(W.s, (int64_t)(n / W.group) * nkb + k / W.group, W.s_dt);
+  } else if constexpr (F == kI8) {
+    return load_dt(W.s, (int64_t)n * (W.K / W.group) + k / W.group, W.s_dt);
+  } else if constexpr (F == kFP4) {
+    return e8m0_f((uint8_t)W.s[(int64_t)n * (W.K / 32) + k / 32]);
+  } else {
+    return 1.0f;
+  }
+}
+
+// Rows [n0, n0 + R) for tokens [t0, t0 + tm), tm <= TB: R x TB accumulators,
+// each decoded vector shared by the block's tokens, scales hoisted per group.
+// Each weight is the reference's fp32 product value * scale rounded once;
+// an E4M3 group whose scale times 2^8 could leave the exact range takes the
+// two-multiply form.
+template <int F, int R, int TB>
+FTM_AVX512 void kmajor_rows(const Slot& W, int n0, const float* x, int ldx, int t0, int tm, float* y, int ldy) {
   const int K = W.K, K16 = K / 16 * 16;
-  for (int n = 0; n < W.N; ++n) {
+  constexpr bool scaled = F == kE4M3 || F == kE5M2 || F == kI8 || F == kFP4;
+  const int GS = F == kFP4 ? 32 : scaled ? W.group : K16;
+  const char* rows[R];
+  for (int r = 0; r < R; ++r) rows[r] = W.w + (int64_t)(n0 + r) * row_bytes<F>(K);
+  const float* xr[TB];
+  for (int i = 0; i < TB; ++i) xr[i] = x + (int64_t)(t0 + (i < tm ? i : 0)) * ldx;
+  __m512 acc[R][TB];
+  for (int r = 0; r < R; ++r)
+    for (int i = 0; i < TB; ++i) acc[r][i] = _mm512_setzero_ps();
+  for (int g0 = 0; g0 < K16; g0 += GS) {
+    const int g1 = std::min(g0 + GS, K16);
+    __m512 sv[R];
+    bool wide = false;
+    for (int r = 0; r < R; ++r) {
+      float s = group_scale<F>(W, n0 + r, g0);
+      if constexpr (F == kE4M3) {
+        wide |= !(fabsf(s) < 0x1p100f);
+        s *= 256.0f;
+      }
+      sv[r] = _mm512_set1_ps(s);
+    }
+    if (F == kE4M3 && wide) {
+      for (int r = 0; r < R; ++r) sv[r] = _mm512_set1_ps(group_scale<F>(W, n0 + r, g0));
+      for (int k = g0; k < g1; k += 16)
+        for (int r = 0; r < R; ++r) {
+          const __m512 w = _mm512_mul_ps(_mm512_mul_ps(dec16<F>(rows[r], k), _mm512_set1_ps(256.0f)), sv[r]);
+          for (int i = 0; i < TB; ++i)
+            if (i < tm) acc[r][i] = _mm512_fmadd_ps(_mm512_loadu_ps(xr[i] + k), w, acc[r][i]);
+        }
+      continue;
+    }
+    for (int k = g0; k < g1; k += 16) {
+      __m512 xv[TB];
+      for (int i = 0; i < TB; ++i) xv[i] = _mm512_loadu_ps(xr[i] + k);
+      for (int r = 0; r < R; ++r) {
+        __m512 w = dec16<F>(rows[r], k);
+        if constexpr (scaled) w = _mm512_mul_ps(w, sv[r]);
+        for (int i = 0; i < TB; ++i)
+          if (i < tm) acc[r][i] = _mm512_fmadd_ps(xv[i], w, acc[r][i]);
+      }
+    }
+  }
+  for (int r = 0; r < R; ++r) {
+    const int n = n0 + r;
     const float b = W.bias ? load_dt(W.bias, n, W.bias_dt) : 0.0f;
-    for (int t0 = 0; t0 < M; t0 += 8) {
-      const int tm = std::min(8, M - t0);
-      __m512 acc[8];
-      for (int i = 0; i < 8; ++i) acc[i] = _mm512_setzero_ps();
-      for (int k = 0; k < K16; k += 16) {
-        const __m512 w = row16(W, n, k);
-        for (int i = 0; i < tm; ++i)
-          acc[i] = _mm512_fmadd_ps(_mm512_loadu_ps(x + (int64_t)(t0 + i) * ldx + k), w, acc[i]);
-      }
-      for (int i = 0; i < tm; ++i) {
-        float s = _mm512_reduce_add_ps(acc[i]);
-        for (int k = K16; k < K; ++k) s = fmaf(x[(int64_t)(t0 + i) * ldx + k], deq(W, n, k), s);
-        y[(int64_t)(t0 + i) * ldy + n] = s + b;
-      }
+    for (int i = 0; i < tm; ++i) {
+      float s = _mm512_reduce_add_ps(acc[r][i]);
+      for (int k = K16; k < K; ++k) s = fmaf(xr[i][k], deq(W, n, k), s);
+      y[(int64_t)(t0 + i) * ldy + n] = s + b;
     }
   }
 }
 
-// GPTQ, AVX-512: 16 output columns per block, each packed row's 8 K values
-// broadcast against them (N % 16 == 0 here; else the scalar path).
-__attribute__((target("avx512f,avx512bw,avx512vl,avx512dq"))) void proj_gptq_avx512(const Slot& W, const float* x,
-                                                                                   int ldx, int M, float* y,
-                                                                                   int ldy) {
+// K-major projection: blocks of rows (4 for one or two tokens, 2 for up to
+// four, else 1) against blocks of up to 8 tokens, so a decode step keeps
+// several independent FMA chains in flight.
+template <int F>
+FTM_AVX512 void kmajor(const Slot& W, const float* x, int ldx, int M, float* y, int ldy) {
+  const int N = W.N;
+  int n = 0;
+  if (M <= 2) {
+    for (; n + 4 <= N; n += 4) {
+      if (M == 1)
+        kmajor_rows<F, 4, 1>(W, n, x, ldx, 0, 1, y, ldy);
+      else
+        kmajor_rows<F, 4, 2>(W, n, x, ldx, 0, 2, y, ldy);
+    }
+  } else if (M <= 4) {
+    for (; n + 2 <= N; n += 2) kmajor_rows<F, 2, 4>(W, n, x, ldx, 0, M, y, ldy);
+  }
+  for (; n < N; ++n)
+    for (int t0 = 0; t0 < M; t0 += 8) kmajor_rows<F, 1, 8>(W, n, x, ldx, t0, std::min(8, M - t0), y, ldy);
+}
+
+FTM_AVX512 void proj_kmajor_avx512(const Slot& W, const float* x, int ldx, int M, float* y, int ldy) {
+  switch (W.fmt) {
+    case FTM_FMT_FP8_BLOCK: return kmajor<kE4M3>(W, x, ldx, M, y, ldy);
+    case FTM_FMT_FP8_E5M2_BLOCK: return kmajor<kE5M2>(W, x, ldx, M, y, ldy);
+    case FTM_FMT_INT8_PACKED: return kmajor<kI8>(W, x, ldx, M, y, ldy);
+    case FTM_FMT_MXFP4: return kmajor<kFP4>(W, x, ldx, M, y, ldy);
+    case FTM_FMT_FP32: return kmajor<kF32>(W, x, ldx, M, y, ldy);
+    default: return kmajor<kBF16>(W, x, ldx, M, y, ldy);
+  }
+}
+
+// GPTQ, AVX-512 (N % 16 == 0, K % 8 == 0, group % 8 == 0; else the scalar
+// path).  qweight is [K/8, N] with N contiguous, so the walk is row by row of
+// packed words across all N columns -- one contiguous stream -- with the
+// accumulators of up to two tokens in the output rows (L1-resident) and each
+// group's scales and zero points unpacked once into fp32 rows.
+FTM_AVX512 void proj_gptq_avx512(const Slot& W, const float* x, int ldx, int M, float* y, int ldy) {
   const int N = W.N, K = W.K, G = W.group;
   const uint32_t* qw = (const uint32_t*)W.w;
   const uint32_t* qz = (const uint32_t*)W.z;
-  for (int n0 = 0; n0 < N; n0 += 16) {
-    for (int t0 = 0; t0 < M; t0 += 8) {
-      const int tm = std::min(8, M - t0);
-      __m512 acc[8];
-      for (int i = 0; i < 8; ++i) acc[i] = _mm512_setzero_ps();
-      __m512 s = _mm512_setzero_ps(), zp = _mm512_setzero_ps();
-      for (int kk = 0; kk < K / 8; ++kk) {
-        const int k = 8 * kk;
-        if (k % G == 0) {  // this group's scales and zero points (zero stored minus one)
-          const int g = k / G;
-          float sv[16], zv[16];
-          for (int c = 0; c < 16; ++c) {
-            const int n = n0 + c;
-            sv[c] = load_dt(W.s, (int64_t)g * N + n, W.s_dt);
-            zv[c] = (float)((int)((qz[(int64_t)g * (N / 8) + n / 8] >> (4 * (n & 7))) & 15u) + 1);
-          }
-          s = _mm512_loadu_ps(sv);
-          zp = _mm512_loadu_ps(zv);
-        }
-        const __m512i word = _mm512_loadu_si512((const void*)(qw + (int64_t)kk * N + n0));
-        for (int j = 0; j < 8; ++j) {
-          const __m512i q = _mm512_and_si512(_mm512_srli_epi32(word, 4 * j), _mm512_set1_epi32(15));
-          // s * (q - (z + 1)): the integer difference is exact in fp32, one rounding
-          const __m512 w = _mm512_mul_ps(s, _mm512_sub_ps(_mm512_cvtepi32_ps(q), zp));
-          for (int i = 0; i < tm; ++i)
-            acc[i] = _mm512_fmadd_ps(_mm512_set1_ps(x[(int64_t)(t0 + i) * ldx + k + j]), w, acc[i]);
-        }
+  std::vector<float> sbuf((size_t)N), zbuf((size_t)N);
+  for (int t0 = 0; t0 < M; t0 += 2) {
+    const int tm = std::min(2, M - t0);
+    float* y0 = y + (int64_t)t0 * ldy;
+    float* y1 = y + (int64_t)(t0 + tm - 1) * ldy;  // == y0 for one token
+    const float* x0 = x + (int64_t)t0 * ldx;
+    const float* x1 = x + (int64_t)(t0 + tm - 1) * ldx;
+    memset(y0, 0, sizeof(float) * N);
+    if (tm == 2) memset(y1, 0, sizeof(float) * N);
+    for (int g0 = 0; g0 < K; g0 += G) {
+      const int g = g0 / G, g1 = std::min(g0 + G, K);
+      for (int n = 0; n < N; ++n) {  // zero stored minus one
+        sbuf[(size_t)n] = load_dt(W.s, (int64_t)g * N + n, W.s_dt);
+        zbuf[(size_t)n] = (float)((int)((qz[(int64_t)g * (N / 8) + n / 8] >> (4 * (n & 7))) & 15u) + 1);
       }
-      for (int i = 0; i < tm; ++i) {
-        float* yr = y + (int64_t)(t0 + i) * ldy + n0;
-        _mm512_storeu_ps(yr, acc[i]);
-        if (W.bias)
-          for (int c = 0; c < 16; ++c) yr[c] += load_dt(W.bias, n0 + c, W.bias_dt);
+      for (int k = g0; k < g1; k += 8) {
+        const uint32_t* row = qw + (int64_t)(k / 8) * N;
+        __m512 xb0[8], xb1[8];
+        for (int j = 0; j < 8; ++j) {
+          xb0[j] = _mm512_set1_ps(x0[k + j]);
+          xb1[j] = _mm512_set1_ps(x1[k + j]);
+        }
+        for (int n0 = 0; n0 < N; n0 += 16) {
+          const __m512i word = _mm512_loadu_si512((const void*)(row + n0));
+          const __m512 s = _mm512_loadu_ps(&sbuf[(size_t)n0]), zp = _mm512_loadu_ps(&zbuf[(size_t)n0]);
+          __m512 a0 = _mm512_loadu_ps(y0 + n0), a1 = _mm512_loadu_ps(y1 + n0);
+#pragma GCC unroll 8
+          for (int j = 0; j < 8; ++j) {
+            const __m512i q = _mm512_and_si512(_mm512_srli_epi32(word, 4 * j), _mm512_set1_epi32(15));
+            // s * (q - (z + 1)): the integer difference is exact in fp32, one rounding
+            const __m512 w = _mm512_mul_ps(s, _mm512_sub_ps(_mm512_cvtepi32_ps(q), zp));
+            a0 = _mm512_fmadd_ps(xb0[j], w, a0);
+            if (tm == 2) a1 = _mm512_fmadd_ps(xb1[j], w, a1);
+          }
+          _mm512_storeu_ps(y0 + n0, a0);
+          if (tm == 2) _mm512_storeu_ps(y1 + n0, a1);
+        }
       }
     }
+    if (W.bias)
+      for (int i = 0; i < tm; ++i)
+        for (int n = 0; n < N; ++n) y[(int64_t)(t0 + i) * ldy + n] += load_dt(W.bias, n, W.bias_dt);
   }
 }
 

@@ -90,11 +90,18 @@ class MoeBlock:
         cache, layer_id: a slot pool (:class:`OffloadMoeCache`) holding this
             block's experts as MoE layer ``layer_id``.
         intermediate: the routed experts' intermediate size.
+        hybrid_fetch_fraction: slot-pool blocks only -- with ``0 < f < 1`` each
+            step splits its routed experts between the host CPU and the GPU
+            (:func:`~ftmoe.moe.hybrid.moe_hybrid_forward`, the reference's
+            ``hybrid`` backend); ``"auto"`` takes ``f`` from this GPU's
+            calibration profile when it recommends ``hybrid`` for the pool's
+            format (:mod:`ftmoe.moe.bench_profile`); ``None`` = pure offload.
     """
 
     def __init__(self, *, gate, top_k: int, intermediate: int, renormalize: bool = True, softmax_fp32: bool = True,
                  shared: Optional[tuple] = None, w13=None, w2=None, cache: Optional[OffloadMoeCache] = None,
-                 layer_id: int = 0, act: str = "silu", dtype: torch.dtype = torch.bfloat16) -> None:
+                 layer_id: int = 0, act: str = "silu", dtype: torch.dtype = torch.bfloat16,
+                 hybrid_fetch_fraction=None) -> None:
         if (cache is None) == (w13 is None or w2 is None):
             raise ValueError("MoeBlock needs either in-HBM banks (w13, w2) or a slot pool (cache)")
         self.gate_w = _t(gate).detach().to(dtype).contiguous()
@@ -106,6 +113,15 @@ class MoeBlock:
             gp, up, dp, sg = (_t(m).detach().to(dtype) for m in shared)
             self.shared = {"w13": torch.cat([gp, up], dim=0).contiguous(), "w2": dp.contiguous(),
                            "gate": sg.reshape(1, -1).contiguous()}
+        if hybrid_fetch_fraction == "auto" and cache is not None:
+            from .moe.bench_profile import load_backend_recommendation, load_hybrid_fetch_fraction
+
+            fmt = cache.quant_format
+            hybrid_fetch_fraction = (load_hybrid_fetch_fraction(fmt)
+                                     if load_backend_recommendation(fmt) == "hybrid" else None)
+        elif hybrid_fetch_fraction is not None and cache is None:
+            raise ValueError("hybrid_fetch_fraction applies to slot-pool blocks (cache=...) only")
+        self.hybrid_fetch_fraction = None if hybrid_fetch_fraction is None else float(hybrid_fetch_fraction)
         mode = "softmax_topk" if softmax_fp32 else "softmax_topk_lowp"
         if cache is None:
             self.layer = MoeLayer(w13=w13, w2=w2, num_experts=self.num_experts, hidden=self.hidden,
@@ -127,6 +143,12 @@ class MoeBlock:
         if self.cache is None:
             return self.layer.forward(flat).view(shape)
         ids, w, _ = self.router.route(flat)
+        f = self.hybrid_fetch_fraction
+        if f is not None and 0.0 < f < 1.0:
+            from .moe.hybrid import moe_hybrid_forward
+
+            return moe_hybrid_forward(flat, ids, w, self.cache, self.layer_id, intermediate=self.intermediate,
+                                      fetch_fraction=f, act=self.act, shared=self.shared).view(shape)
         out = moe_offload_forward(flat, ids, w, self.cache, self.layer_id, intermediate=self.intermediate,
                                   act=self.act, shared=self.shared)
         return out.view(shape)
