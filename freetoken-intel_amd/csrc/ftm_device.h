@@ -801,8 +801,12 @@ __device__ __forceinline__ void rows_issue(const ProjSlot& W, const RowGeom<FMT>
 
 // rows_consume_lds: the MFMAs of NT row tiles at once, activations from LDS.  xs
 // holds the current block's token rows from element k0 on (bf16, `pitch`
-// elements apart, nb of them); lane l feeds token row l % 16 of the MFMA and
-// rows >= nb read as zero.  Each activation read feeds all NT tiles' MFMAs.
+// elements apart, nb of them) and, as row zr, a row of zeros at least as long
+// as the wave's range; lane l feeds token row l % 16 of the MFMA, and rows >=
+// nb as well as lanes whose K position is out of range read the zero row, so
+// one address select per wave-load replaces a select per activation register
+// and the reads of a wave-load use immediate offsets.  Each activation read
+// feeds all NT tiles' MFMAs.
 // Post-scaled formats accumulate each quantisation group in its own register
 // (LPG wave-loads per group, the window starting on a group boundary, or the
 // whole window inside one group when LPG == NLW) and apply the scales once at
@@ -810,7 +814,7 @@ __device__ __forceinline__ void rows_issue(const ProjSlot& W, const RowGeom<FMT>
 template <int FMT, int NLW, int NT, int LPG, bool PAIRED>
 __device__ __forceinline__ void rows_consume_lds(const ProjSlot& W, const RowGeom<FMT> (&G)[NT], int Lw, int L_hi,
                                                  const RowStream<FMT, NLW> (&S)[NT], const uint16_t* xs, int k0,
-                                                 int pitch, int nb, f32x4 (&acc)[NT]) {
+                                                 int pitch, int nb, int zr, f32x4 (&acc)[NT]) {
   using F = KMajor<FMT>;
   static_assert(NLW % LPG == 0, "groups tile the window");
   const int lane = threadIdx.x & 63;
@@ -818,9 +822,8 @@ __device__ __forceinline__ void rows_consume_lds(const ProjSlot& W, const RowGeo
   const int m = lane & 15;
   const bool upper = m >= 8;
   const int K = W.K;
-  const bool mok = m < nb;
-  const uint16_t* xrow = xs + (mok ? m : 0) * pitch;
-  const u32x4 zero = (u32x4){0u, 0u, 0u, 0u};
+  const uint16_t* zrow = xs + zr * pitch;
+  const int rbase = (m < nb ? m : zr) * pitch - k0;  // lane's row, element kk at rbase + kk
   constexpr int NP = F::kPostScale ? NLW / LPG : 1;
   f32x4 part[NT][NP];
 #pragma unroll
@@ -831,11 +834,10 @@ __device__ __forceinline__ void rows_consume_lds(const ProjSlot& W, const RowGeo
   for (int b = 0; b < NLW; ++b) {
     const int L = Lw + b;
     const int kk = L * F::kLoadK + F::kLaneK * g;
-    const bool ok = mok && (L < L_hi) && (kk < K);
+    const uint16_t* xb = (L < L_hi) && (kk < K) ? xs + (rbase + kk) : zrow;
 #pragma unroll
     for (int q = 0; q < F::kMfma; ++q) {
-      const u32x4 xa = *(const u32x4*)(xrow + (ok ? kk + 8 * q - k0 : 0));
-      const u32x4 av = ok ? xa : zero;
+      const u32x4 av = *(const u32x4*)(xb + 8 * q);
 #pragma unroll
       for (int t = 0; t < NT; ++t) {
         const u32x4 r = S[t].raw[b];

@@ -1523,9 +1523,11 @@ __global__ __launch_bounds__(kBlock) void k_stage_b(const LayerArgs a) {
 // order) but hold no registers and depend on nothing the weights wait for,
 // so the whole dependent chain (expert table -> token list -> activations)
 // overlaps the weight latency.  The MFMAs read the activations from LDS right
-// where they are used.  Tokens are taken kXT at a time (MFMA rows kXT..15
-// read zero).
+// where they are used.  Tokens are taken kXT at a time; each wave's region
+// holds kXT token rows and a zero row (index kXT) that MFMA rows kXT..15 and
+// out-of-range lanes read.
 constexpr int kXT = 4;
+constexpr int kXR = kXT + 1;  // LDS rows per wave region
 // Dynamic LDS a launch may ask for without raising the kernel's attribute.
 constexpr int kDynLdsMax = 65536;
 extern __shared__ __align__(16) uint16_t ftm_xl_lds[];
@@ -1536,6 +1538,12 @@ extern __shared__ __align__(16) uint16_t ftm_xl_lds[];
 // 64 or 128).
 __host__ __device__ __forceinline__ int xl_pitch(int K, int split) {
   return ((K + 127) / 128 + split - 1) / split * 128 + 8;
+}
+
+// Zero row kXT of a wave's region (the whole pitch; only this wave reads it).
+__device__ __forceinline__ void xl_zero_row(uint16_t* xw, int pitch) {
+  const int lane = threadIdx.x & 63;
+  for (int e = 8 * lane; e < pitch; e += 8 * 64) *(u32x4*)(xw + kXT * pitch + e) = (u32x4){0u, 0u, 0u, 0u};
 }
 
 // Work record of routed expert u (see kRecWords).
@@ -1618,7 +1626,8 @@ __device__ void stage_a_xl_body(const LayerArgs& a, const ProjSlot& W, int Iu, i
     rows_issue<EFMT, kRowsNLW, true>(W, G[t], L_lo, L_hi, S[t]);
   }
   const int pitch = xl_pitch(H, KS);
-  uint16_t* xw = ftm_xl_lds + kp * kXT * pitch;
+  uint16_t* xw = ftm_xl_lds + kp * kXR * pitch;
+  xl_zero_row(xw, pitch);
   const int k0 = L_lo * F::kLoadK, k1 = min(L_hi * F::kLoadK, W.K);
   float bg[NT], bu[NT];
 #pragma unroll
@@ -1645,7 +1654,7 @@ __device__ void stage_a_xl_body(const LayerArgs& a, const ProjSlot& W, int Iu, i
         for (int t = 0; t < NT; ++t) rows_issue<EFMT, kRowsNLW, true>(W, G[t], Lw, L_hi, S[t]);
       }
       __builtin_amdgcn_s_waitcnt(0);  // weights and this wave's LDS copy have landed
-      rows_consume_lds<EFMT, kRowsNLW, NT, LPG, true>(W, G, Lw, L_hi, S, xw, k0, pitch, nb, acc);
+      rows_consume_lds<EFMT, kRowsNLW, NT, LPG, true>(W, G, Lw, L_hi, S, xw, k0, pitch, nb, kXT, acc);
     }
     // MFMA rows 0..kXT-1 (the block's tokens) live in lanes 0..15
     if (lane < 16) {
@@ -1722,7 +1731,8 @@ __device__ void stage_b_ks_body(const LayerArgs& a, const ProjSlot& W, int c0, i
   G[0] = RowGeom<EFMT>(W, c0 + n, W.group > 0 ? c0 / W.group : 0, W.group > 0 ? (c0 + 8) / W.group : 0);
   rows_issue<EFMT, kRowsNLW, true>(W, G[0], L_lo, L_hi, S[0]);
   const int pitch = xl_pitch(a.Imax, KS);
-  uint16_t* xw = ftm_xl_lds + kp * kXT * pitch;
+  uint16_t* xw = ftm_xl_lds + kp * kXR * pitch;
+  xl_zero_row(xw, pitch);
   const int k0 = L_lo * F::kLoadK, k1 = min(L_hi * F::kLoadK, W.K);
   const float bn = (W.bias != nullptr && kp == 0) ? load_scalar(W.bias, c0 + n, W.bias_dt) : 0.0f;
   for (int mb = mb0; mb < cnt; mb += kXT) {
@@ -1734,7 +1744,7 @@ __device__ void stage_b_ks_body(const LayerArgs& a, const ProjSlot& W, int c0, i
     for (int Lw = L_lo; Lw < L_hi; Lw += kRowsNLW) {
       if (Lw != L_lo || (mb > mb0 && multi)) rows_issue<EFMT, kRowsNLW, true>(W, G[0], Lw, L_hi, S[0]);
       __builtin_amdgcn_s_waitcnt(0);  // weights and this wave's LDS copy have landed
-      rows_consume_lds<EFMT, kRowsNLW, 1, LPG, true>(W, G, Lw, L_hi, S, xw, k0, pitch, nb, acc);
+      rows_consume_lds<EFMT, kRowsNLW, 1, LPG, true>(W, G, Lw, L_hi, S, xw, k0, pitch, nb, kXT, acc);
     }
     // MFMA rows 0..kXT-1 (the block's tokens) live in lanes 0..15, lane n = column c0 + n
     if (lane < 16) red[kp * 16 + lane] = acc[0];
@@ -1807,7 +1817,7 @@ static bool gq_b_ok(const ftm_moe_layer& L, int T) {
   if (L.hidden % kGqNB != 0 || L.inter % 128 != 0 || T > kGqBMaxT) return false;
   if (L.shared_inter > 0) {
     const int imax = L.inter > L.shared_inter ? L.inter : L.shared_inter;
-    if (L.shared_inter % 8 != 0 || 4 * kXT * xl_pitch(imax, 4) * 2 > kDynLdsMax) return false;
+    if (L.shared_inter % 8 != 0 || 4 * kXR * xl_pitch(imax, 4) * 2 > kDynLdsMax) return false;
   }
   return (L.inter / 128 + 1) / 2 * 128 <= kGqMaxKR;
 }
@@ -1871,7 +1881,8 @@ __device__ void stage_b_xl_body(const LayerArgs& a, const ProjSlot& W, int cnt, 
   }
   const int K = W.K;
   const int pitch = xl_pitch(a.Imax, 1);
-  uint16_t* xw = ftm_xl_lds + wv * kXT * pitch;
+  uint16_t* xw = ftm_xl_lds + wv * kXR * pitch;
+  xl_zero_row(xw, pitch);
   for (int mb = 0; mb < cnt; mb += kXT) {
     const int nb = min(kXT, cnt - mb);
     int pr[kXT];
@@ -1889,7 +1900,7 @@ __device__ void stage_b_xl_body(const LayerArgs& a, const ProjSlot& W, int cnt, 
         for (int t = 0; t < NT; ++t) rows_issue<EFMT, kRowsNLW, false>(W, G[t], Lw, hi, S[t]);
       }
       __builtin_amdgcn_s_waitcnt(0);  // weights and this wave's LDS copy have landed
-      rows_consume_lds<EFMT, kRowsNLW, NT, LPG, false>(W, G, Lw, hi, S, xw, 0, pitch, nb, acc);
+      rows_consume_lds<EFMT, kRowsNLW, NT, LPG, false>(W, G, Lw, hi, S, xw, 0, pitch, nb, kXT, acc);
     }
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
@@ -2694,7 +2705,7 @@ static XlPlan xl_plan_a(const ftm_moe_layer& L, int T) {
     // routed rows: one window per wave (the bf16 shared rows may take several)
     if (!pf_window_fits<FMT>(L.hidden, 4)) return p;
     if (L.hidden % 8 != 0) return p;
-    if (4 * kXT * xl_pitch(L.hidden, 4) * 2 > kDynLdsMax) return p;
+    if (4 * kXR * xl_pitch(L.hidden, 4) * 2 > kDynLdsMax) return p;
     p.lpg = xl_lpg<FMT>(L.w13, 4);
     if (p.lpg == 0) return p;
     p.nt = 1;
@@ -2714,7 +2725,7 @@ static XlPlan xl_plan_b(const ftm_moe_layer& L, int T) {
     if (L.inter % 8 != 0 || (L.shared_inter > 0 && L.shared_inter % 8 != 0)) return p;
     // the LDS regions are sized for the wider of the routed and shared rows
     const int imax = L.inter > L.shared_inter ? L.inter : L.shared_inter;
-    if (4 * kXT * xl_pitch(imax, 1) * 2 > kDynLdsMax) return p;
+    if (4 * kXR * xl_pitch(imax, 1) * 2 > kDynLdsMax) return p;
     p.lpg = xl_lpg<FMT>(L.w2, 1);
     if (p.lpg == 0) return p;
     p.nt = 1;
@@ -2740,7 +2751,7 @@ static XlPlan ks_plan_b(const ftm_moe_layer& L, int T) {
     if (L.shared_inter > 0 && (!pf_window_fits<FTM_FMT_BF16>(L.shared_inter, 4) || L.shared_inter % 8 != 0))
       return p;
     const int imax = L.inter > L.shared_inter ? L.inter : L.shared_inter;
-    if (4 * kXT * xl_pitch(imax, 4) * 2 > kDynLdsMax) return p;
+    if (4 * kXR * xl_pitch(imax, 4) * 2 > kDynLdsMax) return p;
     p.lpg = xl_lpg<FMT>(L.w2, 4);
     p.ok = p.lpg != 0;
     return p;
@@ -2795,7 +2806,7 @@ static void launch_stages(const LayerArgs& a, int gridA, int gridB, hipStream_t 
       const int items = maxU * (a.L.inter / 8) + (a.L.shared_inter > 0 ? a.L.shared_inter / 8 : 0);
       const XlPlan pa = xl_plan_a<FMT, AT>(a.L, a.T);
       if (pa.ok) {
-        const size_t lds = 4u * kXT * (size_t)xl_pitch(a.L.hidden, 4) * 2u;
+        const size_t lds = 4u * kXR * (size_t)xl_pitch(a.L.hidden, 4) * 2u;
         const int nt = pa.nt;
         const int itemsx = maxU * (a.L.inter / (8 * nt)) + (a.L.shared_inter > 0 ? a.L.shared_inter / (8 * nt) : 0);
 #define FTM_XLA(NT, LPG) hipLaunchKernelGGL((k_stage_a_xl<FMT, NT, LPG>), dim3(itemsx), dim3(kBlock), lds, st, a)
@@ -2812,7 +2823,7 @@ static void launch_stages(const LayerArgs& a, int gridA, int gridB, hipStream_t 
       if (gq_b_ok(a.L, a.T) && AT == FTM_DT_BF16) {
         // the shared expert's (token block, 16 columns) items + routed items of 128 columns
         const size_t lds_r = 4u * (kGqXT + 1) * (size_t)gq_pitch(kGqMaxKR) * 2u;
-        const size_t lds_s = a.L.shared_inter > 0 ? 4u * kXT * (size_t)xl_pitch(a.Imax, 4) * 2u : 0u;
+        const size_t lds_s = a.L.shared_inter > 0 ? 4u * kXR * (size_t)xl_pitch(a.Imax, 4) * 2u : 0u;
         const int maxU = a.L.num_experts < a.T * a.L.topk ? a.L.num_experts : a.T * a.L.topk;
         const int grid = gq_b_sh_items(a.L, a.T) + maxU * (a.L.hidden / kGqNB);
         hipLaunchKernelGGL(k_stage_b_gq, dim3(grid), dim3(kBlock), lds_r > lds_s ? lds_r : lds_s, st, a);
@@ -2820,7 +2831,7 @@ static void launch_stages(const LayerArgs& a, int gridA, int gridB, hipStream_t 
         hipLaunchKernelGGL((k_stage_b<FMT, AT>), dim3(gridB), dim3(kBlock), 0, st, a);
       }
     } else if (pb.ok) {
-      const size_t lds = 4u * kXT * (size_t)xl_pitch(a.Imax, 1) * 2u;
+      const size_t lds = 4u * kXR * (size_t)xl_pitch(a.Imax, 1) * 2u;
       const int nt = pb.nt;
       const int maxU = a.L.num_experts < a.T * a.L.topk ? a.L.num_experts : a.T * a.L.topk;
       const int gridx = (maxU + (a.L.shared_inter > 0 ? 1 : 0)) * (a.L.hidden / (64 * nt));
@@ -2829,7 +2840,7 @@ static void launch_stages(const LayerArgs& a, int gridA, int gridB, hipStream_t 
 #undef FTM_XLB
     } else if (const XlPlan pk = ks_plan_b<FMT, AT>(a.L, a.T); pk.ok) {
       const int maxU = a.L.num_experts < a.T * a.L.topk ? a.L.num_experts : a.T * a.L.topk;
-      const size_t lds = 4u * kXT * (size_t)xl_pitch(a.Imax, 4) * 2u;  // the regions stage_b_ks_body lays out
+      const size_t lds = 4u * kXR * (size_t)xl_pitch(a.Imax, 4) * 2u;  // the regions stage_b_ks_body lays out
       const int gridk = (maxU + (a.L.shared_inter > 0 ? 1 : 0)) * (a.L.hidden / 16);
       if (pk.lpg == 2)
         hipLaunchKernelGGL((k_stage_b_ks<FMT, 2>), dim3(gridk), dim3(kBlock), lds, st, a);
