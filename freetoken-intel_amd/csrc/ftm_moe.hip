@@ -980,6 +980,13 @@ constexpr int kGqMaxT = 16;
 
 __host__ __device__ __forceinline__ constexpr int gq_pitch(int KR) { return KR + 8; }
 
+// Zero row kGqXT of a wave's region (MFMA rows >= the block's tokens read it).
+__device__ __forceinline__ void gq_zero_row(uint16_t* xw) {
+  const int lane = threadIdx.x & 63;
+  for (int e = 8 * lane; e < kGqMaxKR; e += 8 * 64)
+    *(u32x4*)(xw + kGqXT * gq_pitch(kGqMaxKR) + e) = (u32x4){0u, 0u, 0u, 0u};
+}
+
 struct GqGroup {
   u32x4 raw[4];  // 4 wave-loads of 32 K: lane (g, rl) holds k8 row 4 b + g, columns ncol .. ncol + 3
   u32x4 scv;
@@ -1001,28 +1008,25 @@ __device__ __forceinline__ void gq_issue(Rsrc wres, Rsrc sres, Rsrc zres, uint32
 constexpr int kGqLoads = 6;  // vector loads per gq_issue
 
 // One group: MFMAs over its 4 wave-loads, then acc += s * (partial - (128 + z + 1) * sum x).
+// The token rows' sums over the group come from one more MFMA per wave-load
+// against a tile of ones, already in the output layout (lane (g, j) holds
+// rows 4 g .. 4 g + 3), instead of VALU sums and cross-lane shuffles.
 __device__ __forceinline__ void gq_group(const GqGroup& G, const uint16_t* xrow, int kofs, uint32_t ncol,
                                          uint32_t sbytes, int s_dt, f32x4 (&acc)[4]) {
   const int lane = threadIdx.x & 63, g = lane >> 4;
-  const u32x4 zero = (u32x4){0u, 0u, 0u, 0u};
+  const u32x4 ones = (u32x4){0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u};  // bf16 1.0
   f32x4 tmp[4];
 #pragma unroll
   for (int c = 0; c < 4; ++c) tmp[c] = (f32x4){0.f, 0.f, 0.f, 0.f};
-  float xs = 0.0f;
+  f32x4 sxr = (f32x4){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int b = 0; b < 4; ++b) {
     const u32x4 av = perm_gptq(*(const u32x4*)(xrow + kofs + 32 * b + 8 * g));
-    xs += sum_a8(av, zero);
+    sxr = mfma_bf16(av, ones, sxr);
     const uint32_t wv[4] = {G.raw[b].x, G.raw[b].y, G.raw[b].z, G.raw[b].w};
 #pragma unroll
     for (int c = 0; c < 4; ++c) tmp[c] = mfma_bf16(av, gptq_word_to_bf16(wv[c]), tmp[c]);
   }
-  float sx = xs;
-  sx += __shfl_xor(sx, 16);
-  sx += __shfl_xor(sx, 32);
-  float sxr[4];
-#pragma unroll
-  for (int rr = 0; rr < 4; ++rr) sxr[rr] = __shfl(sx, 4 * g + rr);
   const uint32_t sw[4] = {G.scv.x, G.scv.y, G.scv.z, G.scv.w};
 #pragma unroll
   for (int c = 0; c < 4; ++c) {
@@ -1086,7 +1090,6 @@ __device__ void stage_a_gq(const LayerArgs& a, const ProjSlot& W, int Iu, int it
   const Rsrc lres = make_rsrc(list, (uint32_t)cnt * 4u);
   constexpr int pitch = gq_pitch(kGqMaxKR);
   uint16_t* xw = ftm_xl_lds + wave * (kGqXT + 1) * pitch;
-  for (int e = 8 * lane; e < kGqMaxKR; e += 8 * 64) *(u32x4*)(xw + kGqXT * pitch + e) = (u32x4){0u, 0u, 0u, 0u};
   float bias_g[EPI], bias_u[EPI];
 #pragma unroll
   for (int q = 0; q < EPI; ++q) {
@@ -1111,6 +1114,7 @@ __device__ void stage_a_gq(const LayerArgs& a, const ProjSlot& W, int Iu, int it
     if (hi > lo) {
       GqGroup GA, GB;
       gq_issue(wres, sres, zres, ncol, N, lo, sbytes, GA);  // weights first,
+      gq_zero_row(xw);                                      // (the last block's reduction used it)
       gq_fill(pr, nb, a.x, KP, H, k0, kr, pitch, xw);       // then the token rows
       const uint16_t* xrow = xw + (rl < nb ? rl : kGqXT) * pitch;
       // two group buffers: the next group is in flight while this one is multiplied
@@ -1135,6 +1139,7 @@ __device__ void stage_a_gq(const LayerArgs& a, const ProjSlot& W, int Iu, int it
         }
       }
     }
+    __syncthreads();  // red aliases the token rows: every wave is past its MFMAs
 #pragma unroll
     for (int c = 0; c < 4; ++c) red[(wave * 4 + c) * 64 + lane] = acc[c];
     __syncthreads();
@@ -1167,7 +1172,10 @@ static bool gq_ok(const ftm_moe_layer& L, int T) {
 
 __global__ __launch_bounds__(kBlock) void k_stage_a_gq(const LayerArgs a) {
   constexpr int NT = 64;
-  __shared__ f32x4 red[4 * 2 * 4 * 64];  // also the shared-expert body's reduction buffer
+  // The reduction buffer (16 KiB routed, 32 KiB for the shared-expert body)
+  // aliases the dynamic token-row regions (41 KiB), so a workgroup holds 41
+  // KiB of LDS and three fit a CU.
+  f32x4* red = (f32x4*)ftm_xl_lds;
   const int I = a.L.inter;
   const int tilesR = I / NT;
   int item = blockIdx.x;
@@ -1224,7 +1232,6 @@ __device__ void stage_b_gq(const LayerArgs& a, const ProjSlot& W, int it, int cn
   const Rsrc wtres = make_rsrc(a.wts, (uint32_t)a.T * (uint32_t)KP * 4u);
   constexpr int pitch = gq_pitch(kGqMaxKR);
   uint16_t* xw = ftm_xl_lds + wave * (kGqXT + 1) * pitch;
-  for (int e = 8 * lane; e < kGqMaxKR; e += 8 * 64) *(u32x4*)(xw + kGqXT * pitch + e) = (u32x4){0u, 0u, 0u, 0u};
   float bias_n[EPI];
 #pragma unroll
   for (int q = 0; q < EPI; ++q) {
@@ -1250,6 +1257,7 @@ __device__ void stage_b_gq(const LayerArgs& a, const ProjSlot& W, int it, int cn
     if (hi > lo) {
       GqGroup GA, GB;
       gq_issue(wres, sres, zres, ncol, N, lo, sbytes, GA);       // weights first,
+      gq_zero_row(xw);                                           // (the last block's reduction used it)
       gq_fill(pr, nb, a.hbuf, 1, a.Imax, k0, kr, pitch, xw);     // then the h rows
       const uint16_t* xrow = xw + (rl < nb ? rl : kGqXT) * pitch;
       for (int grp = lo; grp < hi; grp += 2) {
@@ -1272,6 +1280,7 @@ __device__ void stage_b_gq(const LayerArgs& a, const ProjSlot& W, int it, int cn
         }
       }
     }
+    __syncthreads();  // red aliases the h rows: every wave is past its MFMAs
 #pragma unroll
     for (int c = 0; c < 4; ++c) red[(wave * 4 + c) * 64 + lane] = acc[c];
     __syncthreads();
@@ -1823,7 +1832,10 @@ static bool gq_b_ok(const ftm_moe_layer& L, int T) {
 }
 
 __global__ __launch_bounds__(kBlock) void k_stage_b_gq(const LayerArgs a) {
-  __shared__ f32x4 red[4 * 4 * 64];
+  // routed items: the reduction buffer (16 KiB) aliases the h-row regions;
+  // the shared expert's K-split items keep a small one of their own (their
+  // waves' regions are in use while other waves reduce)
+  __shared__ f32x4 red_s[4 * 16];
   const int H = a.L.hidden;
   const int tilesR = H / kGqNB;
   const int nSh = gq_b_sh_items(a.L, a.T);
@@ -1833,7 +1845,7 @@ __global__ __launch_bounds__(kBlock) void k_stage_b_gq(const LayerArgs a) {
     const int kp = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const ProjSlot W = shared_view(a.L.shared_w2, H, a.L.shared_inter);
     stage_b_ks_body<FTM_FMT_BF16, kRowsNLW>(a, W, c0, min(a.T, (b + 1) * kGqBShXT), nullptr, nullptr, a.L.topk, kp,
-                                            red, b * kGqBShXT);
+                                            red_s, b * kGqBShXT);
     return;
   }
   const int ritem = item - nSh;
@@ -1852,7 +1864,7 @@ __global__ __launch_bounds__(kBlock) void k_stage_b_gq(const LayerArgs a) {
     if (threadIdx.x == 0) atomicOr(&a.ctrl[kCtrlError], 1);
     return;
   }
-  stage_b_gq(a, proj_slot(a.L.w2, slot), it, cnt, list, red);
+  stage_b_gq(a, proj_slot(a.L.w2, slot), it, cnt, list, (f32x4*)ftm_xl_lds);
 }
 
 // Stage B item body: NT x 64 output columns of one expert; in each 64-column
