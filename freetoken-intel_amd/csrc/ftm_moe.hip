@@ -980,11 +980,25 @@ constexpr int kGqMaxT = 16;
 
 __host__ __device__ __forceinline__ constexpr int gq_pitch(int KR) { return KR + 8; }
 
-// Zero row kGqXT of a wave's region (MFMA rows >= the block's tokens read it).
-__device__ __forceinline__ void gq_zero_row(uint16_t* xw) {
+// LDS layout of the GPTQ decode stages: wave w's kGqXT token rows at
+// w * kGqXT * pitch, pitch = gq_pitch(the layer's per-wave K range), so the
+// region is no larger than the layer needs; the reduction buffer (red_bytes)
+// aliases the start of it; then ONE zero row, past both, that MFMA rows past
+// the block's tokens read (shared by the workgroup's waves).
+__host__ __device__ __forceinline__ int gq_wave_kr(int K, int ks) { return ((K + 127) / 128 + ks - 1) / ks * 128; }
+__host__ __device__ __forceinline__ int gq_zrow_off(int waves, int pitch, int red_bytes) {
+  const int rows = waves * kGqXT * pitch;
+  return rows > red_bytes / 2 ? rows : red_bytes / 2;  // in elements
+}
+__host__ __device__ __forceinline__ size_t gq_lds_bytes(int waves, int K, int ks, int red_bytes) {
+  const int pitch = gq_pitch(gq_wave_kr(K, ks));
+  return ((size_t)gq_zrow_off(waves, pitch, red_bytes) + (size_t)pitch) * 2u;
+}
+// Each wave writes the whole zero row itself (identical values) before it
+// reads it, so no barrier is needed.
+__device__ __forceinline__ void gq_zero_row(uint16_t* zrow, int kr) {
   const int lane = threadIdx.x & 63;
-  for (int e = 8 * lane; e < kGqMaxKR; e += 8 * 64)
-    *(u32x4*)(xw + kGqXT * gq_pitch(kGqMaxKR) + e) = (u32x4){0u, 0u, 0u, 0u};
+  for (int e = 8 * lane; e < kr; e += 8 * 64) *(u32x4*)(zrow + e) = (u32x4){0u, 0u, 0u, 0u};
 }
 
 struct GqGroup {
@@ -1067,18 +1081,60 @@ __device__ __forceinline__ void gq_fill(const int (&pr)[kGqXT], int nb, const vo
   }
 }
 
-// Item: 64 channels of one expert; waves 0-1 take the 64 gate columns and
-// waves 2-3 the 64 up columns, each over half of the K groups.
-template <int NT>
+// A wave's groups [lo, hi) through two group buffers: group g + 1 is in
+// flight while group g is multiplied.  GA already holds group lo (issued
+// before the caller's token-row copy).  A third buffer (group g + 2 in flight
+// too) measured slower on C2 at T=16: w13 37.1 -> 39.3 us, w2 23.4 -> 30.5.
+__device__ __forceinline__ void gq_pipeline(Rsrc wres, Rsrc sres, Rsrc zres, uint32_t ncol, int N, uint32_t sbytes,
+                                            int s_dt, int lo, int hi, const uint16_t* xrow, GqGroup& GA,
+                                            f32x4 (&acc)[4]) {
+  GqGroup GB;
+  for (int grp = lo; grp < hi; grp += 2) {
+    const bool two = grp + 1 < hi;
+    if (two) {
+      gq_issue(wres, sres, zres, ncol, N, grp + 1, sbytes, GB);
+      wait_vm<kGqLoads>();  // group grp (and the copy) landed
+    } else {
+      __builtin_amdgcn_s_waitcnt(0);
+    }
+    gq_group(GA, xrow, (grp - lo) * 128, ncol, sbytes, s_dt, acc);
+    if (two) {
+      if (grp + 2 < hi) {
+        gq_issue(wres, sres, zres, ncol, N, grp + 2, sbytes, GA);
+        wait_vm<kGqLoads>();
+      } else {
+        __builtin_amdgcn_s_waitcnt(0);
+      }
+      gq_group(GB, xrow, (grp + 1 - lo) * 128, ncol, sbytes, s_dt, acc);
+    }
+  }
+}
+
+// Item: 64 channels of one expert; waves [0, KS) take the 64 gate columns and
+// waves [KS, 2 KS) the 64 up columns, each over 1 / KS of the K groups (KS = 2:
+// a 256-thread workgroup, rows of up to kGqMaxKR elements per wave; KS = 4: 512
+// threads, half the rows per wave, twice the waves -- and bytes in flight --
+// per CU at the same LDS).
+template <int KS>
+struct GqA {
+  static constexpr int kThreads = 2 * KS * 64;
+  static constexpr int kKR = kGqMaxKR * 2 / KS;  // a wave's K range bound
+  // token rows + zero row, at least the reduction buffer (32 KiB: 8 waves x
+  // 4 sub-tiles, or the shared-expert body's)
+  static constexpr int kRedBytes = 32768;
+  static size_t lds(int K) { return gq_lds_bytes(2 * KS, K, KS, kRedBytes); }
+};
+
+template <int NT, int KS>
 __device__ void stage_a_gq(const LayerArgs& a, const ProjSlot& W, int Iu, int it, int cnt, const int32_t* list,
                            f32x4* red) {
-  constexpr int EPI = 16 * NT / kBlock;
+  constexpr int EPI = 16 * NT / GqA<KS>::kThreads;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int rl = lane & 15;
   const int H = a.L.hidden, KP = a.KP, N = W.N;
-  const int tile = wave >> 1;
+  const int tile = wave / KS;
   int lo, hi;
-  wave_k_range<FTM_FMT_GPTQ_INT4>(W, wave & 1, 2, lo, hi);
+  wave_k_range<FTM_FMT_GPTQ_INT4>(W, wave % KS, KS, lo, hi);
   const int k0 = lo * 128, kr = (hi - lo) * 128;
   const uint32_t sbytes = W.s_dt == FTM_DT_F32 ? 4u : 2u;
   const int ngroups = (W.K + 127) / 128;
@@ -1088,12 +1144,15 @@ __device__ void stage_a_gq(const LayerArgs& a, const ProjSlot& W, int Iu, int it
   const int col0 = (tile == 0 ? 0 : Iu) + it * NT;
   const uint32_t ncol = col0 + 4 * rl < N ? (uint32_t)(col0 + 4 * rl) : kOOB;
   const Rsrc lres = make_rsrc(list, (uint32_t)cnt * 4u);
-  constexpr int pitch = gq_pitch(kGqMaxKR);
-  uint16_t* xw = ftm_xl_lds + wave * (kGqXT + 1) * pitch;
+  const int kr_max = gq_wave_kr(W.K, KS);
+  const int pitch = gq_pitch(kr_max);
+  uint16_t* xw = ftm_xl_lds + wave * kGqXT * pitch;
+  uint16_t* zrow = ftm_xl_lds + gq_zrow_off(2 * KS, pitch, GqA<KS>::kRedBytes);
+  gq_zero_row(zrow, kr_max);
   float bias_g[EPI], bias_u[EPI];
 #pragma unroll
   for (int q = 0; q < EPI; ++q) {
-    const int j = (threadIdx.x + q * kBlock) % NT;
+    const int j = (threadIdx.x + q * GqA<KS>::kThreads) % NT;
     bias_g[q] = W.bias != nullptr ? load_scalar(W.bias, it * NT + j, W.bias_dt) : 0.0f;
     bias_u[q] = W.bias != nullptr ? load_scalar(W.bias, Iu + it * NT + j, W.bias_dt) : 0.0f;
   }
@@ -1105,39 +1164,18 @@ __device__ void stage_a_gq(const LayerArgs& a, const ProjSlot& W, int Iu, int it
     int pe[EPI];
 #pragma unroll
     for (int q = 0; q < EPI; ++q) {
-      const int i = (threadIdx.x + q * kBlock) / NT;
+      const int i = (threadIdx.x + q * GqA<KS>::kThreads) / NT;
       pe[q] = i < kGqXT ? pair_of_row(lres, true, mb + i, cnt, KP, 0) : -1;
     }
     f32x4 acc[4];
 #pragma unroll
     for (int c = 0; c < 4; ++c) acc[c] = (f32x4){0.f, 0.f, 0.f, 0.f};
     if (hi > lo) {
-      GqGroup GA, GB;
+      GqGroup GA;
       gq_issue(wres, sres, zres, ncol, N, lo, sbytes, GA);  // weights first,
-      gq_zero_row(xw);                                      // (the last block's reduction used it)
       gq_fill(pr, nb, a.x, KP, H, k0, kr, pitch, xw);       // then the token rows
-      const uint16_t* xrow = xw + (rl < nb ? rl : kGqXT) * pitch;
-      // two group buffers: the next group is in flight while this one is multiplied
-      // (a third buffer, 219 VGPRs at occupancy 2, measured no faster)
-      for (int grp = lo; grp < hi; grp += 2) {
-        const bool two = grp + 1 < hi;
-        if (two) {
-          gq_issue(wres, sres, zres, ncol, N, grp + 1, sbytes, GB);
-          wait_vm<kGqLoads>();  // group grp (and the copy) landed
-        } else {
-          __builtin_amdgcn_s_waitcnt(0);
-        }
-        gq_group(GA, xrow, (grp - lo) * 128, ncol, sbytes, W.s_dt, acc);
-        if (two) {
-          if (grp + 2 < hi) {
-            gq_issue(wres, sres, zres, ncol, N, grp + 2, sbytes, GA);
-            wait_vm<kGqLoads>();
-          } else {
-            __builtin_amdgcn_s_waitcnt(0);
-          }
-          gq_group(GB, xrow, (grp + 1 - lo) * 128, ncol, sbytes, W.s_dt, acc);
-        }
-      }
+      const uint16_t* xrow = rl < nb ? xw + rl * pitch : zrow;
+      gq_pipeline(wres, sres, zres, ncol, N, sbytes, W.s_dt, lo, hi, xrow, GA, acc);
     }
     __syncthreads();  // red aliases the token rows: every wave is past its MFMAs
 #pragma unroll
@@ -1145,12 +1183,16 @@ __device__ void stage_a_gq(const LayerArgs& a, const ProjSlot& W, int Iu, int it
     __syncthreads();
 #pragma unroll
     for (int q = 0; q < EPI; ++q) {
-      const int idx = threadIdx.x + q * kBlock;
+      const int idx = threadIdx.x + q * GqA<KS>::kThreads;
       const int i = idx / NT, j = idx % NT;
       const int c = j & 3, jj = j >> 2;
       const int ln = jj + 16 * (i >> 2), rr = i & 3;
-      const float g4 = red[(0 * 4 + c) * 64 + ln][rr] + red[(1 * 4 + c) * 64 + ln][rr];
-      const float u4 = red[(2 * 4 + c) * 64 + ln][rr] + red[(3 * 4 + c) * 64 + ln][rr];
+      float g4 = 0.0f, u4 = 0.0f;
+#pragma unroll
+      for (int p = 0; p < KS; ++p) {
+        g4 += red[(p * 4 + c) * 64 + ln][rr];
+        u4 += red[((KS + p) * 4 + c) * 64 + ln][rr];
+      }
       const float gs = W.bias != nullptr ? g4 + bias_g[q] : g4;
       const float us = W.bias != nullptr ? u4 + bias_u[q] : u4;
       if (pe[q] >= 0) {
@@ -1162,15 +1204,22 @@ __device__ void stage_a_gq(const LayerArgs& a, const ProjSlot& W, int Iu, int it
   }
 }
 
-// Layers the GPTQ decode stage A with activations in LDS takes.
-static bool gq_ok(const ftm_moe_layer& L, int T) {
+// Layers the GPTQ decode stage A with activations in LDS takes (0 = none),
+// and its K split: 4 for one or two tokens when every wave's quarter of the K
+// groups fits and there is no shared expert (whose body needs 256-thread
+// workgroups), else 2.  Measured on C2 (w13 us, KS 2 -> 4): T=1 15.9 -> 11.5,
+// T=4 19.1 -> 21.4, T=16 37.6 -> 44.2.
+static int gq_ks(const ftm_moe_layer& L, int T) {
   const ftm_proj& A = L.w13;
-  if (A.fmt != FTM_FMT_GPTQ_INT4 || L.act_dtype != FTM_DT_BF16 || A.group != 128) return false;
-  if (L.hidden % 128 != 0 || L.inter % 64 != 0 || T > kGqMaxT) return false;
-  return (L.hidden / 128 + 1) / 2 * 128 <= kGqMaxKR;  // half of the K groups per wave
+  if (A.fmt != FTM_FMT_GPTQ_INT4 || L.act_dtype != FTM_DT_BF16 || A.group != 128) return 0;
+  if (L.hidden % 128 != 0 || L.inter % 64 != 0 || T > kGqMaxT) return 0;
+  if (T <= 2 && L.shared_inter <= 0 && (L.hidden / 128 + 3) / 4 * 128 <= GqA<4>::kKR) return 4;
+  return (L.hidden / 128 + 1) / 2 * 128 <= GqA<2>::kKR ? 2 : 0;  // half of the K groups per wave
 }
+static bool gq_ok(const ftm_moe_layer& L, int T) { return gq_ks(L, T) != 0; }
 
-__global__ __launch_bounds__(kBlock) void k_stage_a_gq(const LayerArgs a) {
+template <int KS>
+__global__ __launch_bounds__(GqA<KS>::kThreads) void k_stage_a_gq(const LayerArgs a) {
   constexpr int NT = 64;
   // The reduction buffer (16 KiB routed, 32 KiB for the shared-expert body)
   // aliases the dynamic token-row regions (41 KiB), so a workgroup holds 41
@@ -1188,8 +1237,8 @@ __global__ __launch_bounds__(kBlock) void k_stage_a_gq(const LayerArgs a) {
       if (threadIdx.x == 0) atomicOr(&a.ctrl[kCtrlError], 1);
       return;
     }
-    stage_a_gq<NT>(a, proj_slot(a.L.w13, slot), I, it, cnt, a.lists + (size_t)e * a.T, red);
-  } else {
+    stage_a_gq<NT, KS>(a, proj_slot(a.L.w13, slot), I, it, cnt, a.lists + (size_t)e * a.T, red);
+  } else if constexpr (KS == 2) {
     item -= nRouted * tilesR;
     const int Is = a.L.shared_inter;
     if (Is <= 0 || item >= Is / 16) return;
@@ -1206,6 +1255,7 @@ __global__ __launch_bounds__(kBlock) void k_stage_a_gq(const LayerArgs a) {
 // summed through LDS, router-weighted, and written to the slot buffer rows
 // (k_combine sums them).
 constexpr int kGqNB = 128;  // output columns per stage-B item
+constexpr int kGqBRedBytes = 16384;  // its reduction buffer: 4 waves x 4 sub-tiles x 64 lanes x 16 B
 // Measured on C2 (w2, against the register-fed k_stage_b): T=4 18.6 -> 11.6
 // us, T=16 39.5 -> 29.3, T=24 46.3 -> 36.0, T=32 49.6 -> 41.0; T=64 55.3 ->
 // 56.5, so it stops at 32 tokens.
@@ -1230,8 +1280,11 @@ __device__ void stage_b_gq(const LayerArgs& a, const ProjSlot& W, int it, int cn
   const uint32_t ncol = col0 + 4 * rl < N ? (uint32_t)(col0 + 4 * rl) : kOOB;
   const Rsrc lres = make_rsrc(list, (uint32_t)cnt * 4u);
   const Rsrc wtres = make_rsrc(a.wts, (uint32_t)a.T * (uint32_t)KP * 4u);
-  constexpr int pitch = gq_pitch(kGqMaxKR);
-  uint16_t* xw = ftm_xl_lds + wave * (kGqXT + 1) * pitch;
+  const int kr_max = gq_wave_kr(W.K, 2);
+  const int pitch = gq_pitch(kr_max);
+  uint16_t* xw = ftm_xl_lds + wave * kGqXT * pitch;
+  uint16_t* zrow = ftm_xl_lds + gq_zrow_off(4, pitch, kGqBRedBytes);
+  gq_zero_row(zrow, kr_max);
   float bias_n[EPI];
 #pragma unroll
   for (int q = 0; q < EPI; ++q) {
@@ -1255,30 +1308,11 @@ __device__ void stage_b_gq(const LayerArgs& a, const ProjSlot& W, int it, int cn
 #pragma unroll
     for (int c = 0; c < 4; ++c) acc[c] = (f32x4){0.f, 0.f, 0.f, 0.f};
     if (hi > lo) {
-      GqGroup GA, GB;
+      GqGroup GA;
       gq_issue(wres, sres, zres, ncol, N, lo, sbytes, GA);       // weights first,
-      gq_zero_row(xw);                                           // (the last block's reduction used it)
       gq_fill(pr, nb, a.hbuf, 1, a.Imax, k0, kr, pitch, xw);     // then the h rows
-      const uint16_t* xrow = xw + (rl < nb ? rl : kGqXT) * pitch;
-      for (int grp = lo; grp < hi; grp += 2) {
-        const bool two = grp + 1 < hi;
-        if (two) {
-          gq_issue(wres, sres, zres, ncol, N, grp + 1, sbytes, GB);
-          wait_vm<kGqLoads>();
-        } else {
-          __builtin_amdgcn_s_waitcnt(0);
-        }
-        gq_group(GA, xrow, (grp - lo) * 128, ncol, sbytes, W.s_dt, acc);
-        if (two) {
-          if (grp + 2 < hi) {
-            gq_issue(wres, sres, zres, ncol, N, grp + 2, sbytes, GA);
-            wait_vm<kGqLoads>();
-          } else {
-            __builtin_amdgcn_s_waitcnt(0);
-          }
-          gq_group(GB, xrow, (grp + 1 - lo) * 128, ncol, sbytes, W.s_dt, acc);
-        }
-      }
+      const uint16_t* xrow = rl < nb ? xw + rl * pitch : zrow;
+      gq_pipeline(wres, sres, zres, ncol, N, sbytes, W.s_dt, lo, hi, xrow, GA, acc);
     }
     __syncthreads();  // red aliases the h rows: every wave is past its MFMAs
 #pragma unroll
@@ -2806,9 +2840,11 @@ static void launch_stages(const LayerArgs& a, int gridA, int gridB, hipStream_t 
   }
   if (which & 1) {
     if constexpr (FMT == FTM_FMT_GPTQ_INT4) {
-      if (gq_ok(a.L, a.T) && AT == FTM_DT_BF16) {
-        const size_t lds = 4u * (kGqXT + 1) * (size_t)gq_pitch(kGqMaxKR) * 2u;
-        hipLaunchKernelGGL(k_stage_a_gq, dim3(gridA), dim3(kBlock), lds, st, a);
+      if (const int ks = gq_ks(a.L, a.T); ks != 0 && AT == FTM_DT_BF16) {
+        if (ks == 4)
+          hipLaunchKernelGGL(k_stage_a_gq<4>, dim3(gridA), dim3(GqA<4>::kThreads), GqA<4>::lds(a.L.hidden), st, a);
+        else
+          hipLaunchKernelGGL(k_stage_a_gq<2>, dim3(gridA), dim3(GqA<2>::kThreads), GqA<2>::lds(a.L.hidden), st, a);
       } else {
         hipLaunchKernelGGL((k_stage_a<FMT, AT>), dim3(gridA), dim3(kBlock), 0, st, a);
       }
@@ -2834,7 +2870,7 @@ static void launch_stages(const LayerArgs& a, int gridA, int gridB, hipStream_t 
     if constexpr (FMT == FTM_FMT_GPTQ_INT4) {
       if (gq_b_ok(a.L, a.T) && AT == FTM_DT_BF16) {
         // the shared expert's (token block, 16 columns) items + routed items of 128 columns
-        const size_t lds_r = 4u * (kGqXT + 1) * (size_t)gq_pitch(kGqMaxKR) * 2u;
+        const size_t lds_r = gq_lds_bytes(4, a.L.inter, 2, kGqBRedBytes);
         const size_t lds_s = a.L.shared_inter > 0 ? 4u * kXR * (size_t)xl_pitch(a.Imax, 4) * 2u : 0u;
         const int maxU = a.L.num_experts < a.T * a.L.topk ? a.L.num_experts : a.T * a.L.topk;
         const int grid = gq_b_sh_items(a.L, a.T) + maxU * (a.L.hidden / kGqNB);
