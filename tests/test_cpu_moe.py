@@ -107,3 +107,24 @@ def test_split_rule_matches_the_reference():
     assert HY.split_experts(ids, 0.8, max_fetch=1) == {1, 3, 7, 9}
     assert HY.split_experts(ids, 1.0) is None and HY.split_experts(ids, 0.0) is None
     assert HY.split_experts(torch.tensor([[4, -1]]), 0.5) is None  # one expert: nothing to split
+
+
+@pytest.mark.skipif(not O.ref_cpu_moe_available(), reason="oracle/_ref not built (needs /root/reference)")
+@pytest.mark.parametrize("name", ["c1_int8", "c2_gptq", "c3_fp8"])
+def test_cpu_half_matches_the_reference_cpu_kernel(name):
+    """Against the reference's own CPU MoE (cpu_moe.cpp freetoken_cpu_moe_forward_fast,
+    built unmodified into oracle/_ref) on the same experts dequantized to fp32 (the
+    reference's CPU path takes dense fp32 banks: python/freetoken/kernel/cpu_moe.py:
+    460-461): the packed-bank decode and the fp32 SwiGLU + combine agree to fp32
+    reassociation."""
+    cfg = replace(S.SMALL[name], E=6)
+    syn = S.generate(cfg, T=5, seed=504)
+    L, keep = _host(syn)
+    spec = oracle_spec(syn)
+    gu = np.stack([O.dequant(spec["w13"], e) for e in range(cfg.E)]).astype(np.float32)
+    dn = np.stack([O.dequant(spec["w2"], e) for e in range(cfg.E)]).astype(np.float32)
+    x = syn.x.float()
+    ids, w = _routing(syn, 5, 4)
+    got = HY.cpu_moe_forward(L, x, torch.from_numpy(ids), torch.from_numpy(w), threads=2)
+    ref = O.ref_cpu_moe_forward_fast(x.numpy(), ids, w, gu, dn, threads=1)
+    np.testing.assert_allclose(got.numpy(), ref, rtol=1e-4, atol=1e-5 * np.abs(ref).max())
