@@ -29,7 +29,7 @@ python/freetoken/models/loader.py:693-925), restated for this build:
 * :func:`attach_offload_cache` wires the banks into an
   :class:`~ftmoe.moe.offload_cache.OffloadMoeCache` with the attributes the
   slot API reads (``gptq_group_size``, ``int8_k_gate_up`` / ``int8_k_down``,
-  ``fp8_block_size``; MXFP4 biases as extra metadata), and
+  ``fp8_block_size``; MXFP4 biases as two more per-slot banks), and
   :func:`moe_layer_from_banks` builds the in-HBM :class:`~ftmoe.layer.MoeLayer`
   of one layer from them.
 """
