@@ -489,8 +489,8 @@ int validate(const ftm_moe_layer* L, const float* x, int T, const int32_t* ids, 
 
 int run_call(const Call& c) {
   const int E = c.L.num_experts, H = c.L.hidden, T = c.T;
+  if (T == 0) return FTM_OK;  // (out may be null then)
   memset(c.out, 0, sizeof(float) * (size_t)T * H);
-  if (T == 0) return FTM_OK;
   for (int64_t i = 0; i < (int64_t)T * c.L.topk; ++i)
     if (c.ids[i] >= E) return FTM_ERR_DIM;
   const bool vec = have_avx512() && !c.force_scalar;

@@ -33,10 +33,13 @@ int32_t lru_victim(int32_t cache_size, const int64_t* usage) {
   return best;
 }
 
-void take_slot(int32_t victim, int32_t new_id, int64_t step, int32_t* slot_for_id, int32_t* id_of_slot,
-               int64_t* usage) {
+// State arrays come from the caller: an out-of-range id or slot in them (a
+// corrupt map) is skipped here, never followed, and the final resync rebuilds
+// slot_for_id from id_of_slot alone.
+void take_slot(int32_t victim, int32_t new_id, int64_t step, int32_t num_ids, int32_t* slot_for_id,
+               int32_t* id_of_slot, int64_t* usage) {
   const int32_t old_id = id_of_slot[victim];
-  if (old_id >= 0) slot_for_id[old_id] = -1;
+  if (old_id >= 0 && old_id < num_ids) slot_for_id[old_id] = -1;
   id_of_slot[victim] = new_id;
   slot_for_id[new_id] = victim;
   usage[victim] = step;
@@ -80,16 +83,17 @@ int ftm_lru_ensure(int32_t layer_id, int32_t num_layers, int32_t num_experts, in
   *step = st;
   for (int32_t e : seen) {  // phase 1: hits
     const int32_t s = slot_for_id[base + e];
-    if (s != -1) usage[s] = st;
+    if (s >= 0 && s < cache_size) usage[s] = st;
   }
   // phase 2: the misses, fixed before any eviction, in ascending expert id
   std::vector<int32_t> missing;
   for (int32_t e = 0; e < num_experts; ++e)
-    if (seen_flag[(size_t)e] && slot_for_id[base + e] == -1) missing.push_back(e);
+    if (seen_flag[(size_t)e] && !(slot_for_id[base + e] >= 0 && slot_for_id[base + e] < cache_size))
+      missing.push_back(e);
   int32_t num = 0;
   for (int32_t e : missing) {
     const int32_t victim = lru_victim(cache_size, usage);
-    take_slot(victim, base + e, st, slot_for_id, id_of_slot, usage);
+    take_slot(victim, base + e, st, num_layers * num_experts, slot_for_id, id_of_slot, usage);
     evict_slots[num] = victim;
     src_rows[num] = e;
     ++num;
@@ -113,11 +117,11 @@ int ftm_lru_materialize(int32_t layer_id, int32_t num_layers, int32_t num_expert
   *step = st;
   for (int32_t e = 0; e < num_experts; ++e) {
     const int32_t s = slot_for_id[base + e];
-    if (s != -1) usage[s] = st;
+    if (s >= 0 && s < cache_size) usage[s] = st;
   }
   std::vector<int32_t> missing;
   for (int32_t e = 0; e < num_experts; ++e)
-    if (slot_for_id[base + e] == -1) missing.push_back(e);
+    if (!(slot_for_id[base + e] >= 0 && slot_for_id[base + e] < cache_size)) missing.push_back(e);
   int32_t num = 0;
   for (int32_t e : missing) {
     int32_t victim = -1;
@@ -127,7 +131,7 @@ int ftm_lru_materialize(int32_t layer_id, int32_t num_layers, int32_t num_expert
         break;
       }
     if (victim < 0) victim = lru_victim(cache_size, usage);
-    take_slot(victim, base + e, st, slot_for_id, id_of_slot, usage);
+    take_slot(victim, base + e, st, num_layers * num_experts, slot_for_id, id_of_slot, usage);
     evict_slots[num] = victim;
     src_rows[num] = e;
     ++num;
