@@ -176,9 +176,10 @@ bool fast_layer(const ftm_moe_layer* L, const void* x) {
   return aligned16(x);
 }
 
+// xq_ready: the router launch quantised the input (launch_router's quant)
 hipError_t run_experts(const ftm_moe_layer& L, const void* x, int T, void* out, char* ws, const WsLayout& wl,
-                       hipStream_t st) {
-  return fast_layer(&L, x) ? launch_experts(L, x, T, out, ws, wl, st)
+                       hipStream_t st, bool xq_ready = false) {
+  return fast_layer(&L, x) ? launch_experts(L, x, T, out, ws, wl, st, 7, nullptr, xq_ready)
                            : launch_experts_generic(L, x, T, out, ws, wl, st);
 }
 
@@ -225,12 +226,14 @@ int ftm_moe_forward(const ftm_moe_layer* layer, const void* x, int32_t num_token
   const int rows = layer->num_experts + (layer->shared_inter > 0 ? 1 : 0);
   // small decode batches on the lean kernels route inside stage A (no top-k launch)
   const bool fused = fast_layer(layer, x) && lean_route_ok(*layer, num_tokens);
+  // the router launch also quantises the input of an MXFP4 stage A
+  const bool xq = mx_stage_a(*layer, num_tokens);
   if (!fused && route_topk_fused(*layer, num_tokens)) {  // router + top-k in one launch
-    hipError_t e = launch_route_topk(*layer, x, num_tokens, topk_ids, topk_w, logits, ws, wl, st);
-    if (e == hipSuccess) e = run_experts(*layer, x, num_tokens, out, ws, wl, st);
+    hipError_t e = launch_route_topk(*layer, x, num_tokens, topk_ids, topk_w, logits, ws, wl, st, true);
+    if (e == hipSuccess) e = run_experts(*layer, x, num_tokens, out, ws, wl, st, xq);
     return hip_rc(e);
   }
-  hipError_t e = launch_router(*layer, x, num_tokens, 0, rows, ws, wl, st);
+  hipError_t e = launch_router(*layer, x, num_tokens, 0, rows, ws, wl, st, true);
   if (fused) {
     const RouteOut ro = {topk_ids, topk_w, logits};
     if (e == hipSuccess) e = launch_experts(*layer, x, num_tokens, out, ws, wl, st, 7, &ro);
@@ -238,7 +241,7 @@ int ftm_moe_forward(const ftm_moe_layer* layer, const void* x, int32_t num_token
   }
   if (e == hipSuccess)
     e = launch_topk(*layer, num_tokens, nullptr, 0, nullptr, nullptr, topk_ids, topk_w, logits, ws, wl, st);
-  if (e == hipSuccess) e = run_experts(*layer, x, num_tokens, out, ws, wl, st);
+  if (e == hipSuccess) e = run_experts(*layer, x, num_tokens, out, ws, wl, st, xq);
   return hip_rc(e);
 }
 
@@ -280,17 +283,19 @@ int ftm_moe_forward_stage(const ftm_moe_layer* layer, const void* x, int32_t num
   const bool fused = lean_route_ok(*layer, num_tokens);  // routing runs in stage A
   const bool rt = !fused && route_topk_fused(*layer, num_tokens);  // the router launch also routes
   const RouteOut ro = {nullptr, nullptr, nullptr};
+  // the router stage quantises the input of an MXFP4 stage A, as ftm_moe_forward's router launch does
   if (stage == FTM_STAGE_ROUTER)
-    e = rt ? launch_route_topk(*layer, x, num_tokens, nullptr, nullptr, nullptr, ws, wl, st)
+    e = rt ? launch_route_topk(*layer, x, num_tokens, nullptr, nullptr, nullptr, ws, wl, st, true)
            : launch_router(*layer, x, num_tokens, 0, layer->num_experts + (layer->shared_inter > 0 ? 1 : 0), ws, wl,
-                           st);
+                           st, true);
   else if (stage == FTM_STAGE_TOPK)
     e = fused || rt
             ? hipSuccess
             : launch_topk(*layer, num_tokens, nullptr, 0, nullptr, nullptr, nullptr, nullptr, nullptr, ws, wl, st);
   else
     e = launch_experts(*layer, x, num_tokens, out, ws, wl, st,
-                       stage == FTM_STAGE_W13 ? 1 : stage == FTM_STAGE_W2 ? 2 : 4, fused ? &ro : nullptr);
+                       stage == FTM_STAGE_W13 ? 1 : stage == FTM_STAGE_W2 ? 2 : 4, fused ? &ro : nullptr,
+                       mx_stage_a(*layer, num_tokens));
   return hip_rc(e);
 }
 

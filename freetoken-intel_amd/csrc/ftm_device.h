@@ -72,6 +72,25 @@ __device__ __forceinline__ float load_scalar(const void* p, int64_t i, int dt) {
   return bf16_to_f32(((const uint16_t*)p)[i]);
 }
 
+// Raw bits of element i of a scalar array (2- or 4-byte dtype) and their
+// value, for loads issued ahead of a kernel's weight stream but used only in
+// its epilogue: vector loads complete in order, so converting right after the
+// load would wait for every weight load issued before it.  opaque_bits at the
+// point of use pins the conversion (and the wait) there; without it the
+// compiler may hoist a loop-invariant conversion back up to the load.
+__device__ __forceinline__ uint32_t load_bits(const void* p, int64_t i, int dt) {
+  return dt == FTM_DT_F32 ? ((const uint32_t*)p)[i] : (uint32_t)((const uint16_t*)p)[i];
+}
+__device__ __forceinline__ float bits_to_f32(uint32_t b, int dt) {
+  if (dt == FTM_DT_F32) return __uint_as_float(b);
+  if (dt == FTM_DT_F16) return f16_to_f32((uint16_t)b);
+  return __uint_as_float(b << 16);
+}
+__device__ __forceinline__ uint32_t opaque_bits(uint32_t b) {
+  asm volatile("" : "+v"(b));
+  return b;
+}
+
 __device__ __forceinline__ void store_scalar(void* p, int64_t i, int dt, float v) {
   if (dt == FTM_DT_F32) ((float*)p)[i] = v;
   else if (dt == FTM_DT_F16) ((uint16_t*)p)[i] = f32_to_f16(v);

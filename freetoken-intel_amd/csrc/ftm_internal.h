@@ -51,8 +51,18 @@ constexpr int kMaxExperts = 512;
 constexpr int kCtrlTileCnt = kCtrlExpertCnt + kMaxExperts;  // [H/64] combine arrivals
 constexpr int kMaxColTiles = FTM_WS_CTRL_BYTES / 4 - kCtrlTileCnt;
 
+// MXFP4 decode: the layer input quantised for the scaled fp8 x fp4 MFMAs.
+// Per token row, per 128-element chunk of the hidden dimension, kMxChunk
+// bytes: 128 e4m3 "hi" values, 128 e4m3 "lo" values, then the e8m0 scale
+// bytes of the chunk's four 32-element blocks as (hi, lo) pairs and 8 zero
+// bytes.  x = hi * 2^(s_hi - 127) + lo * 2^(s_lo - 127) reproduces every bf16
+// input within 2^-13 of its block's maximum exactly (rows past the hidden
+// size are zeros).
+constexpr int kMxChunk = 272;
+__host__ __device__ inline int mx_row_bytes(int H) { return (H + 127) / 128 * kMxChunk; }
+
 struct WsLayout {
-  size_t misc, logits, wts, ids, lists, uniq, ucnt, recs, hbuf, ybuf, total;
+  size_t misc, logits, wts, ids, lists, uniq, ucnt, recs, hbuf, ybuf, xq, total;
   int T, E, KP, Imax;
 };
 
@@ -77,13 +87,17 @@ inline WsLayout ws_layout(const ftm_moe_layer& L, int T) {
   w.recs = o;   o = align_up(o + 4 * (size_t)kRecWords * (w.E + 1), 256);
   w.hbuf = o;   o = align_up(o + act * Tt * w.KP * w.Imax, 256);
   w.ybuf = o;   o = align_up(o + 4 * Tt * w.KP * (size_t)L.hidden, 256);
+  const bool mx = L.w13.fmt == FTM_FMT_MXFP4 && L.act_dtype == FTM_DT_BF16;
+  w.xq = o;     o = align_up(o + (mx ? Tt * (size_t)mx_row_bytes(L.hidden) : 0), 256);
   w.total = o;
   return w;
 }
 
 // ---- launchers (ftm_moe.hip); all return hipError_t of the launch
+// quant: also quantise the input for the MXFP4 stage A (mx_stage_a) in the
+// same launch; the expert stages are then launched with xq_ready.
 hipError_t launch_router(const ftm_moe_layer& L, const void* x, int T, int row_begin, int row_end, char* ws,
-                         const WsLayout& wl, hipStream_t st);
+                         const WsLayout& wl, hipStream_t st, bool quant = false);
 hipError_t launch_topk(const ftm_moe_layer& L, int T, const void* logits_in, int logits_dt,
                        const int32_t* ids_in, const float* w_in, int32_t* ids_out, float* w_out,
                        float* logits_out, char* ws, const WsLayout& wl, hipStream_t st);
@@ -94,9 +108,14 @@ struct RouteOut {
   float* logits;
 };
 // ro: route inside the expert stages where lean_route_ok allows it (the caller
-// then launches no top-k); which: bit 0 = stage A, bit 1 = stage B, bit 2 = combine.
+// then launches no top-k); which: bit 0 = stage A, bit 1 = stage B, bit 2 = combine;
+// xq_ready: the router launch has quantised the input (launch_router's quant).
 hipError_t launch_experts(const ftm_moe_layer& L, const void* x, int T, void* out, char* ws,
-                          const WsLayout& wl, hipStream_t st, int which = 7, const RouteOut* ro = nullptr);
+                          const WsLayout& wl, hipStream_t st, int which = 7, const RouteOut* ro = nullptr,
+                          bool xq_ready = false);
+// Stage A of MXFP4 layers on scaled MFMAs over the quantised input (the xq
+// workspace region, written by k_quant_mx or a router launch with quant).
+bool mx_stage_a(const ftm_moe_layer& L, int T);
 // Prefill side of the crossover (ftm_gemm.hip): whether the tiled GEMM stages
 // take this layer at T tokens, and their launch (which: bit 0 = w13, bit 1 = w2).
 bool gemm_path_ok(const ftm_moe_layer& L, int T);
@@ -129,7 +148,7 @@ inline bool lean_route_ok(const ftm_moe_layer& L, int T) {
 // not route inside stage A: bf16 activations, a router matrix, T <= 16.
 bool route_topk_fused(const ftm_moe_layer& L, int T);
 hipError_t launch_route_topk(const ftm_moe_layer& L, const void* x, int T, int32_t* ids_out, float* w_out,
-                             float* logits_out, char* ws, const WsLayout& wl, hipStream_t st);
+                             float* logits_out, char* ws, const WsLayout& wl, hipStream_t st, bool quant = false);
 
 hipError_t launch_linear(const ftm_proj& P, int slot, const void* x, int x_dt, int M, void* out,
                          int out_dt, const void* bias, int bias_dt, int final_dt, hipStream_t st);

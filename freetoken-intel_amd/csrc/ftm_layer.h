@@ -30,6 +30,7 @@ struct LayerArgs {
   int32_t* recs;    // [E+1, kRecWords] work records of the routed experts
   char* hbuf;       // [T*KP, Imax] act dtype
   float* ybuf;      // [T*KP, H]
+  uint8_t* xq;      // [T, mx_row_bytes(H)]  MXFP4 layers: the quantised input (kMxChunk layout)
 };
 
 inline LayerArgs make_args(const ftm_moe_layer& L, const void* x, void* out, int T, char* ws,
@@ -56,6 +57,7 @@ inline LayerArgs make_args(const ftm_moe_layer& L, const void* x, void* out, int
   a.recs = (int32_t*)(ws + wl.recs);
   a.hbuf = ws + wl.hbuf;
   a.ybuf = (float*)(ws + wl.ybuf);
+  a.xq = (uint8_t*)(ws + wl.xq);
   return a;
 }
 

@@ -33,6 +33,104 @@
 
 namespace ftm {
 
+// ---------------------------------------------------------------- MXFP4 decode on scaled MFMAs
+// The routed MXFP4 rows of stage A run on v_mfma_scale_f32_16x16x128_f8f6f4:
+// the weights go in as they are stored (e2m1 nibbles, e8m0 block scales) and
+// the activations as two e4m3 terms with e8m0 block scales (k_quant_mx), so
+// no weight is decoded by the vector ALUs.  Operand layout of one 16 x 16 x
+// 128 step (columns = 16 weight rows, K = one wave-load):
+//   B (e2m1): lane l holds K [32 g, 32 g + 32) of column l % 16 (g = l / 16)
+//             in its 4 low registers -- the 16 bytes a K-major wave-load
+//             puts there -- and that block's scale in scale_b;
+//   A (e4m3): lane l holds token row l % 16 at K [16 g, 16 g + 16) and
+//             [64 + 16 g, 64 + 16 g + 16) (8 registers), and in scale_a the
+//             scale of the row's block g (K [32 g, 32 g + 32)).
+typedef int i32x8 __attribute__((ext_vector_type(8)));
+
+// |v| < 448 to e4m3fn, round to nearest even (the callers keep |v| < 257).
+__device__ __forceinline__ uint32_t f32_to_e4m3(float v) {
+  const uint32_t sgn = (__float_as_uint(v) >> 24) & 0x80u;
+  const float a = fabsf(v);
+  uint32_t code;
+  if (a < 0x1p-6f) {
+    // subnormals: steps of 2^-9 (8 steps round up to the smallest normal, code 8)
+    code = (uint32_t)__builtin_rintf(a * 512.0f);
+  } else {
+    const uint32_t ab = __float_as_uint(a);
+    const float m = __uint_as_float((ab & 0x7fffffu) | 0x3f800000u);  // significand in [1, 2)
+    // a carry of the rounded mantissa moves into the exponent field
+    code = ((ab >> 23) - 120u) * 8u + (uint32_t)__builtin_rintf((m - 1.0f) * 8.0f);
+  }
+  return sgn | code;
+}
+__device__ __forceinline__ float e4m3_to_f32(uint32_t c) {
+  const uint32_t e = (c >> 3) & 15u, m = c & 7u;
+  const float mag = e == 0 ? (float)m * 0x1p-9f : __uint_as_float(((e + 120u) << 23) | (m << 20));
+  return (c & 0x80u) ? -mag : mag;
+}
+
+// One 32-element block of a token row (T rows of H bf16) per 4 lanes, 8
+// elements a lane: with E = floor(log2 max|x|) the hi scale is 2^(E - 7), so
+// the block maps into [-256, 256); hi = e4m3(x / s_hi) and lo = e4m3((x /
+// s_hi - hi) * 16) with s_lo = s_hi / 16.  The residual of a bf16 value is
+// exact in fp32 and, for |x| >= 2^(E - 13), exact in e4m3, so hi + lo is the
+// input itself there (the smaller ones are off by at most 2^(E - 21)).
+// Blocks past H are zeros; a block holding Inf or NaN gets NaN scales (0xff).
+// Piece i (8 elements) of the T x H input; callers run whole quads of lanes
+// (i and the piece count are multiples of 4 at every quad boundary).
+__device__ __forceinline__ void quant_mx_piece(const uint16_t* __restrict__ x, int T, int H,
+                                               uint8_t* __restrict__ xq, int i) {
+  const int nq = (H + 127) / 128 * 16;  // 8-element pieces of a row, padding included
+  if (i >= T * nq) return;  // whole quads (blocks) leave together
+  const int t = i / nq, q = i - t * nq;
+  const int k0 = 8 * q;
+  u32x4 w = (u32x4){0u, 0u, 0u, 0u};
+  if (k0 < H) w = *(const u32x4*)(x + (size_t)t * H + k0);  // H % 32 == 0: a block is whole or past the end
+  float v[8];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    v[2 * j] = __uint_as_float(w[j] << 16);
+    v[2 * j + 1] = __uint_as_float(w[j] & 0xffff0000u);
+  }
+  // largest |x| bit pattern of the block (Inf and NaN: >= 0x7f800000)
+  int mb = 0;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) mb = max(mb, (int)(__float_as_uint(v[j]) & 0x7fffffffu));
+  mb = max(mb, dpp_i<kDppXor1>(mb));
+  mb = max(mb, dpp_i<kDppXor2>(mb));
+  // E + 120 clamped to >= 0 (amax < 2^-120 keeps |x / s_hi| < 2^8 as well)
+  const uint32_t chi = (uint32_t)max((mb >> 23) - 7, 0);
+  const uint32_t clo = chi >= 4u ? chi - 4u : 0u;
+  const float inv = __uint_as_float((254u - chi) << 23);        // 1 / s_hi
+  const float flo = __uint_as_float((127u + chi - clo) << 23);  // s_hi / s_lo
+  uint32_t hw[2], lw[2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    hw[h] = lw[h] = 0u;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float sv = v[4 * h + j] * inv;
+      const uint32_t c = f32_to_e4m3(sv);
+      hw[h] |= c << (8 * j);
+      lw[h] |= f32_to_e4m3((sv - e4m3_to_f32(c)) * flo) << (8 * j);
+    }
+  }
+  const int c = q >> 4, p = q & 15;
+  uint8_t* o = xq + (size_t)t * (size_t)((H + 127) / 128 * kMxChunk) + (size_t)c * kMxChunk;
+  *(u32x2*)(o + 8 * p) = (u32x2){hw[0], hw[1]};
+  *(u32x2*)(o + 128 + 8 * p) = (u32x2){lw[0], lw[1]};
+  if ((p & 3) == 0) *(uint16_t*)(o + 256 + (p >> 1)) = (uint16_t)(mb < 0x7f800000 ? (chi | (clo << 8)) : 0xffffu);
+  if (p == 0) *(u32x2*)(o + 264) = (u32x2){0u, 0u};
+}
+
+__host__ __device__ __forceinline__ int quant_mx_threads(int T, int H) { return T * ((H + 127) / 128 * 16); }
+
+// The quantisation as a launch of its own (when no router launch carries it).
+__global__ __launch_bounds__(kBlock) void k_quant_mx(const uint16_t* __restrict__ x, int T, int H,
+                                                     uint8_t* __restrict__ xq) {
+  quant_mx_piece(x, T, H, xq, blockIdx.x * kBlock + threadIdx.x);
+}
+
 // ============================================================== router GEMV
 // logit = round_act( sum_k x[k]*G[k] (+ b) ).  The fp32 sum has a fixed order
 // (per lane: 8-element chunks c = lane + 64*s in ascending s, fma in element
@@ -100,8 +198,15 @@ __device__ __forceinline__ void router_row_tile(const LayerArgs& a, int r, int t
   }
 }
 
-__global__ __launch_bounds__(kBlock) void k_router(const LayerArgs a, int row_begin) {
+// Workgroups past `rows` (first token block only) quantise the input for the
+// MXFP4 scaled-MFMA stage A instead (quant_mx_piece), off its critical path.
+__global__ __launch_bounds__(kBlock) void k_router(const LayerArgs a, int row_begin, int rows) {
   const int wave = threadIdx.x >> 6;
+  if ((int)blockIdx.x >= rows) {
+    if (blockIdx.y == 0)
+      quant_mx_piece((const uint16_t*)a.x, a.T, a.L.hidden, a.xq, ((int)blockIdx.x - rows) * kBlock + threadIdx.x);
+    return;
+  }
   router_row_tile(a, row_begin + blockIdx.x, blockIdx.y * 4 * kRouterTPW + wave);
 }
 
@@ -223,6 +328,12 @@ __device__ __forceinline__ void router_rows_tile(const LayerArgs& a, int r0, int
 
 __global__ __launch_bounds__(kBlock) void k_router_rows(const LayerArgs a, int row_begin, int row_end) {
   const int wave = threadIdx.x >> 6;
+  const int rb = (row_end - row_begin + kRouterRB - 1) / kRouterRB;
+  if ((int)blockIdx.x >= rb) {  // as in k_router
+    if (blockIdx.y == 0)
+      quant_mx_piece((const uint16_t*)a.x, a.T, a.L.hidden, a.xq, ((int)blockIdx.x - rb) * kBlock + threadIdx.x);
+    return;
+  }
   router_rows_tile(a, row_begin + blockIdx.x * kRouterRB, row_end, blockIdx.y * 4 * kRouterTPW + wave * kRouterTPW);
 }
 
@@ -681,13 +792,19 @@ __global__ __launch_bounds__(64 * kTopk1Waves) void k_route_topk1(const LayerArg
   __shared__ int s_last;
   const int wave = threadIdx.x >> 6;
   static_assert(kRouteRows * 4 == kTopk1Waves && 4 * kRouterTPW >= kTopk1MaxT, "16 waves: 4 rows x 16 tokens");
+  const int nrwg = (row_end + kRouteRows - 1) / kRouteRows;
+  if ((int)blockIdx.x >= nrwg) {  // workgroups past the router's quantise the input (as in k_router)
+    quant_mx_piece((const uint16_t*)a.x, a.T, a.L.hidden, a.xq,
+                   ((int)blockIdx.x - nrwg) * (64 * kTopk1Waves) + threadIdx.x);
+    return;
+  }
   const int r = (int)blockIdx.x * kRouteRows + (wave & 3);
   if (r < row_end) router_row_tile(a, r, wave >> 2);
   // publish this workgroup's logits; the last arrival sees every workgroup's
   __syncthreads();
   if (threadIdx.x < 64) {
     __threadfence();
-    if (threadIdx.x == 0) s_last = (atomicAdd(&a.ctrl[kCtrlArriveTopk], 1) == (int)gridDim.x - 1);
+    if (threadIdx.x == 0) s_last = (atomicAdd(&a.ctrl[kCtrlArriveTopk], 1) == nrwg - 1);
     __threadfence();
   }
   __syncthreads();
@@ -1624,33 +1741,85 @@ __device__ __forceinline__ void block_pairs(const LayerArgs& a, const ExpertRec*
   }
 }
 
-// Copies elements [k0, k1) of the rows of the pairs pr (-1 = none) into xw
-// (row i at xw + i * pitch).  Row of pair p: src + (p / div) * row_elems
-// elements.  Returns after issuing the direct global->LDS loads.
-__device__ __forceinline__ void xl_fill_wave(const int (&pr)[kXT], const void* src, int div, int row_elems, int k0,
-                                             int k1, uint16_t* xw, int pitch) {
+// Copies bytes [b0, b0 + nbytes) of the rows of the pairs pr (-1 = none)
+// into dst (row i at dst + i * pitch bytes).  Row of pair p: src + (p / div) *
+// row_bytes.  Returns after issuing the direct global->LDS loads (16 bytes a
+// lane; b0, nbytes, row_bytes and pitch are multiples of 16).
+__device__ __forceinline__ void lds_fill_rows(const int (&pr)[kXT], const void* src, int div, size_t row_bytes,
+                                              size_t b0, uint32_t nbytes, char* dst, uint32_t pitch) {
   typedef __attribute__((address_space(1))) const void* GPtr;
   typedef __attribute__((address_space(3))) void* LPtr;
   const uint32_t lane = threadIdx.x & 63;
-  const uint32_t nbytes = 2u * (uint32_t)(k1 - k0);
 #pragma unroll
   for (int i = 0; i < kXT; ++i) {
     if (pr[i] >= 0) {
-      const char* row = (const char*)src + ((size_t)(pr[i] / div) * (size_t)row_elems + (size_t)k0) * 2u;
-      char* dst = (char*)(xw + i * pitch);
+      const char* row = (const char*)src + (size_t)(pr[i] / div) * row_bytes + b0;
+      char* d = dst + i * pitch;
       for (uint32_t c = 0; c < nbytes; c += 16u * kWave) {
         if (c + 16u * lane < nbytes)
-          __builtin_amdgcn_global_load_lds((GPtr)(row + c + 16u * lane), (LPtr)(dst + c), 16, 0, 0);
+          __builtin_amdgcn_global_load_lds((GPtr)(row + c + 16u * lane), (LPtr)(d + c), 16, 0, 0);
       }
+    }
+  }
+}
+
+// Elements [k0, k1) of bf16 rows of row_elems elements (see lds_fill_rows).
+__device__ __forceinline__ void xl_fill_wave(const int (&pr)[kXT], const void* src, int div, int row_elems, int k0,
+                                             int k1, uint16_t* xw, int pitch) {
+  lds_fill_rows(pr, src, div, 2u * (size_t)row_elems, 2u * (size_t)k0, 2u * (uint32_t)(k1 - k0), (char*)xw,
+                2u * (uint32_t)pitch);
+}
+
+// LDS bytes per token row of one wave's region on the MX path: its wave-loads'
+// chunks plus 16 (shifts banks).
+__host__ __device__ __forceinline__ int mx_pitch(int nL, int split) {
+  return (nL + split - 1) / split * kMxChunk + 16;
+}
+
+// rows_consume_lds for the MX path: xs holds the block's token rows as
+// chunks from wave-load L_lo on (nb rows, `pitch` bytes apart).  No zero
+// row: MFMA rows >= nb read row 0 (their outputs are never stored; an MFMA
+// row depends on its own A row only), and wave-loads past L_hi read the last
+// chunk in range against zero weights (out-of-range weight loads return 0,
+// scale 2^-127), which adds 0 since every quantised value is finite.
+template <int NLW, int NT>
+__device__ __forceinline__ void rows_consume_mx(int Lw, int L_lo, int L_hi,
+                                                const RowStream<FTM_FMT_MXFP4, NLW> (&S)[NT], const uint8_t* xs,
+                                                int pitch, int nb, f32x4 (&acc)[NT]) {
+  const int lane = threadIdx.x & 63;
+  const int g = lane >> 4;
+  const int m = lane & 15;
+  const uint8_t* rb = xs + (m < nb ? m : 0) * pitch - L_lo * kMxChunk;
+#pragma unroll
+  for (int b = 0; b < NLW; ++b) {
+    const int L = Lw + b;
+    const uint8_t* cb = rb + min(L, L_hi - 1) * kMxChunk;
+    const u32x4 h0 = *(const u32x4*)(cb + 16 * g);
+    const u32x4 h1 = *(const u32x4*)(cb + 64 + 16 * g);
+    const u32x4 l0 = *(const u32x4*)(cb + 128 + 16 * g);
+    const u32x4 l1 = *(const u32x4*)(cb + 192 + 16 * g);
+    const uint32_t sc = *(const uint16_t*)(cb + 256 + 2 * g);
+    const i32x8 ahi = {(int)h0.x, (int)h0.y, (int)h0.z, (int)h0.w, (int)h1.x, (int)h1.y, (int)h1.z, (int)h1.w};
+    const i32x8 alo = {(int)l0.x, (int)l0.y, (int)l0.z, (int)l0.w, (int)l1.x, (int)l1.y, (int)l1.z, (int)l1.w};
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      const u32x4 r = S[t].raw[b];
+      const i32x8 bw = {(int)r.x, (int)r.y, (int)r.z, (int)r.w, 0, 0, 0, 0};
+      const int e8 = ((S[t].vmask >> b) & 1u) ? (int)((S[t].sw[b] >> S[t].sh) & 0xffu) : 0;
+      acc[t] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(ahi, bw, acc[t], 0, 4, 0, (int)(sc & 0xffu), 0, e8);
+      acc[t] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(alo, bw, acc[t], 0, 4, 0, (int)(sc >> 8), 0, e8);
     }
   }
 }
 
 // Stage A item body: NT x 8 channels (per tile 8 gate + 8 up rows) of one
 // expert, K split over the 4 waves and reduced through LDS.
-template <int EFMT, int NT, int LPG>
+// MX: MXFP4 rows on scaled MFMAs, activations from the quantised input xq.
+// NLW: wave-loads per prefetch window.
+template <int EFMT, int NT, int LPG, bool MX = false, int NLW = kRowsNLW>
 __device__ void stage_a_xl_body(const LayerArgs& a, const ProjSlot& W, int Iu, int c0, int cnt,
                                 const ExpertRec* rec, const int32_t* list, int shared_col, int kp, f32x4* red) {
+  static_assert(!MX || EFMT == FTM_FMT_MXFP4, "scaled MFMAs take MXFP4 rows");
   using F = KMajor<EFMT>;
   constexpr int KS = 4;
   const int lane = threadIdx.x & 63;
@@ -1658,46 +1827,54 @@ __device__ void stage_a_xl_body(const LayerArgs& a, const ProjSlot& W, int Iu, i
   const int H = a.L.hidden;
   const int nL = fmt_loads<EFMT>(W.K);
   const int L_lo = kp * nL / KS, L_hi = (kp + 1) * nL / KS;
-  const bool multi = L_hi - L_lo > kRowsNLW;
+  const bool multi = L_hi - L_lo > NLW;
   RowGeom<EFMT> G[NT];
-  RowStream<EFMT, kRowsNLW> S[NT];
+  RowStream<EFMT, NLW> S[NT];
 #pragma unroll
   for (int t = 0; t < NT; ++t) {
     const int ct = c0 + 8 * t;
     const int lrow = n < 8 ? ct + n : Iu + ct + (n - 8);
     G[t] = RowGeom<EFMT>(W, lrow, W.group > 0 ? ct / W.group : 0, W.group > 0 ? (Iu + ct) / W.group : 0);
-    rows_issue<EFMT, kRowsNLW, true>(W, G[t], L_lo, L_hi, S[t]);
+    rows_issue<EFMT, NLW, true>(W, G[t], L_lo, L_hi, S[t]);
   }
-  const int pitch = xl_pitch(H, KS);
+  const int pitch = MX ? mx_pitch(nL, KS) : xl_pitch(H, KS);
   uint16_t* xw = ftm_xl_lds + kp * kXR * pitch;
-  xl_zero_row(xw, pitch);
+  uint8_t* xm = (uint8_t*)ftm_xl_lds + kp * kXT * pitch;  // MX: kXT rows, no zero row
+  if constexpr (!MX) xl_zero_row(xw, pitch);
   const int k0 = L_lo * F::kLoadK, k1 = min(L_hi * F::kLoadK, W.K);
-  float bg[NT], bu[NT];
+  uint32_t bg[NT], bu[NT];  // bias bits, converted in the epilogue
 #pragma unroll
   for (int t = 0; t < NT; ++t) {
-    bg[t] = bu[t] = 0.0f;
+    bg[t] = bu[t] = 0u;
     if (W.bias != nullptr && n < 8 && kp == 0) {
-      bg[t] = load_scalar(W.bias, c0 + 8 * t + n, W.bias_dt);
-      bu[t] = load_scalar(W.bias, Iu + c0 + 8 * t + n, W.bias_dt);
+      bg[t] = load_bits(W.bias, c0 + 8 * t + n, W.bias_dt);
+      bu[t] = load_bits(W.bias, Iu + c0 + 8 * t + n, W.bias_dt);
     }
   }
   for (int mb = 0; mb < cnt; mb += kXT) {
     const int nb = min(kXT, cnt - mb);
     int pr[kXT];
     block_pairs(a, rec, list, shared_col, cnt, mb, pr);
-    xl_fill_wave(pr, a.x, a.KP, H, k0, k1, xw, pitch);
+    if constexpr (MX)
+      lds_fill_rows(pr, a.xq, a.KP, (size_t)mx_row_bytes(H), (size_t)L_lo * kMxChunk,
+                    (uint32_t)(L_hi - L_lo) * kMxChunk, (char*)xm, (uint32_t)pitch);
+    else
+      xl_fill_wave(pr, a.x, a.KP, H, k0, k1, xw, pitch);
     f32x4 acc[NT];
 #pragma unroll
     for (int t = 0; t < NT; ++t) acc[t] = (f32x4){0.f, 0.f, 0.f, 0.f};
-    for (int Lw = L_lo; Lw < L_hi; Lw += kRowsNLW) {
+    for (int Lw = L_lo; Lw < L_hi; Lw += NLW) {
       // further windows, or the first again for a later token block when the
       // range needs several (re-reads hit L2)
       if (Lw != L_lo || (mb > 0 && multi)) {
 #pragma unroll
-        for (int t = 0; t < NT; ++t) rows_issue<EFMT, kRowsNLW, true>(W, G[t], Lw, L_hi, S[t]);
+        for (int t = 0; t < NT; ++t) rows_issue<EFMT, NLW, true>(W, G[t], Lw, L_hi, S[t]);
       }
       __builtin_amdgcn_s_waitcnt(0);  // weights and this wave's LDS copy have landed
-      rows_consume_lds<EFMT, kRowsNLW, NT, LPG, true>(W, G, Lw, L_hi, S, xw, k0, pitch, nb, kXT, acc);
+      if constexpr (MX)
+        rows_consume_mx<NLW, NT>(Lw, L_lo, L_hi, S, xm, pitch, nb, acc);
+      else
+        rows_consume_lds<EFMT, NLW, NT, LPG, true>(W, G, Lw, L_hi, S, xw, k0, pitch, nb, kXT, acc);
     }
     // MFMA rows 0..kXT-1 (the block's tokens) live in lanes 0..15
     if (lane < 16) {
@@ -1711,10 +1888,12 @@ __device__ void stage_a_xl_body(const LayerArgs& a, const ProjSlot& W, int Iu, i
         f32x4 v = red[t * KS * 16 + n];
 #pragma unroll
         for (int j = 1; j < KS; ++j) v += red[(t * KS + j) * 16 + n];
+        const float bgf = bits_to_f32(opaque_bits(bg[t]), W.bias_dt);
+        const float buf = bits_to_f32(opaque_bits(bu[t]), W.bias_dt);
 #pragma unroll
         for (int r = 0; r < kXT; ++r) {
-          const float gs = v[r] + bg[t];
-          const float us = dpp_f<kDppRowShl8>(v[r]) + bu[t];
+          const float gs = v[r] + bgf;
+          const float us = dpp_f<kDppRowShl8>(v[r]) + buf;
           if (lane < 8 && r < nb) {
             const float h = act_fn(a.L.act, gs, us, a.L.swiglu_alpha, a.L.swiglu_limit);
             store_scalar(a.hbuf, (size_t)pr[r] * a.Imax + c0 + 8 * t + n, FTM_DT_BF16, h);
@@ -1726,9 +1905,14 @@ __device__ void stage_a_xl_body(const LayerArgs& a, const ProjSlot& W, int Iu, i
   }
 }
 
-// NT x 8 channels per workgroup: routed items first, then the shared expert's.
-template <int FMT, int NT, int LPG>
-__global__ __launch_bounds__(kBlock) void k_stage_a_xl(const LayerArgs a) {
+// NT x 8 channels per workgroup: routed items first, then the shared expert's
+// (SH = false: a layer without one).  Without the bf16 body the kernel is
+// held to 5 waves per SIMD (<= 102 registers): measured on MI355X (C4 MXFP4
+// T=32, scaled-MFMA rows) 72.2 us against 76.8 at the compiler's 116
+// registers (4 waves) and 92.2 at 6 waves (spills).
+template <int FMT, int NT, int LPG, int NLWM = kRowsNLW, bool SH = true>
+__global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(SH ? 1 : 5))) void k_stage_a_xl(
+    const LayerArgs a) {
   __shared__ f32x4 red[NT * 4 * 16];
   const int kp = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int I = a.L.inter;
@@ -1743,9 +1927,9 @@ __global__ __launch_bounds__(kBlock) void k_stage_a_xl(const LayerArgs a) {
       return;
     }
     const ProjSlot W = proj_slot(a.L.w13, rec.slot);
-    stage_a_xl_body<FMT, NT, LPG>(a, W, I, (item % ti) * 8 * NT, rec.cnt, &rec, a.lists + (size_t)rec.e * a.T, 0,
-                                  kp, red);
-  } else {
+    stage_a_xl_body<FMT, NT, LPG, FMT == FTM_FMT_MXFP4, NLWM>(a, W, I, (item % ti) * 8 * NT, rec.cnt, &rec,
+                                                         a.lists + (size_t)rec.e * a.T, 0, kp, red);
+  } else if constexpr (SH) {
     const int sitem = item - nRouted * ti;
     const int Is = a.L.shared_inter;
     if (Is <= 0 || sitem >= Is / (8 * NT)) return;
@@ -1777,7 +1961,7 @@ __device__ void stage_b_ks_body(const LayerArgs& a, const ProjSlot& W, int c0, i
   uint16_t* xw = ftm_xl_lds + kp * kXR * pitch;
   xl_zero_row(xw, pitch);
   const int k0 = L_lo * F::kLoadK, k1 = min(L_hi * F::kLoadK, W.K);
-  const float bn = (W.bias != nullptr && kp == 0) ? load_scalar(W.bias, c0 + n, W.bias_dt) : 0.0f;
+  const uint32_t bn = (W.bias != nullptr && kp == 0) ? load_bits(W.bias, c0 + n, W.bias_dt) : 0u;  // epilogue
   for (int mb = mb0; mb < cnt; mb += kXT) {
     const int nb = min(kXT, cnt - mb);
     int pr[kXT];
@@ -1796,11 +1980,12 @@ __device__ void stage_b_ks_body(const LayerArgs& a, const ProjSlot& W, int c0, i
       f32x4 v = red[n];
 #pragma unroll
       for (int j = 1; j < KS; ++j) v += red[j * 16 + n];
+      const float bnf = bits_to_f32(opaque_bits(bn), W.bias_dt);
 #pragma unroll
       for (int r = 0; r < kXT; ++r)
         if (r < nb) {
           const float wr = __uint_as_float(sload4(a.wts, 4u * (uint32_t)pr[r]));  // router weight or shared gate
-          a.ybuf[(size_t)pr[r] * H + c0 + n] = (v[r] + bn) * wr;
+          a.ybuf[(size_t)pr[r] * H + c0 + n] = (v[r] + bnf) * wr;
         }
     }
     __syncthreads();
@@ -2624,15 +2809,18 @@ hipError_t launch_ws_init(void* ws, hipStream_t st) {
 }
 
 hipError_t launch_router(const ftm_moe_layer& L, const void* x, int T, int row_begin, int row_end, char* ws,
-                         const WsLayout& wl, hipStream_t st) {
+                         const WsLayout& wl, hipStream_t st, bool quant) {
   const LayerArgs a = make_args(L, x, nullptr, T, ws, wl);
   if (row_end - row_begin <= 0 || T <= 0) return hipSuccess;
   const int tpb = 4 * kRouterTPW;
+  const int nq = quant && mx_stage_a(L, T) ? (quant_mx_threads(T, L.hidden) + kBlock - 1) / kBlock : 0;
   if (T >= kRouterMinT)
-    hipLaunchKernelGGL(k_router_rows, dim3((row_end - row_begin + kRouterRB - 1) / kRouterRB, (T + tpb - 1) / tpb),
+    hipLaunchKernelGGL(k_router_rows,
+                       dim3((row_end - row_begin + kRouterRB - 1) / kRouterRB + nq, (T + tpb - 1) / tpb),
                        dim3(kBlock), 0, st, a, row_begin, row_end);
   else
-    hipLaunchKernelGGL(k_router, dim3(row_end - row_begin, (T + tpb - 1) / tpb), dim3(kBlock), 0, st, a, row_begin);
+    hipLaunchKernelGGL(k_router, dim3(row_end - row_begin + nq, (T + tpb - 1) / tpb), dim3(kBlock), 0, st, a,
+                       row_begin, row_end - row_begin);
   return hipGetLastError();
 }
 
@@ -2642,10 +2830,11 @@ bool route_topk_fused(const ftm_moe_layer& L, int T) {
 }
 
 hipError_t launch_route_topk(const ftm_moe_layer& L, const void* x, int T, int32_t* ids_out, float* w_out,
-                             float* logits_out, char* ws, const WsLayout& wl, hipStream_t st) {
+                             float* logits_out, char* ws, const WsLayout& wl, hipStream_t st, bool quant) {
   const LayerArgs a = make_args(L, x, nullptr, T, ws, wl);
   const int rows = L.num_experts + (L.shared_inter > 0 ? 1 : 0);
-  const dim3 grid((rows + kRouteRows - 1) / kRouteRows), block(64 * kTopk1Waves);
+  const int nq = quant && mx_stage_a(L, T) ? (quant_mx_threads(T, L.hidden) + 64 * kTopk1Waves - 1) / (64 * kTopk1Waves) : 0;
+  const dim3 grid((rows + kRouteRows - 1) / kRouteRows + nq), block(64 * kTopk1Waves);
 #define FTM_RT_NV(M)                                                                                         \
   if (L.num_experts <= 256)                                                                                  \
     hipLaunchKernelGGL((k_route_topk1<M, 4>), grid, block, 0, st, a, rows, ids_out, w_out, logits_out);     \
@@ -2752,12 +2941,18 @@ static XlPlan xl_plan_a(const ftm_moe_layer& L, int T) {
     if (!pf_window_fits<FMT>(L.hidden, 4)) return p;
     if (L.hidden % 8 != 0) return p;
     if (4 * kXR * xl_pitch(L.hidden, 4) * 2 > kDynLdsMax) return p;
+    if (FMT == FTM_FMT_MXFP4 && 4 * kXT * mx_pitch((L.hidden + 127) / 128, 4) > kDynLdsMax) return p;
     p.lpg = xl_lpg<FMT>(L.w13, 4);
     if (p.lpg == 0) return p;
     p.nt = 1;
     p.ok = true;
     return p;
   }
+}
+
+bool mx_stage_a(const ftm_moe_layer& L, int T) {
+  return L.w13.fmt == FTM_FMT_MXFP4 && L.act_dtype == FTM_DT_BF16 && !gemm_path_ok(L, T) &&
+         xl_plan_a<FTM_FMT_MXFP4, FTM_DT_BF16>(L, T).ok;
 }
 
 template <int FMT, int AT>
@@ -2806,7 +3001,7 @@ static XlPlan ks_plan_b(const ftm_moe_layer& L, int T) {
 
 // which: bit 0 = stage A (w13 + act), bit 1 = stage B (w2), bit 2 = combine
 template <int FMT, int AT>
-static void launch_stages(const LayerArgs& a, int gridA, int gridB, hipStream_t st, int which) {
+static void launch_stages(const LayerArgs& a, int gridA, int gridB, hipStream_t st, int which, bool xq_ready) {
   const bool lean = FMT == FTM_FMT_FP8_BLOCK && AT == FTM_DT_BF16 && a.lean;
   if (lean) {
     const int maxU = a.L.num_experts < a.T * a.L.topk ? a.L.num_experts : a.T * a.L.topk;
@@ -2854,11 +3049,33 @@ static void launch_stages(const LayerArgs& a, int gridA, int gridB, hipStream_t 
       const int items = maxU * (a.L.inter / 8) + (a.L.shared_inter > 0 ? a.L.shared_inter / 8 : 0);
       const XlPlan pa = xl_plan_a<FMT, AT>(a.L, a.T);
       if (pa.ok) {
-        const size_t lds = 4u * kXR * (size_t)xl_pitch(a.L.hidden, 4) * 2u;
+        size_t lds = 4u * kXR * (size_t)xl_pitch(a.L.hidden, 4) * 2u;
+        if (FMT == FTM_FMT_MXFP4) {
+          // routed MXFP4 rows on scaled MFMAs: quantise the input first; the
+          // bf16 regions only for a shared expert's items
+          const size_t ldm = 4u * kXT * (size_t)mx_pitch((a.L.hidden + 127) / 128, 4);
+          lds = a.L.shared_inter > 0 && lds > ldm ? lds : ldm;
+          if (!xq_ready)  // else the router launch has quantised it
+            hipLaunchKernelGGL(k_quant_mx, dim3((quant_mx_threads(a.T, a.L.hidden) + kBlock - 1) / kBlock),
+                               dim3(kBlock), 0, st, (const uint16_t*)a.x, a.T, a.L.hidden, a.xq);
+        }
         const int nt = pa.nt;
         const int itemsx = maxU * (a.L.inter / (8 * nt)) + (a.L.shared_inter > 0 ? a.L.shared_inter / (8 * nt) : 0);
-#define FTM_XLA(NT, LPG) hipLaunchKernelGGL((k_stage_a_xl<FMT, NT, LPG>), dim3(itemsx), dim3(kBlock), lds, st, a)
-        if (pa.lpg == 2) FTM_XLA(1, 2); else FTM_XLA(1, kRowsNLW);
+#define FTM_XLA(NT, LPG, NLW) \
+  hipLaunchKernelGGL((k_stage_a_xl<FMT, NT, LPG, NLW>), dim3(itemsx), dim3(kBlock), lds, st, a)
+#define FTM_XLM(NLW)                                                                                          \
+  if (a.L.shared_inter > 0)                                                                                   \
+    hipLaunchKernelGGL((k_stage_a_xl<FMT, 1, kRowsNLW, NLW, true>), dim3(itemsx), dim3(kBlock), lds, st, a); \
+  else                                                                                                        \
+    hipLaunchKernelGGL((k_stage_a_xl<FMT, 1, kRowsNLW, NLW, false>), dim3(itemsx), dim3(kBlock), lds, st, a)
+        if constexpr (FMT == FTM_FMT_MXFP4) {
+          // the window sized to a wave's range: no wave-loads past it issued or multiplied
+          const int r = ((a.L.hidden + 127) / 128 + 3) / 4;
+          if (r <= 4) { FTM_XLM(4); } else if (r <= 6) { FTM_XLM(6); } else { FTM_XLM(8); }
+#undef FTM_XLM
+        } else {
+          if (pa.lpg == 2) FTM_XLA(1, 2, kRowsNLW); else FTM_XLA(1, kRowsNLW, kRowsNLW);
+        }
 #undef FTM_XLA
       } else {
         hipLaunchKernelGGL((k_stage_a_rows<FMT, AT>), dim3(items), dim3(kBlock), 0, st, a);
@@ -2905,15 +3122,15 @@ static void launch_stages(const LayerArgs& a, int gridA, int gridB, hipStream_t 
 }
 
 template <int FMT>
-static void launch_stages_dt(const LayerArgs& a, int gridA, int gridB, hipStream_t st, int which) {
+static void launch_stages_dt(const LayerArgs& a, int gridA, int gridB, hipStream_t st, int which, bool xq_ready) {
   if (a.L.act_dtype == FTM_DT_F32)
-    launch_stages<FMT, FTM_DT_F32>(a, gridA, gridB, st, which);
+    launch_stages<FMT, FTM_DT_F32>(a, gridA, gridB, st, which, xq_ready);
   else
-    launch_stages<FMT, FTM_DT_BF16>(a, gridA, gridB, st, which);
+    launch_stages<FMT, FTM_DT_BF16>(a, gridA, gridB, st, which, xq_ready);
 }
 
 hipError_t launch_experts(const ftm_moe_layer& L, const void* x, int T, void* out, char* ws,
-                          const WsLayout& wl, hipStream_t st, int which, const RouteOut* ro) {
+                          const WsLayout& wl, hipStream_t st, int which, const RouteOut* ro, bool xq_ready) {
   if (gemm_path_ok(L, T)) {
     // above the token crossover the expert stages are tiled GEMMs
     if (which & 3) launch_gemm_stages(L, x, T, out, ws, wl, st, which & 3);
@@ -2933,11 +3150,11 @@ hipError_t launch_experts(const ftm_moe_layer& L, const void* x, int T, void* ou
   const int gridA = maxU * (L.inter / NT) + (has_sh ? L.shared_inter / 16 : 0);
   const int gridB = (maxU + has_sh) * (L.hidden / 64);
   switch (L.w13.fmt) {
-    case FTM_FMT_BF16: launch_stages_dt<FTM_FMT_BF16>(a, gridA, gridB, st, which); break;
-    case FTM_FMT_FP8_BLOCK: launch_stages_dt<FTM_FMT_FP8_BLOCK>(a, gridA, gridB, st, which); break;
-    case FTM_FMT_GPTQ_INT4: launch_stages_dt<FTM_FMT_GPTQ_INT4>(a, gridA, gridB, st, which); break;
-    case FTM_FMT_INT8_PACKED: launch_stages_dt<FTM_FMT_INT8_PACKED>(a, gridA, gridB, st, which); break;
-    case FTM_FMT_MXFP4: launch_stages_dt<FTM_FMT_MXFP4>(a, gridA, gridB, st, which); break;
+    case FTM_FMT_BF16: launch_stages_dt<FTM_FMT_BF16>(a, gridA, gridB, st, which, xq_ready); break;
+    case FTM_FMT_FP8_BLOCK: launch_stages_dt<FTM_FMT_FP8_BLOCK>(a, gridA, gridB, st, which, xq_ready); break;
+    case FTM_FMT_GPTQ_INT4: launch_stages_dt<FTM_FMT_GPTQ_INT4>(a, gridA, gridB, st, which, xq_ready); break;
+    case FTM_FMT_INT8_PACKED: launch_stages_dt<FTM_FMT_INT8_PACKED>(a, gridA, gridB, st, which, xq_ready); break;
+    case FTM_FMT_MXFP4: launch_stages_dt<FTM_FMT_MXFP4>(a, gridA, gridB, st, which, xq_ready); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();

@@ -67,3 +67,23 @@ def assert_close(got, ref, atol=ATOL, rtol=RTOL, what="output"):
 
 def to_f32(t):
     return t.detach().float().cpu().numpy()
+
+
+# Relative RMS error bound of the MXFP4 decode path (activations as two e4m3
+# terms): a bf16 output and a bf16 intermediate keep ||got - ref|| / ||ref||
+# near 2e-3; the input rounded to one e4m3 term (the lo term lost) puts it
+# near 3e-2 (the oracle-side check in test_mx_quant.py).
+MX_REL_RMS = 8e-3
+
+
+def rel_rms(got, ref) -> float:
+    got = np.asarray(got, np.float64)
+    ref = np.asarray(ref, np.float64)
+    return float(np.linalg.norm(got - ref) / max(np.linalg.norm(ref), 1e-30))
+
+
+def wide_range_x(T, H, seed):
+    """bf16 [T, H] inputs whose elements span 2^-14 .. 2^3 inside each 32-wide block."""
+    g = torch.Generator().manual_seed(seed)
+    e = torch.randint(-14, 3, (T, H), generator=g).float()
+    return (torch.randn(T, H, generator=g) * torch.exp2(e)).to(torch.bfloat16)

@@ -12,7 +12,7 @@ import pytest
 import torch
 
 import ftm_oracle as O
-from ftm_helpers import ATOL, RTOL, assert_close, np_, oracle_spec, to_f32
+from ftm_helpers import ATOL, MX_REL_RMS, RTOL, assert_close, np_, oracle_spec, rel_rms, to_f32, wide_range_x
 
 from ftmoe import synthetic as S
 
@@ -122,6 +122,31 @@ def test_c4_mxfp4_full_shape_matches_oracle(gpu, c4_full, T):
     from dataclasses import replace
 
     _run_and_check(replace(c4_full, x=c4_full.x[:T].contiguous()), gpu)
+
+
+@pytest.mark.parametrize("T", [1, 4, 13, 32])
+def test_mxfp4_decode_wide_range_inputs(gpu, T):
+    """The MXFP4 decode stage A feeds the input to scaled fp8 x fp4 MFMAs as
+    two e4m3 terms per element: with elements spanning 2^-14 .. 2^3 inside
+    every 32-wide block the output stays at bf16 precision (relative RMS
+    error MX_REL_RMS; one e4m3 term would give about 3e-2).  H = 320 is not a
+    multiple of the 128-wide chunks (zero-padded tail)."""
+    from dataclasses import replace
+
+    syn = S.generate(S.SMALL["c4_mxfp4"], T=T, seed=50 + T)
+    syn = replace(syn, x=wide_range_x(T, syn.cfg.H, seed=T))
+    _, _, ref, out = _run_and_check(syn, gpu)
+    err = rel_rms(to_f32(out), ref["out"])
+    assert err < MX_REL_RMS, err
+
+
+def test_c4_mxfp4_full_shape_wide_range_inputs(gpu, c4_full):
+    from dataclasses import replace
+
+    syn = replace(c4_full, x=wide_range_x(32, c4_full.cfg.H, seed=99).to(gpu))
+    _, _, ref, out = _run_and_check(syn, gpu)
+    err = rel_rms(to_f32(out), ref["out"])
+    assert err < MX_REL_RMS, err
 
 
 def test_c4_mxfp4_prefill_token_subset(gpu, c4_full):
