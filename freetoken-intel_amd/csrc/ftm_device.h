@@ -830,7 +830,12 @@ __device__ __forceinline__ void rows_issue(const ProjSlot& W, const RowGeom<FMT>
 // (LPG wave-loads per group, the window starting on a group boundary, or the
 // whole window inside one group when LPG == NLW) and apply the scales once at
 // the end, so no MFMA waits on a VALU read of its own result mid-window.
-template <int FMT, int NLW, int NT, int LPG, bool PAIRED>
+// NOZ: no zero row (zr unused).  MFMA rows >= nb read row 0 instead (their
+// outputs are never stored; an MFMA row depends on its own A row only), a
+// wave-load past L_hi reads the last one in range against zero weights
+// (out-of-range weight loads return 0, post-scales 0), and lanes past K read
+// the region's tail, which the caller keeps at zero.
+template <int FMT, int NLW, int NT, int LPG, bool PAIRED, bool NOZ = false>
 __device__ __forceinline__ void rows_consume_lds(const ProjSlot& W, const RowGeom<FMT> (&G)[NT], int Lw, int L_hi,
                                                  const RowStream<FMT, NLW> (&S)[NT], const uint16_t* xs, int k0,
                                                  int pitch, int nb, int zr, f32x4 (&acc)[NT]) {
@@ -842,7 +847,7 @@ __device__ __forceinline__ void rows_consume_lds(const ProjSlot& W, const RowGeo
   const bool upper = m >= 8;
   const int K = W.K;
   const uint16_t* zrow = xs + zr * pitch;
-  const int rbase = (m < nb ? m : zr) * pitch - k0;  // lane's row, element kk at rbase + kk
+  const int rbase = (m < nb ? m : NOZ ? 0 : zr) * pitch - k0;  // lane's row, element kk at rbase + kk
   constexpr int NP = F::kPostScale ? NLW / LPG : 1;
   f32x4 part[NT][NP];
 #pragma unroll
@@ -852,8 +857,8 @@ __device__ __forceinline__ void rows_consume_lds(const ProjSlot& W, const RowGeo
 #pragma unroll
   for (int b = 0; b < NLW; ++b) {
     const int L = Lw + b;
-    const int kk = L * F::kLoadK + F::kLaneK * g;
-    const uint16_t* xb = (L < L_hi) && (kk < K) ? xs + (rbase + kk) : zrow;
+    const int kk = (NOZ ? min(L, L_hi - 1) : L) * F::kLoadK + F::kLaneK * g;
+    const uint16_t* xb = NOZ ? xs + (rbase + kk) : (L < L_hi) && (kk < K) ? xs + (rbase + kk) : zrow;
 #pragma unroll
     for (int q = 0; q < F::kMfma; ++q) {
       const u32x4 av = *(const u32x4*)(xb + 8 * q);

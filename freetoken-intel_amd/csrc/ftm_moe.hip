@@ -1905,13 +1905,19 @@ __device__ void stage_a_xl_body(const LayerArgs& a, const ProjSlot& W, int Iu, i
   }
 }
 
+// Minimum waves per SIMD the LDS-activation kernels are compiled for: 5 (<=
+// 102 registers) for MXFP4 rows in windows of up to 6 wave-loads without a
+// shared expert's bf16 body, where that needs no spills; otherwise the
+// compiler's choice.  Measured on MI355X (C4 MXFP4 T=32, k_stage_a_xl with
+// scaled-MFMA rows): 72.2 us against 76.8 at the compiler's 116 registers
+// (4 waves) and 92.2 at 6 waves (spills).
+template <int FMT, int NLW, bool SH>
+constexpr int kXlWaves = (FMT == FTM_FMT_MXFP4 && NLW <= 6 && !SH) ? 5 : 1;
+
 // NT x 8 channels per workgroup: routed items first, then the shared expert's
-// (SH = false: a layer without one).  Without the bf16 body the kernel is
-// held to 5 waves per SIMD (<= 102 registers): measured on MI355X (C4 MXFP4
-// T=32, scaled-MFMA rows) 72.2 us against 76.8 at the compiler's 116
-// registers (4 waves) and 92.2 at 6 waves (spills).
+// (SH = false: a layer without one, and no bf16 body in the kernel).
 template <int FMT, int NT, int LPG, int NLWM = kRowsNLW, bool SH = true>
-__global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(SH ? 1 : 5))) void k_stage_a_xl(
+__global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(kXlWaves<FMT, NLWM, SH>))) void k_stage_a_xl(
     const LayerArgs a) {
   __shared__ f32x4 red[NT * 4 * 16];
   const int kp = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -1942,7 +1948,9 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(SH ? 1 :
 // expert, K split over the 4 waves and reduced through LDS (the stage-A xl
 // data path with plain rows).  For small batches whose 64-column items would
 // leave CUs idle and whose rows are too long for one window per wave.
-template <int EFMT, int LPG>
+// NLW: wave-loads per prefetch window; NOZ: regions of kXT rows without the
+// zero row (rows_consume_lds), their tails past K cleared once here.
+template <int EFMT, int LPG, int NLW = kRowsNLW, bool NOZ = false>
 __device__ void stage_b_ks_body(const LayerArgs& a, const ProjSlot& W, int c0, int cnt, const ExpertRec* rec,
                                 const int32_t* list, int shared_col, int kp, f32x4* red, int mb0 = 0) {
   using F = KMajor<EFMT>;
@@ -1952,15 +1960,27 @@ __device__ void stage_b_ks_body(const LayerArgs& a, const ProjSlot& W, int c0, i
   const int H = a.L.hidden;
   const int nL = fmt_loads<EFMT>(W.K);
   const int L_lo = kp * nL / KS, L_hi = (kp + 1) * nL / KS;
-  const bool multi = L_hi - L_lo > kRowsNLW;
+  const bool multi = L_hi - L_lo > NLW;
   RowGeom<EFMT> G[1];
-  RowStream<EFMT, kRowsNLW> S[1];
+  RowStream<EFMT, NLW> S[1];
   G[0] = RowGeom<EFMT>(W, c0 + n, W.group > 0 ? c0 / W.group : 0, W.group > 0 ? (c0 + 8) / W.group : 0);
-  rows_issue<EFMT, kRowsNLW, true>(W, G[0], L_lo, L_hi, S[0]);
+  rows_issue<EFMT, NLW, true>(W, G[0], L_lo, L_hi, S[0]);
   const int pitch = xl_pitch(a.Imax, KS);
-  uint16_t* xw = ftm_xl_lds + kp * kXR * pitch;
-  xl_zero_row(xw, pitch);
+  uint16_t* xw = ftm_xl_lds + kp * (NOZ ? kXT : kXR) * pitch;
   const int k0 = L_lo * F::kLoadK, k1 = min(L_hi * F::kLoadK, W.K);
+  if constexpr (NOZ) {
+    // elements [k1, L_hi * kLoadK) of each row (the last wave's only): read by
+    // lanes past K, never filled
+    const int t0 = k1 - k0, tl = L_hi * F::kLoadK - k1;
+    if (tl > 0) {
+      for (int e = lane; e < kXT * tl; e += 64) {
+        const int r = e / tl;
+        xw[r * pitch + t0 + (e - r * tl)] = 0;
+      }
+    }
+  } else {
+    xl_zero_row(xw, pitch);
+  }
   const uint32_t bn = (W.bias != nullptr && kp == 0) ? load_bits(W.bias, c0 + n, W.bias_dt) : 0u;  // epilogue
   for (int mb = mb0; mb < cnt; mb += kXT) {
     const int nb = min(kXT, cnt - mb);
@@ -1968,10 +1988,10 @@ __device__ void stage_b_ks_body(const LayerArgs& a, const ProjSlot& W, int c0, i
     block_pairs(a, rec, list, shared_col, cnt, mb, pr);
     xl_fill_wave(pr, a.hbuf, 1, a.Imax, k0, k1, xw, pitch);
     f32x4 acc[1] = {(f32x4){0.f, 0.f, 0.f, 0.f}};
-    for (int Lw = L_lo; Lw < L_hi; Lw += kRowsNLW) {
-      if (Lw != L_lo || (mb > mb0 && multi)) rows_issue<EFMT, kRowsNLW, true>(W, G[0], Lw, L_hi, S[0]);
+    for (int Lw = L_lo; Lw < L_hi; Lw += NLW) {
+      if (Lw != L_lo || (mb > mb0 && multi)) rows_issue<EFMT, NLW, true>(W, G[0], Lw, L_hi, S[0]);
       __builtin_amdgcn_s_waitcnt(0);  // weights and this wave's LDS copy have landed
-      rows_consume_lds<EFMT, kRowsNLW, 1, LPG, true>(W, G, Lw, L_hi, S, xw, k0, pitch, nb, kXT, acc);
+      rows_consume_lds<EFMT, NLW, 1, LPG, true, NOZ>(W, G, Lw, L_hi, S, xw, k0, pitch, nb, kXT, acc);
     }
     // MFMA rows 0..kXT-1 (the block's tokens) live in lanes 0..15, lane n = column c0 + n
     if (lane < 16) red[kp * 16 + lane] = acc[0];
@@ -1992,9 +2012,15 @@ __device__ void stage_b_ks_body(const LayerArgs& a, const ProjSlot& W, int c0, i
   }
 }
 
-// 16 output columns per workgroup: routed items first, then the shared expert's.
-template <int FMT, int LPG>
-__global__ __launch_bounds__(kBlock) void k_stage_b_ks(const LayerArgs a) {
+// 16 output columns per workgroup: routed items first, then the shared
+// expert's.  SH = false (a layer without one): no bf16 body, and NOZ regions
+// for the formats whose zero byte decodes to 0 (the zero weights of
+// rows_consume_lds's NOZ contract; INT8's offset-binary 0 is -128).
+template <int FMT>
+constexpr bool kKsNoz = FMT != FTM_FMT_INT8_PACKED;
+template <int FMT, int LPG, int NLWM = kRowsNLW, bool SH = true>
+__global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(kXlWaves<FMT, NLWM, SH>))) void k_stage_b_ks(
+    const LayerArgs a) {
   __shared__ f32x4 red[4 * 16];
   const int kp = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int H = a.L.hidden;
@@ -2013,8 +2039,9 @@ __global__ __launch_bounds__(kBlock) void k_stage_b_ks(const LayerArgs a) {
       if (threadIdx.x == 0) atomicOr(&a.ctrl[kCtrlError], 1);
       return;
     }
-    stage_b_ks_body<FMT, LPG>(a, proj_slot(a.L.w2, rec.slot), c0, rec.cnt, &rec, list, 0, kp, red);
-  } else {
+    stage_b_ks_body<FMT, LPG, NLWM, !SH && kKsNoz<FMT>>(a, proj_slot(a.L.w2, rec.slot), c0, rec.cnt, &rec, list, 0,
+                                                        kp, red);
+  } else if constexpr (SH) {
     const int sitem = item - nRouted * tn;
     const int Is = a.L.shared_inter;
     if (Is <= 0 || sitem >= tn) return;
@@ -3105,12 +3132,25 @@ static void launch_stages(const LayerArgs& a, int gridA, int gridB, hipStream_t 
 #undef FTM_XLB
     } else if (const XlPlan pk = ks_plan_b<FMT, AT>(a.L, a.T); pk.ok) {
       const int maxU = a.L.num_experts < a.T * a.L.topk ? a.L.num_experts : a.T * a.L.topk;
-      const size_t lds = 4u * kXR * (size_t)xl_pitch(a.Imax, 4) * 2u;  // the regions stage_b_ks_body lays out
-      const int gridk = (maxU + (a.L.shared_inter > 0 ? 1 : 0)) * (a.L.hidden / 16);
-      if (pk.lpg == 2)
-        hipLaunchKernelGGL((k_stage_b_ks<FMT, 2>), dim3(gridk), dim3(kBlock), lds, st, a);
-      else
-        hipLaunchKernelGGL((k_stage_b_ks<FMT, kRowsNLW>), dim3(gridk), dim3(kBlock), lds, st, a);
+      const bool sh = a.L.shared_inter > 0;
+      // the regions stage_b_ks_body lays out (kXT rows each when NOZ)
+      const size_t lds = 4u * (sh || !kKsNoz<FMT> ? kXR : kXT) * (size_t)xl_pitch(a.Imax, 4) * 2u;
+      const int gridk = (maxU + (sh ? 1 : 0)) * (a.L.hidden / 16);
+#define FTM_KSB(LPG, NLW)                                                                          \
+  if (sh)                                                                                          \
+    hipLaunchKernelGGL((k_stage_b_ks<FMT, LPG, NLW, true>), dim3(gridk), dim3(kBlock), lds, st, a); \
+  else                                                                                             \
+    hipLaunchKernelGGL((k_stage_b_ks<FMT, LPG, NLW, false>), dim3(gridk), dim3(kBlock), lds, st, a)
+      if constexpr (FMT == FTM_FMT_MXFP4) {
+        // the window sized to a wave's range (no post-scale groups to align)
+        const int r = ((a.L.inter + 127) / 128 + 3) / 4;
+        if (r <= 4) { FTM_KSB(4, 4); } else if (r <= 6) { FTM_KSB(6, 6); } else { FTM_KSB(kRowsNLW, kRowsNLW); }
+      } else if (pk.lpg == 2) {
+        FTM_KSB(2, kRowsNLW);
+      } else {
+        FTM_KSB(kRowsNLW, kRowsNLW);
+      }
+#undef FTM_KSB
     } else {
       hipLaunchKernelGGL((k_stage_b<FMT, AT>), dim3(gridB), dim3(kBlock), 0, st, a);
     }
