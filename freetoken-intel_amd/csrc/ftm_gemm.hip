@@ -840,9 +840,11 @@ bool gemm_path_ok(const ftm_moe_layer& L, int T) {
       (L.w13.group % kGK != 0 || L.w2.group % kGK != 0))
     return false;
   if (L.apply_router_weight_on_input) return false;
-  // above the crossover: on average at least kGemmMinRows tokens per routed expert
+  // above the crossover: on average at least kGemmMinRows tokens per routed
+  // expert (MXFP4: more than that, up to which its scaled-MFMA decode path wins)
   const long pairs = (long)T * L.topk;
   const long maxU = L.num_experts < pairs ? L.num_experts : pairs;
+  if (f == FTM_FMT_MXFP4 && T <= kXlMaxTMx) return pairs > (long)kGemmMinRows * maxU;
   return pairs >= (long)kGemmMinRows * maxU;
 }
 

@@ -25,12 +25,17 @@ constexpr int kRecPairs = 4;
 // vs 16.7, T=4 30.7 vs 34.5, T=8 54.5 vs 54.5, T=16 92.4 vs 88.1.  MXFP4
 // stage A (C4, w13 us) keeps the LDS path up to kXlMaxTMx: T=8 67.4 -> 54.8,
 // T=16 90.9 -> 76.7, and with its scale bytes fetched 16 at a time T=24
-// 106.6 -> 89.3, T=32 115.6 -> 100.1.
+// 106.6 -> 89.3, T=32 115.6 -> 100.1.  On scaled MFMAs (and the K-split
+// stage B beside it) it also beats the register-fed kernels and the GEMM
+// tiles up to 16 tokens per expert (C4, w13 + w2 us): T=64 200 -> 153 (rows
+// kernels), T=128 288 -> 235 (tiles); at T=256 (32 per expert) the tiles win,
+// 326 against 401.  MXFP4 layers therefore take the tiles only above 16
+// tokens per expert (gemm_path_ok) and the LDS path up to kXlMaxTMx tokens.
 constexpr int kXlMaxT = 4;
-constexpr int kXlMaxTMx = 32;
+constexpr int kXlMaxTMx = 256;
 // the top-k compaction writes work records up to this many tokens (the xl
 // stage A and the K-split stage B read them)
-constexpr int kRecMaxT = 32;
+constexpr int kRecMaxT = 256;
 // Decode batches up to kLeanRouteMaxT tokens (top-k up to kLeanRouteMaxK) route
 // inside the lean stage A, which takes the top-k launch out of the layer's
 // chain of dependent launches.  Every stage-A workgroup then spends ~3 us

@@ -3008,13 +3008,14 @@ static XlPlan xl_plan_b(const ftm_moe_layer& L, int T) {
 // 9.7 us, T=4 29.5 -> 20.9, T=8 38.0 -> 28.6, T=16 48.3 -> 38.3, T=24 56.2 ->
 // 46.3, T=32 60.3 -> 52.2.
 constexpr int kBksMaxT = 32;
+constexpr int kBksMaxTMx = kXlMaxTMx;  // MXFP4: beside the scaled-MFMA stage A
 template <int FMT, int AT>
 static XlPlan ks_plan_b(const ftm_moe_layer& L, int T) {
   XlPlan p{false, 1, kRowsNLW};
   if constexpr (FMT == FTM_FMT_GPTQ_INT4 || AT != FTM_DT_BF16) {
     return p;
   } else {
-    if (T > kBksMaxT || T > kRecMaxT || L.hidden % 16 != 0) return p;
+    if (T > (FMT == FTM_FMT_MXFP4 ? kBksMaxTMx : kBksMaxT) || T > kRecMaxT || L.hidden % 16 != 0) return p;
     if (!pf_window_fits<FMT>(L.inter, 4) || L.inter % 8 != 0) return p;
     if (L.shared_inter > 0 && (!pf_window_fits<FTM_FMT_BF16>(L.shared_inter, 4) || L.shared_inter % 8 != 0))
       return p;

@@ -208,16 +208,22 @@ def test_stage_kernel_names_follow_the_dispatch():
     gq.hidden = 2176  # 17 groups: a wave's half would be 1152 wide
     gq.w13.K, gq.w2.N = 2176, 2176
     assert name(gq, 4, nat.STAGE_W13) == "k_stage_a"
-    # MXFP4 (C4 shape): stage A keeps activations in LDS up to 32 tokens; stage
-    # B splits w2's 2880-wide K over the waves up to 32 (more than one window)
+    # MXFP4 (C4 shape): stage A on scaled MFMAs with activations in LDS and
+    # stage B with w2's 2880-wide K split over the waves, up to 16 tokens per
+    # expert (T = 128 on 32 experts, top-4); the GEMM tiles above
     mx = _layer(E=32, H=2880, I=2880, k=4)
     mx.w13 = _proj(N=2 * 2880, K=2880, num_slots=8, fmt=nat.FMT_MXFP4, group=32)
     mx.w2 = _proj(N=2880, K=2880, num_slots=8, fmt=nat.FMT_MXFP4, group=32)
-    for T in (1, 8, 32):
+    for T in (1, 8, 32, 64, 128):
         assert name(mx, T, nat.STAGE_W13) == "k_stage_a_xl", T
-    assert name(mx, 33, nat.STAGE_W13) == "k_stage_a_rows"
-    for T in (1, 4, 32):
         assert name(mx, T, nat.STAGE_W2) == "k_stage_b_ks", T
-    assert name(mx, 33, nat.STAGE_W2) == "k_stage_b"
+    assert name(mx, 129, nat.STAGE_W13) == "k_gemm_a_ring"
+    assert name(mx, 129, nat.STAGE_W2) == "k_gemm_b"
+    # many experts: the LDS path up to 256 tokens, the register-fed kernels above
+    mx.num_experts = 256
+    assert name(mx, 256, nat.STAGE_W13) == "k_stage_a_xl"
+    assert name(mx, 256, nat.STAGE_W2) == "k_stage_b_ks"
+    assert name(mx, 257, nat.STAGE_W13) == "k_stage_a_rows"
+    assert name(mx, 257, nat.STAGE_W2) == "k_stage_b"
     f32 = _layer(E=8, H=256, I=128, k=2, act_dtype=nat.DT_F32)
     assert name(f32, 4, nat.STAGE_W13) is None  # f32 activations need the bf16 router: invalid layer

@@ -116,9 +116,9 @@ def c4_full(gpu):
 @pytest.mark.parametrize("T", [1, 16, 32, 128])
 def test_c4_mxfp4_full_shape_matches_oracle(gpu, c4_full, T):
     """MXFP4 at the C4 shape (H = I = 2880, 32 experts, top-4 on biased logits,
-    clamped SwiGLU with biases): stage A with activations in LDS and stage B
-    with K split over the waves up to 32 tokens; at 128 (every expert hit,
-    16 tokens per expert) the tiled stages."""
+    clamped SwiGLU with biases): stage A on scaled MFMAs with activations in
+    LDS and stage B with K split over the waves up to 16 tokens per expert
+    (T = 128)."""
     from dataclasses import replace
 
     _run_and_check(replace(c4_full, x=c4_full.x[:T].contiguous()), gpu)
@@ -138,6 +138,18 @@ def test_mxfp4_decode_wide_range_inputs(gpu, T):
     _, _, ref, out = _run_and_check(syn, gpu)
     err = rel_rms(to_f32(out), ref["out"])
     assert err < MX_REL_RMS, err
+
+
+@pytest.mark.parametrize("T", [64, 200, 256])
+def test_mxfp4_many_experts_lds_path(gpu, T):
+    """MXFP4 on 128 experts, top-2 (1 to 4 tokens per expert): the scaled-MFMA
+    stage A and the K-split stage B up to 256 tokens, the input quantised by
+    the router-rows launch, the work records written by the multi-workgroup
+    top-k (64, 200) and the block top-k (256)."""
+    from dataclasses import replace
+
+    syn = S.generate(replace(S.SMALL["c4_mxfp4"], E=128, k=2), T=T, seed=60 + T)
+    _run_and_check(syn, gpu)
 
 
 def test_c4_mxfp4_full_shape_wide_range_inputs(gpu, c4_full):
