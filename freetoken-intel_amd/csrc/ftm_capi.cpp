@@ -227,7 +227,7 @@ int ftm_moe_forward(const ftm_moe_layer* layer, const void* x, int32_t num_token
   // small decode batches on the lean kernels route inside stage A (no top-k launch)
   const bool fused = fast_layer(layer, x) && lean_route_ok(*layer, num_tokens);
   // the router launch also quantises the input of an MXFP4 stage A
-  const bool xq = mx_stage_a(*layer, num_tokens);
+  const bool xq = mx_input(*layer, num_tokens);
   if (!fused && route_topk_fused(*layer, num_tokens)) {  // router + top-k in one launch
     hipError_t e = launch_route_topk(*layer, x, num_tokens, topk_ids, topk_w, logits, ws, wl, st, true);
     if (e == hipSuccess) e = run_experts(*layer, x, num_tokens, out, ws, wl, st, xq);
@@ -295,7 +295,7 @@ int ftm_moe_forward_stage(const ftm_moe_layer* layer, const void* x, int32_t num
   else
     e = launch_experts(*layer, x, num_tokens, out, ws, wl, st,
                        stage == FTM_STAGE_W13 ? 1 : stage == FTM_STAGE_W2 ? 2 : 4, fused ? &ro : nullptr,
-                       mx_stage_a(*layer, num_tokens));
+                       mx_input(*layer, num_tokens));
   return hip_rc(e);
 }
 

@@ -32,6 +32,7 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef int i32x8 __attribute__((ext_vector_type(8)));  // operands of the scaled (f8f6f4) MFMAs
 
 constexpr int kWave = 64;
 constexpr int kBlock = 256;  // 4 waves per workgroup everywhere

@@ -47,6 +47,7 @@ struct GemmTile {
   int u, m0, cnt;
 };
 
+template <int MT = kGM>
 __device__ __forceinline__ GemmTile gemm_find_tile(const LayerArgs& a, int mtile, int nRouted, bool shared) {
   const int lane = threadIdx.x & 63;
   // lane l owns compact experts 8l .. 8l+7 (E <= 512)
@@ -57,7 +58,7 @@ __device__ __forceinline__ GemmTile gemm_find_tile(const LayerArgs& a, int mtile
   for (int j = 0; j < 8; ++j) {
     const int u = 8 * lane + j;
     c[j] = u < nRouted ? (int)bload4(cres, 4u * (uint32_t)u) : 0;
-    v[j] = (c[j] + kGM - 1) / kGM;
+    v[j] = (c[j] + MT - 1) / MT;
     lsum += v[j];
   }
   // exclusive prefix over lanes
@@ -76,7 +77,7 @@ __device__ __forceinline__ GemmTile gemm_find_tile(const LayerArgs& a, int mtile
     for (int j = 0; j < 8; ++j) {
       if (found_u < 0 && mtile >= base && mtile < base + v[j]) {
         found_u = 8 * lane + j;
-        found_m0 = (mtile - base) * kGM;
+        found_m0 = (mtile - base) * MT;
         found_cnt = c[j];
       }
       base += v[j];
@@ -88,9 +89,9 @@ __device__ __forceinline__ GemmTile gemm_find_tile(const LayerArgs& a, int mtile
     t.cnt = __shfl(found_cnt, src);
   } else if (shared) {
     const int st = mtile - total;
-    if (st * kGM < a.T) {
+    if (st * MT < a.T) {
       t.u = nRouted;
-      t.m0 = st * kGM;
+      t.m0 = st * MT;
       t.cnt = a.T;
     }
   }
@@ -99,6 +100,7 @@ __device__ __forceinline__ GemmTile gemm_find_tile(const LayerArgs& a, int mtile
 
 // Routed M tiles (device total) for the item -> tile mapping of a stage whose
 // routed part has ntn N tiles per M tile.
+template <int MT = kGM>
 __device__ __forceinline__ int gemm_routed_mtiles(const LayerArgs& a, int nRouted) {
   const int lane = threadIdx.x & 63;
   const Rsrc cres = make_rsrc(a.ucnt, (uint32_t)(a.L.num_experts + 1) * 4u);
@@ -106,7 +108,7 @@ __device__ __forceinline__ int gemm_routed_mtiles(const LayerArgs& a, int nRoute
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
     const int u = 8 * lane + j;
-    lsum += u < nRouted ? ((int)bload4(cres, 4u * (uint32_t)u) + kGM - 1) / kGM : 0;
+    lsum += u < nRouted ? ((int)bload4(cres, 4u * (uint32_t)u) + MT - 1) / MT : 0;
   }
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) lsum += __shfl_xor(lsum, off);
@@ -736,6 +738,242 @@ __global__ __launch_bounds__(kBlock) void k_gemm_a_ring(const LayerArgs a) {
   gemm_a_item<FMT, true>(a, xcd_item(blockIdx.x, gridDim.x), ftm_ring_lds, nullptr);
 }
 
+// ---------------------------------------------------------------- scaled-MFMA tiles (MXFP4 stage A)
+// Stage A of MXFP4 layers above the crossover on v_mfma_scale_f32_16x16x128_f8f6f4
+// with the decode path's operand layouts (ftm_moe.hip): the weights go in as
+// stored (e2m1 nibbles, e8m0 block scales), the input as its two-term e4m3
+// split (the xq workspace region: kMxChunk bytes per token and 128 K, written
+// by the router launch or k_quant_mx).  No weight is decoded.
+// Tile: MT tokens x 128 weight rows (64 gate + 64 up channels), K steps of
+// 128.  The four waves sit 2 x 2, each MT/2 tokens x 64 rows (MT/32 x 4
+// blocks of 16 x 16: 32 gate + 32 up rows), so one A read feeds four weight
+// blocks and one B read MT/32 token blocks.  A three-stage LDS ring is filled
+// by direct global->LDS copies two K steps ahead: per stage the tile's token
+// chunks (kMxChunk bytes each, 16-byte slots in order), its weight rows (64
+// bytes per row, slot q of row r holding piece q ^ ring_fw(r), so the 16 rows
+// of one B read hit distinct banks) and the rows' four e8m0 bytes of the step
+// (16-bit copies, which land one per 4-byte LDS slot).  At MT = 64 two
+// workgroups fit a CU, so one's barriers, prologue and epilogue overlap the
+// other's MFMAs.
+constexpr int kMxK = 128;  // K per step
+template <int MT>
+struct MxPlan {
+  static constexpr int kMI = MT / 32;                              // 16-token blocks per wave
+  static constexpr int kACopies = MT * (kMxChunk / 16) / 64;       // 16-byte copies of the A chunks per stage
+  static constexpr int kABytes = kACopies * 1024;
+  static constexpr int kWBytes = 128 * 64;
+  static constexpr int kSBytes = 256 * 4;                          // 128 rows x 2 halves, one 4-byte slot each
+  static constexpr int kStage = kABytes + kWBytes + kSBytes;
+  static constexpr int kStages = 3;
+  static constexpr int kLds = kStages * kStage;
+  // copies per wave per stage: A copies w, w + 4, ...; two W copies; one scale copy
+  static constexpr int kAMax = (kACopies + 3) / 4;
+  static constexpr int kLoadsMax = kAMax + 3;
+  static_assert(MT * (kMxChunk / 16) % 64 == 0 && kLoadsMax < 64, "copy shape");
+};
+
+// The kernel's dynamic LDS (mx_gemm_ok checks it against the CU's 160 KiB).
+template <int MT>
+__host__ __device__ __forceinline__ size_t mx_tile_lds() { return (size_t)MxPlan<MT>::kLds; }
+
+// NT consecutive 64-channel tiles (c0, c0 + 64, ... below Iu) of one M tile:
+// the token rows' sources and the epilogue's pairs are resolved once, and
+// the next tile's first two stages are issued before this tile's epilogue.
+template <int MT>
+__device__ void gemm_a_mx_body(const LayerArgs& a, const ProjSlot& W, int Iu, int c0, int NT, int m0, int cnt,
+                               const int32_t* list, char* lds) {
+  using P = MxPlan<MT>;
+  constexpr int MI = P::kMI;
+  typedef __attribute__((address_space(1))) const void* GPtr;
+  typedef __attribute__((address_space(3))) void* LPtr;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave & 1, wn = wave >> 1;
+  const int g = lane >> 4, m = lane & 15;
+  const int K = W.K, KP = a.KP;
+  const int nsteps = (K + kMxK - 1) / kMxK;
+  const size_t xrow = (size_t)mx_row_bytes(a.L.hidden);
+  const uint32_t rb = (uint32_t)K / 2;    // e2m1 bytes per weight row (a multiple of 16)
+  const uint32_t kgb = (uint32_t)K / 32;  // e8m0 bytes per row (even: K % 64 == 0)
+  const Rsrc lres = make_rsrc(list, (uint32_t)a.T * 4u);
+  const int p0 = pair_of_row(lres, true, m0, cnt, KP, 0);
+  const int na = (P::kACopies - wave + 3) / 4;  // this wave's A copies per stage
+
+  // ---- A copy sources: slot s = token row s / 17, piece s % 17 (rows past
+  // the tile's tokens repeat its first)
+  const char* asrc[P::kAMax];
+#pragma unroll
+  for (int i = 0; i < P::kAMax; ++i) {
+    const int sl = 64 * (4 * i + wave) + lane;
+    const int r = sl / (kMxChunk / 16), pc = sl - r * (kMxChunk / 16);
+    int pr = r < MT ? pair_of_row(lres, true, m0 + r, cnt, KP, 0) : -1;
+    pr = pr >= 0 ? pr : p0;
+    asrc[i] = (const char*)a.xq + (size_t)(pr / KP) * xrow + 16 * pc;
+  }
+  // the pairs of this lane's output rows (epilogue)
+  int pe[MI][4];
+#pragma unroll
+  for (int mi = 0; mi < MI; ++mi)
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      pe[mi][r] = pair_of_row(lres, true, m0 + (MT / 2) * wm + 16 * mi + 4 * g + r, cnt, KP, 0);
+
+  // ---- per-tile weight sources.  W slot s = row s / 4, slot s % 4 holding
+  // piece (s % 4) ^ ring_fw(row); a piece past the row's end (last K step)
+  // re-reads the row's first: finite e2m1 codes against zero activations.
+  // Scale slot s = row s / 2, bytes 2 (s % 2), +1 of the step's four (past
+  // the row's end its first two, against zero activations).
+  const char* wrow[2];
+  uint32_t wpo[2];
+  const char* srow;
+  auto tile_sources = [&](int cc) {
+    auto grow = [&](int r) { return r < 64 ? cc + r : Iu + cc + (r - 64); };
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int sl = 64 * (4 * i + wave) + lane;
+      const int r = sl >> 2;
+      wrow[i] = (const char*)W.w + (size_t)grow(r) * rb;
+      wpo[i] = 16u * (uint32_t)((sl & 3) ^ ring_fw(r));
+    }
+    srow = (const char*)W.s + (size_t)grow((64 * wave + lane) >> 1) * kgb;
+  };
+  const uint32_t sho = 2u * (uint32_t)(lane & 1);
+  auto issue = [&](int kb, int slot) {
+    char* st = lds + slot * P::kStage;
+#pragma unroll
+    for (int i = 0; i < P::kAMax; ++i)
+      if (i < na)
+        __builtin_amdgcn_global_load_lds((GPtr)(asrc[i] + (size_t)kb * kMxChunk),
+                                         (LPtr)(st + 1024 * (4 * i + wave)), 16, 0, 0);
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const uint32_t off = 64u * (uint32_t)kb + wpo[i];
+      __builtin_amdgcn_global_load_lds((GPtr)(wrow[i] + (off + 16u <= rb ? off : 0u)),
+                                       (LPtr)(st + P::kABytes + 1024 * (4 * i + wave)), 16, 0, 0);
+    }
+    const uint32_t so = 4u * (uint32_t)kb + sho;
+    __builtin_amdgcn_global_load_lds((GPtr)(srow + (so + 2u <= kgb ? so : 0u)),
+                                     (LPtr)(st + P::kABytes + P::kWBytes + 256 * wave), 2, 0, 0);
+  };
+  const int pro = nsteps < P::kStages - 1 ? nsteps : P::kStages - 1;
+  tile_sources(c0);
+  for (int kb = 0; kb < pro; ++kb) issue(kb, kb);
+
+  int brow[4];
+#pragma unroll
+  for (int nj = 0; nj < 4; ++nj) brow[nj] = (nj < 2 ? 32 * wn + 16 * nj : 64 + 32 * wn + 16 * (nj - 2)) + m;
+  for (int t = 0; t < NT; ++t) {
+    const int cc = c0 + 64 * t;
+    uint32_t bgb[2], bub[2];  // bias bits (converted in the epilogue)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int ch = cc + 32 * wn + 16 * j + m;
+      bgb[j] = W.bias != nullptr ? load_bits(W.bias, ch, W.bias_dt) : 0u;
+      bub[j] = W.bias != nullptr ? load_bits(W.bias, Iu + ch, W.bias_dt) : 0u;
+    }
+    f32x4 acc[MI][4];
+#pragma unroll
+    for (int mi = 0; mi < MI; ++mi)
+#pragma unroll
+      for (int nj = 0; nj < 4; ++nj) acc[mi][nj] = (f32x4){0.f, 0.f, 0.f, 0.f};
+    for (int kb = 0; kb < nsteps; ++kb) {
+      // this wave's copies of stage kb have landed (the next stage's, and
+      // the bias loads issued after them, may be in flight), then every
+      // wave's have; every wave is also done with stage kb - 1 (its reads fed
+      // MFMAs that have issued).  A plain barrier: __syncthreads' release
+      // fence would wait for every copy in flight, the next stage's too.
+      if (kb + 1 < nsteps) {
+        if (na == P::kAMax) wait_vm<P::kLoadsMax>(); else wait_vm<P::kLoadsMax - 1>();
+      } else {
+        wait_vm<0>();
+      }
+      asm volatile("s_barrier" ::: "memory");
+      if (kb + P::kStages - 1 < nsteps) issue(kb + P::kStages - 1, (kb + P::kStages - 1) % P::kStages);
+      const char* st = lds + (kb % P::kStages) * P::kStage;
+      i32x8 bw[4];
+      int sb[4];
+#pragma unroll
+      for (int nj = 0; nj < 4; ++nj) {
+        const u32x4 r = *(const u32x4*)(st + P::kABytes + brow[nj] * 64 + 16 * (g ^ ring_fw(brow[nj])));
+        bw[nj] = (i32x8){(int)r.x, (int)r.y, (int)r.z, (int)r.w, 0, 0, 0, 0};
+        const uint32_t sv = *(const uint32_t*)(st + P::kABytes + P::kWBytes + 4 * (2 * brow[nj] + (g >> 1)));
+        sb[nj] = (int)((sv >> (8 * (g & 1))) & 0xffu);
+      }
+#pragma unroll
+      for (int mi = 0; mi < MI; ++mi) {
+        const char* cb = st + ((MT / 2) * wm + 16 * mi + m) * kMxChunk;
+        const u32x4 h0 = *(const u32x4*)(cb + 16 * g);
+        const u32x4 h1 = *(const u32x4*)(cb + 64 + 16 * g);
+        const u32x4 l0 = *(const u32x4*)(cb + 128 + 16 * g);
+        const u32x4 l1 = *(const u32x4*)(cb + 192 + 16 * g);
+        const uint32_t sc = *(const uint16_t*)(cb + 256 + 2 * g);
+        const i32x8 ahi = {(int)h0.x, (int)h0.y, (int)h0.z, (int)h0.w, (int)h1.x, (int)h1.y, (int)h1.z, (int)h1.w};
+        const i32x8 alo = {(int)l0.x, (int)l0.y, (int)l0.z, (int)l0.w, (int)l1.x, (int)l1.y, (int)l1.z, (int)l1.w};
+#pragma unroll
+        for (int nj = 0; nj < 4; ++nj) {
+          acc[mi][nj] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(ahi, bw[nj], acc[mi][nj], 0, 4, 0,
+                                                                         (int)(sc & 0xffu), 0, sb[nj]);
+          acc[mi][nj] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(alo, bw[nj], acc[mi][nj], 0, 4, 0,
+                                                                         (int)(sc >> 8), 0, sb[nj]);
+        }
+      }
+    }
+    if (t + 1 < NT) {
+      // every wave is done with the ring (its last reads fed MFMAs that have
+      // issued): the next tile's first stages go out before this epilogue
+      asm volatile("s_barrier" ::: "memory");
+      tile_sources(cc + 64);
+      for (int kb = 0; kb < pro; ++kb) issue(kb, kb);
+    }
+
+    // ---- epilogue: h = act(gate + b_g, up + b_u), bf16, for the tile's real rows
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int ch = cc + 32 * wn + 16 * j + m;
+      const float bg = bits_to_f32(opaque_bits(bgb[j]), W.bias_dt);
+      const float bu = bits_to_f32(opaque_bits(bub[j]), W.bias_dt);
+#pragma unroll
+      for (int mi = 0; mi < MI; ++mi)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          if (pe[mi][r] >= 0) {
+            const float h = act_fn(a.L.act, acc[mi][j][r] + bg, acc[mi][j + 2][r] + bu, a.L.swiglu_alpha,
+                                   a.L.swiglu_limit);
+            store_scalar(a.hbuf, (size_t)pe[mi][r] * a.Imax + ch, FTM_DT_BF16, h);
+          }
+        }
+    }
+  }
+}
+
+// Routed MXFP4 stage A tiles (a layer without a shared expert, mx_gemm_ok):
+// one workgroup per (M tile, kMxNT consecutive N tiles), items in XCD-aware
+// order.
+constexpr int kMxM = 64;   // tokens per tile: two workgroups per CU
+constexpr int kMxNT = 3;   // 64-channel tiles per workgroup
+__global__ __launch_bounds__(kBlock) void k_gemm_a_mx(const LayerArgs a) {
+  const int item = xcd_item(blockIdx.x, gridDim.x);
+  const int I = a.L.inter;
+  const int nRouted = a.ctrl[kCtrlNRouted];
+  const int ntn = (I / 64 + kMxNT - 1) / kMxNT;
+  const int routed_items = gemm_routed_mtiles<kMxM>(a, nRouted) * ntn;
+  if (item >= routed_items) return;
+  const GemmTile t = gemm_find_tile<kMxM>(a, item / ntn, nRouted, false);
+  if (t.u < 0) return;
+  // wave-uniform values in scalar registers, so the buffer descriptors built
+  // from them are scalar too (no per-load waterfall loops)
+  const int e = __builtin_amdgcn_readfirstlane(a.uniq[t.u]);
+  const int slot = __builtin_amdgcn_readfirstlane(a.L.slot_of_expert ? a.L.slot_of_expert[e] : e);
+  if (slot < 0 || slot >= a.L.w13.num_slots) {
+    if (threadIdx.x == 0) atomicOr(&a.ctrl[kCtrlError], 1);
+    return;
+  }
+  const int n0 = (item % ntn) * kMxNT;
+  const int nt = I / 64 - n0 < kMxNT ? I / 64 - n0 : kMxNT;
+  gemm_a_mx_body<kMxM>(a, proj_slot(a.L.w13, slot), I, 64 * n0, nt, __builtin_amdgcn_readfirstlane(t.m0),
+                       __builtin_amdgcn_readfirstlane(t.cnt), a.lists + (size_t)e * a.T, (char*)ftm_ring_lds);
+}
+
 // ---------------------------------------------------------------- stage B (w2 -> slot buffer)
 template <int WFMT>
 __device__ void gemm_b_body(const LayerArgs& a, const ProjSlot& W, int n0, int m0, int cnt, const int32_t* list,
@@ -870,7 +1108,14 @@ static size_t ring_lds_a(const ftm_moe_layer& L) {
   const int rows = f == FTM_FMT_FP8_BLOCK ? 2 : f == FTM_FMT_INT8_PACKED ? 128 : 0;
   return (size_t)kRingA + (size_t)rows * g * 4;
 }
-const char* gemm_a_kernel_name(const ftm_moe_layer& L) { return ring_ok(L) ? "k_gemm_a_ring" : "k_gemm_a"; }
+bool mx_gemm_ok(const ftm_moe_layer& L) {
+  return L.w13.fmt == FTM_FMT_MXFP4 && L.act_dtype == FTM_DT_BF16 && L.shared_inter == 0 &&
+         mx_tile_lds<kMxM>() <= 160u * 1024u;
+}
+
+const char* gemm_a_kernel_name(const ftm_moe_layer& L) {
+  return mx_gemm_ok(L) ? "k_gemm_a_mx" : ring_ok(L) ? "k_gemm_a_ring" : "k_gemm_a";
+}
 
 template <int FMT>
 static void ring_lds_attr() {
@@ -884,10 +1129,23 @@ static void ring_lds_attr() {
 }
 
 template <int FMT>
-static void launch_gemm_t(const LayerArgs& a, hipStream_t st, int which) {
+static void launch_gemm_t(const LayerArgs& a, hipStream_t st, int which, bool xq_ready) {
   const ftm_moe_layer& L = a.L;
   const long pairs = (long)a.T * L.topk;
   const long maxU = L.num_experts < pairs ? L.num_experts : pairs;
+  if (FMT == FTM_FMT_MXFP4 && (which & 1) && mx_gemm_ok(L)) {
+    // stage A on the scaled-MFMA tiles, over the quantised input
+    static bool attr = false;
+    if (!attr) {
+      (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&k_gemm_a_mx),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)mx_tile_lds<kMxM>());
+      attr = true;
+    }
+    if (!xq_ready) launch_quant_mx(a.x, a.T, L.hidden, a.xq, st);
+    const long items = (pairs / kMxM + maxU + 1) * ((L.inter / 64 + kMxNT - 1) / kMxNT);
+    hipLaunchKernelGGL(k_gemm_a_mx, dim3((unsigned)items), dim3(kBlock), mx_tile_lds<kMxM>(), st, a);
+    which &= ~1;
+  }
   const long mt_routed = pairs / kGM + maxU + 1;
   const long mt_shared = L.shared_inter > 0 ? (a.T + kGM - 1) / kGM : 0;
   const long items_a = mt_routed * (L.inter / 64) + mt_shared * (L.shared_inter > 0 ? L.shared_inter / 64 : 0);
@@ -910,13 +1168,13 @@ static void launch_gemm_t(const LayerArgs& a, hipStream_t st, int which) {
 }
 
 void launch_gemm_stages(const ftm_moe_layer& L, const void* x, int T, void* out, char* ws, const WsLayout& wl,
-                        hipStream_t st, int which) {
+                        hipStream_t st, int which, bool xq_ready) {
   const LayerArgs a = make_args(L, x, out, T, ws, wl);
   switch (L.w13.fmt) {
-    case FTM_FMT_FP8_BLOCK: launch_gemm_t<FTM_FMT_FP8_BLOCK>(a, st, which); break;
-    case FTM_FMT_INT8_PACKED: launch_gemm_t<FTM_FMT_INT8_PACKED>(a, st, which); break;
-    case FTM_FMT_MXFP4: launch_gemm_t<FTM_FMT_MXFP4>(a, st, which); break;
-    default: launch_gemm_t<FTM_FMT_BF16>(a, st, which); break;
+    case FTM_FMT_FP8_BLOCK: launch_gemm_t<FTM_FMT_FP8_BLOCK>(a, st, which, xq_ready); break;
+    case FTM_FMT_INT8_PACKED: launch_gemm_t<FTM_FMT_INT8_PACKED>(a, st, which, xq_ready); break;
+    case FTM_FMT_MXFP4: launch_gemm_t<FTM_FMT_MXFP4>(a, st, which, xq_ready); break;
+    default: launch_gemm_t<FTM_FMT_BF16>(a, st, which, xq_ready); break;
   }
 }
 

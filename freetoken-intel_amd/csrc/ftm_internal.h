@@ -119,14 +119,21 @@ hipError_t launch_experts(const ftm_moe_layer& L, const void* x, int T, void* ou
                           const WsLayout& wl, hipStream_t st, int which = 7, const RouteOut* ro = nullptr,
                           bool xq_ready = false);
 // Stage A of MXFP4 layers on scaled MFMAs over the quantised input (the xq
-// workspace region, written by k_quant_mx or a router launch with quant).
+// workspace region, written by k_quant_mx or a router launch with quant):
+// the LDS decode stage (mx_stage_a) or the GEMM tiles (mx_gemm_ok above the
+// crossover); mx_input: either.
 bool mx_stage_a(const ftm_moe_layer& L, int T);
+bool mx_input(const ftm_moe_layer& L, int T);
 // Prefill side of the crossover (ftm_gemm.hip): whether the tiled GEMM stages
 // take this layer at T tokens, and their launch (which: bit 0 = w13, bit 1 = w2).
 bool gemm_path_ok(const ftm_moe_layer& L, int T);
 const char* gemm_a_kernel_name(const ftm_moe_layer& L);  // the stage A tile kernel the layer takes
 void launch_gemm_stages(const ftm_moe_layer& L, const void* x, int T, void* out, char* ws, const WsLayout& wl,
-                        hipStream_t st, int which);
+                        hipStream_t st, int which, bool xq_ready = false);
+// MXFP4 stage A on the scaled-MFMA tiles (k_gemm_a_mx) above the crossover.
+bool mx_gemm_ok(const ftm_moe_layer& L);
+// k_quant_mx: the input (T x H bf16) into the xq region's two-term e4m3 split.
+void launch_quant_mx(const void* x, int T, int H, uint8_t* xq, hipStream_t st);
 // The lean FP8 decode kernels (ftm_moe.hip) cover H = 2048 (a 512-element K
 // range per wave in stage A), I = 512 (one 8-load window per wave in stage
 // B), fp32 block-128 scales, no projection biases, bf16 activations and a

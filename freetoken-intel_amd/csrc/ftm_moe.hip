@@ -45,8 +45,6 @@ namespace ftm {
 //   A (e4m3): lane l holds token row l % 16 at K [16 g, 16 g + 16) and
 //             [64 + 16 g, 64 + 16 g + 16) (8 registers), and in scale_a the
 //             scale of the row's block g (K [32 g, 32 g + 32)).
-typedef int i32x8 __attribute__((ext_vector_type(8)));
-
 // |v| < 448 to e4m3fn, round to nearest even (the callers keep |v| < 257).
 __device__ __forceinline__ uint32_t f32_to_e4m3(float v) {
   const uint32_t sgn = (__float_as_uint(v) >> 24) & 0x80u;
@@ -198,13 +196,17 @@ __device__ __forceinline__ void router_row_tile(const LayerArgs& a, int r, int t
   }
 }
 
-// Workgroups past `rows` (first token block only) quantise the input for the
-// MXFP4 scaled-MFMA stage A instead (quant_mx_piece), off its critical path.
+// Workgroups past `rows` quantise the input for the MXFP4 scaled-MFMA stage
+// A instead (quant_mx_piece), off its critical path: quantisation block
+// (x - rows) * gridDim.y + y.
+__device__ __forceinline__ void router_quant_block(const LayerArgs& a, int qb) {
+  quant_mx_piece((const uint16_t*)a.x, a.T, a.L.hidden, a.xq, qb * kBlock + threadIdx.x);
+}
+
 __global__ __launch_bounds__(kBlock) void k_router(const LayerArgs a, int row_begin, int rows) {
   const int wave = threadIdx.x >> 6;
   if ((int)blockIdx.x >= rows) {
-    if (blockIdx.y == 0)
-      quant_mx_piece((const uint16_t*)a.x, a.T, a.L.hidden, a.xq, ((int)blockIdx.x - rows) * kBlock + threadIdx.x);
+    router_quant_block(a, ((int)blockIdx.x - rows) * (int)gridDim.y + (int)blockIdx.y);
     return;
   }
   router_row_tile(a, row_begin + blockIdx.x, blockIdx.y * 4 * kRouterTPW + wave);
@@ -330,8 +332,7 @@ __global__ __launch_bounds__(kBlock) void k_router_rows(const LayerArgs a, int r
   const int wave = threadIdx.x >> 6;
   const int rb = (row_end - row_begin + kRouterRB - 1) / kRouterRB;
   if ((int)blockIdx.x >= rb) {  // as in k_router
-    if (blockIdx.y == 0)
-      quant_mx_piece((const uint16_t*)a.x, a.T, a.L.hidden, a.xq, ((int)blockIdx.x - rb) * kBlock + threadIdx.x);
+    router_quant_block(a, ((int)blockIdx.x - rb) * (int)gridDim.y + (int)blockIdx.y);
     return;
   }
   router_rows_tile(a, row_begin + blockIdx.x * kRouterRB, row_end, blockIdx.y * 4 * kRouterTPW + wave * kRouterTPW);
@@ -2840,14 +2841,16 @@ hipError_t launch_router(const ftm_moe_layer& L, const void* x, int T, int row_b
   const LayerArgs a = make_args(L, x, nullptr, T, ws, wl);
   if (row_end - row_begin <= 0 || T <= 0) return hipSuccess;
   const int tpb = 4 * kRouterTPW;
-  const int nq = quant && mx_stage_a(L, T) ? (quant_mx_threads(T, L.hidden) + kBlock - 1) / kBlock : 0;
+  const int ty = (T + tpb - 1) / tpb;
+  // quantisation blocks spread over the grid's token-block rows (ceil(nq / ty) columns)
+  const int nq = quant && mx_input(L, T) ? (quant_mx_threads(T, L.hidden) + kBlock - 1) / kBlock : 0;
+  const int qx = (nq + ty - 1) / ty;
   if (T >= kRouterMinT)
-    hipLaunchKernelGGL(k_router_rows,
-                       dim3((row_end - row_begin + kRouterRB - 1) / kRouterRB + nq, (T + tpb - 1) / tpb),
+    hipLaunchKernelGGL(k_router_rows, dim3((row_end - row_begin + kRouterRB - 1) / kRouterRB + qx, ty),
                        dim3(kBlock), 0, st, a, row_begin, row_end);
   else
-    hipLaunchKernelGGL(k_router, dim3(row_end - row_begin + nq, (T + tpb - 1) / tpb), dim3(kBlock), 0, st, a,
-                       row_begin, row_end - row_begin);
+    hipLaunchKernelGGL(k_router, dim3(row_end - row_begin + qx, ty), dim3(kBlock), 0, st, a, row_begin,
+                       row_end - row_begin);
   return hipGetLastError();
 }
 
@@ -2860,7 +2863,7 @@ hipError_t launch_route_topk(const ftm_moe_layer& L, const void* x, int T, int32
                              float* logits_out, char* ws, const WsLayout& wl, hipStream_t st, bool quant) {
   const LayerArgs a = make_args(L, x, nullptr, T, ws, wl);
   const int rows = L.num_experts + (L.shared_inter > 0 ? 1 : 0);
-  const int nq = quant && mx_stage_a(L, T) ? (quant_mx_threads(T, L.hidden) + 64 * kTopk1Waves - 1) / (64 * kTopk1Waves) : 0;
+  const int nq = quant && mx_input(L, T) ? (quant_mx_threads(T, L.hidden) + 64 * kTopk1Waves - 1) / (64 * kTopk1Waves) : 0;
   const dim3 grid((rows + kRouteRows - 1) / kRouteRows + nq), block(64 * kTopk1Waves);
 #define FTM_RT_NV(M)                                                                                         \
   if (L.num_experts <= 256)                                                                                  \
@@ -2980,6 +2983,15 @@ static XlPlan xl_plan_a(const ftm_moe_layer& L, int T) {
 bool mx_stage_a(const ftm_moe_layer& L, int T) {
   return L.w13.fmt == FTM_FMT_MXFP4 && L.act_dtype == FTM_DT_BF16 && !gemm_path_ok(L, T) &&
          xl_plan_a<FTM_FMT_MXFP4, FTM_DT_BF16>(L, T).ok;
+}
+
+bool mx_input(const ftm_moe_layer& L, int T) {
+  return mx_stage_a(L, T) || (gemm_path_ok(L, T) && mx_gemm_ok(L));
+}
+
+void launch_quant_mx(const void* x, int T, int H, uint8_t* xq, hipStream_t st) {
+  hipLaunchKernelGGL(k_quant_mx, dim3((quant_mx_threads(T, H) + kBlock - 1) / kBlock), dim3(kBlock), 0, st,
+                     (const uint16_t*)x, T, H, xq);
 }
 
 template <int FMT, int AT>
@@ -3174,7 +3186,7 @@ hipError_t launch_experts(const ftm_moe_layer& L, const void* x, int T, void* ou
                           const WsLayout& wl, hipStream_t st, int which, const RouteOut* ro, bool xq_ready) {
   if (gemm_path_ok(L, T)) {
     // above the token crossover the expert stages are tiled GEMMs
-    if (which & 3) launch_gemm_stages(L, x, T, out, ws, wl, st, which & 3);
+    if (which & 3) launch_gemm_stages(L, x, T, out, ws, wl, st, which & 3, xq_ready);
     which &= 4;
     if (which == 0) return hipGetLastError();
   }

@@ -309,6 +309,27 @@ def test_prefill_gemm_path_matches_oracle(gpu, name, T):
     _run_and_check(syn, gpu)
 
 
+@pytest.mark.parametrize("T", [256, 600])
+def test_mxfp4_tiles_wide_range_inputs(gpu, T):
+    """MXFP4 above the crossover: stage A on the scaled-MFMA tiles (128-token
+    M tiles, partly filled at 64 and 150 tokens per expert; H = 320 ends in a
+    half K step) with inputs spanning 2^-14 .. 2^3 inside each 32-wide block:
+    the output stays at bf16 precision (relative RMS MX_REL_RMS).  Caller
+    routing then quantises the input in its own launch (no router launch)."""
+    from dataclasses import replace
+
+    syn = S.generate(S.SMALL["c4_mxfp4"], T=T, seed=70 + T)
+    syn = replace(syn, x=wide_range_x(T, syn.cfg.H, seed=T))
+    layer, dsyn, ref, out = _run_and_check(syn, gpu)
+    err = rel_rms(to_f32(out), ref["out"])
+    assert err < MX_REL_RMS, err
+    ids = torch.from_numpy(np.ascontiguousarray(ref["ids"], np.int32)).to(gpu)
+    w = torch.from_numpy(np.ascontiguousarray(ref["w"], np.float32)).to(gpu)
+    out_r = layer.forward_routed(dsyn.x, ids, w)
+    torch.cuda.synchronize()
+    assert_close(to_f32(out_r), ref["out"], what="MXFP4 tiles, caller routing")
+
+
 def test_prefill_gemm_full_c3_token_subset(gpu):
     """C3 at its prefill size (T=2048, all 256 experts hit): the layer runs on
     the whole batch; a token's output depends only on its own row, so 48
