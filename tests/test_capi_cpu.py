@@ -217,7 +217,7 @@ def test_stage_kernel_names_follow_the_dispatch():
     for T in (1, 8, 32, 64, 128):
         assert name(mx, T, nat.STAGE_W13) == "k_stage_a_xl", T
         assert name(mx, T, nat.STAGE_W2) == "k_stage_b_ks", T
-    assert name(mx, 129, nat.STAGE_W13) == "k_gemm_a_ring"
+    assert name(mx, 129, nat.STAGE_W13) == "k_gemm_a_mx"  # scaled-MFMA tiles (no shared expert)
     assert name(mx, 129, nat.STAGE_W2) == "k_gemm_b"
     # many experts: the LDS path up to 256 tokens, the register-fed kernels above
     mx.num_experts = 256
