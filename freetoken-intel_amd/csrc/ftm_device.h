@@ -366,6 +366,25 @@ __device__ __forceinline__ ProjSlot proj_slot(const ftm_proj& P, int slot) {
   return v;
 }
 
+// e4m3fn conversions on the hardware converts (v_cvt_pk_fp8_f32 rounds to
+// nearest even; checked on MI355X bit for bit against a software RNE over
+// every f32 with |v| < 448 and 12 trailing zero bits, subnormals and ties
+// included, and v_cvt_f32_fp8 over all 256 codes).  The callers keep |v| <
+// 257, so nothing saturates.
+// Two values -> two codes in bits 0-7 and 8-15.
+__device__ __forceinline__ uint32_t f32x2_to_e4m3(float a, float b) {
+  return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false) & 0xffffu;
+}
+// Four values -> four codes, a in bits 0-7.
+__device__ __forceinline__ uint32_t f32x4_to_e4m3(float a, float b, float c, float d) {
+  return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(c, d, __builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false), true);
+}
+// Code in byte B of w -> its value.
+template <int B>
+__device__ __forceinline__ float e4m3_at(uint32_t w) {
+  return __builtin_amdgcn_cvt_f32_fp8((int)w, B);
+}
+
 // ---------------------------------------------------------------- K-major engine
 // Formats whose weight rows are contiguous along K: FP8 block, INT8 packed,
 // MXFP4, BF16.  One "wave-load" = every lane loading 16 bytes of its row

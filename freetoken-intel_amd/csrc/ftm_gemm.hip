@@ -776,31 +776,43 @@ struct MxPlan {
 template <int MT>
 __host__ __device__ __forceinline__ size_t mx_tile_lds() { return (size_t)MxPlan<MT>::kLds; }
 
-// NT consecutive 64-channel tiles (c0, c0 + 64, ... below Iu) of one M tile:
-// the token rows' sources and the epilogue's pairs are resolved once, and
-// the next tile's first two stages are issued before this tile's epilogue.
-template <int MT>
-__device__ void gemm_a_mx_body(const LayerArgs& a, const ProjSlot& W, int Iu, int c0, int NT, int m0, int cnt,
-                               const int32_t* list, char* lds) {
+// Stage A writes h quantised for stage B's scaled MFMAs (the same two-term
+// e4m3 split and kMxChunk layout as the input, rows by pair, in the h
+// buffer): a wave's 32 channels of a token are one 32-element block, so its
+// scale comes from a 16-lane DPP max.  Staged through LDS and copied out in
+// 16-byte pieces per row: [hi 64][lo 64][scale words 4], kMxStgPitch apart.
+constexpr int kMxStgPitch = 144;
+
+// NT consecutive N tiles of one M tile -- stage A: 64 channels (gate + up
+// rows) each; stage B (STB): 128 output columns (w2 rows) each.  The token
+// rows' sources and the epilogue's pairs are resolved once, and the next
+// tile's first two stages are issued before this tile's epilogue.
+template <int MT, bool STB>
+__device__ void gemm_mx_body(const LayerArgs& a, const ProjSlot& W, int Iu, int c0, int NT, int m0, int cnt,
+                             const int32_t* list, char* lds) {
   using P = MxPlan<MT>;
   constexpr int MI = P::kMI;
+  constexpr int kTileN = STB ? 128 : 64;
   typedef __attribute__((address_space(1))) const void* GPtr;
   typedef __attribute__((address_space(3))) void* LPtr;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave & 1, wn = wave >> 1;
   const int g = lane >> 4, m = lane & 15;
-  const int K = W.K, KP = a.KP;
+  const int K = W.K, KP = a.KP, H = a.L.hidden;
   const int nsteps = (K + kMxK - 1) / kMxK;
-  const size_t xrow = (size_t)mx_row_bytes(a.L.hidden);
   const uint32_t rb = (uint32_t)K / 2;    // e2m1 bytes per weight row (a multiple of 16)
   const uint32_t kgb = (uint32_t)K / 32;  // e8m0 bytes per row (even: K % 64 == 0)
   const Rsrc lres = make_rsrc(list, (uint32_t)a.T * 4u);
   const int p0 = pair_of_row(lres, true, m0, cnt, KP, 0);
   const int na = (P::kACopies - wave + 3) / 4;  // this wave's A copies per stage
+  // A rows: stage A the quantised input by token, stage B the quantised h by pair
+  const uint8_t* abase = STB ? (const uint8_t*)a.hbuf : a.xq;
+  const size_t arow = (size_t)mx_row_bytes(STB ? a.Imax : H);
+  const int adiv = STB ? 1 : KP;
 
-  // ---- A copy sources: slot s = token row s / 17, piece s % 17 (rows past
-  // the tile's tokens repeat its first)
+  // ---- A copy sources: slot s = tile row s / 17, piece s % 17 (rows past
+  // the tile's pairs repeat its first)
   const char* asrc[P::kAMax];
 #pragma unroll
   for (int i = 0; i < P::kAMax; ++i) {
@@ -808,34 +820,42 @@ __device__ void gemm_a_mx_body(const LayerArgs& a, const ProjSlot& W, int Iu, in
     const int r = sl / (kMxChunk / 16), pc = sl - r * (kMxChunk / 16);
     int pr = r < MT ? pair_of_row(lres, true, m0 + r, cnt, KP, 0) : -1;
     pr = pr >= 0 ? pr : p0;
-    asrc[i] = (const char*)a.xq + (size_t)(pr / KP) * xrow + 16 * pc;
+    asrc[i] = (const char*)abase + (size_t)(pr / adiv) * arow + 16 * pc;
   }
-  // the pairs of this lane's output rows (epilogue)
+  // the pairs of this lane's output rows (epilogue) and, stage B, their router weights
   int pe[MI][4];
+  float we[MI][4];
+  const Rsrc wres = make_rsrc(a.wts, (uint32_t)a.T * (uint32_t)KP * 4u);
 #pragma unroll
   for (int mi = 0; mi < MI; ++mi)
 #pragma unroll
-    for (int r = 0; r < 4; ++r)
+    for (int r = 0; r < 4; ++r) {
       pe[mi][r] = pair_of_row(lres, true, m0 + (MT / 2) * wm + 16 * mi + 4 * g + r, cnt, KP, 0);
+      we[mi][r] = STB ? __uint_as_float(bload4(wres, pe[mi][r] >= 0 ? 4u * (uint32_t)pe[mi][r] : kOOB)) : 0.0f;
+    }
 
   // ---- per-tile weight sources.  W slot s = row s / 4, slot s % 4 holding
   // piece (s % 4) ^ ring_fw(row); a piece past the row's end (last K step)
-  // re-reads the row's first: finite e2m1 codes against zero activations.
+  // re-reads the row's first: finite e2m1 codes against zero activations
+  // (stage B rows past N repeat row N - 1; their columns are not stored).
   // Scale slot s = row s / 2, bytes 2 (s % 2), +1 of the step's four (past
   // the row's end its first two, against zero activations).
   const char* wrow[2];
   uint32_t wpo[2];
   const char* srow;
+  auto grow = [&](int cc, int r) {
+    if constexpr (STB) return cc + r < W.N ? cc + r : W.N - 1;
+    return r < 64 ? cc + r : Iu + cc + (r - 64);
+  };
   auto tile_sources = [&](int cc) {
-    auto grow = [&](int r) { return r < 64 ? cc + r : Iu + cc + (r - 64); };
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       const int sl = 64 * (4 * i + wave) + lane;
       const int r = sl >> 2;
-      wrow[i] = (const char*)W.w + (size_t)grow(r) * rb;
+      wrow[i] = (const char*)W.w + (size_t)grow(cc, r) * rb;
       wpo[i] = 16u * (uint32_t)((sl & 3) ^ ring_fw(r));
     }
-    srow = (const char*)W.s + (size_t)grow((64 * wave + lane) >> 1) * kgb;
+    srow = (const char*)W.s + (size_t)grow(cc, (64 * wave + lane) >> 1) * kgb;
   };
   const uint32_t sho = 2u * (uint32_t)(lane & 1);
   auto issue = [&](int kb, int slot) {
@@ -861,15 +881,17 @@ __device__ void gemm_a_mx_body(const LayerArgs& a, const ProjSlot& W, int Iu, in
 
   int brow[4];
 #pragma unroll
-  for (int nj = 0; nj < 4; ++nj) brow[nj] = (nj < 2 ? 32 * wn + 16 * nj : 64 + 32 * wn + 16 * (nj - 2)) + m;
+  for (int nj = 0; nj < 4; ++nj)
+    brow[nj] = (STB ? 64 * wn + 16 * nj : nj < 2 ? 32 * wn + 16 * nj : 64 + 32 * wn + 16 * (nj - 2)) + m;
   for (int t = 0; t < NT; ++t) {
-    const int cc = c0 + 64 * t;
-    uint32_t bgb[2], bub[2];  // bias bits (converted in the epilogue)
+    const int cc = c0 + kTileN * t;
+    uint32_t bb[4];  // bias bits (converted in the epilogue): stage A gate j, up j; stage B column nj
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int ch = cc + 32 * wn + 16 * j + m;
-      bgb[j] = W.bias != nullptr ? load_bits(W.bias, ch, W.bias_dt) : 0u;
-      bub[j] = W.bias != nullptr ? load_bits(W.bias, Iu + ch, W.bias_dt) : 0u;
+    for (int j = 0; j < 4; ++j) {
+      int ch;
+      if constexpr (STB) ch = cc + 64 * wn + 16 * j + m;
+      else ch = (j < 2 ? 0 : Iu) + cc + 32 * wn + 16 * (j & 1) + m;
+      bb[j] = W.bias != nullptr && ch < W.N ? load_bits(W.bias, ch, W.bias_dt) : 0u;
     }
     f32x4 acc[MI][4];
 #pragma unroll
@@ -878,10 +900,10 @@ __device__ void gemm_a_mx_body(const LayerArgs& a, const ProjSlot& W, int Iu, in
       for (int nj = 0; nj < 4; ++nj) acc[mi][nj] = (f32x4){0.f, 0.f, 0.f, 0.f};
     for (int kb = 0; kb < nsteps; ++kb) {
       // this wave's copies of stage kb have landed (the next stage's, and
-      // the bias loads issued after them, may be in flight), then every
-      // wave's have; every wave is also done with stage kb - 1 (its reads fed
-      // MFMAs that have issued).  A plain barrier: __syncthreads' release
-      // fence would wait for every copy in flight, the next stage's too.
+      // loads issued after them, may be in flight), then every wave's have;
+      // every wave is also done with stage kb - 1 (its reads fed MFMAs that
+      // have issued).  A plain barrier: __syncthreads' release fence would
+      // wait for every copy in flight, the next stage's too.
       if (kb + 1 < nsteps) {
         if (na == P::kAMax) wait_vm<P::kLoadsMax>(); else wait_vm<P::kLoadsMax - 1>();
       } else {
@@ -918,44 +940,106 @@ __device__ void gemm_a_mx_body(const LayerArgs& a, const ProjSlot& W, int Iu, in
         }
       }
     }
+    // every wave is done with the ring (its last reads fed MFMAs that have
+    // issued): the next tile's first stages go out before this epilogue, into
+    // slots 0 and 1; stage A stages its output rows in slot 2
+    asm volatile("s_barrier" ::: "memory");
     if (t + 1 < NT) {
-      // every wave is done with the ring (its last reads fed MFMAs that have
-      // issued): the next tile's first stages go out before this epilogue
-      asm volatile("s_barrier" ::: "memory");
-      tile_sources(cc + 64);
+      tile_sources(cc + kTileN);
       for (int kb = 0; kb < pro; ++kb) issue(kb, kb);
     }
 
-    // ---- epilogue: h = act(gate + b_g, up + b_u), bf16, for the tile's real rows
+    if constexpr (STB) {
+      // ---- stage B epilogue: router-weighted fp32 rows into the slot buffer
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int ch = cc + 32 * wn + 16 * j + m;
-      const float bg = bits_to_f32(opaque_bits(bgb[j]), W.bias_dt);
-      const float bu = bits_to_f32(opaque_bits(bub[j]), W.bias_dt);
+      for (int nj = 0; nj < 4; ++nj) {
+        const int col = cc + 64 * wn + 16 * nj + m;
+        const float bn = bits_to_f32(opaque_bits(bb[nj]), W.bias_dt);
+#pragma unroll
+        for (int mi = 0; mi < MI; ++mi)
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            if (pe[mi][r] >= 0 && col < W.N) a.ybuf[(size_t)pe[mi][r] * H + col] = (acc[mi][nj][r] + bn) * we[mi][r];
+      }
+    } else {
+      // ---- stage A epilogue: h = bf16(act(gate + b_g, up + b_u)), split into
+      // e4m3 hi + lo over the wave's 32-channel block of each token row
+      char* stg = lds + 2 * P::kStage;
+      int* stg_pe = (int*)(stg + MT * kMxStgPitch);
+      const float bg0 = bits_to_f32(opaque_bits(bb[0]), W.bias_dt), bg1 = bits_to_f32(opaque_bits(bb[1]), W.bias_dt);
+      const float bu0 = bits_to_f32(opaque_bits(bb[2]), W.bias_dt), bu1 = bits_to_f32(opaque_bits(bb[3]), W.bias_dt);
 #pragma unroll
       for (int mi = 0; mi < MI; ++mi)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          if (pe[mi][r] >= 0) {
-            const float h = act_fn(a.L.act, acc[mi][j][r] + bg, acc[mi][j + 2][r] + bu, a.L.swiglu_alpha,
-                                   a.L.swiglu_limit);
-            store_scalar(a.hbuf, (size_t)pe[mi][r] * a.Imax + ch, FTM_DT_BF16, h);
+          const int tr = (MT / 2) * wm + 16 * mi + 4 * g + r;
+          const float h0 = bf16_to_f32(f32_to_bf16(
+              act_fn(a.L.act, acc[mi][0][r] + bg0, acc[mi][2][r] + bu0, a.L.swiglu_alpha, a.L.swiglu_limit)));
+          const float h1 = bf16_to_f32(f32_to_bf16(
+              act_fn(a.L.act, acc[mi][1][r] + bg1, acc[mi][3][r] + bu1, a.L.swiglu_alpha, a.L.swiglu_limit)));
+          // the block's largest |h| bit pattern over the row's 16 lanes (Inf / NaN: >= 0x7f800000)
+          int mb = max((int)(__float_as_uint(h0) & 0x7fffffffu), (int)(__float_as_uint(h1) & 0x7fffffffu));
+          mb = max(mb, dpp_i<kDppXor1>(mb));
+          mb = max(mb, dpp_i<kDppXor2>(mb));
+          mb = max(mb, dpp_i<kDppHalfMirror>(mb));
+          mb = max(mb, dpp_i<kDppMirror>(mb));
+          const uint32_t chi = (uint32_t)max((mb >> 23) - 7, 0);
+          const uint32_t clo = chi >= 4u ? chi - 4u : 0u;
+          const float inv = __uint_as_float((254u - chi) << 23);
+          const float flo = __uint_as_float((127u + chi - clo) << 23);
+          const float s0 = h0 * inv, s1 = h1 * inv;
+          const uint32_t q = f32x2_to_e4m3(s0, s1);
+          const uint32_t l = f32x2_to_e4m3((s0 - e4m3_at<0>(q)) * flo, (s1 - e4m3_at<1>(q)) * flo);
+          char* row = stg + tr * kMxStgPitch;
+          row[32 * wn + m] = (char)q;
+          row[32 * wn + 16 + m] = (char)(q >> 8);
+          row[64 + 32 * wn + m] = (char)l;
+          row[64 + 32 * wn + 16 + m] = (char)(l >> 8);
+          if (m == 0) {
+            *(uint16_t*)(row + 128 + 2 * wn) = (uint16_t)(mb < 0x7f800000 ? (chi | (clo << 8)) : 0xffffu);
+            stg_pe[tr] = pe[mi][r];
           }
         }
+      asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+      // copy out: per row 4 hi pieces, 4 lo pieces, the scale word; the last
+      // tile of an I with a half chunk also clears that chunk's other half
+      uint8_t* hq = (uint8_t*)a.hbuf;
+      const size_t hrow = (size_t)mx_row_bytes(a.Imax);
+      const int chunk = cc / 128, half = (cc / 64) & 1;
+      const bool clear = cc + 64 == Iu && half == 0;
+      const int pieces = clear ? 18 : 9;
+      for (int q = tid; q < MT * pieces; q += kBlock) {
+        const int tr = q / pieces, k = q - tr * pieces;
+        const int p = stg_pe[tr];
+        if (p < 0) continue;
+        uint8_t* dst = hq + (size_t)p * hrow + (size_t)chunk * kMxChunk;
+        const char* src = stg + tr * kMxStgPitch;
+        if (k < 8) {
+          *(u32x4*)(dst + (k < 4 ? 64 * half + 16 * k : 128 + 64 * half + 16 * (k - 4))) = *(const u32x4*)(src + 16 * k);
+        } else if (k == 8) {
+          *(uint32_t*)(dst + 256 + 4 * half) = *(const uint32_t*)(src + 128);
+        } else if (k < 17) {
+          const int kk = k - 9;  // the other half: zeros
+          *(u32x4*)(dst + (kk < 4 ? 64 + 16 * kk : 128 + 64 + 16 * (kk - 4))) = (u32x4){0u, 0u, 0u, 0u};
+        } else {
+          *(uint32_t*)(dst + 260) = 0u;
+        }
+      }
     }
   }
 }
 
-// Routed MXFP4 stage A tiles (a layer without a shared expert, mx_gemm_ok):
-// one workgroup per (M tile, kMxNT consecutive N tiles), items in XCD-aware
-// order.
+// Routed MXFP4 expert tiles on the scaled MFMAs (a layer without a shared
+// expert, mx_gemm_ok): one workgroup per (M tile, kMxNT consecutive N
+// tiles), items in XCD-aware order.  STB: stage B (w2, the quantised h).
 constexpr int kMxM = 64;   // tokens per tile: two workgroups per CU
-constexpr int kMxNT = 3;   // 64-channel tiles per workgroup
-__global__ __launch_bounds__(kBlock) void k_gemm_a_mx(const LayerArgs a) {
+constexpr int kMxNT = 3;   // N tiles per workgroup
+template <bool STB>
+__global__ __launch_bounds__(kBlock) void k_gemm_mx(const LayerArgs a) {
   const int item = xcd_item(blockIdx.x, gridDim.x);
-  const int I = a.L.inter;
   const int nRouted = a.ctrl[kCtrlNRouted];
-  const int ntn = (I / 64 + kMxNT - 1) / kMxNT;
+  const int tiles = STB ? (a.L.hidden + 127) / 128 : a.L.inter / 64;
+  const int ntn = (tiles + kMxNT - 1) / kMxNT;
   const int routed_items = gemm_routed_mtiles<kMxM>(a, nRouted) * ntn;
   if (item >= routed_items) return;
   const GemmTile t = gemm_find_tile<kMxM>(a, item / ntn, nRouted, false);
@@ -964,14 +1048,24 @@ __global__ __launch_bounds__(kBlock) void k_gemm_a_mx(const LayerArgs a) {
   // from them are scalar too (no per-load waterfall loops)
   const int e = __builtin_amdgcn_readfirstlane(a.uniq[t.u]);
   const int slot = __builtin_amdgcn_readfirstlane(a.L.slot_of_expert ? a.L.slot_of_expert[e] : e);
-  if (slot < 0 || slot >= a.L.w13.num_slots) {
+  const ftm_proj& PW = STB ? a.L.w2 : a.L.w13;
+  const int n0 = (item % ntn) * kMxNT;
+  const int nt = tiles - n0 < kMxNT ? tiles - n0 : kMxNT;
+  const int32_t* list = a.lists + (size_t)e * a.T;
+  const int m0 = __builtin_amdgcn_readfirstlane(t.m0), cnt = __builtin_amdgcn_readfirstlane(t.cnt);
+  if (slot < 0 || slot >= PW.num_slots) {
+    if (STB) {  // non-resident expert: its rows contribute zeros
+      const int H = a.L.hidden;
+      for (int idx = threadIdx.x; idx < kMxM * 128 * nt; idx += kBlock) {
+        const int mm = m0 + idx / (128 * nt), col = 128 * n0 + idx % (128 * nt);
+        if (mm < cnt && col < H) a.ybuf[(size_t)list[mm] * H + col] = 0.0f;
+      }
+    }
     if (threadIdx.x == 0) atomicOr(&a.ctrl[kCtrlError], 1);
     return;
   }
-  const int n0 = (item % ntn) * kMxNT;
-  const int nt = I / 64 - n0 < kMxNT ? I / 64 - n0 : kMxNT;
-  gemm_a_mx_body<kMxM>(a, proj_slot(a.L.w13, slot), I, 64 * n0, nt, __builtin_amdgcn_readfirstlane(t.m0),
-                       __builtin_amdgcn_readfirstlane(t.cnt), a.lists + (size_t)e * a.T, (char*)ftm_ring_lds);
+  gemm_mx_body<kMxM, STB>(a, proj_slot(PW, slot), a.L.inter, (STB ? 128 : 64) * n0, nt, m0, cnt, list,
+                          (char*)ftm_ring_lds);
 }
 
 // ---------------------------------------------------------------- stage B (w2 -> slot buffer)
@@ -1114,7 +1208,7 @@ bool mx_gemm_ok(const ftm_moe_layer& L) {
 }
 
 const char* gemm_a_kernel_name(const ftm_moe_layer& L) {
-  return mx_gemm_ok(L) ? "k_gemm_a_mx" : ring_ok(L) ? "k_gemm_a_ring" : "k_gemm_a";
+  return mx_gemm_ok(L) ? "k_gemm_mx" : ring_ok(L) ? "k_gemm_a_ring" : "k_gemm_a";
 }
 
 template <int FMT>
@@ -1133,18 +1227,28 @@ static void launch_gemm_t(const LayerArgs& a, hipStream_t st, int which, bool xq
   const ftm_moe_layer& L = a.L;
   const long pairs = (long)a.T * L.topk;
   const long maxU = L.num_experts < pairs ? L.num_experts : pairs;
-  if (FMT == FTM_FMT_MXFP4 && (which & 1) && mx_gemm_ok(L)) {
-    // stage A on the scaled-MFMA tiles, over the quantised input
+  if (FMT == FTM_FMT_MXFP4 && mx_gemm_ok(L)) {
+    // both stages on the scaled-MFMA tiles: stage A over the quantised input,
+    // writing h quantised the same way for stage B
     static bool attr = false;
     if (!attr) {
-      (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&k_gemm_a_mx),
+      (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&k_gemm_mx<false>),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)mx_tile_lds<kMxM>());
+      (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&k_gemm_mx<true>),
                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)mx_tile_lds<kMxM>());
       attr = true;
     }
-    if (!xq_ready) launch_quant_mx(a.x, a.T, L.hidden, a.xq, st);
-    const long items = (pairs / kMxM + maxU + 1) * ((L.inter / 64 + kMxNT - 1) / kMxNT);
-    hipLaunchKernelGGL(k_gemm_a_mx, dim3((unsigned)items), dim3(kBlock), mx_tile_lds<kMxM>(), st, a);
-    which &= ~1;
+    const long mt = pairs / kMxM + maxU + 1;
+    if (which & 1) {
+      if (!xq_ready) launch_quant_mx(a.x, a.T, L.hidden, a.xq, st);
+      const long items = mt * ((L.inter / 64 + kMxNT - 1) / kMxNT);
+      hipLaunchKernelGGL(k_gemm_mx<false>, dim3((unsigned)items), dim3(kBlock), mx_tile_lds<kMxM>(), st, a);
+    }
+    if (which & 2) {
+      const long items = mt * (((L.hidden + 127) / 128 + kMxNT - 1) / kMxNT);
+      hipLaunchKernelGGL(k_gemm_mx<true>, dim3((unsigned)items), dim3(kBlock), mx_tile_lds<kMxM>(), st, a);
+    }
+    return;
   }
   const long mt_routed = pairs / kGM + maxU + 1;
   const long mt_shared = L.shared_inter > 0 ? (a.T + kGM - 1) / kGM : 0;

@@ -90,9 +90,11 @@ inline WsLayout ws_layout(const ftm_moe_layer& L, int T) {
   w.uniq = o;   o = align_up(o + 4 * (size_t)(w.E + 1), 256);
   w.ucnt = o;   o = align_up(o + 4 * (size_t)(w.E + 1), 256);
   w.recs = o;   o = align_up(o + 4 * (size_t)kRecWords * (w.E + 1), 256);
-  w.hbuf = o;   o = align_up(o + act * Tt * w.KP * w.Imax, 256);
-  w.ybuf = o;   o = align_up(o + 4 * Tt * w.KP * (size_t)L.hidden, 256);
+  // MXFP4 layers: h also as the scaled-MFMA tiles' quantised rows (kMxChunk layout by pair)
   const bool mx = L.w13.fmt == FTM_FMT_MXFP4 && L.act_dtype == FTM_DT_BF16;
+  const size_t hb = act * Tt * w.KP * w.Imax, hq = mx ? Tt * w.KP * (size_t)mx_row_bytes(w.Imax) : 0;
+  w.hbuf = o;   o = align_up(o + (hb > hq ? hb : hq), 256);
+  w.ybuf = o;   o = align_up(o + 4 * Tt * w.KP * (size_t)L.hidden, 256);
   w.xq = o;     o = align_up(o + (mx ? Tt * (size_t)mx_row_bytes(L.hidden) : 0), 256);
   w.total = o;
   return w;

@@ -45,28 +45,6 @@ namespace ftm {
 //   A (e4m3): lane l holds token row l % 16 at K [16 g, 16 g + 16) and
 //             [64 + 16 g, 64 + 16 g + 16) (8 registers), and in scale_a the
 //             scale of the row's block g (K [32 g, 32 g + 32)).
-// |v| < 448 to e4m3fn, round to nearest even (the callers keep |v| < 257).
-__device__ __forceinline__ uint32_t f32_to_e4m3(float v) {
-  const uint32_t sgn = (__float_as_uint(v) >> 24) & 0x80u;
-  const float a = fabsf(v);
-  uint32_t code;
-  if (a < 0x1p-6f) {
-    // subnormals: steps of 2^-9 (8 steps round up to the smallest normal, code 8)
-    code = (uint32_t)__builtin_rintf(a * 512.0f);
-  } else {
-    const uint32_t ab = __float_as_uint(a);
-    const float m = __uint_as_float((ab & 0x7fffffu) | 0x3f800000u);  // significand in [1, 2)
-    // a carry of the rounded mantissa moves into the exponent field
-    code = ((ab >> 23) - 120u) * 8u + (uint32_t)__builtin_rintf((m - 1.0f) * 8.0f);
-  }
-  return sgn | code;
-}
-__device__ __forceinline__ float e4m3_to_f32(uint32_t c) {
-  const uint32_t e = (c >> 3) & 15u, m = c & 7u;
-  const float mag = e == 0 ? (float)m * 0x1p-9f : __uint_as_float(((e + 120u) << 23) | (m << 20));
-  return (c & 0x80u) ? -mag : mag;
-}
-
 // One 32-element block of a token row (T rows of H bf16) per 4 lanes, 8
 // elements a lane: with E = floor(log2 max|x|) the hi scale is 2^(E - 7), so
 // the block maps into [-256, 256); hi = e4m3(x / s_hi) and lo = e4m3((x /
@@ -104,14 +82,10 @@ __device__ __forceinline__ void quant_mx_piece(const uint16_t* __restrict__ x, i
   uint32_t hw[2], lw[2];
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
-    hw[h] = lw[h] = 0u;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const float sv = v[4 * h + j] * inv;
-      const uint32_t c = f32_to_e4m3(sv);
-      hw[h] |= c << (8 * j);
-      lw[h] |= f32_to_e4m3((sv - e4m3_to_f32(c)) * flo) << (8 * j);
-    }
+    const float s0 = v[4 * h] * inv, s1 = v[4 * h + 1] * inv, s2 = v[4 * h + 2] * inv, s3 = v[4 * h + 3] * inv;
+    hw[h] = f32x4_to_e4m3(s0, s1, s2, s3);
+    lw[h] = f32x4_to_e4m3((s0 - e4m3_at<0>(hw[h])) * flo, (s1 - e4m3_at<1>(hw[h])) * flo,
+                          (s2 - e4m3_at<2>(hw[h])) * flo, (s3 - e4m3_at<3>(hw[h])) * flo);
   }
   const int c = q >> 4, p = q & 15;
   uint8_t* o = xq + (size_t)t * (size_t)((H + 127) / 128 * kMxChunk) + (size_t)c * kMxChunk;
@@ -3255,7 +3229,7 @@ const char* stage_kernel_name(const ftm_moe_layer& L, int T, int stage) {
     case FTM_STAGE_W2: break;
     default: return nullptr;
   }
-  if (gemm_path_ok(L, T)) return stage == FTM_STAGE_W13 ? gemm_a_kernel_name(L) : "k_gemm_b";
+  if (gemm_path_ok(L, T)) return stage == FTM_STAGE_W13 || mx_gemm_ok(L) ? gemm_a_kernel_name(L) : "k_gemm_b";
   switch (L.w13.fmt) {
     case FTM_FMT_BF16: return expert_kernel_name_dt<FTM_FMT_BF16>(L, T, stage);
     case FTM_FMT_FP8_BLOCK: return expert_kernel_name_dt<FTM_FMT_FP8_BLOCK>(L, T, stage);

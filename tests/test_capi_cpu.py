@@ -217,8 +217,8 @@ def test_stage_kernel_names_follow_the_dispatch():
     for T in (1, 8, 32, 64, 128):
         assert name(mx, T, nat.STAGE_W13) == "k_stage_a_xl", T
         assert name(mx, T, nat.STAGE_W2) == "k_stage_b_ks", T
-    assert name(mx, 129, nat.STAGE_W13) == "k_gemm_a_mx"  # scaled-MFMA tiles (no shared expert)
-    assert name(mx, 129, nat.STAGE_W2) == "k_gemm_b"
+    assert name(mx, 129, nat.STAGE_W13) == "k_gemm_mx"  # scaled-MFMA tiles (no shared expert)
+    assert name(mx, 129, nat.STAGE_W2) == "k_gemm_mx"
     # many experts: the LDS path up to 256 tokens, the register-fed kernels above
     mx.num_experts = 256
     assert name(mx, 256, nat.STAGE_W13) == "k_stage_a_xl"
