@@ -738,61 +738,59 @@ __global__ __launch_bounds__(kBlock) void k_gemm_a_ring(const LayerArgs a) {
   gemm_a_item<FMT, true>(a, xcd_item(blockIdx.x, gridDim.x), ftm_ring_lds, nullptr);
 }
 
-// ---------------------------------------------------------------- scaled-MFMA tiles (MXFP4 stage A)
-// Stage A of MXFP4 layers above the crossover on v_mfma_scale_f32_16x16x128_f8f6f4
-// with the decode path's operand layouts (ftm_moe.hip): the weights go in as
-// stored (e2m1 nibbles, e8m0 block scales), the input as its two-term e4m3
-// split (the xq workspace region: kMxChunk bytes per token and 128 K, written
-// by the router launch or k_quant_mx).  No weight is decoded.
-// Tile: MT tokens x 128 weight rows (64 gate + 64 up channels), K steps of
-// 128.  The four waves sit 2 x 2, each MT/2 tokens x 64 rows (MT/32 x 4
-// blocks of 16 x 16: 32 gate + 32 up rows), so one A read feeds four weight
-// blocks and one B read MT/32 token blocks.  A three-stage LDS ring is filled
-// by direct global->LDS copies two K steps ahead: per stage the tile's token
-// chunks (kMxChunk bytes each, 16-byte slots in order), its weight rows (64
-// bytes per row, slot q of row r holding piece q ^ ring_fw(r), so the 16 rows
-// of one B read hit distinct banks) and the rows' four e8m0 bytes of the step
-// (16-bit copies, which land one per 4-byte LDS slot).  At MT = 64 two
-// workgroups fit a CU, so one's barriers, prologue and epilogue overlap the
-// other's MFMAs.
-constexpr int kMxK = 128;  // K per step
-template <int MT>
+// ---------------------------------------------------------------- scaled-MFMA tiles (MXFP4)
+// The expert stages of MXFP4 layers above the crossover on
+// v_mfma_scale_f32_16x16x128_f8f6f4 with the decode path's operand layouts
+// (ftm_moe.hip): the weights go in as stored (e2m1 nibbles, e8m0 block
+// scales), the activations as their two-term e4m3 split (kMxChunk bytes per
+// row and 128 K: the input by token in the xq region, written by the router
+// launch or k_quant_mx; h by pair in the h buffer, written by stage A's
+// epilogue).  No weight is decoded.
+// Tile: MT rows (pairs) x 256 weight rows -- stage A 128 gate + 128 up
+// channels, stage B 256 output columns -- K steps of 128.  Eight waves sit
+// 2 x 4, each MT/2 rows x 64 weight rows (MT/32 x 4 blocks of 16 x 16), so
+// one A read feeds four weight blocks and one B read MT/32 row blocks, and
+// each byte copied to LDS feeds 4-8x as many MFMAs as a 64 x 64-channel tile
+// (the copies, not the MFMAs, bound the smaller tiles).  A three-stage LDS
+// ring is filled by direct global->LDS copies two K steps ahead: per stage
+// the tile's row chunks (16-byte slots in order), its weight rows (64 bytes
+// per row, slot q of row r holding piece q ^ ring_fw(r), so the 16 rows of
+// one B read hit distinct banks) and the rows' four e8m0 bytes of the step
+// (16-bit copies, which land one per 4-byte LDS slot).
+constexpr int kMxK = 128;      // K per step
+constexpr int kMxThreads = 512;
+constexpr int kMxNR = 256;     // weight rows per tile
+template <int MT, int S = 3>
 struct MxPlan {
-  static constexpr int kMI = MT / 32;                              // 16-token blocks per wave
-  static constexpr int kACopies = MT * (kMxChunk / 16) / 64;       // 16-byte copies of the A chunks per stage
+  static constexpr int kMI = MT / 32;                            // 16-row blocks per wave
+  static constexpr int kACopies = MT * (kMxChunk / 16) / 64;     // 16-byte copies of the A chunks per stage
   static constexpr int kABytes = kACopies * 1024;
-  static constexpr int kWBytes = 128 * 64;
-  static constexpr int kSBytes = 256 * 4;                          // 128 rows x 2 halves, one 4-byte slot each
+  static constexpr int kWBytes = kMxNR * 64;
+  static constexpr int kSBytes = kMxNR * 2 * 4;                  // 2 halves per row, one 4-byte slot each
   static constexpr int kStage = kABytes + kWBytes + kSBytes;
-  static constexpr int kStages = 3;
+  static constexpr int kStages = S;
   static constexpr int kLds = kStages * kStage;
-  // copies per wave per stage: A copies w, w + 4, ...; two W copies; one scale copy
-  static constexpr int kAMax = (kACopies + 3) / 4;
+  // copies per wave per stage: A copies w, w + 8, ...; two W copies; one scale copy
+  static constexpr int kAMax = (kACopies + 7) / 8;
   static constexpr int kLoadsMax = kAMax + 3;
   static_assert(MT * (kMxChunk / 16) % 64 == 0 && kLoadsMax < 64, "copy shape");
+  static_assert(MT * kMxChunk + MT * 4 <= kStage, "stage A's output rows fit one ring slot");
+  static_assert(S == 2 || S == 3, "ring depth");
 };
 
-// The kernel's dynamic LDS (mx_gemm_ok checks it against the CU's 160 KiB).
-template <int MT>
-__host__ __device__ __forceinline__ size_t mx_tile_lds() { return (size_t)MxPlan<MT>::kLds; }
+template <int MT, int S>
+__host__ __device__ __forceinline__ size_t mx_tile_lds() { return (size_t)MxPlan<MT, S>::kLds; }
 
-// Stage A writes h quantised for stage B's scaled MFMAs (the same two-term
-// e4m3 split and kMxChunk layout as the input, rows by pair, in the h
-// buffer): a wave's 32 channels of a token are one 32-element block, so its
-// scale comes from a 16-lane DPP max.  Staged through LDS and copied out in
-// 16-byte pieces per row: [hi 64][lo 64][scale words 4], kMxStgPitch apart.
-constexpr int kMxStgPitch = 144;
-
-// NT consecutive N tiles of one M tile -- stage A: 64 channels (gate + up
-// rows) each; stage B (STB): 128 output columns (w2 rows) each.  The token
-// rows' sources and the epilogue's pairs are resolved once, and the next
-// tile's first two stages are issued before this tile's epilogue.
-template <int MT, bool STB>
+// NT consecutive N tiles of one M tile (stage A: 128 channels each; stage B,
+// STB: 256 output columns each).  The A rows' sources and the epilogue's
+// pairs are resolved once, and the next tile's first two stages are issued
+// before this tile's epilogue.
+template <int MT, int S, bool STB>
 __device__ void gemm_mx_body(const LayerArgs& a, const ProjSlot& W, int Iu, int c0, int NT, int m0, int cnt,
                              const int32_t* list, char* lds) {
-  using P = MxPlan<MT>;
+  using P = MxPlan<MT, S>;
   constexpr int MI = P::kMI;
-  constexpr int kTileN = STB ? 128 : 64;
+  constexpr int kTileN = STB ? kMxNR : kMxNR / 2;
   typedef __attribute__((address_space(1))) const void* GPtr;
   typedef __attribute__((address_space(3))) void* LPtr;
   const int tid = threadIdx.x, lane = tid & 63;
@@ -805,7 +803,7 @@ __device__ void gemm_mx_body(const LayerArgs& a, const ProjSlot& W, int Iu, int 
   const uint32_t kgb = (uint32_t)K / 32;  // e8m0 bytes per row (even: K % 64 == 0)
   const Rsrc lres = make_rsrc(list, (uint32_t)a.T * 4u);
   const int p0 = pair_of_row(lres, true, m0, cnt, KP, 0);
-  const int na = (P::kACopies - wave + 3) / 4;  // this wave's A copies per stage
+  const int na = (P::kACopies - wave + 7) / 8;  // this wave's A copies per stage
   // A rows: stage A the quantised input by token, stage B the quantised h by pair
   const uint8_t* abase = STB ? (const uint8_t*)a.hbuf : a.xq;
   const size_t arow = (size_t)mx_row_bytes(STB ? a.Imax : H);
@@ -816,7 +814,7 @@ __device__ void gemm_mx_body(const LayerArgs& a, const ProjSlot& W, int Iu, int 
   const char* asrc[P::kAMax];
 #pragma unroll
   for (int i = 0; i < P::kAMax; ++i) {
-    const int sl = 64 * (4 * i + wave) + lane;
+    const int sl = 64 * (8 * i + wave) + lane;
     const int r = sl / (kMxChunk / 16), pc = sl - r * (kMxChunk / 16);
     int pr = r < MT ? pair_of_row(lres, true, m0 + r, cnt, KP, 0) : -1;
     pr = pr >= 0 ? pr : p0;
@@ -836,21 +834,24 @@ __device__ void gemm_mx_body(const LayerArgs& a, const ProjSlot& W, int Iu, int 
 
   // ---- per-tile weight sources.  W slot s = row s / 4, slot s % 4 holding
   // piece (s % 4) ^ ring_fw(row); a piece past the row's end (last K step)
-  // re-reads the row's first: finite e2m1 codes against zero activations
-  // (stage B rows past N repeat row N - 1; their columns are not stored).
+  // re-reads the row's first: finite e2m1 codes against zero activations.
+  // Rows past the projection (the last tile) repeat its last row; their
+  // outputs are dropped (stage B) or zeroed (stage A's channels past I).
   // Scale slot s = row s / 2, bytes 2 (s % 2), +1 of the step's four (past
   // the row's end its first two, against zero activations).
   const char* wrow[2];
   uint32_t wpo[2];
   const char* srow;
   auto grow = [&](int cc, int r) {
-    if constexpr (STB) return cc + r < W.N ? cc + r : W.N - 1;
-    return r < 64 ? cc + r : Iu + cc + (r - 64);
+    int row;
+    if constexpr (STB) row = cc + r;
+    else row = r < kMxNR / 2 ? cc + r : Iu + cc + (r - kMxNR / 2);
+    return row < W.N ? row : W.N - 1;
   };
   auto tile_sources = [&](int cc) {
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
-      const int sl = 64 * (4 * i + wave) + lane;
+      const int sl = 64 * (8 * i + wave) + lane;
       const int r = sl >> 2;
       wrow[i] = (const char*)W.w + (size_t)grow(cc, r) * rb;
       wpo[i] = 16u * (uint32_t)((sl & 3) ^ ring_fw(r));
@@ -864,12 +865,12 @@ __device__ void gemm_mx_body(const LayerArgs& a, const ProjSlot& W, int Iu, int 
     for (int i = 0; i < P::kAMax; ++i)
       if (i < na)
         __builtin_amdgcn_global_load_lds((GPtr)(asrc[i] + (size_t)kb * kMxChunk),
-                                         (LPtr)(st + 1024 * (4 * i + wave)), 16, 0, 0);
+                                         (LPtr)(st + 1024 * (8 * i + wave)), 16, 0, 0);
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       const uint32_t off = 64u * (uint32_t)kb + wpo[i];
       __builtin_amdgcn_global_load_lds((GPtr)(wrow[i] + (off + 16u <= rb ? off : 0u)),
-                                       (LPtr)(st + P::kABytes + 1024 * (4 * i + wave)), 16, 0, 0);
+                                       (LPtr)(st + P::kABytes + 1024 * (8 * i + wave)), 16, 0, 0);
     }
     const uint32_t so = 4u * (uint32_t)kb + sho;
     __builtin_amdgcn_global_load_lds((GPtr)(srow + (so + 2u <= kgb ? so : 0u)),
@@ -882,7 +883,7 @@ __device__ void gemm_mx_body(const LayerArgs& a, const ProjSlot& W, int Iu, int 
   int brow[4];
 #pragma unroll
   for (int nj = 0; nj < 4; ++nj)
-    brow[nj] = (STB ? 64 * wn + 16 * nj : nj < 2 ? 32 * wn + 16 * nj : 64 + 32 * wn + 16 * (nj - 2)) + m;
+    brow[nj] = (STB ? 64 * wn + 16 * nj : nj < 2 ? 32 * wn + 16 * nj : kMxNR / 2 + 32 * wn + 16 * (nj - 2)) + m;
   for (int t = 0; t < NT; ++t) {
     const int cc = c0 + kTileN * t;
     uint32_t bb[4];  // bias bits (converted in the epilogue): stage A gate j, up j; stage B column nj
@@ -904,10 +905,10 @@ __device__ void gemm_mx_body(const LayerArgs& a, const ProjSlot& W, int Iu, int 
       // every wave is also done with stage kb - 1 (its reads fed MFMAs that
       // have issued).  A plain barrier: __syncthreads' release fence would
       // wait for every copy in flight, the next stage's too.
-      if (kb + 1 < nsteps) {
+      if (S == 3 && kb + 1 < nsteps) {
         if (na == P::kAMax) wait_vm<P::kLoadsMax>(); else wait_vm<P::kLoadsMax - 1>();
       } else {
-        wait_vm<0>();
+        wait_vm<0>();  // two stages: nothing is issued past stage kb yet
       }
       asm volatile("s_barrier" ::: "memory");
       if (kb + P::kStages - 1 < nsteps) issue(kb + P::kStages - 1, (kb + P::kStages - 1) % P::kStages);
@@ -942,7 +943,7 @@ __device__ void gemm_mx_body(const LayerArgs& a, const ProjSlot& W, int Iu, int 
     }
     // every wave is done with the ring (its last reads fed MFMAs that have
     // issued): the next tile's first stages go out before this epilogue, into
-    // slots 0 and 1; stage A stages its output rows in slot 2
+    // slots 0 .. S - 2; stage A stages its output rows in slot S - 1
     asm volatile("s_barrier" ::: "memory");
     if (t + 1 < NT) {
       tile_sources(cc + kTileN);
@@ -962,21 +963,26 @@ __device__ void gemm_mx_body(const LayerArgs& a, const ProjSlot& W, int Iu, int 
             if (pe[mi][r] >= 0 && col < W.N) a.ybuf[(size_t)pe[mi][r] * H + col] = (acc[mi][nj][r] + bn) * we[mi][r];
       }
     } else {
-      // ---- stage A epilogue: h = bf16(act(gate + b_g, up + b_u)), split into
-      // e4m3 hi + lo over the wave's 32-channel block of each token row
-      char* stg = lds + 2 * P::kStage;
-      int* stg_pe = (int*)(stg + MT * kMxStgPitch);
+      // ---- stage A epilogue: h = bf16(act(gate + b_g, up + b_u)) (zero for
+      // channels past I), split into e4m3 hi + lo over the wave's 32-channel
+      // block of each row; the tile's 128 channels are one whole chunk, staged
+      // in slot 2 in the chunk layout and copied out in 16-byte pieces
+      char* stg = lds + (S - 1) * P::kStage;
+      int* stg_pe = (int*)(stg + MT * kMxChunk);
       const float bg0 = bits_to_f32(opaque_bits(bb[0]), W.bias_dt), bg1 = bits_to_f32(opaque_bits(bb[1]), W.bias_dt);
       const float bu0 = bits_to_f32(opaque_bits(bb[2]), W.bias_dt), bu1 = bits_to_f32(opaque_bits(bb[3]), W.bias_dt);
+      const bool in0 = cc + 32 * wn + m < Iu, in1 = cc + 32 * wn + 16 + m < Iu;
 #pragma unroll
       for (int mi = 0; mi < MI; ++mi)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int tr = (MT / 2) * wm + 16 * mi + 4 * g + r;
-          const float h0 = bf16_to_f32(f32_to_bf16(
+          float h0 = bf16_to_f32(f32_to_bf16(
               act_fn(a.L.act, acc[mi][0][r] + bg0, acc[mi][2][r] + bu0, a.L.swiglu_alpha, a.L.swiglu_limit)));
-          const float h1 = bf16_to_f32(f32_to_bf16(
+          float h1 = bf16_to_f32(f32_to_bf16(
               act_fn(a.L.act, acc[mi][1][r] + bg1, acc[mi][3][r] + bu1, a.L.swiglu_alpha, a.L.swiglu_limit)));
+          h0 = in0 ? h0 : 0.0f;
+          h1 = in1 ? h1 : 0.0f;
           // the block's largest |h| bit pattern over the row's 16 lanes (Inf / NaN: >= 0x7f800000)
           int mb = max((int)(__float_as_uint(h0) & 0x7fffffffu), (int)(__float_as_uint(h1) & 0x7fffffffu));
           mb = max(mb, dpp_i<kDppXor1>(mb));
@@ -990,40 +996,27 @@ __device__ void gemm_mx_body(const LayerArgs& a, const ProjSlot& W, int Iu, int 
           const float s0 = h0 * inv, s1 = h1 * inv;
           const uint32_t q = f32x2_to_e4m3(s0, s1);
           const uint32_t l = f32x2_to_e4m3((s0 - e4m3_at<0>(q)) * flo, (s1 - e4m3_at<1>(q)) * flo);
-          char* row = stg + tr * kMxStgPitch;
+          char* row = stg + tr * kMxChunk;
           row[32 * wn + m] = (char)q;
           row[32 * wn + 16 + m] = (char)(q >> 8);
-          row[64 + 32 * wn + m] = (char)l;
-          row[64 + 32 * wn + 16 + m] = (char)(l >> 8);
+          row[128 + 32 * wn + m] = (char)l;
+          row[128 + 32 * wn + 16 + m] = (char)(l >> 8);
           if (m == 0) {
-            *(uint16_t*)(row + 128 + 2 * wn) = (uint16_t)(mb < 0x7f800000 ? (chi | (clo << 8)) : 0xffffu);
+            *(uint16_t*)(row + 256 + 2 * wn) = (uint16_t)(mb < 0x7f800000 ? (chi | (clo << 8)) : 0xffffu);
             stg_pe[tr] = pe[mi][r];
           }
         }
       asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-      // copy out: per row 4 hi pieces, 4 lo pieces, the scale word; the last
-      // tile of an I with a half chunk also clears that chunk's other half
+      // copy out the chunk of each real row (its last 16 bytes: 8 scale bytes
+      // and 8 bytes nothing reads)
       uint8_t* hq = (uint8_t*)a.hbuf;
       const size_t hrow = (size_t)mx_row_bytes(a.Imax);
-      const int chunk = cc / 128, half = (cc / 64) & 1;
-      const bool clear = cc + 64 == Iu && half == 0;
-      const int pieces = clear ? 18 : 9;
-      for (int q = tid; q < MT * pieces; q += kBlock) {
-        const int tr = q / pieces, k = q - tr * pieces;
+      for (int q = tid; q < MT * (kMxChunk / 16); q += kMxThreads) {
+        const int tr = q / (kMxChunk / 16), k = q - tr * (kMxChunk / 16);
         const int p = stg_pe[tr];
-        if (p < 0) continue;
-        uint8_t* dst = hq + (size_t)p * hrow + (size_t)chunk * kMxChunk;
-        const char* src = stg + tr * kMxStgPitch;
-        if (k < 8) {
-          *(u32x4*)(dst + (k < 4 ? 64 * half + 16 * k : 128 + 64 * half + 16 * (k - 4))) = *(const u32x4*)(src + 16 * k);
-        } else if (k == 8) {
-          *(uint32_t*)(dst + 256 + 4 * half) = *(const uint32_t*)(src + 128);
-        } else if (k < 17) {
-          const int kk = k - 9;  // the other half: zeros
-          *(u32x4*)(dst + (kk < 4 ? 64 + 16 * kk : 128 + 64 + 16 * (kk - 4))) = (u32x4){0u, 0u, 0u, 0u};
-        } else {
-          *(uint32_t*)(dst + 260) = 0u;
-        }
+        if (p >= 0)
+          *(u32x4*)(hq + (size_t)p * hrow + (size_t)(cc / 128) * kMxChunk + 16 * k) =
+              *(const u32x4*)(stg + tr * kMxChunk + 16 * k);
       }
     }
   }
@@ -1032,17 +1025,16 @@ __device__ void gemm_mx_body(const LayerArgs& a, const ProjSlot& W, int Iu, int 
 // Routed MXFP4 expert tiles on the scaled MFMAs (a layer without a shared
 // expert, mx_gemm_ok): one workgroup per (M tile, kMxNT consecutive N
 // tiles), items in XCD-aware order.  STB: stage B (w2, the quantised h).
-constexpr int kMxM = 64;   // tokens per tile: two workgroups per CU
-constexpr int kMxNT = 3;   // N tiles per workgroup
-template <bool STB>
-__global__ __launch_bounds__(kBlock) void k_gemm_mx(const LayerArgs a) {
+constexpr int kMxNT = 2;   // N tiles per workgroup
+template <int MT, int S, bool STB>
+__global__ __launch_bounds__(kMxThreads) void k_gemm_mx(const LayerArgs a) {
   const int item = xcd_item(blockIdx.x, gridDim.x);
   const int nRouted = a.ctrl[kCtrlNRouted];
-  const int tiles = STB ? (a.L.hidden + 127) / 128 : a.L.inter / 64;
+  const int tiles = STB ? (a.L.hidden + kMxNR - 1) / kMxNR : (a.L.inter + kMxNR / 2 - 1) / (kMxNR / 2);
   const int ntn = (tiles + kMxNT - 1) / kMxNT;
-  const int routed_items = gemm_routed_mtiles<kMxM>(a, nRouted) * ntn;
+  const int routed_items = gemm_routed_mtiles<MT>(a, nRouted) * ntn;
   if (item >= routed_items) return;
-  const GemmTile t = gemm_find_tile<kMxM>(a, item / ntn, nRouted, false);
+  const GemmTile t = gemm_find_tile<MT>(a, item / ntn, nRouted, false);
   if (t.u < 0) return;
   // wave-uniform values in scalar registers, so the buffer descriptors built
   // from them are scalar too (no per-load waterfall loops)
@@ -1051,21 +1043,21 @@ __global__ __launch_bounds__(kBlock) void k_gemm_mx(const LayerArgs a) {
   const ftm_proj& PW = STB ? a.L.w2 : a.L.w13;
   const int n0 = (item % ntn) * kMxNT;
   const int nt = tiles - n0 < kMxNT ? tiles - n0 : kMxNT;
+  const int tn = STB ? kMxNR : kMxNR / 2;
   const int32_t* list = a.lists + (size_t)e * a.T;
   const int m0 = __builtin_amdgcn_readfirstlane(t.m0), cnt = __builtin_amdgcn_readfirstlane(t.cnt);
   if (slot < 0 || slot >= PW.num_slots) {
     if (STB) {  // non-resident expert: its rows contribute zeros
       const int H = a.L.hidden;
-      for (int idx = threadIdx.x; idx < kMxM * 128 * nt; idx += kBlock) {
-        const int mm = m0 + idx / (128 * nt), col = 128 * n0 + idx % (128 * nt);
+      for (int idx = threadIdx.x; idx < MT * tn * nt; idx += kMxThreads) {
+        const int mm = m0 + idx / (tn * nt), col = tn * n0 + idx % (tn * nt);
         if (mm < cnt && col < H) a.ybuf[(size_t)list[mm] * H + col] = 0.0f;
       }
     }
     if (threadIdx.x == 0) atomicOr(&a.ctrl[kCtrlError], 1);
     return;
   }
-  gemm_mx_body<kMxM, STB>(a, proj_slot(PW, slot), a.L.inter, (STB ? 128 : 64) * n0, nt, m0, cnt, list,
-                          (char*)ftm_ring_lds);
+  gemm_mx_body<MT, S, STB>(a, proj_slot(PW, slot), a.L.inter, tn * n0, nt, m0, cnt, list, (char*)ftm_ring_lds);
 }
 
 // ---------------------------------------------------------------- stage B (w2 -> slot buffer)
@@ -1203,8 +1195,8 @@ static size_t ring_lds_a(const ftm_moe_layer& L) {
   return (size_t)kRingA + (size_t)rows * g * 4;
 }
 bool mx_gemm_ok(const ftm_moe_layer& L) {
-  return L.w13.fmt == FTM_FMT_MXFP4 && L.act_dtype == FTM_DT_BF16 && L.shared_inter == 0 &&
-         mx_tile_lds<kMxM>() <= 160u * 1024u;
+  static_assert(MxPlan<128, 3>::kLds <= 160 * 1024, "the 128-row tile's ring fits a CU's LDS");
+  return L.w13.fmt == FTM_FMT_MXFP4 && L.act_dtype == FTM_DT_BF16 && L.shared_inter == 0;
 }
 
 const char* gemm_a_kernel_name(const ftm_moe_layer& L) {
@@ -1222,6 +1214,30 @@ static void ring_lds_attr() {
   }
 }
 
+template <int MT, int S>
+static void launch_gemm_mx(const LayerArgs& a, hipStream_t st, int which, bool xq_ready, long pairs, long maxU) {
+  const ftm_moe_layer& L = a.L;
+  static bool attr = false;
+  if (!attr) {
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&k_gemm_mx<MT, S, false>),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)MxPlan<MT, S>::kLds);
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&k_gemm_mx<MT, S, true>),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)MxPlan<MT, S>::kLds);
+    attr = true;
+  }
+  const long mt = pairs / MT + maxU + 1;
+  const size_t lds = mx_tile_lds<MT, S>();
+  if (which & 1) {
+    if (!xq_ready) launch_quant_mx(a.x, a.T, L.hidden, a.xq, st);
+    const long items = mt * (((L.inter + kMxNR / 2 - 1) / (kMxNR / 2) + kMxNT - 1) / kMxNT);
+    hipLaunchKernelGGL((k_gemm_mx<MT, S, false>), dim3((unsigned)items), dim3(kMxThreads), lds, st, a);
+  }
+  if (which & 2) {
+    const long items = mt * (((L.hidden + kMxNR - 1) / kMxNR + kMxNT - 1) / kMxNT);
+    hipLaunchKernelGGL((k_gemm_mx<MT, S, true>), dim3((unsigned)items), dim3(kMxThreads), lds, st, a);
+  }
+}
+
 template <int FMT>
 static void launch_gemm_t(const LayerArgs& a, hipStream_t st, int which, bool xq_ready) {
   const ftm_moe_layer& L = a.L;
@@ -1229,25 +1245,10 @@ static void launch_gemm_t(const LayerArgs& a, hipStream_t st, int which, bool xq
   const long maxU = L.num_experts < pairs ? L.num_experts : pairs;
   if (FMT == FTM_FMT_MXFP4 && mx_gemm_ok(L)) {
     // both stages on the scaled-MFMA tiles: stage A over the quantised input,
-    // writing h quantised the same way for stage B
-    static bool attr = false;
-    if (!attr) {
-      (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&k_gemm_mx<false>),
-                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)mx_tile_lds<kMxM>());
-      (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&k_gemm_mx<true>),
-                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)mx_tile_lds<kMxM>());
-      attr = true;
-    }
-    const long mt = pairs / kMxM + maxU + 1;
-    if (which & 1) {
-      if (!xq_ready) launch_quant_mx(a.x, a.T, L.hidden, a.xq, st);
-      const long items = mt * ((L.inter / 64 + kMxNT - 1) / kMxNT);
-      hipLaunchKernelGGL(k_gemm_mx<false>, dim3((unsigned)items), dim3(kBlock), mx_tile_lds<kMxM>(), st, a);
-    }
-    if (which & 2) {
-      const long items = mt * (((L.hidden + 127) / 128 + kMxNT - 1) / kMxNT);
-      hipLaunchKernelGGL(k_gemm_mx<true>, dim3((unsigned)items), dim3(kBlock), mx_tile_lds<kMxM>(), st, a);
-    }
+    // writing h quantised the same way for stage B.  128-row M tiles from 128
+    // pairs per expert on average, 64 below.
+    if (pairs >= 128 * maxU) launch_gemm_mx<128, 3>(a, st, which, xq_ready, pairs, maxU);
+    else launch_gemm_mx<64, 3>(a, st, which, xq_ready, pairs, maxU);
     return;
   }
   const long mt_routed = pairs / kGM + maxU + 1;
