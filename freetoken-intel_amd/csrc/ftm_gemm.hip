@@ -690,12 +690,13 @@ __device__ __forceinline__ void ring_a(const LayerArgs& a, const ProjSlot& W, in
   }
 }
 
-template <int FMT, bool RING>
+// SONLY: the shared expert's items only (its routed experts run elsewhere)
+template <int FMT, bool RING, bool SONLY = false>
 __device__ __forceinline__ void gemm_a_item(const LayerArgs& a, int item, uint16_t* sA, uint16_t* sB) {
   const int I = a.L.inter, Is = a.L.shared_inter;
   const int nRouted = a.ctrl[kCtrlNRouted];
   const int ntn = I / 64;
-  const int routed_items = gemm_routed_mtiles(a, nRouted) * ntn;
+  const int routed_items = SONLY ? 0 : gemm_routed_mtiles(a, nRouted) * ntn;
   if (item < routed_items) {
     const GemmTile t = gemm_find_tile(a, item / ntn, nRouted, false);
     if (t.u < 0) return;
@@ -733,9 +734,9 @@ extern __shared__ __attribute__((aligned(16))) uint16_t ftm_ring_lds[];
 
 // The ring tiles (dynamic LDS: ring + the layer's tile scales), items in
 // XCD-aware order.
-template <int FMT>
+template <int FMT, bool SONLY = false>
 __global__ __launch_bounds__(kBlock) void k_gemm_a_ring(const LayerArgs a) {
-  gemm_a_item<FMT, true>(a, xcd_item(blockIdx.x, gridDim.x), ftm_ring_lds, nullptr);
+  gemm_a_item<FMT, true, SONLY>(a, xcd_item(blockIdx.x, gridDim.x), ftm_ring_lds, nullptr);
 }
 
 // ---------------------------------------------------------------- scaled-MFMA tiles (MXFP4)
@@ -760,35 +761,39 @@ __global__ __launch_bounds__(kBlock) void k_gemm_a_ring(const LayerArgs a) {
 constexpr int kMxK = 128;      // K per step
 constexpr int kMxThreads = 512;
 constexpr int kMxNR = 256;     // weight rows per tile
-template <int MT, int S = 3>
+template <int MT, int S = 3, bool F8 = false>
 struct MxPlan {
   static constexpr int kMI = MT / 32;                            // 16-row blocks per wave
   static constexpr int kACopies = MT * (kMxChunk / 16) / 64;     // 16-byte copies of the A chunks per stage
   static constexpr int kABytes = kACopies * 1024;
-  static constexpr int kWBytes = kMxNR * 64;
-  static constexpr int kSBytes = kMxNR * 2 * 4;                  // 2 halves per row, one 4-byte slot each
+  static constexpr int kWRow = F8 ? 128 : 64;                    // weight bytes per row per step
+  static constexpr int kWPieces = kWRow / 16;
+  static constexpr int kWBytes = kMxNR * kWRow;
+  static constexpr int kSBytes = F8 ? 0 : kMxNR * 2 * 4;         // e8m0: 2 halves per row, one 4-byte slot each
   static constexpr int kStage = kABytes + kWBytes + kSBytes;
   static constexpr int kStages = S;
   static constexpr int kLds = kStages * kStage;
-  // copies per wave per stage: A copies w, w + 8, ...; two W copies; one scale copy
+  // copies per wave per stage: A copies w, w + 8, ...; kWPieces / 2 W copies; one e8m0 copy
   static constexpr int kAMax = (kACopies + 7) / 8;
-  static constexpr int kLoadsMax = kAMax + 3;
+  static constexpr int kWCopies = kWPieces / 2;
+  static constexpr int kLoadsMax = kAMax + kWCopies + (F8 ? 0 : 1);
   static_assert(MT * (kMxChunk / 16) % 64 == 0 && kLoadsMax < 64, "copy shape");
   static_assert(MT * kMxChunk + MT * 4 <= kStage, "stage A's output rows fit one ring slot");
   static_assert(S == 2 || S == 3, "ring depth");
 };
 
-template <int MT, int S>
-__host__ __device__ __forceinline__ size_t mx_tile_lds() { return (size_t)MxPlan<MT, S>::kLds; }
+template <int MT, int S, bool F8>
+__host__ __device__ __forceinline__ size_t mx_tile_lds() { return (size_t)MxPlan<MT, S, F8>::kLds; }
 
 // NT consecutive N tiles of one M tile (stage A: 128 channels each; stage B,
 // STB: 256 output columns each).  The A rows' sources and the epilogue's
 // pairs are resolved once, and the next tile's first two stages are issued
 // before this tile's epilogue.
-template <int MT, int S, bool STB>
+template <int WFMT, int MT, int S, bool STB>
 __device__ void gemm_mx_body(const LayerArgs& a, const ProjSlot& W, int Iu, int c0, int NT, int m0, int cnt,
                              const int32_t* list, char* lds) {
-  using P = MxPlan<MT, S>;
+  constexpr bool F8 = WFMT == FTM_FMT_FP8_BLOCK;
+  using P = MxPlan<MT, S, F8>;
   constexpr int MI = P::kMI;
   constexpr int kTileN = STB ? kMxNR : kMxNR / 2;
   typedef __attribute__((address_space(1))) const void* GPtr;
@@ -799,13 +804,14 @@ __device__ void gemm_mx_body(const LayerArgs& a, const ProjSlot& W, int Iu, int 
   const int g = lane >> 4, m = lane & 15;
   const int K = W.K, KP = a.KP, H = a.L.hidden;
   const int nsteps = (K + kMxK - 1) / kMxK;
-  const uint32_t rb = (uint32_t)K / 2;    // e2m1 bytes per weight row (a multiple of 16)
-  const uint32_t kgb = (uint32_t)K / 32;  // e8m0 bytes per row (even: K % 64 == 0)
+  const uint32_t rb = F8 ? (uint32_t)K : (uint32_t)K / 2;  // bytes per weight row (a multiple of 16)
+  const uint32_t kgb = (uint32_t)K / 32;  // MXFP4: e8m0 bytes per row (even: K % 64 == 0)
+  const int nkb = K / 128;                 // FP8: 128-wide scale blocks along K
   const Rsrc lres = make_rsrc(list, (uint32_t)a.T * 4u);
   const int p0 = pair_of_row(lres, true, m0, cnt, KP, 0);
   const int na = (P::kACopies - wave + 7) / 8;  // this wave's A copies per stage
   // A rows: stage A the quantised input by token, stage B the quantised h by pair
-  const uint8_t* abase = STB ? (const uint8_t*)a.hbuf : a.xq;
+  const uint8_t* abase = STB ? a.hq : a.xq;
   const size_t arow = (size_t)mx_row_bytes(STB ? a.Imax : H);
   const int adiv = STB ? 1 : KP;
 
@@ -832,16 +838,19 @@ __device__ void gemm_mx_body(const LayerArgs& a, const ProjSlot& W, int Iu, int 
       we[mi][r] = STB ? __uint_as_float(bload4(wres, pe[mi][r] >= 0 ? 4u * (uint32_t)pe[mi][r] : kOOB)) : 0.0f;
     }
 
-  // ---- per-tile weight sources.  W slot s = row s / 4, slot s % 4 holding
-  // piece (s % 4) ^ ring_fw(row); a piece past the row's end (last K step)
-  // re-reads the row's first: finite e2m1 codes against zero activations.
-  // Rows past the projection (the last tile) repeat its last row; their
-  // outputs are dropped (stage B) or zeroed (stage A's channels past I).
-  // Scale slot s = row s / 2, bytes 2 (s % 2), +1 of the step's four (past
-  // the row's end its first two, against zero activations).
-  const char* wrow[2];
-  uint32_t wpo[2];
-  const char* srow;
+  // ---- per-tile weight sources.  W slot s = row s / kWPieces, slot s %
+  // kWPieces holding that piece xor a swizzle of the row (ring_fw for 4
+  // pieces, ring_fa for 8); a piece past the row's end (last K step) re-reads
+  // the row's first: finite codes against zero activations.  Rows past the
+  // projection (the last tile) repeat its last row; their outputs are
+  // dropped (stage B) or zeroed (stage A's channels past I).  MXFP4 scale
+  // slot s = row s / 2, bytes 2 (s % 2), +1 of the step's four (past the
+  // row's end its first two, against zero activations).
+  constexpr int WC = P::kWCopies;
+  const char* wrow[WC];
+  uint32_t wpo[WC];
+  const char* srow = nullptr;
+  auto swz = [](int r) { return F8 ? ring_fa(r) : ring_fw(r); };
   auto grow = [&](int cc, int r) {
     int row;
     if constexpr (STB) row = cc + r;
@@ -850,13 +859,13 @@ __device__ void gemm_mx_body(const LayerArgs& a, const ProjSlot& W, int Iu, int 
   };
   auto tile_sources = [&](int cc) {
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
+    for (int i = 0; i < WC; ++i) {
       const int sl = 64 * (8 * i + wave) + lane;
-      const int r = sl >> 2;
+      const int r = sl / P::kWPieces;
       wrow[i] = (const char*)W.w + (size_t)grow(cc, r) * rb;
-      wpo[i] = 16u * (uint32_t)((sl & 3) ^ ring_fw(r));
+      wpo[i] = 16u * (uint32_t)((sl % P::kWPieces) ^ swz(r));
     }
-    srow = (const char*)W.s + (size_t)grow(cc, (64 * wave + lane) >> 1) * kgb;
+    if constexpr (!F8) srow = (const char*)W.s + (size_t)grow(cc, (64 * wave + lane) >> 1) * kgb;
   };
   const uint32_t sho = 2u * (uint32_t)(lane & 1);
   auto issue = [&](int kb, int slot) {
@@ -867,14 +876,16 @@ __device__ void gemm_mx_body(const LayerArgs& a, const ProjSlot& W, int Iu, int 
         __builtin_amdgcn_global_load_lds((GPtr)(asrc[i] + (size_t)kb * kMxChunk),
                                          (LPtr)(st + 1024 * (8 * i + wave)), 16, 0, 0);
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const uint32_t off = 64u * (uint32_t)kb + wpo[i];
+    for (int i = 0; i < WC; ++i) {
+      const uint32_t off = (uint32_t)P::kWRow * (uint32_t)kb + wpo[i];
       __builtin_amdgcn_global_load_lds((GPtr)(wrow[i] + (off + 16u <= rb ? off : 0u)),
                                        (LPtr)(st + P::kABytes + 1024 * (8 * i + wave)), 16, 0, 0);
     }
-    const uint32_t so = 4u * (uint32_t)kb + sho;
-    __builtin_amdgcn_global_load_lds((GPtr)(srow + (so + 2u <= kgb ? so : 0u)),
-                                     (LPtr)(st + P::kABytes + P::kWBytes + 256 * wave), 2, 0, 0);
+    if constexpr (!F8) {
+      const uint32_t so = 4u * (uint32_t)kb + sho;
+      __builtin_amdgcn_global_load_lds((GPtr)(srow + (so + 2u <= kgb ? so : 0u)),
+                                       (LPtr)(st + P::kABytes + P::kWBytes + 256 * wave), 2, 0, 0);
+    }
   };
   const int pro = nsteps < P::kStages - 1 ? nsteps : P::kStages - 1;
   tile_sources(c0);
@@ -913,14 +924,30 @@ __device__ void gemm_mx_body(const LayerArgs& a, const ProjSlot& W, int Iu, int 
       asm volatile("s_barrier" ::: "memory");
       if (kb + P::kStages - 1 < nsteps) issue(kb + P::kStages - 1, (kb + P::kStages - 1) % P::kStages);
       const char* st = lds + (kb % P::kStages) * P::kStage;
+      // FP8: the step's fp32 block scales of this wave's rows (stage A: gate, up; stage B: its 64 columns)
+      float fs0 = 1.0f, fs1 = 1.0f;
+      if constexpr (F8) {
+        const int b0 = STB ? (cc + 64 * wn) / 128 : cc / 128, b1 = STB ? b0 : (Iu + cc) / 128;
+        fs0 = __uint_as_float(sload4(W.s, 4u * (uint32_t)(b0 * nkb + kb)));
+        fs1 = __uint_as_float(sload4(W.s, 4u * (uint32_t)(b1 * nkb + kb)));
+      }
       i32x8 bw[4];
       int sb[4];
 #pragma unroll
       for (int nj = 0; nj < 4; ++nj) {
-        const u32x4 r = *(const u32x4*)(st + P::kABytes + brow[nj] * 64 + 16 * (g ^ ring_fw(brow[nj])));
-        bw[nj] = (i32x8){(int)r.x, (int)r.y, (int)r.z, (int)r.w, 0, 0, 0, 0};
-        const uint32_t sv = *(const uint32_t*)(st + P::kABytes + P::kWBytes + 4 * (2 * brow[nj] + (g >> 1)));
-        sb[nj] = (int)((sv >> (8 * (g & 1))) & 0xffu);
+        const char* wr = st + P::kABytes + brow[nj] * P::kWRow;
+        if constexpr (F8) {
+          // e4m3 B operand: K [16 g, 16 g + 16) and [64 + 16 g, ...) of the step
+          const u32x4 r0 = *(const u32x4*)(wr + 16 * (g ^ ring_fa(brow[nj])));
+          const u32x4 r1 = *(const u32x4*)(wr + 16 * ((4 + g) ^ ring_fa(brow[nj])));
+          bw[nj] = (i32x8){(int)r0.x, (int)r0.y, (int)r0.z, (int)r0.w, (int)r1.x, (int)r1.y, (int)r1.z, (int)r1.w};
+          sb[nj] = 127;
+        } else {
+          const u32x4 r = *(const u32x4*)(wr + 16 * (g ^ ring_fw(brow[nj])));
+          bw[nj] = (i32x8){(int)r.x, (int)r.y, (int)r.z, (int)r.w, 0, 0, 0, 0};
+          const uint32_t sv = *(const uint32_t*)(st + P::kABytes + P::kWBytes + 4 * (2 * brow[nj] + (g >> 1)));
+          sb[nj] = (int)((sv >> (8 * (g & 1))) & 0xffu);
+        }
       }
 #pragma unroll
       for (int mi = 0; mi < MI; ++mi) {
@@ -934,10 +961,20 @@ __device__ void gemm_mx_body(const LayerArgs& a, const ProjSlot& W, int Iu, int 
         const i32x8 alo = {(int)l0.x, (int)l0.y, (int)l0.z, (int)l0.w, (int)l1.x, (int)l1.y, (int)l1.z, (int)l1.w};
 #pragma unroll
         for (int nj = 0; nj < 4; ++nj) {
-          acc[mi][nj] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(ahi, bw[nj], acc[mi][nj], 0, 4, 0,
-                                                                         (int)(sc & 0xffu), 0, sb[nj]);
-          acc[mi][nj] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(alo, bw[nj], acc[mi][nj], 0, 4, 0,
-                                                                         (int)(sc >> 8), 0, sb[nj]);
+          constexpr int kB = F8 ? 0 : 4;  // B format: e4m3 or e2m1
+          if constexpr (F8) {
+            // the step's partial sums scaled by the block scale of these rows
+            f32x4 tq = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(ahi, bw[nj], (f32x4){0.f, 0.f, 0.f, 0.f},
+                                                                        0, kB, 0, (int)(sc & 0xffu), 0, sb[nj]);
+            tq = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(alo, bw[nj], tq, 0, kB, 0, (int)(sc >> 8), 0,
+                                                                  sb[nj]);
+            acc[mi][nj] += tq * ((STB || nj < 2) ? fs0 : fs1);
+          } else {
+            acc[mi][nj] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(ahi, bw[nj], acc[mi][nj], 0, kB, 0,
+                                                                           (int)(sc & 0xffu), 0, sb[nj]);
+            acc[mi][nj] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(alo, bw[nj], acc[mi][nj], 0, kB, 0,
+                                                                           (int)(sc >> 8), 0, sb[nj]);
+          }
         }
       }
     }
@@ -1009,7 +1046,7 @@ __device__ void gemm_mx_body(const LayerArgs& a, const ProjSlot& W, int Iu, int 
       asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
       // copy out the chunk of each real row (its last 16 bytes: 8 scale bytes
       // and 8 bytes nothing reads)
-      uint8_t* hq = (uint8_t*)a.hbuf;
+      uint8_t* hq = a.hq;
       const size_t hrow = (size_t)mx_row_bytes(a.Imax);
       for (int q = tid; q < MT * (kMxChunk / 16); q += kMxThreads) {
         const int tr = q / (kMxChunk / 16), k = q - tr * (kMxChunk / 16);
@@ -1026,7 +1063,7 @@ __device__ void gemm_mx_body(const LayerArgs& a, const ProjSlot& W, int Iu, int 
 // expert, mx_gemm_ok): one workgroup per (M tile, kMxNT consecutive N
 // tiles), items in XCD-aware order.  STB: stage B (w2, the quantised h).
 constexpr int kMxNT = 2;   // N tiles per workgroup
-template <int MT, int S, bool STB>
+template <int WFMT, int MT, int S, bool STB>
 __global__ __launch_bounds__(kMxThreads) void k_gemm_mx(const LayerArgs a) {
   const int item = xcd_item(blockIdx.x, gridDim.x);
   const int nRouted = a.ctrl[kCtrlNRouted];
@@ -1057,7 +1094,7 @@ __global__ __launch_bounds__(kMxThreads) void k_gemm_mx(const LayerArgs a) {
     if (threadIdx.x == 0) atomicOr(&a.ctrl[kCtrlError], 1);
     return;
   }
-  gemm_mx_body<MT, S, STB>(a, proj_slot(PW, slot), a.L.inter, tn * n0, nt, m0, cnt, list, (char*)ftm_ring_lds);
+  gemm_mx_body<WFMT, MT, S, STB>(a, proj_slot(PW, slot), a.L.inter, tn * n0, nt, m0, cnt, list, (char*)ftm_ring_lds);
 }
 
 // ---------------------------------------------------------------- stage B (w2 -> slot buffer)
@@ -1114,12 +1151,12 @@ __device__ void gemm_b_body(const LayerArgs& a, const ProjSlot& W, int n0, int m
     }
 }
 
-template <int FMT>
+template <int FMT, bool SONLY = false>
 __device__ __forceinline__ void gemm_b_item(const LayerArgs& a, int item, uint16_t* sA, uint16_t* sB) {
   const int H = a.L.hidden, Is = a.L.shared_inter;
   const int nRouted = a.ctrl[kCtrlNRouted];
   const int ntn = H / 64;
-  const int routed_items = gemm_routed_mtiles(a, nRouted) * ntn;
+  const int routed_items = SONLY ? 0 : gemm_routed_mtiles(a, nRouted) * ntn;
   if (item < routed_items) {
     const GemmTile t = gemm_find_tile(a, item / ntn, nRouted, false);
     if (t.u < 0) return;
@@ -1147,11 +1184,11 @@ __device__ __forceinline__ void gemm_b_item(const LayerArgs& a, int item, uint16
   }
 }
 
-template <int FMT>
+template <int FMT, bool SONLY = false>
 __global__ __launch_bounds__(kBlock) void k_gemm_b(const LayerArgs a) {
   __shared__ __attribute__((aligned(16))) uint16_t sA[2 * kGM * kGPitch];
   __shared__ __attribute__((aligned(16))) uint16_t sB[2 * 64 * kGPitch];
-  gemm_b_item<FMT>(a, blockIdx.x, sA, sB);
+  gemm_b_item<FMT, SONLY>(a, blockIdx.x, sA, sB);
 }
 
 // ---------------------------------------------------------------- launch
@@ -1195,46 +1232,59 @@ static size_t ring_lds_a(const ftm_moe_layer& L) {
   return (size_t)kRingA + (size_t)rows * g * 4;
 }
 bool mx_gemm_ok(const ftm_moe_layer& L) {
-  static_assert(MxPlan<128, 3>::kLds <= 160 * 1024, "the 128-row tile's ring fits a CU's LDS");
-  return L.w13.fmt == FTM_FMT_MXFP4 && L.act_dtype == FTM_DT_BF16 && L.shared_inter == 0;
+  static_assert(MxPlan<128, 3, false>::kLds <= 160 * 1024 && MxPlan<64, 3, true>::kLds <= 160 * 1024,
+                "the tiles' rings fit a CU's LDS");
+  // the ring tiles take the shared expert's items (their tile scales fit)
+  return mx_fmt(L) && (L.shared_inter == 0 || ring_ok(L));
 }
 
 const char* gemm_a_kernel_name(const ftm_moe_layer& L) {
   return mx_gemm_ok(L) ? "k_gemm_mx" : ring_ok(L) ? "k_gemm_a_ring" : "k_gemm_a";
 }
 
-template <int FMT>
+template <int FMT, bool SONLY = false>
 static void ring_lds_attr() {
   static bool done = false;  // once per instantiation (setting it twice is harmless)
   if (!done) {
     // a failure here surfaces as the launch error that follows
-    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&k_gemm_a_ring<FMT>),
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&k_gemm_a_ring<FMT, SONLY>),
                               hipFuncAttributeMaxDynamicSharedMemorySize, kRingA + kRingScaleBytes);
     done = true;
   }
 }
 
-template <int MT, int S>
+template <int WFMT, int MT, int S>
 static void launch_gemm_mx(const LayerArgs& a, hipStream_t st, int which, bool xq_ready, long pairs, long maxU) {
+  constexpr bool F8 = WFMT == FTM_FMT_FP8_BLOCK;
   const ftm_moe_layer& L = a.L;
   static bool attr = false;
   if (!attr) {
-    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&k_gemm_mx<MT, S, false>),
-                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)MxPlan<MT, S>::kLds);
-    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&k_gemm_mx<MT, S, true>),
-                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)MxPlan<MT, S>::kLds);
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&k_gemm_mx<WFMT, MT, S, false>),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)MxPlan<MT, S, F8>::kLds);
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&k_gemm_mx<WFMT, MT, S, true>),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)MxPlan<MT, S, F8>::kLds);
     attr = true;
   }
   const long mt = pairs / MT + maxU + 1;
-  const size_t lds = mx_tile_lds<MT, S>();
+  const size_t lds = mx_tile_lds<MT, S, F8>();
+  // the bf16 shared expert (if any) on the bf16 tiles, its items only
+  const long mt_shared = L.shared_inter > 0 ? (a.T + kGM - 1) / kGM : 0;
   if (which & 1) {
     if (!xq_ready) launch_quant_mx(a.x, a.T, L.hidden, a.xq, st);
     const long items = mt * (((L.inter + kMxNR / 2 - 1) / (kMxNR / 2) + kMxNT - 1) / kMxNT);
-    hipLaunchKernelGGL((k_gemm_mx<MT, S, false>), dim3((unsigned)items), dim3(kMxThreads), lds, st, a);
+    hipLaunchKernelGGL((k_gemm_mx<WFMT, MT, S, false>), dim3((unsigned)items), dim3(kMxThreads), lds, st, a);
+    if (mt_shared > 0) {
+      ring_lds_attr<WFMT, true>();
+      hipLaunchKernelGGL((k_gemm_a_ring<WFMT, true>), dim3((unsigned)(mt_shared * (L.shared_inter / 64))),
+                         dim3(kBlock), (size_t)kRingA, st, a);
+    }
   }
   if (which & 2) {
     const long items = mt * (((L.hidden + kMxNR - 1) / kMxNR + kMxNT - 1) / kMxNT);
-    hipLaunchKernelGGL((k_gemm_mx<MT, S, true>), dim3((unsigned)items), dim3(kMxThreads), lds, st, a);
+    hipLaunchKernelGGL((k_gemm_mx<WFMT, MT, S, true>), dim3((unsigned)items), dim3(kMxThreads), lds, st, a);
+    if (mt_shared > 0)
+      hipLaunchKernelGGL((k_gemm_b<WFMT, true>), dim3((unsigned)(mt_shared * (L.hidden / 64))), dim3(kBlock), 0,
+                         st, a);
   }
 }
 
@@ -1243,13 +1293,21 @@ static void launch_gemm_t(const LayerArgs& a, hipStream_t st, int which, bool xq
   const ftm_moe_layer& L = a.L;
   const long pairs = (long)a.T * L.topk;
   const long maxU = L.num_experts < pairs ? L.num_experts : pairs;
-  if (FMT == FTM_FMT_MXFP4 && mx_gemm_ok(L)) {
-    // both stages on the scaled-MFMA tiles: stage A over the quantised input,
-    // writing h quantised the same way for stage B.  128-row M tiles from 128
-    // pairs per expert on average, 64 below.
-    if (pairs >= 128 * maxU) launch_gemm_mx<128, 3>(a, st, which, xq_ready, pairs, maxU);
-    else launch_gemm_mx<64, 3>(a, st, which, xq_ready, pairs, maxU);
-    return;
+  if constexpr (FMT == FTM_FMT_MXFP4 || FMT == FTM_FMT_FP8_BLOCK) {
+    if (mx_gemm_ok(L)) {
+      // both stages' routed experts on the scaled-MFMA tiles: stage A over the
+      // quantised input, writing h quantised the same way for stage B.  MXFP4:
+      // 128-row M tiles from 128 pairs per expert on average, 64 below; FP8
+      // (twice the weight bytes in the ring): 64.
+      if constexpr (FMT == FTM_FMT_MXFP4) {
+        if (pairs >= 128 * maxU) {
+          launch_gemm_mx<FMT, 128, 3>(a, st, which, xq_ready, pairs, maxU);
+          return;
+        }
+      }
+      launch_gemm_mx<FMT, 64, 3>(a, st, which, xq_ready, pairs, maxU);
+      return;
+    }
   }
   const long mt_routed = pairs / kGM + maxU + 1;
   const long mt_shared = L.shared_inter > 0 ? (a.T + kGM - 1) / kGM : 0;

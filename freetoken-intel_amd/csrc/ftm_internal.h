@@ -65,9 +65,18 @@ constexpr int kMaxColTiles = FTM_WS_CTRL_BYTES / 4 - kCtrlTileCnt;
 // size are zeros).
 constexpr int kMxChunk = 272;
 __host__ __device__ inline int mx_row_bytes(int H) { return (H + 127) / 128 * kMxChunk; }
+// Weight formats the scaled-MFMA stages take (bf16 activations): MXFP4, and
+// FP8 e4m3 with 128 x 128 blocks (the block scale applied to each K step's
+// partial sums).
+inline bool mx_fmt(const ftm_moe_layer& L) {
+  if (L.act_dtype != FTM_DT_BF16) return false;
+  if (L.w13.fmt == FTM_FMT_MXFP4) return true;
+  return L.w13.fmt == FTM_FMT_FP8_BLOCK && L.w13.group == 128 && L.w2.group == 128 &&
+         L.w13.s_dtype == FTM_DT_F32 && L.w2.s_dtype == FTM_DT_F32 && L.hidden % 128 == 0 && L.inter % 128 == 0;
+}
 
 struct WsLayout {
-  size_t misc, logits, wts, ids, lists, uniq, ucnt, recs, hbuf, ybuf, xq, total;
+  size_t misc, logits, wts, ids, lists, uniq, ucnt, recs, hbuf, ybuf, hq, xq, total;
   int T, E, KP, Imax;
 };
 
@@ -90,11 +99,12 @@ inline WsLayout ws_layout(const ftm_moe_layer& L, int T) {
   w.uniq = o;   o = align_up(o + 4 * (size_t)(w.E + 1), 256);
   w.ucnt = o;   o = align_up(o + 4 * (size_t)(w.E + 1), 256);
   w.recs = o;   o = align_up(o + 4 * (size_t)kRecWords * (w.E + 1), 256);
-  // MXFP4 layers: h also as the scaled-MFMA tiles' quantised rows (kMxChunk layout by pair)
-  const bool mx = L.w13.fmt == FTM_FMT_MXFP4 && L.act_dtype == FTM_DT_BF16;
-  const size_t hb = act * Tt * w.KP * w.Imax, hq = mx ? Tt * w.KP * (size_t)mx_row_bytes(w.Imax) : 0;
-  w.hbuf = o;   o = align_up(o + (hb > hq ? hb : hq), 256);
+  w.hbuf = o;   o = align_up(o + act * Tt * w.KP * w.Imax, 256);
   w.ybuf = o;   o = align_up(o + 4 * Tt * w.KP * (size_t)L.hidden, 256);
+  // layers the scaled-MFMA stages take: the input and h quantised (kMxChunk
+  // layout, by token and by pair)
+  const bool mx = mx_fmt(L);
+  w.hq = o;     o = align_up(o + (mx ? Tt * w.KP * (size_t)mx_row_bytes(w.Imax) : 0), 256);
   w.xq = o;     o = align_up(o + (mx ? Tt * (size_t)mx_row_bytes(L.hidden) : 0), 256);
   w.total = o;
   return w;

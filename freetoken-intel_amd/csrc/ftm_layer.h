@@ -30,7 +30,8 @@ struct LayerArgs {
   int32_t* recs;    // [E+1, kRecWords] work records of the routed experts
   char* hbuf;       // [T*KP, Imax] act dtype
   float* ybuf;      // [T*KP, H]
-  uint8_t* xq;      // [T, mx_row_bytes(H)]  MXFP4 layers: the quantised input (kMxChunk layout)
+  uint8_t* hq;      // [T*KP, mx_row_bytes(Imax)]  mx_fmt layers: h quantised by stage A's scaled-MFMA tiles
+  uint8_t* xq;      // [T, mx_row_bytes(H)]  mx_fmt layers: the quantised input (kMxChunk layout)
 };
 
 inline LayerArgs make_args(const ftm_moe_layer& L, const void* x, void* out, int T, char* ws,
@@ -57,6 +58,7 @@ inline LayerArgs make_args(const ftm_moe_layer& L, const void* x, void* out, int
   a.recs = (int32_t*)(ws + wl.recs);
   a.hbuf = ws + wl.hbuf;
   a.ybuf = (float*)(ws + wl.ybuf);
+  a.hq = (uint8_t*)(ws + wl.hq);
   a.xq = (uint8_t*)(ws + wl.xq);
   return a;
 }

@@ -172,9 +172,10 @@ def test_stage_kernel_names_follow_the_dispatch():
         assert name(c3, T, nat.STAGE_COMBINE) == "", T
     for T in (17, 64, 256):
         assert name(c3, T, nat.STAGE_W2) == "k_stage_b_lean", T
-    # 512 tokens x top-8 = 16 pairs per expert on all 256 experts: GEMM stages
-    assert name(c3, 512, nat.STAGE_W13) == "k_gemm_a_ring"
-    assert name(c3, 512, nat.STAGE_W2) == "k_gemm_b"
+    # 512 tokens x top-8 = 16 pairs per expert on all 256 experts: GEMM
+    # stages, the routed experts on the scaled-MFMA tiles (FP8 128 x 128 blocks)
+    assert name(c3, 512, nat.STAGE_W13) == "k_gemm_mx"
+    assert name(c3, 512, nat.STAGE_W2) == "k_gemm_mx"
     # 3..16 tokens: router and top-k in one launch (the top-k stage launches nothing)
     for T in (3, 16):
         assert name(c3, T, nat.STAGE_ROUTER) == "k_route_topk1", T
@@ -193,7 +194,7 @@ def test_stage_kernel_names_follow_the_dispatch():
     assert name(small, 5, nat.STAGE_W13) == "k_stage_a_rows"
     assert name(small, 5, nat.STAGE_W2) == "k_stage_b_ks"  # K split over the waves up to 32 tokens
     assert name(small, 33, nat.STAGE_W2) == "k_stage_b"
-    assert name(small, 64, nat.STAGE_W13) == "k_gemm_a_ring"
+    assert name(small, 64, nat.STAGE_W13) == "k_gemm_mx"  # FP8 128 x 128 blocks: scaled-MFMA tiles
     # GPTQ group 128: activation rows in LDS up to 16 tokens while half of the
     # hidden size fits a wave's K range (1024), the register-fed kernel above
     gq = _layer(E=128, H=2048, I=768, k=8)
