@@ -261,6 +261,25 @@ __device__ __forceinline__ u32x4 bload16(Rsrc r, uint32_t off) {
 __device__ __forceinline__ uint32_t bload4(Rsrc r, uint32_t off) {
   return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
 }
+// Device-coherent accesses (the SC1 cache-policy bit): the load misses every
+// cache another XCD's writes could leave stale, the store is written through
+// to where every XCD reads it.  Data one workgroup hands to another inside a
+// launch travels this way; a producer waits for its stores' acknowledgement
+// (s_waitcnt) before its arrival, a consumer loads after seeing the count.
+// An agent-scope fence would write back (release: buffer_wbl2) or invalidate
+// (acquire: buffer_inv) the whole L2 of the XCD instead, once per workgroup.
+constexpr int kAuxDev = 16;
+__device__ __forceinline__ uint32_t bload4_dev(Rsrc r, uint32_t off) {
+  return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, kAuxDev);
+}
+template <class V>
+__device__ __forceinline__ void store_dev(V* p, V v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+template <class V>
+__device__ __forceinline__ V load_dev(const V* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 __device__ __forceinline__ uint32_t bload2(Rsrc r, uint32_t off) {
   return (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0);
 }

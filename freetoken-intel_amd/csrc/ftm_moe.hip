@@ -116,7 +116,9 @@ __global__ __launch_bounds__(kBlock) void k_quant_mx(const uint16_t* __restrict_
 constexpr int kRouterTPW = 4;  // tokens per wave
 constexpr int kRouterSteps = 4;  // 512-element chunk steps per load group
 
-// Logits of row r for tokens tb + 4 i (i < kRouterTPW), by one wave.
+// Logits of row r for tokens tb + 4 i (i < kRouterTPW), by one wave (COH:
+// stored device-coherent, for a reader in the same launch).
+template <bool COH = false>
 __device__ __forceinline__ void router_row_tile(const LayerArgs& a, int r, int tb) {
   const int E = a.L.num_experts, H = a.L.hidden, T = a.T;
   const void* grow = (r < E) ? (const void*)((const uint16_t*)a.L.gate_w + (size_t)r * H) : a.L.shared_gate;
@@ -165,7 +167,10 @@ __device__ __forceinline__ void router_row_tile(const LayerArgs& a, int r, int t
     if (lane == 0 && t < T) {
       float z = v;
       if (r < E && a.L.gate_b != nullptr) z = v + bf16_to_f32(((const uint16_t*)a.L.gate_b)[r]);
-      a.logits[(size_t)t * (E + 1) + r] = round_to(z, a.L.act_dtype);
+      if constexpr (COH)
+        store_dev(&a.logits[(size_t)t * (E + 1) + r], round_to(z, a.L.act_dtype));
+      else
+        a.logits[(size_t)t * (E + 1) + r] = round_to(z, a.L.act_dtype);
     }
   }
 }
@@ -427,7 +432,7 @@ __device__ __forceinline__ void sort_desc32(uint32_t (&k)[NV]) {
 // NV = candidates per lane (E <= 64 * NV).
 // The router's logits of token t, lane l holding experts l + 64 i (issued
 // ahead of use by the multi-token top-k loop).
-template <int NV>
+template <int NV, bool COH = false>
 __device__ __forceinline__ void route_load(const LayerArgs& a, int t, uint32_t (&raw)[NV]) {
   const int E = a.L.num_experts;
   const int lane = threadIdx.x & 63;
@@ -435,7 +440,8 @@ __device__ __forceinline__ void route_load(const LayerArgs& a, int t, uint32_t (
 #pragma unroll
   for (int i = 0; i < NV; ++i) {
     const int e = lane + 64 * i;
-    raw[i] = bload4(lres, (e < E && t < a.T) ? ((uint32_t)t * (uint32_t)(E + 1) + (uint32_t)e) * 4u : kOOB);
+    const uint32_t off = (e < E && t < a.T) ? ((uint32_t)t * (uint32_t)(E + 1) + (uint32_t)e) * 4u : kOOB;
+    raw[i] = COH ? bload4_dev(lres, off) : bload4(lres, off);
   }
 }
 
@@ -466,7 +472,7 @@ __device__ __forceinline__ void fold_repeats(int& sel_e, float& sel_w, int E, in
 }
 
 // use_pre: take the router logits of t from pre (route_load, router path only).
-template <int MODE, int NV>
+template <int MODE, int NV, bool COH = false>
 __device__ __forceinline__ void route_token_pre(const LayerArgs& a, int t, const void* logits_in, int logits_dt,
                                                 const int32_t* ids_in, const float* w_in, float* logits_out,
                                                 int& sel_e, float& sel_w, bool use_pre,
@@ -494,7 +500,7 @@ __device__ __forceinline__ void route_token_pre(const LayerArgs& a, int t, const
 #pragma unroll
       for (int i = 0; i < NV; ++i) raw[i] = pre[i];
     } else {
-      route_load<NV>(a, t, raw);
+      route_load<NV, COH>(a, t, raw);
     }
 #pragma unroll
     for (int i = 0; i < NV; ++i) v[i] = (lane + 64 * i < E) ? __uint_as_float(raw[i]) : -INFINITY;
@@ -595,12 +601,12 @@ __device__ __forceinline__ void route_token_pre(const LayerArgs& a, int t, const
   sel_w = round_to(sel_w, act_dt);
 }
 
-template <int MODE, int NV>
+template <int MODE, int NV, bool COH = false>
 __device__ __forceinline__ void route_token(const LayerArgs& a, int t, const void* logits_in, int logits_dt,
                                             const int32_t* ids_in, const float* w_in, float* logits_out,
                                             int& sel_e, float& sel_w) {
   const uint32_t none[NV] = {};
-  route_token_pre<MODE, NV>(a, t, logits_in, logits_dt, ids_in, w_in, logits_out, sel_e, sel_w, false, none);
+  route_token_pre<MODE, NV, COH>(a, t, logits_in, logits_dt, ids_in, w_in, logits_out, sel_e, sel_w, false, none);
 }
 
 // Zero the slot rows of token t's pairs that have no expert (caller routing
@@ -638,7 +644,7 @@ __device__ __forceinline__ void emit_token(const LayerArgs& a, int t, int sel_e,
       if (w_out) w_out[(size_t)t * k + lane] = sel_w;
       const int pos = atomicAdd(&cnt[sel_e], 1);
       if (pos < T) {
-        a.lists[(size_t)sel_e * T + pos] = p;
+        store_dev(&a.lists[(size_t)sel_e * T + pos], p);  // k_topk's last workgroup reads the lists
         if (s_first != nullptr && pos < kRecPairs) s_first[sel_e * kRecPairs + pos] = p;
         listed = true;
       } else {  // more than T pairs for one expert (fold_repeats rules it out): dropped, flagged
@@ -656,7 +662,7 @@ __device__ __forceinline__ void emit_token(const LayerArgs& a, int t, int sel_e,
   // every slot no stage writes is zeroed (k_combine sums all of a token's slots)
   zero_skipped_slots(a, t, lane < k && !listed);
   if (lane == 0 && a.L.shared_inter > 0) {
-    const float sl = a.logits[(size_t)t * (E + 1) + E];
+    const float sl = load_dev(&a.logits[(size_t)t * (E + 1) + E]);  // k_route_topk1: another workgroup's logit
     a.wts[t * KP + k] = round_to(1.0f / (1.0f + expf(-sl)), a.L.act_dtype);
   }
 }
@@ -703,7 +709,7 @@ __device__ __forceinline__ void compact_experts(const LayerArgs& a, int32_t* cnt
       rec[2] = a.L.slot_of_expert ? a.L.slot_of_expert[e] : e;
 #pragma unroll
       for (int i = 0; i < kRecPairs; ++i)
-        rec[3 + i] = i < c ? (s_first != nullptr ? s_first[e * kRecPairs + i] : list[i]) : -1;
+        rec[3 + i] = i < c ? (s_first != nullptr ? s_first[e * kRecPairs + i] : load_dev(&list[i])) : -1;
       rec[kRecWords - 1] = 0;
       int32_t* dst = a.recs + (size_t)u * kRecWords;
 #pragma unroll
@@ -774,14 +780,12 @@ __global__ __launch_bounds__(64 * kTopk1Waves) void k_route_topk1(const LayerArg
     return;
   }
   const int r = (int)blockIdx.x * kRouteRows + (wave & 3);
-  if (r < row_end) router_row_tile(a, r, wave >> 2);
-  // publish this workgroup's logits; the last arrival sees every workgroup's
+  if (r < row_end) router_row_tile<true>(a, r, wave >> 2);
+  // publish this workgroup's logits (device-coherent stores, acknowledged
+  // before the arrival); the last arrival reads every workgroup's
+  __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
-  if (threadIdx.x < 64) {
-    __threadfence();
-    if (threadIdx.x == 0) s_last = (atomicAdd(&a.ctrl[kCtrlArriveTopk], 1) == nrwg - 1);
-    __threadfence();
-  }
+  if (threadIdx.x == 0) s_last = (atomicAdd(&a.ctrl[kCtrlArriveTopk], 1) == nrwg - 1);
   __syncthreads();
   if (!s_last) return;
   const int E = a.L.num_experts, T = a.T;
@@ -790,7 +794,7 @@ __global__ __launch_bounds__(64 * kTopk1Waves) void k_route_topk1(const LayerArg
   for (int t = wave; t < T; t += kTopk1Waves) {
     int sel_e;
     float sel_w;
-    route_token<MODE, NV>(a, t, nullptr, 0, nullptr, nullptr, logits_out, sel_e, sel_w);
+    route_token<MODE, NV, true>(a, t, nullptr, 0, nullptr, nullptr, logits_out, sel_e, sel_w);
     emit_token(a, t, sel_e, sel_w, ids_out, w_out, s_cnt, s_first);
   }
   __syncthreads();
@@ -815,12 +819,12 @@ __global__ __launch_bounds__(kBlock) void k_topk(const LayerArgs a, const void* 
   }
   __shared__ int s_last;
   __shared__ int s_wsum[4];
-  __threadfence();
+  // the lists' device-coherent stores acknowledged before the arrival
+  __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   if (threadIdx.x == 0) s_last = (atomicAdd(&a.ctrl[kCtrlArriveTopk], 1) == (int)gridDim.x - 1);
   __syncthreads();
   if (!s_last) return;
-  __threadfence();
   compact_experts<4>(a, cnt, true, s_wsum);
   if (threadIdx.x == 0) a.ctrl[kCtrlArriveTopk] = 0;
 }
@@ -913,7 +917,7 @@ __global__ __launch_bounds__(64 * kTopkBlkWaves) void k_topk_blk(const LayerArgs
       if (slot >= 0) {
         const int e = slot & 511, pos = s_cnt[e] + (slot >> 9);
         if (pos < T) {
-          a.lists[(size_t)e * T + pos] = t * KP + lane;
+          store_dev(&a.lists[(size_t)e * T + pos], t * KP + lane);
         } else {  // more than T pairs for one expert (fold_repeats rules it out): dropped, flagged, slot zeroed
           atomicOr(&a.ctrl[kCtrlError], 4);
           float* row = a.ybuf + (size_t)(t * KP + lane) * a.L.hidden;
@@ -922,15 +926,12 @@ __global__ __launch_bounds__(64 * kTopkBlkWaves) void k_topk_blk(const LayerArgs
       }
     }
   }
-  // The barrier makes every wave's stores visible within the workgroup; one
-  // wave's device-scope fence then publishes them all before the arrival (a
-  // fence per wave costs an L2 write-back each).
+  // Every wave's device-coherent list stores acknowledged, then the arrival
+  // (the last workgroup reads the lists device-coherent: no fence, which
+  // would write back or invalidate the whole L2 of the XCD).
+  __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
-  if (threadIdx.x < 64) {
-    __threadfence();
-    if (threadIdx.x == 0) s_last = (atomicAdd(&a.ctrl[kCtrlArriveTopk], 1) == (int)gridDim.x - 1);
-    __threadfence();
-  }
+  if (threadIdx.x == 0) s_last = (atomicAdd(&a.ctrl[kCtrlArriveTopk], 1) == (int)gridDim.x - 1);
   __syncthreads();
   if (!s_last) return;
   compact_experts<kTopkBlkWaves>(a, gcnt, true, s_wsum);
