@@ -244,12 +244,15 @@ class ConfigBench:
         torch.cuda.synchronize()
         return round(f0.elapsed_time(f1) * 1e3 / steps, 2), ok
 
-    def stage_times(self, T: int, reps: int = 15) -> dict:
+    def stage_times(self, T: int, reps: int = 15, passes: int = 4) -> dict:
         """Average duration of each of the five stage launches at T tokens: each
-        stage is launched as a group of NL consecutive launches, one per rotated
-        layer (each layer with its own workspace, so the groups keep every
-        layer's stage order), between two events on the launch stream; a sleep
-        kernel queued first lets the host run ahead."""
+        stage is launched as a group of `passes` x NL consecutive launches, the
+        rotated layers in turn (each layer with its own workspace, so the groups
+        keep every layer's stage order; a stage launched again on its workspace
+        recomputes the same outputs), between two events on the launch stream,
+        so the cost of each group boundary (the event, the first launch's ramp)
+        is spread over passes x NL launches; a sleep kernel queued first lets
+        the host run ahead."""
         import numpy as np
         import torch
 
@@ -271,12 +274,13 @@ class ConfigBench:
             ev = [torch.cuda.Event(enable_timing=True) for _ in range(len(stages) + 1)]
             for k, st in enumerate(stages):
                 ev[k].record()
-                for l in range(NL):
-                    self.layers[l].forward_stage(xs[(i + l) % NX], out, st, ws=wss[l])
+                for _ in range(passes):
+                    for l in range(NL):
+                        self.layers[l].forward_stage(xs[(i + l) % NX], out, st, ws=wss[l])
             ev[-1].record()
             evs.append((ev, i))
         torch.cuda.synchronize()
-        us = {name: float(np.mean([ev[k].elapsed_time(ev[k + 1]) for ev, _ in evs])) * 1e3 / NL
+        us = {name: float(np.mean([ev[k].elapsed_time(ev[k + 1]) for ev, _ in evs])) * 1e3 / (NL * passes)
               for k, name in enumerate(("router", "topk", "w13", "w2", "combine"))}
         # realised unique experts of the same (layer, batch) pairs
         uniq = []
