@@ -1060,15 +1060,19 @@ __device__ void gemm_mx_body(const LayerArgs& a, const ProjSlot& W, int Iu, int 
 }
 
 // Routed MXFP4 expert tiles on the scaled MFMAs (a layer without a shared
-// expert, mx_gemm_ok): one workgroup per (M tile, kMxNT consecutive N
+// expert, mx_gemm_ok): one workgroup per (M tile, ntpw consecutive N
 // tiles), items in XCD-aware order.  STB: stage B (w2, the quantised h).
-constexpr int kMxNT = 2;   // N tiles per workgroup
+// N tiles per workgroup: stage A 1, stage B 2.  Measured on MI355X (prefill,
+// w13 / w2 us): C4 T=4096 one tile 829-834 / 421, two 861 / 399, three 913 /
+// 425; C3 T=2048 one 297-303 / 218, two 304 / 191, three 412 / 185.
+constexpr int kMxNTA = 1;
+constexpr int kMxNTB = 2;
 template <int WFMT, int MT, int S, bool STB>
-__global__ __launch_bounds__(kMxThreads) void k_gemm_mx(const LayerArgs a) {
+__global__ __launch_bounds__(kMxThreads) void k_gemm_mx(const LayerArgs a, int ntpw) {
   const int item = xcd_item(blockIdx.x, gridDim.x);
   const int nRouted = a.ctrl[kCtrlNRouted];
   const int tiles = STB ? (a.L.hidden + kMxNR - 1) / kMxNR : (a.L.inter + kMxNR / 2 - 1) / (kMxNR / 2);
-  const int ntn = (tiles + kMxNT - 1) / kMxNT;
+  const int ntn = (tiles + ntpw - 1) / ntpw;
   const int routed_items = gemm_routed_mtiles<MT>(a, nRouted) * ntn;
   if (item >= routed_items) return;
   const GemmTile t = gemm_find_tile<MT>(a, item / ntn, nRouted, false);
@@ -1078,8 +1082,8 @@ __global__ __launch_bounds__(kMxThreads) void k_gemm_mx(const LayerArgs a) {
   const int e = __builtin_amdgcn_readfirstlane(a.uniq[t.u]);
   const int slot = __builtin_amdgcn_readfirstlane(a.L.slot_of_expert ? a.L.slot_of_expert[e] : e);
   const ftm_proj& PW = STB ? a.L.w2 : a.L.w13;
-  const int n0 = (item % ntn) * kMxNT;
-  const int nt = tiles - n0 < kMxNT ? tiles - n0 : kMxNT;
+  const int n0 = (item % ntn) * ntpw;
+  const int nt = tiles - n0 < ntpw ? tiles - n0 : ntpw;
   const int tn = STB ? kMxNR : kMxNR / 2;
   const int32_t* list = a.lists + (size_t)e * a.T;
   const int m0 = __builtin_amdgcn_readfirstlane(t.m0), cnt = __builtin_amdgcn_readfirstlane(t.cnt);
@@ -1271,8 +1275,9 @@ static void launch_gemm_mx(const LayerArgs& a, hipStream_t st, int which, bool x
   const long mt_shared = L.shared_inter > 0 ? (a.T + kGM - 1) / kGM : 0;
   if (which & 1) {
     if (!xq_ready) launch_quant_mx(a.x, a.T, L.hidden, a.xq, st);
-    const long items = mt * (((L.inter + kMxNR / 2 - 1) / (kMxNR / 2) + kMxNT - 1) / kMxNT);
-    hipLaunchKernelGGL((k_gemm_mx<WFMT, MT, S, false>), dim3((unsigned)items), dim3(kMxThreads), lds, st, a);
+    const int ntA = kMxNTA;
+    const long items = mt * (((L.inter + kMxNR / 2 - 1) / (kMxNR / 2) + ntA - 1) / ntA);
+    hipLaunchKernelGGL((k_gemm_mx<WFMT, MT, S, false>), dim3((unsigned)items), dim3(kMxThreads), lds, st, a, ntA);
     if (mt_shared > 0) {
       ring_lds_attr<WFMT, true>();
       hipLaunchKernelGGL((k_gemm_a_ring<WFMT, true>), dim3((unsigned)(mt_shared * (L.shared_inter / 64))),
@@ -1280,8 +1285,9 @@ static void launch_gemm_mx(const LayerArgs& a, hipStream_t st, int which, bool x
     }
   }
   if (which & 2) {
-    const long items = mt * (((L.hidden + kMxNR - 1) / kMxNR + kMxNT - 1) / kMxNT);
-    hipLaunchKernelGGL((k_gemm_mx<WFMT, MT, S, true>), dim3((unsigned)items), dim3(kMxThreads), lds, st, a);
+    const int ntB = kMxNTB;
+    const long items = mt * (((L.hidden + kMxNR - 1) / kMxNR + ntB - 1) / ntB);
+    hipLaunchKernelGGL((k_gemm_mx<WFMT, MT, S, true>), dim3((unsigned)items), dim3(kMxThreads), lds, st, a, ntB);
     if (mt_shared > 0)
       hipLaunchKernelGGL((k_gemm_b<WFMT, true>), dim3((unsigned)(mt_shared * (L.hidden / 64))), dim3(kBlock), 0,
                          st, a);
