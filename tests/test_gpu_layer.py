@@ -407,6 +407,43 @@ def test_negative_expert_ids_are_skipped(gpu, name, T):
     assert_close(to_f32(out), ref["out"], what=f"{name} layer with skipped pairs")
 
 
+@pytest.mark.parametrize("name,T", [("c1_int8", 3), ("c1_int8", 9), ("c2_gptq", 5), ("c4_mxfp4", 7),
+                                    ("c3_nosh", 20), ("c3_full", 20)])
+def test_call_with_no_routed_expert(gpu, name, T):
+    """Caller routing whose every pair has no expert (a chunk past the last
+    distinct expert of the device-LRU offload step), through each decode stage
+    B (k_stage_b_xl at 3 tokens, k_stage_b_ks, k_stage_b_gq, k_stage_b_lean at
+    20): no routed expert runs, every slot was zeroed by the top-k, and the
+    output is exactly zero without a shared expert and the shared expert's
+    contribution with one (c3_full)."""
+    from dataclasses import replace
+
+    if name == "c3_full":
+        cfg = S.CONFIGS["c3_fp8"]
+    elif name == "c3_nosh":
+        cfg = replace(S.CONFIGS["c3_fp8"], shared_inter=0)
+    else:
+        cfg = S.SMALL[name]
+    syn = S.generate(cfg, T=T, seed=130 + T)
+    ids = np.full((T, syn.cfg.k), -1, np.int32)
+    w = np.zeros((T, syn.cfg.k), np.float32)
+    dsyn = syn.to(gpu)
+    layer = S.build_layer(dsyn)
+    ids_d, w_d = torch.from_numpy(ids).to(gpu), torch.from_numpy(w).to(gpu)
+    for _ in range(2):  # the second call starts from the counters the first one left
+        # a freed NaN block of the output's size: the caching allocator hands it
+        # back as the output, so an output nobody writes shows up as NaN
+        junk = torch.full((T, syn.cfg.H), float("nan"), dtype=dsyn.x.dtype, device=gpu)
+        del junk
+        out = layer.forward_routed(dsyn.x, ids_d, w_d)
+        torch.cuda.synchronize()
+        if syn.cfg.shared_inter == 0:
+            assert torch.count_nonzero(out.float()).item() == 0, f"{name}: output not zero"
+        else:
+            ref = O.layer_reference(oracle_spec(syn), np_(syn.x), ids=ids, w=w)
+            assert_close(to_f32(out), ref["out"], what=f"{name}: the shared expert alone")
+
+
 @pytest.mark.parametrize("name,T", [("c3_fp8", 1), ("c3_fp8", 2), ("c3_fp8", 9), ("c3_fp8", 300), ("c3_full", 1),
                                     ("c3_full", 2), ("c2_gptq", 2)])
 def test_repeated_expert_in_a_token_counts_twice(gpu, name, T):
