@@ -1101,6 +1101,197 @@ __global__ __launch_bounds__(kMxThreads) void k_gemm_mx(const LayerArgs a, int n
   gemm_mx_body<WFMT, MT, S, STB>(a, proj_slot(PW, slot), a.L.inter, tn * n0, nt, m0, cnt, list, (char*)ftm_ring_lds);
 }
 
+// Stage B (w2) of FP8 routed experts with weights fed from registers: the
+// tile's quantised h rows (64 rows x K / 128 chunks, at most 69.6 KB) are
+// copied into LDS once and stay there; each wave loads the e4m3 B operands
+// of its 32 columns straight into VGPRs with buffer loads (no LDS ring, no
+// per-step barrier), the next N tile's operands in flight during the current
+// tile's MFMAs.  One workgroup per (M tile, ntpw consecutive 128-column N
+// tiles), four waves, two workgroups per CU.  K = I, a multiple of 128 up to
+// 512.  The products, the per-step fp32 block scales and the epilogue are
+// those of gemm_mx_body's stage B, in the same order, so the output is the same.
+constexpr int kRbThreads = 256;
+constexpr int kRbMT = 64;
+constexpr int kRbKS = 4;     // K steps at most (K <= 512)
+constexpr int kRbNT = 128;   // output columns per N tile (one FP8 scale block)
+constexpr int kRbNTW = 8;    // N tiles per workgroup
+constexpr int kRbA = kRbMT * kRbKS * kMxChunk;
+constexpr int kRbLds = kRbA + kRbMT * 8;  // + the rows' pairs and router weights
+static_assert(2 * kRbLds <= 160 * 1024, "two workgroups per CU");
+
+__global__ __launch_bounds__(kRbThreads, 2) void k_gemm_mxb_f8(const LayerArgs a, int ntpw) {
+  const int item = xcd_item(blockIdx.x, gridDim.x);
+  const int nRouted = a.ctrl[kCtrlNRouted];
+  const int H = a.L.hidden;
+  const int tiles = (H + kRbNT - 1) / kRbNT;
+  const int ntn = (tiles + ntpw - 1) / ntpw;
+  const int routed_items = gemm_routed_mtiles<kRbMT>(a, nRouted) * ntn;
+  if (item >= routed_items) return;
+  const GemmTile t = gemm_find_tile<kRbMT>(a, item / ntn, nRouted, false);
+  if (t.u < 0) return;
+  const int e = __builtin_amdgcn_readfirstlane(a.uniq[t.u]);
+  const int slot = __builtin_amdgcn_readfirstlane(a.L.slot_of_expert ? a.L.slot_of_expert[e] : e);
+  const int n0 = __builtin_amdgcn_readfirstlane((item % ntn) * ntpw);
+  const int nt = tiles - n0 < ntpw ? tiles - n0 : ntpw;
+  const int32_t* list = a.lists + (size_t)e * a.T;
+  const int m0 = __builtin_amdgcn_readfirstlane(t.m0), cnt = __builtin_amdgcn_readfirstlane(t.cnt);
+  const int tid = threadIdx.x;
+  if (slot < 0 || slot >= a.L.w2.num_slots) {  // non-resident expert: its rows contribute zeros
+    for (int idx = tid; idx < kRbMT * kRbNT * nt; idx += kRbThreads) {
+      const int mm = m0 + idx / (kRbNT * nt), col = kRbNT * n0 + idx % (kRbNT * nt);
+      if (mm < cnt && col < H) a.ybuf[(size_t)list[mm] * H + col] = 0.0f;
+    }
+    if (tid == 0) atomicOr(&a.ctrl[kCtrlError], 1);
+    return;
+  }
+  const ProjSlot W = proj_slot(a.L.w2, slot);
+  char* lds = (char*)ftm_ring_lds;
+  int* lpe = (int*)(lds + kRbA);
+  float* lwe = (float*)(lpe + kRbMT);
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int g = lane >> 4, m = lane & 15;
+  const int K = W.K, KP = a.KP;
+  const int nsteps = K / 128;
+  const Rsrc lres = make_rsrc(list, (uint32_t)a.T * 4u);
+  const int p0 = pair_of_row(lres, true, m0, cnt, KP, 0);
+  const size_t hrow = (size_t)mx_row_bytes(a.Imax);
+
+  // the rows' pairs (rows past the tile's pairs: -1) and router weights
+  if (tid < kRbMT) {
+    const int pr = pair_of_row(lres, true, m0 + tid, cnt, KP, 0);
+    lpe[tid] = pr;
+    lwe[tid] = pr >= 0 ? a.wts[pr] : 0.0f;
+  }
+
+  // ---- B operands: column c = 128 tile + 32 wave + 16 nj + m, K bytes
+  // [16 g, 16 g + 16) and [64 + 16 g, ...) of each 128-wide step (the
+  // operand layout of gemm_mx_body).  Every load is issued unconditionally
+  // (columns past N and tiles past the item's last read as zeros through an
+  // out-of-range offset, without memory traffic), so each tile's loads are
+  // the same 16 in flight whatever the branches did and the compiler's
+  // counted waits stop at the tile being used.
+  const Rsrc wres = make_rsrc(W.w, (uint32_t)K * (uint32_t)W.N);
+  // the columns' bias bits, in the same batch (a layer without bias: an
+  // empty descriptor, zeros); converted in the epilogue
+  const bool b32 = W.bias_dt == FTM_DT_F32;
+  const Rsrc bres = make_rsrc(W.bias, W.bias != nullptr ? (uint32_t)W.N * (b32 ? 4u : 2u) : 0u);
+  const int nkb = nsteps;
+  // tile t's operands (and bias bits) into w / bb; tiles past the item's
+  // last read nothing (an out-of-range offset), so every iteration issues
+  // the same loads and the compiler's counted waits stop at the tile in use
+  auto load_w = [&](int t, u32x4 (&w)[2][kRbKS][2], uint32_t (&bb)[2]) {
+    const bool live = t < nt;
+#pragma unroll
+    for (int nj = 0; nj < 2; ++nj) {
+      const uint32_t col = (uint32_t)(kRbNT * (n0 + t) + 32 * wave + 16 * nj + m);
+      const uint32_t bo = live ? col * (b32 ? 4u : 2u) : kOOB;
+      bb[nj] = b32 ? __builtin_amdgcn_raw_buffer_load_b32(bres, bo, 0, 0)
+                   : (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(bres, bo, 0, 0);
+    }
+#pragma unroll
+    for (int nj = 0; nj < 2; ++nj) {
+      const uint32_t rowoff =
+          (uint32_t)(kRbNT * (n0 + t) + 32 * wave + 16 * nj + m) * (uint32_t)K + 16u * (uint32_t)g;
+#pragma unroll
+      for (int kb = 0; kb < kRbKS; ++kb)
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+          w[nj][kb][h] =
+              bload16(wres, live && kb < nsteps ? rowoff + 128u * (uint32_t)kb + 64u * (uint32_t)h : kOOB);
+    }
+  };
+
+  // ---- the A tile: piece q (16 bytes) = step q / 1088, row (q / 17) % 64,
+  // piece q % 17 of that step's 272-byte chunk, at LDS byte 16 q (rows past
+  // the tile's pairs repeat its first; steps past K re-read step 0 and are
+  // never used)
+  constexpr int kPieces = kRbMT * kRbKS * (kMxChunk / 16);
+  constexpr int kPPT = kPieces / kRbThreads;
+  static_assert(kPieces % kRbThreads == 0, "A pieces per thread");
+  u32x4 wa[2][kRbKS][2], wb[2][kRbKS][2];
+  uint32_t ba[2], bb2[2];
+  load_w(0, wa, ba);
+  __syncthreads();  // the rows' pairs
+  {
+    u32x4 av[kPPT];
+#pragma unroll
+    for (int i = 0; i < kPPT; ++i) {
+      const int q = tid + kRbThreads * i;
+      const int kb = q / (kRbMT * (kMxChunk / 16)), rem = q - kb * (kRbMT * (kMxChunk / 16));
+      const int r = rem / (kMxChunk / 16), pc = rem - r * (kMxChunk / 16);
+      const int pr = lpe[r];
+      const int kc = kb < nsteps ? kb : 0;
+      av[i] = *(const u32x4*)(a.hq + (size_t)(pr >= 0 ? pr : p0) * hrow + (size_t)kc * kMxChunk + 16 * pc);
+    }
+    load_w(1, wb, bb2);
+#pragma unroll
+    for (int i = 0; i < kPPT; ++i) *(u32x4*)(lds + 16 * (tid + kRbThreads * i)) = av[i];
+  }
+  __syncthreads();  // the A tile is in LDS
+
+  // router-weighted fp32 rows into the slot buffer: rows past the tile's
+  // pairs and columns past H are stored to an out-of-range offset (dropped)
+  const Rsrc yres = make_rsrc(a.ybuf, (uint32_t)a.T * (uint32_t)KP * (uint32_t)H * 4u);
+  auto run_tile = [&](int t, const u32x4 (&w)[2][kRbKS][2], const uint32_t (&bb)[2]) {
+    const int tile = n0 + t;
+    f32x4 acc[4][2];
+#pragma unroll
+    for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+      for (int nj = 0; nj < 2; ++nj) acc[mi][nj] = (f32x4){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kb = 0; kb < kRbKS; ++kb) {
+      if (kb < nsteps) {
+        // the step's fp32 block scale of this wave's columns (one 128-block per N tile)
+        const float fs = __uint_as_float(sload4(W.s, 4u * (uint32_t)(tile * nkb + kb)));
+#pragma unroll
+        for (int mi = 0; mi < 4; ++mi) {
+          const char* cb = lds + (kb * kRbMT + 16 * mi + m) * kMxChunk;
+          const u32x4 h0 = *(const u32x4*)(cb + 16 * g);
+          const u32x4 h1 = *(const u32x4*)(cb + 64 + 16 * g);
+          const u32x4 l0 = *(const u32x4*)(cb + 128 + 16 * g);
+          const u32x4 l1 = *(const u32x4*)(cb + 192 + 16 * g);
+          const uint32_t sc = *(const uint16_t*)(cb + 256 + 2 * g);
+          const i32x8 ahi = {(int)h0.x, (int)h0.y, (int)h0.z, (int)h0.w, (int)h1.x, (int)h1.y, (int)h1.z, (int)h1.w};
+          const i32x8 alo = {(int)l0.x, (int)l0.y, (int)l0.z, (int)l0.w, (int)l1.x, (int)l1.y, (int)l1.z, (int)l1.w};
+#pragma unroll
+          for (int nj = 0; nj < 2; ++nj) {
+            const u32x4 r0 = w[nj][kb][0], r1 = w[nj][kb][1];
+            const i32x8 bw = {(int)r0.x, (int)r0.y, (int)r0.z, (int)r0.w, (int)r1.x, (int)r1.y, (int)r1.z, (int)r1.w};
+            f32x4 tq = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(ahi, bw, (f32x4){0.f, 0.f, 0.f, 0.f}, 0, 0,
+                                                                        0, (int)(sc & 0xffu), 0, 127);
+            tq = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(alo, bw, tq, 0, 0, 0, (int)(sc >> 8), 0, 127);
+            acc[mi][nj] += tq * fs;
+          }
+        }
+      }
+    }
+#pragma unroll
+    for (int nj = 0; nj < 2; ++nj) {
+      const int col = kRbNT * tile + 32 * wave + 16 * nj + m;
+      const float bn = bits_to_f32(opaque_bits(bb[nj]), W.bias_dt);
+#pragma unroll
+      for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int row = 16 * mi + 4 * g + r;
+          const int pe = lpe[row];
+          const uint32_t off = pe >= 0 && col < H ? 4u * ((uint32_t)pe * (uint32_t)H + (uint32_t)col) : kOOB;
+          __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint((acc[mi][nj][r] + bn) * lwe[row]), yres, off, 0, 0);
+        }
+    }
+  };
+
+  // tiles in pairs: tile t's operands are in flight during tile t - 1's MFMAs
+  for (int t = 0; t < nt; t += 2) {
+    run_tile(t, wa, ba);
+    load_w(t + 2, wa, ba);
+    if (t + 1 < nt) run_tile(t + 1, wb, bb2);
+    load_w(t + 3, wb, bb2);
+  }
+}
+
 // ---------------------------------------------------------------- stage B (w2 -> slot buffer)
 template <int WFMT>
 __device__ void gemm_b_body(const LayerArgs& a, const ProjSlot& W, int n0, int m0, int cnt, const int32_t* list,
@@ -1257,6 +1448,15 @@ static void ring_lds_attr() {
   }
 }
 
+// Stage B on k_gemm_mxb_f8: FP8 weights, K = I a multiple of 128 up to 512
+// (the whole A tile resident in LDS), and a slot buffer that one buffer
+// descriptor spans (below 2 GiB, so the out-of-range store offset is past it).
+static bool mxb_reg_ok(const LayerArgs& a) {
+  const ftm_moe_layer& L = a.L;
+  return L.w2.fmt == FTM_FMT_FP8_BLOCK && L.w2.K == L.inter && L.inter % 128 == 0 && L.inter <= 128 * kRbKS &&
+         4.0 * (double)a.T * (double)a.KP * (double)L.hidden < 2147483648.0;
+}
+
 template <int WFMT, int MT, int S>
 static void launch_gemm_mx(const LayerArgs& a, hipStream_t st, int which, bool xq_ready, long pairs, long maxU) {
   constexpr bool F8 = WFMT == FTM_FMT_FP8_BLOCK;
@@ -1285,9 +1485,20 @@ static void launch_gemm_mx(const LayerArgs& a, hipStream_t st, int which, bool x
     }
   }
   if (which & 2) {
-    const int ntB = kMxNTB;
-    const long items = mt * (((L.hidden + kMxNR - 1) / kMxNR + ntB - 1) / ntB);
-    hipLaunchKernelGGL((k_gemm_mx<WFMT, MT, S, true>), dim3((unsigned)items), dim3(kMxThreads), lds, st, a, ntB);
+    if (mxb_reg_ok(a) && MT == kRbMT) {
+      static bool rb_attr = false;
+      if (!rb_attr) {
+        (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&k_gemm_mxb_f8),
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, kRbLds);
+        rb_attr = true;
+      }
+      const long items = mt * (((L.hidden + kRbNT - 1) / kRbNT + kRbNTW - 1) / kRbNTW);
+      hipLaunchKernelGGL(k_gemm_mxb_f8, dim3((unsigned)items), dim3(kRbThreads), (size_t)kRbLds, st, a, kRbNTW);
+    } else {
+      const int ntB = kMxNTB;
+      const long items = mt * (((L.hidden + kMxNR - 1) / kMxNR + ntB - 1) / ntB);
+      hipLaunchKernelGGL((k_gemm_mx<WFMT, MT, S, true>), dim3((unsigned)items), dim3(kMxThreads), lds, st, a, ntB);
+    }
     if (mt_shared > 0)
       hipLaunchKernelGGL((k_gemm_b<WFMT, true>), dim3((unsigned)(mt_shared * (L.hidden / 64))), dim3(kBlock), 0,
                          st, a);
