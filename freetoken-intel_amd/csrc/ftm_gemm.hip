@@ -1451,10 +1451,14 @@ static void ring_lds_attr() {
 // Stage B on k_gemm_mxb_f8: FP8 weights, K = I a multiple of 128 up to 512
 // (the whole A tile resident in LDS), and a slot buffer that one buffer
 // descriptor spans (below 2 GiB, so the out-of-range store offset is past it).
-static bool mxb_reg_ok(const LayerArgs& a) {
-  const ftm_moe_layer& L = a.L;
+static bool mxb_reg_ok(const ftm_moe_layer& L, long T, int KP) {
   return L.w2.fmt == FTM_FMT_FP8_BLOCK && L.w2.K == L.inter && L.inter % 128 == 0 && L.inter <= 128 * kRbKS &&
-         4.0 * (double)a.T * (double)a.KP * (double)L.hidden < 2147483648.0;
+         4.0 * (double)T * (double)KP * (double)L.hidden < 2147483648.0;
+}
+
+const char* gemm_b_kernel_name(const ftm_moe_layer& L, int T) {
+  if (!mx_gemm_ok(L)) return "k_gemm_b";
+  return mxb_reg_ok(L, T, L.topk + (L.shared_inter > 0 ? 1 : 0)) ? "k_gemm_mxb_f8" : "k_gemm_mx";
 }
 
 template <int WFMT, int MT, int S>
@@ -1485,7 +1489,7 @@ static void launch_gemm_mx(const LayerArgs& a, hipStream_t st, int which, bool x
     }
   }
   if (which & 2) {
-    if (mxb_reg_ok(a) && MT == kRbMT) {
+    if (mxb_reg_ok(a.L, a.T, a.KP) && MT == kRbMT) {
       static bool rb_attr = false;
       if (!rb_attr) {
         (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&k_gemm_mxb_f8),

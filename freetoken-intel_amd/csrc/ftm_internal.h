@@ -140,6 +140,7 @@ bool mx_input(const ftm_moe_layer& L, int T);
 // take this layer at T tokens, and their launch (which: bit 0 = w13, bit 1 = w2).
 bool gemm_path_ok(const ftm_moe_layer& L, int T);
 const char* gemm_a_kernel_name(const ftm_moe_layer& L);  // the stage A tile kernel the layer takes
+const char* gemm_b_kernel_name(const ftm_moe_layer& L, int T);  // the stage B tile kernel at T tokens
 void launch_gemm_stages(const ftm_moe_layer& L, const void* x, int T, void* out, char* ws, const WsLayout& wl,
                         hipStream_t st, int which, bool xq_ready = false);
 // MXFP4 stage A on the scaled-MFMA tiles (k_gemm_a_mx) above the crossover.

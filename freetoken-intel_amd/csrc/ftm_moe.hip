@@ -3230,7 +3230,7 @@ const char* stage_kernel_name(const ftm_moe_layer& L, int T, int stage) {
     case FTM_STAGE_W2: break;
     default: return nullptr;
   }
-  if (gemm_path_ok(L, T)) return stage == FTM_STAGE_W13 || mx_gemm_ok(L) ? gemm_a_kernel_name(L) : "k_gemm_b";
+  if (gemm_path_ok(L, T)) return stage == FTM_STAGE_W13 ? gemm_a_kernel_name(L) : gemm_b_kernel_name(L, T);
   switch (L.w13.fmt) {
     case FTM_FMT_BF16: return expert_kernel_name_dt<FTM_FMT_BF16>(L, T, stage);
     case FTM_FMT_FP8_BLOCK: return expert_kernel_name_dt<FTM_FMT_FP8_BLOCK>(L, T, stage);

@@ -175,7 +175,11 @@ def test_stage_kernel_names_follow_the_dispatch():
     # 512 tokens x top-8 = 16 pairs per expert on all 256 experts: GEMM
     # stages, the routed experts on the scaled-MFMA tiles (FP8 128 x 128 blocks)
     assert name(c3, 512, nat.STAGE_W13) == "k_gemm_mx"
-    assert name(c3, 512, nat.STAGE_W2) == "k_gemm_mx"
+    # stage B: I = 512 (a multiple of 128 up to 512) keeps the tile's h rows
+    # in LDS and feeds the weights from registers; I = 640 takes the ring tile
+    assert name(c3, 512, nat.STAGE_W2) == "k_gemm_mxb_f8"
+    wide = _layer(E=256, H=2048, I=640, k=8)
+    assert name(wide, 512, nat.STAGE_W2) == "k_gemm_mx"
     # 3..16 tokens: router and top-k in one launch (the top-k stage launches nothing)
     for T in (3, 16):
         assert name(c3, T, nat.STAGE_ROUTER) == "k_route_topk1", T

@@ -309,6 +309,20 @@ def test_prefill_gemm_path_matches_oracle(gpu, name, T):
     _run_and_check(syn, gpu)
 
 
+@pytest.mark.parametrize("H,I", [(320, 384), (256, 128)])
+def test_fp8_prefill_register_fed_stage_b_shapes(gpu, H, I):
+    """FP8 above the crossover with stage B on the register-fed tiles
+    (k_gemm_mxb_f8): K = I of three or one 128-wide steps (fewer than the
+    four the tile unrolls), an odd number of 128-column N tiles and, at
+    H = 320, a last tile half past H (its columns read zeros and are not
+    stored); stage A's K = H = 320 ends in a partial step."""
+    from dataclasses import replace
+
+    cfg = replace(S.SMALL["c3_fp8"], name=f"c3_h{H}_i{I}", H=H, I=I)
+    syn = S.generate(cfg, T=512, seed=90 + I)
+    _run_and_check(syn, gpu)
+
+
 @pytest.mark.parametrize("T", [256, 600])
 def test_mxfp4_tiles_wide_range_inputs(gpu, T):
     """MXFP4 above the crossover: stage A on the scaled-MFMA tiles (128-token
