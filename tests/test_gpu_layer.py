@@ -309,16 +309,17 @@ def test_prefill_gemm_path_matches_oracle(gpu, name, T):
     _run_and_check(syn, gpu)
 
 
-@pytest.mark.parametrize("H,I", [(320, 384), (256, 128)])
-def test_fp8_prefill_register_fed_stage_b_shapes(gpu, H, I):
+@pytest.mark.parametrize("H,I,bias", [(320, 384, False), (256, 128, False), (256, 256, True)])
+def test_fp8_prefill_register_fed_stage_b_shapes(gpu, H, I, bias):
     """FP8 above the crossover with stage B on the register-fed tiles
     (k_gemm_mxb_f8): K = I of three or one 128-wide steps (fewer than the
     four the tile unrolls), an odd number of 128-column N tiles and, at
     H = 320, a last tile half past H (its columns read zeros and are not
-    stored); stage A's K = H = 320 ends in a partial step."""
+    stored); stage A's K = H = 320 ends in a partial step; bf16 expert
+    biases (the tile's 16-bit bias loads)."""
     from dataclasses import replace
 
-    cfg = replace(S.SMALL["c3_fp8"], name=f"c3_h{H}_i{I}", H=H, I=I)
+    cfg = replace(S.SMALL["c3_fp8"], name=f"c3_h{H}_i{I}", H=H, I=I, expert_bias=bias)
     syn = S.generate(cfg, T=512, seed=90 + I)
     _run_and_check(syn, gpu)
 
