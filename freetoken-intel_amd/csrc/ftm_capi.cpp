@@ -25,11 +25,9 @@ namespace {
 constexpr int kMaxDevices = 64;
 std::mutex g_scratch_mu;
 void* g_scratch_ptr[kMaxDevices] = {};
-bool g_scratch_clear[kMaxDevices] = {};  // the control region has been cleared on this device
 
-// This device's scratch address, looked up once; sets `first` when the caller
-// must clear the control region (the first call on the device).
-int scratch_of_current_device(void** ptr, bool* first) {
+// This device's scratch address, looked up once per device.
+int scratch_of_current_device(void** ptr) {
   int dev = -1;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
     (void)hipGetLastError();
@@ -45,8 +43,6 @@ int scratch_of_current_device(void** ptr, bool* first) {
     g_scratch_ptr[dev] = p;
   }
   *ptr = g_scratch_ptr[dev];
-  *first = !g_scratch_clear[dev];
-  g_scratch_clear[dev] = true;
   return FTM_OK;
 }
 
@@ -256,11 +252,14 @@ int ftm_moe_forward_noalloc(const ftm_moe_layer* layer, const void* x, int32_t n
   const size_t need = ws_layout(*layer, num_tokens).total;
   if (need > (size_t)FTM_NOALLOC_SCRATCH_BYTES) return FTM_ERR_WORKSPACE;
   void* ws = nullptr;
-  bool first = false;
-  rc = scratch_of_current_device(&ws, &first);
+  rc = scratch_of_current_device(&ws);
   if (rc != FTM_OK) return rc;
-  // every call leaves the control region zero; it starts zeroed by a fill kernel
-  if (first && launch_ws_init(ws, (hipStream_t)stream) != hipSuccess) return FTM_ERR_HIP;
+  // The scratch keeps whatever the last call on this GPU left, on whichever
+  // stream it ran, and a call that failed part way can leave its counters
+  // set: each call clears the control region with a fill kernel on its own
+  // stream first, so its kernels are ordered after that clear (a kernel, not a
+  // memset, so the call can be captured in a HIP graph).
+  if (launch_ws_init(ws, (hipStream_t)stream) != hipSuccess) return FTM_ERR_HIP;
   return ftm_moe_forward(layer, x, num_tokens, out, topk_ids, topk_w, logits, ws, need, stream);
 }
 

@@ -60,6 +60,44 @@ __device__ __forceinline__ uint16_t f32_to_f16(float f) {
   return __builtin_bit_cast(uint16_t, (_Float16)f);
 }
 
+// e^x in fp32 for the routing arithmetic (softmax numerators, the gpt-oss
+// top-k softmax, the shared expert's sigmoid gate).  Every step is one IEEE
+// operation with a fixed operand order, so a host restatement that performs
+// the same steps (fmaf, rintf, multiplies; no contraction) returns the same
+// bits:
+//   * Cody & Waite range reduction, x = n ln2 + r with n = rint(x log2 e),
+//     ln 2 split into the float nearest it and the float nearest the
+//     remainder, each product folded in by one fused multiply-add;
+//   * e^r on |r| <= ln2 / 2 by its Taylor polynomial of degree 7 in Horner
+//     form (truncation below 2^-27 relative);
+//   * 2^n applied as two exact powers of two (the second product rounds
+//     once, into the subnormal range where the result lies there).
+// x is clamped to [-104, 89] first (e^-104 is below half the smallest
+// subnormal, e^89 above FLT_MAX), so NaN gives 0.  Measured over every float
+// in [-104, 88.7] with a normal result: at most 0.94 ulp from e^x.
+__device__ __forceinline__ float ftm_expf(float x) {
+#pragma clang fp contract(off)
+  const float xc = fminf(fmaxf(x, -104.0f), 89.0f);
+  const float n = rintf(xc * 0x1.715476p+0f);
+  float r = fmaf(n, -0x1.62e43p-1f, xc);
+  r = fmaf(n, 0x1.05c61p-29f, r);
+  float p = 0x1.a01a02p-13f;    // 1/7!
+  p = fmaf(p, r, 0x1.6c16c2p-10f);  // 1/6!
+  p = fmaf(p, r, 0x1.111112p-7f);   // 1/5!
+  p = fmaf(p, r, 0x1.555556p-5f);   // 1/4!
+  p = fmaf(p, r, 0x1.555556p-3f);   // 1/3!
+  p = fmaf(p, r, 0.5f);
+  p = fmaf(p, r, 1.0f);
+  p = fmaf(p, r, 1.0f);
+  const int ni = (int)n, h = ni >> 1;
+  // the last product as fmaf(., ., +0): an explicit fused op leaves the
+  // caller's sums nothing to contract into an FMA
+  return fmaf(p * __uint_as_float((uint32_t)(h + 127) << 23), __uint_as_float((uint32_t)(ni - h + 127) << 23), 0.0f);
+}
+
+// The router's sigmoid gate weight 1 / (1 + e^-z), on ftm_expf.
+__device__ __forceinline__ float ftm_sigmoidf(float z) { return 1.0f / (1.0f + ftm_expf(-z)); }
+
 // Round to the given storage dtype and back (the value a tensor of that dtype holds).
 __device__ __forceinline__ float round_to(float v, int dt) {
   if (dt == FTM_DT_BF16) return bf16_to_f32(f32_to_bf16(v));
@@ -268,6 +306,14 @@ __device__ __forceinline__ uint32_t bload4(Rsrc r, uint32_t off) {
 // (s_waitcnt) before its arrival, a consumer loads after seeing the count.
 // An agent-scope fence would write back (release: buffer_wbl2) or invalidate
 // (acquire: buffer_inv) the whole L2 of the XCD instead, once per workgroup.
+// This ordering is a property of the gfx942 / gfx950 memory system (the SC1
+// bit's write-through and miss-on-load, vector memory returning in order for
+// one wave), not of the HIP memory model: the relaxed arrival atomic itself
+// orders nothing.  Other targets would need the release / acquire pair on the
+// arrival counter, so the build refuses them.
+#if defined(__HIP_DEVICE_COMPILE__) && !defined(__gfx942__) && !defined(__gfx950__)
+#error "the fence-free cross-workgroup hand-over (store_dev / load_dev) assumes gfx942 / gfx950 SC1 coherence"
+#endif
 constexpr int kAuxDev = 16;
 __device__ __forceinline__ uint32_t bload4_dev(Rsrc r, uint32_t off) {
   return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, kAuxDev);

@@ -1452,8 +1452,8 @@ static void ring_lds_attr() {
 // (the whole A tile resident in LDS), and a slot buffer that one buffer
 // descriptor spans (below 2 GiB, so the out-of-range store offset is past it).
 static bool mxb_reg_ok(const ftm_moe_layer& L, long T, int KP) {
-  return L.w2.fmt == FTM_FMT_FP8_BLOCK && L.w2.K == L.inter && L.inter % 128 == 0 && L.inter <= 128 * kRbKS &&
-         4.0 * (double)T * (double)KP * (double)L.hidden < 2147483648.0;
+  return L.w2.fmt == FTM_FMT_FP8_BLOCK && (L.w2.flags & FTM_PROJ_RING_B) == 0 && L.w2.K == L.inter &&
+         L.inter % 128 == 0 && L.inter <= 128 * kRbKS && 4.0 * (double)T * (double)KP * (double)L.hidden < 2147483648.0;
 }
 
 const char* gemm_b_kernel_name(const ftm_moe_layer& L, int T) {

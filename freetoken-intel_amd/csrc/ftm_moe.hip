@@ -523,13 +523,13 @@ __device__ __forceinline__ void route_token_pre(const LayerArgs& a, int t, const
     float ps = 0.0f;
 #pragma unroll
     for (int i = 0; i < NV; ++i)
-      if (lane + 64 * i < E) ps += expf(v[i] - m);
+      if (lane + 64 * i < E) ps += ftm_expf(v[i] - m);
     s = wave_sum_dpp(ps);
   }
 #pragma unroll
   for (int i = 0; i < NV; ++i) {
     if (MODE == FTM_ROUTE_SOFTMAX_TOPK_LOWP)
-      key[i] = (lane + 64 * i < E) ? round_to(expf(v[i] - m) / s, pdt) : -INFINITY;
+      key[i] = (lane + 64 * i < E) ? round_to(ftm_expf(v[i] - m) / s, pdt) : -INFINITY;
     else
       key[i] = v[i];
   }
@@ -586,9 +586,9 @@ __device__ __forceinline__ void route_token_pre(const LayerArgs& a, int t, const
   }
   float p = 0.0f;
   if (lane < k) {
-    if (MODE == FTM_ROUTE_SOFTMAX_TOPK) p = expf(sel_w - m) / s;
+    if (MODE == FTM_ROUTE_SOFTMAX_TOPK) p = ftm_expf(sel_w - m) / s;
     else if (MODE == FTM_ROUTE_SOFTMAX_TOPK_LOWP) p = sel_w;
-    else p = expf(sel_w - top0);
+    else p = ftm_expf(sel_w - top0);
   }
   const float tot = wave_sum_dpp(lane < k ? p : 0.0f);
   if (MODE == FTM_ROUTE_SOFTMAX_TOPK) {
@@ -663,7 +663,7 @@ __device__ __forceinline__ void emit_token(const LayerArgs& a, int t, int sel_e,
   zero_skipped_slots(a, t, lane < k && !listed);
   if (lane == 0 && a.L.shared_inter > 0) {
     const float sl = load_dev(&a.logits[(size_t)t * (E + 1) + E]);  // k_route_topk1: another workgroup's logit
-    a.wts[t * KP + k] = round_to(1.0f / (1.0f + expf(-sl)), a.L.act_dtype);
+    a.wts[t * KP + k] = round_to(ftm_sigmoidf(sl), a.L.act_dtype);
   }
 }
 
@@ -900,7 +900,7 @@ __global__ __launch_bounds__(64 * kTopkBlkWaves) void k_topk_blk(const LayerArgs
     zero_skipped_slots(a, t, lane < k && !(sel_e >= 0 && sel_e < E));
     if (lane == 0 && a.L.shared_inter > 0) {
       const float sl = a.logits[(size_t)t * (E + 1) + E];
-      a.wts[t * KP + k] = round_to(1.0f / (1.0f + expf(-sl)), a.L.act_dtype);
+      a.wts[t * KP + k] = round_to(ftm_sigmoidf(sl), a.L.act_dtype);
     }
   }
   __syncthreads();
@@ -2498,7 +2498,7 @@ __global__ __launch_bounds__(kBlock) void k_stage_a_lean_route(const LayerArgs a
     if (a.L.shared_inter > 0) {
       for (int t = threadIdx.x; t < T; t += kBlock) {
         const float sl = a.logits[(size_t)t * (E + 1) + E];
-        a.wts[t * KP + k] = round_to(1.0f / (1.0f + expf(-sl)), a.L.act_dtype);
+        a.wts[t * KP + k] = round_to(ftm_sigmoidf(sl), a.L.act_dtype);
       }
     }
     for (int u2 = threadIdx.x; u2 < nRouted; u2 += kBlock) {

@@ -55,6 +55,7 @@ WS_ERR_SLOT = 1
 WS_ERR_ID = 2
 WS_ERR_LIST = 4
 
+PROJ_RING_B = 1  # ftm_proj.flags: FP8 stage B on the ring tile (FTM_PROJ_RING_B)
 STAGE_ROUTER = 0
 STAGE_TOPK = 1
 STAGE_W13 = 2
@@ -91,7 +92,7 @@ class FtmProj(ctypes.Structure):
         ("N", ctypes.c_int32),
         ("K", ctypes.c_int32),
         ("num_slots", ctypes.c_int32),
-        ("reserved", ctypes.c_int32),
+        ("flags", ctypes.c_int32),
     ]
 
 

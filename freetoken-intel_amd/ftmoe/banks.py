@@ -58,6 +58,7 @@ class Proj:
     bias: Optional[torch.Tensor] = None
     group: int = 0
     slotted: bool = True
+    flags: int = 0  # ftm_proj.flags (nat.PROJ_RING_B)
     _c: Optional[nat.FtmProj] = field(default=None, repr=False)
 
     def __post_init__(self) -> None:
@@ -94,7 +95,7 @@ class Proj:
             p.N = int(self.N)
             p.K = int(self.K)
             p.num_slots = int(self.num_slots)
-            p.reserved = 0
+            p.flags = int(self.flags)
             self._c = p
         return self._c
 

@@ -162,6 +162,23 @@ def checkpoint_gate_up_interleaved(model_path: str) -> bool:
 # --------------------------------------------------------------------------- safetensors
 
 
+def safetensors_keys(model_path: str) -> list:
+    """Every tensor name of every ``*.safetensors`` shard (headers only, no data)."""
+    from safetensors import safe_open
+
+    names = []
+    for path in sorted(glob.glob(os.path.join(model_path, "*.safetensors"))):
+        with safe_open(path, framework="pt", device="cpu") as f:
+            names.extend(f.keys())
+    return names
+
+
+def checkpoint_has_expert_bias(model_path: str) -> bool:
+    """Whether the routed experts carry projection biases (any ``experts``
+    key ending in ``_bias``: gpt-oss ``gate_up_proj_bias`` / ``down_proj_bias``)."""
+    return any("experts" in n.split(".") and n.endswith("_bias") for n in safetensors_keys(model_path))
+
+
 def iter_safetensors(model_path: str, *, experts_only: bool = True) -> Iterator[Tuple[str, torch.Tensor]]:
     """``(name, tensor)`` over every ``*.safetensors`` shard of ``model_path``
     (file order, then key order), on the CPU; ``experts_only`` keeps the routed
@@ -391,18 +408,25 @@ def deinterleave_rows(t: torch.Tensor) -> torch.Tensor:
 
 
 def stream_moe_expert_sources_mxfp4(tensors: Iterator[Tuple[str, torch.Tensor]], config, *,
-                                    interleaved_gate_up: bool = False) -> Tuple[list, list]:
+                                    interleaved_gate_up: bool = False,
+                                    expert_bias: Optional[bool] = None) -> Tuple[list, list]:
     """MXFP4 per-layer fused tensors ``{gate_up_proj,down_proj}_{blocks,scales}``
     (one ``[E, ...]`` tensor each, weight.py:1276-1349) and, when present,
-    ``_bias`` -> per-layer :class:`MxfpExpertBank` pairs.  A bank is finalized
-    once its blocks and scales are in and, if the checkpoint has biases at
-    all (any ``_bias`` key seen), its bias too -- or at the end of the
-    stream.  ``interleaved_gate_up``: the gpt-oss row order (see
-    :func:`deinterleave_rows`), applied to blocks, scales and bias."""
+    ``_bias`` -> per-layer :class:`MxfpExpertBank` pairs.  ``expert_bias``
+    says whether the checkpoint's banks carry biases (``True`` / ``False``,
+    e.g. from the shards' key names, :func:`checkpoint_has_expert_bias`): a
+    bank is then finalized as soon as its blocks, scales and (if biased) bias
+    are in, so one layer at a time is buffered.  ``None`` (unknown): every
+    bank is finalized at the end of the stream, since a bias may arrive in a
+    later shard than its blocks.  ``interleaved_gate_up``: the gpt-oss row
+    order (see :func:`deinterleave_rows`), applied to blocks, scales and
+    bias."""
     L = int(config.num_layers)
     buf: Dict[tuple, dict] = {}
     done: Dict[tuple, MxfpExpertBank] = {}
-    biased = bool(getattr(config, "expert_bias", False))
+    if expert_bias is None:
+        expert_bias = getattr(config, "expert_bias", None)
+    biased = bool(expert_bias)
 
     def finalize(key):
         parts = buf.pop(key)
@@ -431,6 +455,8 @@ def stream_moe_expert_sources_mxfp4(tensors: Iterator[Tuple[str, torch.Tensor]],
         if tensor.shape[0] != config.num_experts:
             raise ValueError(f"{name}: leading dim {tensor.shape[0]} != num_experts {config.num_experts}")
         key = (layer, bank)
+        if comp == "bias" and expert_bias is False:
+            raise ValueError(f"{name}: an expert bias in a checkpoint declared without expert biases")
         if key in done:
             raise ValueError(f"Layer {layer} {bank!r}: tensor {name!r} arrived after this bank was already "
                              "finalized -- duplicate key or an out-of-order/re-streamed source?")
@@ -439,7 +465,7 @@ def stream_moe_expert_sources_mxfp4(tensors: Iterator[Tuple[str, torch.Tensor]],
             raise ValueError(f"Duplicate MXFP4 component {comp!r} for layer {layer} {bank}")
         parts[comp] = tensor
         biased = biased or comp == "bias"
-        if "blocks" in parts and "scales" in parts and ("bias" in parts or not biased):
+        if expert_bias is not None and "blocks" in parts and "scales" in parts and ("bias" in parts or not biased):
             finalize(key)
     for key in list(buf):
         if "blocks" in buf[key] and "scales" in buf[key]:
@@ -496,7 +522,8 @@ def load_moe_expert_sources(model_path: str, config=None) -> Tuple[list, list]:
         return stream_moe_expert_sources_fp8(src, config, block=checkpoint_fp8_block(model_path))
     if method == "mxfp4":
         return stream_moe_expert_sources_mxfp4(src, config,
-                                               interleaved_gate_up=checkpoint_gate_up_interleaved(model_path))
+                                               interleaved_gate_up=checkpoint_gate_up_interleaved(model_path),
+                                               expert_bias=checkpoint_has_expert_bias(model_path))
     if method == "compressed-tensors" and checkpoint_is_int8_pack_quantized(model_path):
         return stream_moe_expert_sources_int8(src, config)
     raise ValueError(f"{model_path!r}: quantization {method!r} has no packed expert bank in this build "
@@ -620,6 +647,7 @@ __all__ = [
     "GptqExpertBank", "Fp8BlockExpertBank", "MxfpExpertBank", "Int8ExpertBank", "MoeCheckpointConfig",
     "checkpoint_quant_method", "checkpoint_is_int8_pack_quantized", "checkpoint_int8_pack_quantized_group_size",
     "checkpoint_gptq_group_size", "checkpoint_fp8_block", "checkpoint_gate_up_interleaved", "iter_safetensors",
+    "safetensors_keys", "checkpoint_has_expert_bias",
     "stream_moe_expert_sources_gptq", "stream_moe_expert_sources_fp8", "stream_moe_expert_sources_int8",
     "stream_moe_expert_sources_mxfp4", "deinterleave_rows", "moe_checkpoint_config", "load_moe_expert_sources",
     "bank_format", "bank_sources", "attach_offload_cache", "moe_layer_from_banks",

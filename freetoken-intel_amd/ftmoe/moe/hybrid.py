@@ -107,23 +107,46 @@ def cpu_moe_forward(layer, x: torch.Tensor, topk_ids: torch.Tensor, topk_w: torc
 
 class CpuJob:
     """A CPU-half call running on the library's worker thread; :meth:`result`
-    waits for it (once) and returns its fp32 output."""
+    waits for it (once) and returns its fp32 output.
+
+    The worker holds one job at a time and reads this job's buffers until it
+    is waited for, so a job must always be waited for: :meth:`discard` waits
+    and drops the output (the error path of a step), and a job that is
+    garbage-collected without either is waited for then."""
 
     def __init__(self, layer, x, ids, w, mask, out, keep) -> None:
         self._keep = (layer, x, ids, w, mask, out, keep)  # alive until the worker is done with them
         self._out = out
-        self._handle = nat.lib().ftm_cpu_moe_submit(ctypes.byref(layer), x.data_ptr(), int(x.shape[0]),
-                                                    ids.data_ptr(), w.data_ptr(), nat.ptr(mask), 0, out.data_ptr())
-        nat.check(int(self._handle), "ftm_cpu_moe_submit")
+        self._rc: Optional[int] = None
         self._done = False
+        self._handle = int(nat.lib().ftm_cpu_moe_submit(ctypes.byref(layer), x.data_ptr(), int(x.shape[0]),
+                                                        ids.data_ptr(), w.data_ptr(), nat.ptr(mask), 0,
+                                                        out.data_ptr()))
+        nat.check(self._handle, "ftm_cpu_moe_submit")
+
+    def _wait(self) -> int:
+        if self._rc is None:
+            self._rc = int(nat.lib().ftm_cpu_moe_wait(self._handle))
+        return self._rc
 
     def result(self) -> torch.Tensor:
         if self._done:
             raise RuntimeError("CpuJob.result() called twice")
-        rc = nat.lib().ftm_cpu_moe_wait(int(self._handle))
         self._done = True
-        nat.check(rc, "ftm_cpu_moe_wait")
+        nat.check(self._wait(), "ftm_cpu_moe_wait")
         return self._out
+
+    def discard(self) -> None:
+        """Wait for the job to finish and drop its output."""
+        self._wait()
+        self._done = True
+
+    def __del__(self) -> None:
+        if getattr(self, "_rc", 0) is None and getattr(self, "_handle", -1) > 0:
+            try:
+                self._wait()
+            except Exception:  # interpreter shutdown: the library may already be gone
+                pass
 
 
 def split_experts(ids_host: torch.Tensor, fetch_fraction: float, max_fetch: int = -1) -> Optional[set]:
@@ -167,11 +190,15 @@ def moe_hybrid_forward(flat: torch.Tensor, top_idx: torch.Tensor, top_w: torch.T
     w_h = top_w.to("cpu", torch.float32).contiguous()
     out_h = torch.empty(x_h.shape, dtype=torch.float32, pin_memory=flat.is_cuda)
     job = CpuJob(layer, x_h, ids_host.contiguous(), w_h, mask, out_h, keep)
-    # the GPU half: the same routing with the CPU's experts as pairs without an expert
-    on_cpu = mask.to(top_idx.device).bool()[top_idx.clamp(min=0).long()] & (top_idx >= 0)
-    ids_gpu = torch.where(on_cpu, torch.full_like(top_idx, -1), top_idx).to(torch.int32)
-    ids_gpu_host = torch.where(on_cpu.cpu(), torch.full_like(ids_host, -1), ids_host).to(torch.int64)
-    gpu_out = moe_offload_forward(flat, ids_gpu, top_w, cache, layer_id, ids_host=ids_gpu_host, **kw)
+    try:
+        # the GPU half: the same routing with the CPU's experts as pairs without an expert
+        on_cpu = mask.to(top_idx.device).bool()[top_idx.clamp(min=0).long()] & (top_idx >= 0)
+        ids_gpu = torch.where(on_cpu, torch.full_like(top_idx, -1), top_idx).to(torch.int32)
+        ids_gpu_host = torch.where(on_cpu.cpu(), torch.full_like(ids_host, -1), ids_host).to(torch.int64)
+        gpu_out = moe_offload_forward(flat, ids_gpu, top_w, cache, layer_id, ids_host=ids_gpu_host, **kw)
+    except BaseException:
+        job.discard()  # the worker must be done with x_h / out_h before they go, and its slot freed
+        raise
     cpu_out = job.result()
     return (gpu_out.float() + cpu_out.to(flat.device, non_blocking=True)).to(flat.dtype)
 

@@ -101,8 +101,14 @@ typedef struct ftm_proj {
   int32_t N;            /* out features */
   int32_t K;            /* in features */
   int32_t num_slots;    /* slots in the pool (bounds check for slot ids) */
-  int32_t reserved;
+  int32_t flags;        /* 0, or FTM_PROJ_* below */
 } ftm_proj;
+
+/* ftm_proj.flags.  FTM_PROJ_RING_B, on w2: FP8 stage B above the token
+ * crossover runs on the ring tile (k_gemm_mx) even where the register-fed
+ * tile (k_gemm_mxb_f8) would; both compute the same products, block scales
+ * and epilogue in the same order, and tests compare their outputs bitwise. */
+#define FTM_PROJ_RING_B 1
 
 /* One MoE layer: routed banks (w13 = gate||up [2I, H], w2 = down [H, I]),
  * router, activation and an optional always-on dense bf16 shared expert. */
@@ -175,10 +181,13 @@ int ftm_moe_forward(const ftm_moe_layer* layer, const void* x, int32_t num_token
  * workspace is a static device array of FTM_NOALLOC_SCRATCH_BYTES per GPU (the
  * library's own, held until the process ends; FTM_ERR_WORKSPACE when the layer
  * needs more at num_tokens: ftm_moe_workspace_bytes tells); the call allocates
- * nothing.  Every call on one GPU shares that array: calls that overlap on one
- * GPU (several streams or host threads) race.  Its sticky error word is not
- * readable here: use ftm_moe_forward with a workspace to check it.  Same
- * kernels and result as ftm_moe_forward. */
+ * nothing.  Each call first clears the array's control region with a small
+ * fill kernel on `stream` (one launch more than ftm_moe_forward), so a call on
+ * any stream, or after a failed call, starts from a cleared region.  Every call
+ * on one GPU shares that array: calls that overlap on one GPU (several streams
+ * or host threads) race.  Its sticky error word is not readable here: use
+ * ftm_moe_forward with a workspace to check it.  Same kernels and result as
+ * ftm_moe_forward. */
 #define FTM_NOALLOC_SCRATCH_BYTES (16u << 20)
 int ftm_moe_forward_noalloc(const ftm_moe_layer* layer, const void* x, int32_t num_tokens,
                             void* out, int32_t* topk_ids, float* topk_w, float* logits,

@@ -76,6 +76,18 @@ def lib():
         L.orc_f32_to_bf16.argtypes = [ctypes.c_float]
         L.orc_act.restype = ctypes.c_double
         L.orc_act.argtypes = [i32, ctypes.c_double, ctypes.c_double, ctypes.c_double, ctypes.c_double]
+        L.orc_expf.restype = ctypes.c_float
+        L.orc_expf.argtypes = [ctypes.c_float]
+        L.orc_expf_n.restype = None
+        L.orc_expf_n.argtypes = [vp, ctypes.c_int64, vp]
+        L.orc_sigmoidf.restype = ctypes.c_float
+        L.orc_sigmoidf.argtypes = [ctypes.c_float]
+        L.orc_round_f16.restype = ctypes.c_float
+        L.orc_round_f16.argtypes = [ctypes.c_float]
+        L.orc_wave_sum.restype = ctypes.c_float
+        L.orc_wave_sum.argtypes = [vp]
+        L.orc_route.restype = ctypes.c_int
+        L.orc_route.argtypes = [vp, i32, i32, i32, i32, i32, i32, i32, vp, vp]
         _lib = L
     return _lib
 
@@ -247,14 +259,36 @@ def _select(key: np.ndarray, k: int) -> np.ndarray:
     return out
 
 
+_ROUTE_MODES = {"softmax_topk": 0, "softmax_topk_lowp": 1, "topk_softmax": 2}
+_DT = {"f32": D_F32, "fp32": D_F32, "f16": D_F16, "bf16": D_BF16}
+
+
 def route(logits: np.ndarray, k: int, mode: str = "softmax_topk", renormalize: bool = True,
           weight_dt: str = "bf16", prob_dt: str = "bf16"):
-    """Router softmax / top-k / renorm on fp32 logits (already rounded to the logits dtype).
+    """Router softmax / top-k / renorm on fp32 logits (already rounded to the
+    logits dtype), with the GPU kernel's IEEE operations step for step
+    (``orc_route`` in oracle_core.c: its own e^x, the lane-order sums), so
+    routing indices and router weights are bitwise comparable.
 
     * ``softmax_topk``      qwen3_5_moe/__init__.py:1225-1227 (fp32 softmax over E)
     * ``softmax_topk_lowp`` fused_moe.py:92-97, qwen3_moe/__init__.py:473-475 (softmax in the logits dtype)
     * ``topk_softmax``      gpt_oss/__init__.py:350-352 (top-k on logits, softmax over the k)
     Ties break to the lower expert index.  Returns (ids int32 [T,k], weights fp32 [T,k])."""
+    l = np.ascontiguousarray(logits, np.float32)
+    T, E = l.shape
+    ids = np.empty((T, k), np.int32)
+    w = np.empty((T, k), np.float32)
+    rc = lib().orc_route(l.ctypes.data, T, E, k, _ROUTE_MODES[mode], 1 if renormalize else 0, _DT[prob_dt],
+                         _DT[weight_dt], ids.ctypes.data, w.ctypes.data)
+    if rc != 0:
+        raise ValueError(f"orc_route rc={rc} (T={T}, E={E}, k={k})")
+    return ids, w
+
+
+def route_f64(logits: np.ndarray, k: int, mode: str = "softmax_topk", renormalize: bool = True,
+              weight_dt: str = "bf16", prob_dt: str = "bf16"):
+    """The same routing with float64 exp and numpy sums: the textbook
+    arithmetic :func:`route` is checked against (tests/test_oracle.py)."""
     l = np.asarray(logits, np.float32)
     if mode == "topk_softmax":
         ids = _select(l, k)
@@ -277,6 +311,28 @@ def route(logits: np.ndarray, k: int, mode: str = "softmax_topk", renormalize: b
     if renormalize:
         w = round_to(w / round_to(w.sum(axis=1, keepdims=True), prob_dt), prob_dt)
     return ids.astype(np.int32), round_to(w, weight_dt)
+
+
+def expf(x) -> np.ndarray:
+    """The routing e^x (orc_expf) elementwise, fp32."""
+    a = np.ascontiguousarray(x, np.float32)
+    y = np.empty_like(a)
+    lib().orc_expf_n(a.ctypes.data, a.size, y.ctypes.data)
+    return y
+
+
+def sigmoidf(z) -> np.ndarray:
+    """The shared expert's gate weight 1 / (1 + e^-z) on orc_expf, fp32."""
+    f = lib().orc_sigmoidf
+    a = np.asarray(z, np.float32)
+    return np.array([f(float(v)) for v in a.ravel()], np.float32).reshape(a.shape)
+
+
+def wave_sum(v64) -> float:
+    """The kernel's 64-lane sum order (orc_wave_sum)."""
+    a = np.ascontiguousarray(v64, np.float32)
+    assert a.shape == (64,)
+    return float(lib().orc_wave_sum(a.ctypes.data))
 
 
 # ----------------------------------------------------------------- C-backed pieces
@@ -410,7 +466,7 @@ def layer_reference(spec: dict, x_bits: np.ndarray, *, ids: Optional[np.ndarray]
     if sh is not None:
         Is = sh["w2"].shape[1]
         sl = router_logits(x_bits, sh["gate"])  # [T, 1]
-        sw = round_bf16(1.0 / (1.0 + np.exp(-sl.astype(np.float64))))[:, 0]
+        sw = round_bf16(sigmoidf(sl))[:, 0]
         p13 = OracleProj("bf16", sh["w13"], 2 * Is, spec["H"])
         p2 = OracleProj("bf16", sh["w2"], spec["H"], Is)
         ys = expert_forward(p13, p2, 0, x, "silu")

@@ -179,6 +179,159 @@ void orc_router_logits(const uint16_t* x, int T, int H, const uint16_t* G, int R
   free(gf);
 }
 
+/* --------------------------------------------------------------- routing
+ * Router softmax / top-k / renorm with the GPU's IEEE operations step for
+ * step, so that routing indices AND router weights are bitwise equal to the
+ * kernel's (route_token_pre / ftm_expf in the product's device code).  The
+ * arithmetic follows the reference:
+ *   mode 0  softmax over E in fp32, top-k, renorm      qwen3_5_moe/__init__.py:1225-1227
+ *   mode 1  softmax in the logits' dtype, top-k on those probabilities,
+ *           renorm divided in that dtype               fused_moe.py:92-96, qwen3_moe/__init__.py:473-475
+ *   mode 2  top-k on the logits, softmax over the k    gpt_oss/__init__.py:350-352
+ * and the weights are rounded to the activation dtype (fused_moe.py:96).
+ * The reference leaves exp and the summation order to torch; the order
+ * here is the kernel's: lane l of one wave holds experts l, l + 64, ...,
+ * sums their exponentials in that order, and the 64 lane sums are reduced
+ * by wave_sum_tree below.  Ties break to the lower expert index. */
+
+/* e^x: Cody & Waite range reduction x = n ln2 + r (n = rint(x log2 e), ln 2
+ * split into the float nearest it and the float nearest the remainder, each
+ * product folded in by one fmaf), the degree-7 Taylor polynomial of e^r in
+ * Horner form, and 2^n as two exact powers of two.  x is clamped to
+ * [-104, 89] (NaN gives 0).  Within 0.94 ulp of e^x over every float in
+ * [-104, 88.7] whose result is normal (tests/test_oracle.py pins it against
+ * float64 exp). */
+float orc_expf(float x) {
+  const float xc = fminf(fmaxf(x, -104.0f), 89.0f);
+  const float n = rintf(xc * 0x1.715476p+0f);
+  float r = fmaf(n, -0x1.62e43p-1f, xc);
+  r = fmaf(n, 0x1.05c61p-29f, r);
+  float p = 0x1.a01a02p-13f;
+  p = fmaf(p, r, 0x1.6c16c2p-10f);
+  p = fmaf(p, r, 0x1.111112p-7f);
+  p = fmaf(p, r, 0x1.555556p-5f);
+  p = fmaf(p, r, 0x1.555556p-3f);
+  p = fmaf(p, r, 0.5f);
+  p = fmaf(p, r, 1.0f);
+  p = fmaf(p, r, 1.0f);
+  const int ni = (int)n, h = ni >> 1;
+  uint32_t b1 = (uint32_t)(h + 127) << 23, b2 = (uint32_t)(ni - h + 127) << 23;
+  float s1, s2;
+  memcpy(&s1, &b1, 4);
+  memcpy(&s2, &b2, 4);
+  return fmaf(p * s1, s2, 0.0f);
+}
+
+void orc_expf_n(const float* x, int64_t n, float* y) {
+  for (int64_t i = 0; i < n; ++i) y[i] = orc_expf(x[i]);
+}
+
+/* The shared expert's gate weight sigmoid(z) = 1 / (1 + e^-z)
+ * (qwen3_5_moe/__init__.py:1229-1230), on orc_expf. */
+float orc_sigmoidf(float z) { return 1.0f / (1.0f + orc_expf(-z)); }
+
+/* fp32 -> IEEE binary16, round to nearest even (subnormals kept), as fp32. */
+float orc_round_f16(float f) {
+  if (f != f) return f;
+  const float a = fabsf(f);
+  if (a >= 65520.0f) return copysignf(INFINITY, f);
+  if (a == 0.0f) return f;
+  int e;
+  frexpf(a, &e);
+  int q = (e - 1) - 10; /* quantum exponent of the binary16 value */
+  if (q < -24) q = -24;
+  return copysignf(ldexpf(rintf(ldexpf(a, -q)), q), f);
+}
+
+static float round_dt(float v, int dt) {
+  if (dt == D_BF16) return orc_round_bf16(v);
+  if (dt == D_F16) return orc_round_f16(v);
+  return v;
+}
+
+/* The wave-wide sum of 64 lane values in the kernel's DPP order
+ * (wave_sum_dpp): lane pairs i ^ 1, then i ^ 2, then the mirror within 8
+ * lanes (i <-> 7 - i), within 16 (i <-> 15 - i), then
+ * (lane 0 + lane 16) + (lane 32 + lane 48). */
+float orc_wave_sum(const float* v64) {
+  float a[64], b[64];
+  for (int i = 0; i < 64; ++i) a[i] = v64[i] + v64[i ^ 1];
+  for (int i = 0; i < 64; ++i) b[i] = a[i] + a[i ^ 2];
+  for (int i = 0; i < 64; ++i) a[i] = b[i] + b[(i & ~7) | (7 - (i & 7))];
+  for (int i = 0; i < 64; ++i) b[i] = a[i] + a[(i & ~15) | (15 - (i & 15))];
+  return (b[0] + b[16]) + (b[32] + b[48]);
+}
+
+/* Order-preserving image of a key: larger float -> larger image, -0 as +0,
+ * NaN below everything (pack_key's order). */
+static uint32_t key_image(float v) {
+  if (v != v) return 0u;
+  if (v == 0.0f) v = 0.0f;
+  uint32_t b;
+  memcpy(&b, &v, 4);
+  return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+
+/* logits fp32 [T, E] (the values of the logits' dtype); pdt: dtype the
+ * LOWP probabilities are rounded to; wdt: the activation dtype.  ids int32
+ * [T, k], w fp32 [T, k].  Returns 0, or -2 for a bad shape. */
+int orc_route(const float* logits, int T, int E, int k, int mode, int renorm, int pdt, int wdt, int32_t* ids,
+              float* w) {
+  if (T < 0 || E <= 0 || k <= 0 || k > E || k > 64) return -2;
+  float* key = (float*)malloc(sizeof(float) * (size_t)E);
+  char* used = (char*)malloc((size_t)E);
+  for (int t = 0; t < T; ++t) {
+    const float* v = logits + (int64_t)t * E;
+    float m = 0.0f, s = 1.0f;
+    if (mode != 2) {
+      m = -INFINITY;
+      for (int e = 0; e < E; ++e) m = fmaxf(m, v[e]);
+      float lanes[64];
+      for (int l = 0; l < 64; ++l) {
+        float ps = 0.0f;
+        for (int e = l; e < E; e += 64) ps += orc_expf(v[e] - m);
+        lanes[l] = ps;
+      }
+      s = orc_wave_sum(lanes);
+    }
+    for (int e = 0; e < E; ++e) key[e] = mode == 1 ? round_dt(orc_expf(v[e] - m) / s, pdt) : v[e];
+    memset(used, 0, (size_t)E);
+    float sel[64] = {0};
+    for (int j = 0; j < k; ++j) {
+      int best = -1;
+      uint32_t bi = 0;
+      for (int e = 0; e < E; ++e) {
+        if (used[e]) continue;
+        const uint32_t im = key_image(key[e]);
+        if (best < 0 || im > bi) {
+          best = e;
+          bi = im;
+        }
+      }
+      used[best] = 1;
+      ids[(int64_t)t * k + j] = best;
+      sel[j] = key[best] == 0.0f ? 0.0f : key[best];
+    }
+    float p[64] = {0};
+    for (int j = 0; j < k; ++j) {
+      if (mode == 0) p[j] = orc_expf(sel[j] - m) / s;
+      else if (mode == 1) p[j] = sel[j];
+      else p[j] = orc_expf(sel[j] - sel[0]);
+    }
+    const float tot = orc_wave_sum(p);
+    for (int j = 0; j < k; ++j) {
+      float wj;
+      if (mode == 0) wj = renorm ? p[j] / tot : p[j];
+      else if (mode == 1) wj = renorm ? round_dt(p[j] / round_dt(tot, pdt), pdt) : p[j];
+      else wj = p[j] / tot;
+      w[(int64_t)t * k + j] = round_dt(wj, wdt);
+    }
+  }
+  free(key);
+  free(used);
+  return 0;
+}
+
 /* --------------------------------------------------------------- expert
  * One expert (or the dense shared expert) on M rows, double accumulation:
  *   gu = x . W13^T (+ b13)                 fused_fp8_linear.py:172 (fp32 gu)

@@ -1,8 +1,11 @@
-// Host-code driver for the AddressSanitizer / UndefinedBehaviorSanitizer run
-// of the library's host-only parts: the slot-pool LRU (ftm_offload.cpp) and
-// the CPU expert kernel of the hybrid split (ftm_cpu.cpp).  Built by
-// tests/test_host_sanitize.py with g++ -fsanitize=address,undefined; any
-// sanitizer report aborts the process.  Every call is made with random
+// Host-code driver for the sanitizer runs of the library's host-only parts:
+// the slot-pool LRU (ftm_offload.cpp) and the CPU expert kernel of the hybrid
+// split (ftm_cpu.cpp).  Built by tests/test_host_sanitize.py with g++
+// -fsanitize=address,undefined (no argument: every check below) and with
+// -fsanitize=thread (argument "threads": several host threads submitting to
+// and waiting on the async worker, ftm_cpu_moe_submit / ftm_cpu_moe_wait,
+// beside synchronous multi-threaded calls); any sanitizer report fails the
+// process.  Every call is made with random
 // (seeded) shapes, routings, caller state -- valid, and corrupt where the
 // API takes caller-owned state -- and argument errors, and the results are
 // checked for the invariants the Python tests check on the real data.
@@ -10,7 +13,9 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <atomic>
 #include <random>
+#include <thread>
 #include <vector>
 
 #include "ftmoe.h"
@@ -225,7 +230,79 @@ static int cpu_moe_run(std::mt19937& g) {
   return 0;
 }
 
-int main() {
+// One host thread's share of the threaded run: its own layer and buffers,
+// async jobs (the worker holds one job at a time, so submits from other
+// threads wait for this thread's wait) alternating with synchronous calls
+// that fan out over their own pool threads; each result is compared with the
+// same call run synchronously on one thread.
+static int threaded_client(unsigned seed, int iters, std::atomic<int>* failures, std::atomic<int>* done) {
+  std::mt19937 g(seed);
+  const int fmts[] = {FTM_FMT_FP8_BLOCK, FTM_FMT_INT8_PACKED, FTM_FMT_MXFP4, FTM_FMT_GPTQ_INT4, FTM_FMT_BF16};
+  for (int it = 0; it < iters; ++it) {
+    const int fmt = fmts[(seed + it) % 5];
+    const int E = 2 + (int)(g() % 5), H = 64, I = 32, k = 2;
+    Bank b13, b2;
+    ftm_moe_layer L;
+    memset(&L, 0, sizeof(L));
+    if (!make_proj(fmt, E, 2 * I, H, g, b13, L.w13) || !make_proj(fmt, E, H, I, g, b2, L.w2)) continue;
+    L.num_experts = E;
+    L.hidden = H;
+    L.inter = I;
+    L.topk = k;
+    L.swiglu_alpha = 1.702f;
+    L.swiglu_limit = 7.0f;
+    L.act_dtype = FTM_DT_F32;
+    L.h_dtype = FTM_DT_F32;
+    const int T = 1 + (int)(g() % 4);
+    std::vector<float> x((size_t)T * H), w((size_t)T * k), a((size_t)T * H), b((size_t)T * H), c((size_t)T * H);
+    std::normal_distribution<float> nd(0.0f, 1.0f);
+    for (auto& v : x) v = nd(g);
+    for (auto& v : w) v = nd(g);
+    std::vector<int32_t> ids((size_t)T * k);
+    for (int t = 0; t < T; ++t) {
+      ids[(size_t)t * k] = (int32_t)(g() % E);
+      ids[(size_t)t * k + 1] = (ids[(size_t)t * k] + 1) % E;
+    }
+    const int64_t h = ftm_cpu_moe_submit(&L, x.data(), T, ids.data(), w.data(), nullptr, 2, a.data());
+    const int rc_sync = ftm_cpu_moe_forward(&L, x.data(), T, ids.data(), w.data(), nullptr, 3, 0, b.data());
+    const int rc_async = h > 0 ? ftm_cpu_moe_wait(h) : (int)h;
+    const int rc_one = ftm_cpu_moe_forward(&L, x.data(), T, ids.data(), w.data(), nullptr, 1, 0, c.data());
+    if (h <= 0 || rc_async != FTM_OK || rc_sync != FTM_OK || rc_one != FTM_OK) {
+      fprintf(stderr, "threaded client %u: rc submit %lld wait %d sync %d one %d\n", seed, (long long)h, rc_async,
+              rc_sync, rc_one);
+      failures->fetch_add(1);
+      return 1;
+    }
+    for (size_t i = 0; i < c.size(); ++i) {
+      const float tol = 1e-4f * (1.0f + (c[i] < 0 ? -c[i] : c[i]));
+      const float da = a[i] - c[i], db = b[i] - c[i];
+      if (da > tol || da < -tol || db > tol || db < -tol) {
+        fprintf(stderr, "threaded client %u: result %zu differs (%g %g %g)\n", seed, i, a[i], b[i], c[i]);
+        failures->fetch_add(1);
+        return 1;
+      }
+    }
+    done->fetch_add(1);
+  }
+  return 0;
+}
+
+static int threads_run() {
+  std::atomic<int> failures{0}, done{0};
+  std::vector<std::thread> pool;
+  for (unsigned s = 0; s < 4; ++s)
+    pool.emplace_back([s, &failures, &done] { threaded_client(1000u + s, 25, &failures, &done); });
+  for (auto& t : pool) t.join();
+  printf("threaded iterations: %d\n", done.load());
+  return failures.load() == 0 && done.load() >= 60 ? 0 : 1;
+}
+
+int main(int argc, char** argv) {
+  if (argc > 1 && strcmp(argv[1], "threads") == 0) {
+    if (threads_run() != 0) return 1;
+    printf("host sanitize driver (threads): ok\n");
+    return 0;
+  }
   std::mt19937 g(20261202u);
   if (lru_run(g) != 0) return 1;
   if (cpu_moe_run(g) != 0) return 1;

@@ -180,6 +180,14 @@ def test_stage_kernel_names_follow_the_dispatch():
     assert name(c3, 512, nat.STAGE_W2) == "k_gemm_mxb_f8"
     wide = _layer(E=256, H=2048, I=640, k=8)
     assert name(wide, 512, nat.STAGE_W2) == "k_gemm_mx"
+    c3.w2.flags = nat.PROJ_RING_B  # the ring tile on request (tests compare the two)
+    assert name(c3, 512, nat.STAGE_W2) == "k_gemm_mx"
+    c3.w2.flags = 0
+    # the GPU test's shapes (32 experts, top-4, 512 tokens) reach the register-fed tile
+    for H, I in ((384, 384), (256, 128), (256, 256), (640, 512)):
+        Ls = _layer(E=32, H=H, I=I, k=4)
+        assert name(Ls, 512, nat.STAGE_W2) == "k_gemm_mxb_f8", (H, I)
+    assert name(_layer(E=32, H=320, I=384, k=4), 512, nat.STAGE_W2) == "k_gemm_b"  # H % 128 != 0
     # 3..16 tokens: router and top-k in one launch (the top-k stage launches nothing)
     for T in (3, 16):
         assert name(c3, T, nat.STAGE_ROUTER) == "k_route_topk1", T

@@ -128,3 +128,55 @@ def test_cpu_half_matches_the_reference_cpu_kernel(name):
     got = HY.cpu_moe_forward(L, x, torch.from_numpy(ids), torch.from_numpy(w), threads=2)
     ref = O.ref_cpu_moe_forward_fast(x.numpy(), ids, w, gu, dn, threads=1)
     np.testing.assert_allclose(got.numpy(), ref, rtol=1e-4, atol=1e-5 * np.abs(ref).max())
+
+
+def test_hybrid_step_with_a_failing_gpu_half_frees_the_worker(monkeypatch):
+    """A GPU half that raises (bad ids, a stale slot, a pool-size error) must
+    not leave the CPU job running on freed buffers or holding the worker's
+    only slot: the error propagates, and the next hybrid step completes."""
+    from ftmoe.moe import offload_cache as OC
+
+    cfg = replace(S.SMALL["c3_fp8"], E=8)
+    syn = S.generate(cfg, T=4, seed=504)
+    cache = OC.OffloadMoeCache(1, cfg.E, cfg.E, "cpu", quant_format="fp8_block")
+    cache.set_bank_sources({b: [syn.bank[b]] for b in OC._BANK_SCHEMAS["fp8_block"]})
+    ids, w = _routing(syn, 4, 5)
+    ids_t, w_t = torch.from_numpy(ids), torch.from_numpy(w)
+    calls = []
+
+    def failing_gpu_half(*a, **kw):
+        calls.append(1)
+        raise IndexError("stale slot map (simulated)")
+
+    monkeypatch.setattr(OC, "moe_offload_forward", failing_gpu_half)
+    for _ in range(2):  # a second failing step: the worker's slot was freed by the first
+        with pytest.raises(IndexError, match="simulated"):
+            HY.moe_hybrid_forward(syn.x, ids_t, w_t, cache, 0, intermediate=cfg.I, fetch_fraction=0.5)
+    assert len(calls) == 2
+
+    def cpu_only_gpu_half(flat, ids_gpu, top_w, cache_, layer_id, **kw):
+        return torch.zeros(flat.shape, dtype=flat.dtype)
+
+    monkeypatch.setattr(OC, "moe_offload_forward", cpu_only_gpu_half)
+    got = HY.moe_hybrid_forward(syn.x, ids_t, w_t, cache, 0, intermediate=cfg.I, fetch_fraction=0.5)
+    mask = np.zeros(cfg.E, np.uint8)
+    mask[sorted(HY.split_experts(ids_t, 0.5))] = 1
+    L, keep = _host(syn)
+    want = HY.cpu_moe_forward(L, syn.x.float(), ids_t, w_t, torch.from_numpy(mask)).to(syn.x.dtype)
+    assert torch.equal(got, want)
+
+
+def test_uncollected_cpu_job_is_waited_for_on_collection():
+    """A CpuJob dropped without result() is waited for when collected, so the
+    next submit does not block on the worker's only slot."""
+    import gc
+
+    syn = S.generate(replace(S.SMALL["c3_fp8"], E=6), T=3, seed=505)
+    L, keep = _host(syn)
+    x = syn.x.float().contiguous()
+    ids, w = _routing(syn, 3, 6)
+    job = HY.CpuJob(L, x, torch.from_numpy(ids), torch.from_numpy(w), None, torch.empty_like(x), keep)
+    del job
+    gc.collect()
+    job2 = HY.CpuJob(L, x, torch.from_numpy(ids), torch.from_numpy(w), None, torch.empty_like(x), keep)
+    assert torch.equal(job2.result(), HY.cpu_moe_forward(L, x, torch.from_numpy(ids), torch.from_numpy(w)))

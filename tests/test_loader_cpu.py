@@ -5,6 +5,7 @@ streamed back bit for bit from the per-expert (GPTQ/FP8/INT8) or per-layer
 fused (MXFP4) key spellings, gate rows first, gpt-oss's interleaved and biased
 gate_up undone, the reference's known GPTQ fixture value, the loud errors, and
 the slot-pool wiring."""
+import json
 from dataclasses import replace
 from types import SimpleNamespace
 
@@ -185,3 +186,41 @@ def test_attach_offload_cache_wires_the_slot_api(tmp_path, name):
     if fmt == "gptq_int4":
         with pytest.raises(ValueError, match="group_size"):
             LD.attach_offload_cache(gu, dn, num_experts=4, device="cpu")
+
+
+def test_mxfp4_biases_in_a_later_shard(tmp_path):
+    """gpt-oss expert biases stored in a shard after every block and scale:
+    the loader learns from the shards' key names that the checkpoint is
+    biased and waits for each bank's bias (before, a bank was finalized as
+    soon as its blocks and scales arrived, and the late bias was refused as
+    a re-streamed key).  An unknown bias state defers every bank to the end
+    of the stream; a declared bias-free checkpoint refuses a bias."""
+    from safetensors.torch import save_file
+
+    from ckpt_helpers import expert_tensors, quant_config
+
+    syns = _syns("c4_mxfp4")
+    keys = {}
+    for layer, syn in enumerate(syns):
+        keys.update(expert_tensors("mxfp4", syn, layer))
+    weights = {n: t.contiguous() for n, t in keys.items() if not n.endswith("_bias")}
+    biases = {n: t.contiguous() for n, t in keys.items() if n.endswith("_bias")}
+    assert biases
+    save_file(weights, str(tmp_path / "model-00001-of-00002.safetensors"))
+    save_file(biases, str(tmp_path / "model-00002-of-00002.safetensors"))
+    cfg = syns[0].cfg
+    conf = {"architectures": ["GptOssForCausalLM"], "model_type": "gpt_oss", "num_hidden_layers": len(syns),
+            "hidden_size": cfg.H, "moe_intermediate_size": cfg.I, "num_local_experts": cfg.E,
+            "quantization_config": quant_config("mxfp4", cfg)}
+    (tmp_path / "config.json").write_text(json.dumps(conf))
+    assert LD.checkpoint_has_expert_bias(str(tmp_path))
+    gu, dn = LD.load_moe_expert_sources(str(tmp_path))
+    for layer, syn in enumerate(syns):
+        assert torch.equal(gu[layer].bias, syn.bias13) and torch.equal(dn[layer].bias, syn.bias2)
+        assert torch.equal(gu[layer].blocks, syn.bank["blocks_gate_up"])
+    config = LD.moe_checkpoint_config(str(tmp_path))
+    src = lambda: LD.iter_safetensors(str(tmp_path))  # noqa: E731
+    gu2, dn2 = LD.stream_moe_expert_sources_mxfp4(src(), config, interleaved_gate_up=True)  # bias state unknown
+    assert all(torch.equal(a.bias, b.bias) for a, b in zip(gu + dn, gu2 + dn2))
+    with pytest.raises(ValueError, match="declared without expert biases"):
+        LD.stream_moe_expert_sources_mxfp4(src(), config, interleaved_gate_up=True, expert_bias=False)

@@ -376,3 +376,267 @@ def test_experts_match_reference_cpu_moe_kernel():
     ref = O.ref_cpu_moe_forward_fast(x, ids, w, gu, dn, threads=1)
     got = O.moe_experts(spec["w13"], spec["w2"], x, ids, w, E=cfg.E, h_bf16=False)
     np.testing.assert_allclose(got, ref, rtol=1e-4, atol=1e-5)
+
+
+# ------------------------------------------------------------------ routing arithmetic (replayed from the GPU)
+# The oracle's routing runs the kernel's IEEE operations step for step
+# (orc_route: its own e^x, the per-lane and DPP-tree sums), so GPU routing
+# indices and weights are compared bit for bit.  These tests pin that
+# restatement against the mathematics it must compute.
+_LOG2E, _LN2_HI, _LN2_LO = 1.4426950216293335, 0.6931471824645996, 1.9046542121259336e-09
+
+
+def _ulp32(t):
+    """ulp of fp32 at the (normal, non-zero) float64 values t."""
+    e = np.floor(np.log2(np.abs(t)))
+    return np.ldexp(1.0, (e - 23).astype(np.int64))
+
+
+def _exp_inputs():
+    rng = np.random.RandomState(0)
+    k = np.arange(-150, 129)
+    return np.concatenate([
+        rng.uniform(-104.0, 88.7, 400_000), rng.uniform(-1.0, 1.0, 100_000), rng.uniform(-1e-3, 1e-3, 20_000),
+        k * np.log(2.0), k * np.log(2.0) + 1e-6, k * np.log(2.0) - 1e-6, (k + 0.5) * np.log(2.0),
+        [0.0, -0.0, -87.33654, -87.3, -103.9, -100.0, 88.72, 1e-30, -1e-30],
+    ]).astype(np.float32)
+
+
+def _emulated_exp(x, *, drop_lo=False, lo_sign=1.0, degree=7, half=0.5):
+    """The routing e^x restated in numpy (each fused multiply-add taken in
+    float64 and rounded once to fp32), with a switch per plausible slip."""
+    from math import factorial
+
+    f32 = np.float32
+    x = np.clip(np.asarray(x, f32), f32(-104.0), f32(89.0))
+    fma = lambda a, b, c: (a.astype(np.float64) * np.float64(b) + c.astype(np.float64)).astype(f32)
+    n = np.rint(x * f32(_LOG2E)).astype(f32)
+    r = fma(n, -f32(_LN2_HI), x)
+    if not drop_lo:
+        r = fma(n, f32(lo_sign * _LN2_LO), r)
+    coefs = [f32(1.0 / factorial(j)) for j in range(degree, 1, -1)]
+    coefs[-1] = f32(half)
+    p = np.full_like(r, coefs[0])
+    for c in coefs[1:]:
+        p = fma(p, r, np.full_like(r, c))
+    p = fma(p, r, np.ones_like(r))
+    p = fma(p, r, np.ones_like(r))
+    with np.errstate(over="ignore"):
+        return np.ldexp(p.astype(np.float64), n.astype(np.int64)).astype(f32)
+
+
+def _max_ulp_err(got, x):
+    ref = np.exp(np.asarray(x, np.float64))
+    normal = (ref >= 2.0 ** -126) & (ref <= np.finfo(np.float32).max)
+    return float(np.max(np.abs(got[normal].astype(np.float64) - ref[normal]) / _ulp32(ref[normal]))), ref, normal
+
+
+def test_routing_exp_is_faithful_against_float64():
+    """orc_expf (Cody-Waite reduction, degree-7 Taylor in Horner form) is
+    within one ulp of e^x wherever the result is normal, within one
+    subnormal quantum below that, exact at 0, 0 past the underflow point and
+    inf past FLT_MAX."""
+    x = _exp_inputs()
+    got = O.expf(x)
+    err, ref, normal = _max_ulp_err(got, x)
+    assert err <= 1.0, err
+    sub = ref < 2.0 ** -126
+    assert np.all(np.abs(got[sub].astype(np.float64) - ref[sub]) <= 2.0 ** -149)
+    assert np.isinf(got[ref > np.finfo(np.float32).max]).all()
+    assert O.expf(np.float32([0.0, -0.0]))[0] == 1.0 == O.expf(np.float32([-0.0]))[0]
+    assert O.expf(np.float32([-104.0, -200.0, -np.inf]))[0] == 0.0
+    assert np.all(O.expf(np.float32([-104.0, -200.0, -np.inf])) == 0.0)
+    assert np.isinf(O.expf(np.float32([89.0, 1e4]))).all()
+
+
+@pytest.mark.parametrize("slip", ["none", "drop_lo", "lo_sign", "degree5", "half"])
+def test_routing_exp_check_catches_plausible_slips(slip):
+    """The one-ulp bound above separates the routine from the slips a
+    restatement could make: the low part of ln 2 dropped or of the wrong sign,
+    two Taylor terms lost, a wrong coefficient."""
+    x = _exp_inputs()
+    kw = {"none": {}, "drop_lo": {"drop_lo": True}, "lo_sign": {"lo_sign": -1.0}, "degree5": {"degree": 5},
+          "half": {"half": 0.5 + 2.0 ** -10}}[slip]
+    err = _max_ulp_err(_emulated_exp(x, **kw), x)[0]
+    if slip == "none":
+        assert err <= 1.0, err
+    else:
+        assert err > 1.0, (slip, err)
+
+
+def test_wave_sum_takes_every_lane_once():
+    """The DPP-tree order adds each of the 64 lanes exactly once: a one-hot
+    vector returns its value, integer vectors (every partial sum exact) return
+    the exact total, and random vectors stay within the fp32 bound of the
+    float64 sum."""
+    for lane in range(64):
+        v = np.zeros(64, np.float32)
+        v[lane] = 3.0
+        assert O.wave_sum(v) == 3.0, lane
+    v = np.arange(1, 65, dtype=np.float32) * np.float32(7.0)
+    assert O.wave_sum(v) == 7.0 * 64 * 65 / 2
+    rng = np.random.RandomState(1)
+    for _ in range(50):
+        v = rng.rand(64).astype(np.float32) * np.float32(rng.choice([1e-3, 1.0, 1e3]))
+        exact = float(np.sum(v.astype(np.float64)))
+        assert abs(O.wave_sum(v) - exact) <= 6 * 2.0 ** -24 * exact
+
+
+def test_f16_rounding_matches_numpy():
+    """orc_round_f16 (the LOWP probabilities in fp16 logits' dtype) is
+    numpy's round-to-nearest-even binary16 conversion, subnormals and overflow
+    included."""
+    rng = np.random.RandomState(2)
+    edge = np.float32([65504.0, 65519.99, 65520.0, 7e4, 2.0 ** -24, 2.0 ** -25, 3 * 2.0 ** -26, 2.0 ** -14,
+                       2.0 ** -14 - 2.0 ** -25, 1.0 + 2.0 ** -11, 1.0 + 3 * 2.0 ** -11, 0.0, -0.0, -1.5e-6])
+    x = np.concatenate([edge, -edge, (rng.randn(20000) * np.float32(10.0) ** rng.randint(-8, 5, 20000))
+                        .astype(np.float32)])
+    got = np.array([O.lib().orc_round_f16(float(v)) for v in x], np.float32)
+    with np.errstate(over="ignore"):
+        want = x.astype(np.float16).astype(np.float32)
+    np.testing.assert_array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+def _boundary_free_rows(keys, k, margin):
+    """Rows whose k-th key exceeds the (k+1)-th by more than ``margin`` (relative)
+    and whose top k are distinct by the same margin."""
+    srt = np.sort(keys, axis=1)[:, ::-1].astype(np.float64)
+    ok = srt[:, k - 1] > srt[:, k] * (1 + margin) + 1e-30
+    for j in range(k - 1):
+        ok &= srt[:, j] > srt[:, j + 1] * (1 + margin) + 1e-30
+    return ok
+
+
+@pytest.mark.parametrize("mode", ["softmax_topk", "softmax_topk_lowp", "topk_softmax"])
+@pytest.mark.parametrize("E,k", [(16, 2), (32, 4), (100, 6), (128, 8), (256, 8)])
+def test_route_replay_agrees_with_float64_routing(mode, E, k):
+    """orc_route against the textbook float64 softmax / top-k / renorm
+    (route_f64): the same experts wherever no key sits within rounding
+    distance of the top-k boundary; fp32 weights within 4 ulp, and in LOWP
+    mode (every rounding in bf16) within one bf16 ulp."""
+    g = torch.Generator().manual_seed(E * 10 + k)
+    logits = (torch.randn(400, E, generator=g) * 2.0).to(torch.bfloat16).float().numpy()
+    wdt = "bf16" if mode == "softmax_topk_lowp" else "f32"
+    ids, w = O.route(logits, k, mode, True, weight_dt=wdt)
+    ids64, w64 = O.route_f64(logits, k, mode, True, weight_dt=wdt)
+    if mode == "softmax_topk_lowp":
+        m = logits.max(axis=1, keepdims=True)
+        e = np.exp((logits - m).astype(np.float64))
+        keys = e / e.sum(axis=1, keepdims=True)
+        ok = _boundary_free_rows(keys, k, 2.0 ** -6)
+    else:
+        ok = _boundary_free_rows(logits - logits.min(axis=1, keepdims=True) + 1.0, k, 1e-9)
+    assert ok.sum() > 50
+    np.testing.assert_array_equal(ids[ok], ids64[ok])
+    tol = 2.0 ** -7 if mode == "softmax_topk_lowp" else 4 * 2.0 ** -23
+    np.testing.assert_allclose(w[ok], w64[ok], rtol=tol, atol=0)
+
+
+def test_route_renorm_off_and_f16_probabilities():
+    """renormalize=False returns the probabilities themselves; fp16 logits
+    take their LOWP probabilities in fp16."""
+    g = torch.Generator().manual_seed(9)
+    logits = torch.randn(64, 40, generator=g).to(torch.float16).float().numpy()
+    ids, w = O.route(logits, 4, "softmax_topk_lowp", False, weight_dt="f32", prob_dt="f16")
+    m = logits.max(axis=1, keepdims=True)
+    e = np.exp((logits - m).astype(np.float64))
+    p = (e / e.sum(axis=1, keepdims=True)).astype(np.float32).astype(np.float16).astype(np.float32)
+    ok = _boundary_free_rows(p, 4, 2.0 ** -9)
+    np.testing.assert_allclose(w[ok], np.take_along_axis(p, ids, 1)[ok], rtol=2.0 ** -10, atol=0)
+    ids, w = O.route(logits, 4, "softmax_topk", False, weight_dt="f32")
+    np.testing.assert_allclose(w, np.take_along_axis(e / e.sum(1, keepdims=True), ids, 1), rtol=4 * 2.0 ** -23)
+
+
+# ------------------------------------------------------------------ shared expert and on_input, brute force
+def _shared_brute(x_bits, sh):
+    """sigmoid(x . g_s) * down(silu(gate x) * up x) in float64
+    (qwen3_5_moe/__init__.py:1229-1230, 1766-1768), from the bf16 weights:
+    the gate logit and the weight rounded to bf16 (bf16 Linear, bf16
+    sigmoid), h rounded to bf16."""
+    x = O.bf16_bits_to_f32(x_bits).astype(np.float64)
+    W13 = O.bf16_bits_to_f32(sh["w13"]).astype(np.float64)
+    W2 = O.bf16_bits_to_f32(sh["w2"]).astype(np.float64)
+    gs = O.bf16_bits_to_f32(sh["gate"]).astype(np.float64)
+    Is = W2.shape[1]
+    logit = O.round_bf16((x @ gs.T).astype(np.float32)).astype(np.float64)[:, 0]
+    sw = O.round_bf16((1.0 / (1.0 + np.exp(-logit))).astype(np.float32)).astype(np.float64)
+    gu = x @ W13.T
+    g, u = gu[:, :Is], gu[:, Is:]
+    h = O.round_bf16((g / (1.0 + np.exp(-g)) * u).astype(np.float32)).astype(np.float64)
+    return sw, h @ W2.T
+
+
+def test_shared_expert_branch_matches_float64_brute_force():
+    """layer_reference's shared-expert branch against an independent float64
+    restatement: the gate weight bit for bit, the layer within summation-order
+    rounding.  A missing sigmoid, a missing gate, or the gate applied to the
+    routed sum instead fail the same comparison."""
+    from ftmoe import synthetic as S
+
+    syn = S.generate(S.SMALL["c3_fp8"], T=5, seed=21)
+    assert syn.shared is not None
+    spec = oracle_spec(syn)
+    xb = np_(syn.x)
+    res = O.layer_reference(spec, xb)
+    sw, ys = _shared_brute(xb, spec["shared"])
+    np.testing.assert_array_equal(res["shared_w"], sw.astype(np.float32))
+    routed = _brute_layer({k: v for k, v in spec.items() if k != "shared"}, xb, res["ids"], res["w"])
+    brute = routed + sw[:, None] * ys
+    np.testing.assert_allclose(res["out"], brute, rtol=1e-6, atol=1e-9)
+    logit = O.router_logits(xb, spec["shared"]["gate"])[:, 0].astype(np.float64)
+    slips = {"no sigmoid": routed + logit[:, None] * ys, "no gate": routed + ys,
+             "gate on the sum": sw[:, None] * (routed + ys)}
+    for name, wrong in slips.items():
+        assert not np.allclose(res["out"], wrong, rtol=1e-3, atol=1e-6), name
+
+
+def test_router_weight_on_input_matches_float64_brute_force():
+    """apply_router_weight_on_input (fused_moe.py:139-148): the expert runs on
+    round_bf16(w * x) and its output is not weighted again.  Checked against a
+    float64 per-pair restatement; the weight applied after w2 (the default
+    path) or applied twice fails the comparison."""
+    rng = np.random.RandomState(4)
+    E, H, I, T, k = 6, 64, 32, 5, 2
+    w1 = O.f32_to_bf16_bits((rng.randn(E, 2 * I, H) * 0.1).astype(np.float32))
+    w2 = O.f32_to_bf16_bits((rng.randn(E, H, I) * 0.1).astype(np.float32))
+    xb = O.f32_to_bf16_bits(rng.randn(T, H).astype(np.float32))
+    ids = np.stack([rng.choice(E, k, replace=False) for _ in range(T)]).astype(np.int32)
+    w = O.round_bf16(rng.uniform(0.1, 0.9, (T, k)).astype(np.float32))
+    p13, p2 = O.OracleProj("bf16", w1, 2 * I, H), O.OracleProj("bf16", w2, H, I)
+    x = O.bf16_bits_to_f32(xb)
+    got = O.moe_experts(p13, p2, x, ids, w, E=E, on_input=True)
+
+    def brute(on_input, after):
+        out = np.zeros((T, H))
+        for t in range(T):
+            for j in range(k):
+                e = ids[t, j]
+                xi = O.round_bf16((x[t] * w[t, j]).astype(np.float32)) if on_input else x[t]
+                gu = O.bf16_bits_to_f32(w1[e]).astype(np.float64) @ xi.astype(np.float64)
+                g, u = gu[:I], gu[I:]
+                h = O.round_bf16((g / (1 + np.exp(-g)) * u).astype(np.float32)).astype(np.float64)
+                y = O.bf16_bits_to_f32(w2[e]).astype(np.float64) @ h
+                out[t] += (float(w[t, j]) if after else 1.0) * y
+        return out
+
+    np.testing.assert_allclose(got, brute(True, False), rtol=1e-6, atol=1e-9)
+    for name, wrong in {"weight after w2": brute(False, True), "weight twice": brute(True, True)}.items():
+        assert not np.allclose(got, wrong, rtol=1e-2, atol=1e-4), name
+
+
+@pytest.mark.parametrize("E,k", [(128, 8), (256, 8)])
+def test_lowp_adversarial_rows_are_arithmetic_sensitive(E, k):
+    """The adversarial LOWP batch the GPU routing tests use: most rows put a
+    boundary probability within one fp32 ulp of a bf16 midpoint, many tie
+    across the boundary, and on a good share the textbook float64 routing
+    selects other experts than the replayed fp32 arithmetic -- so only
+    bit-identical arithmetic can reproduce the oracle's ids on them."""
+    from lowp_adversarial import adversarial_logits, boundary_stats
+
+    L = adversarial_logits(512, E, k, seed=E)
+    st = boundary_stats(L, k)
+    assert st["near_midpoint"] >= 200, st
+    assert st["boundary_ties"] >= 100, st
+    ids, _ = O.route(L, k, "softmax_topk_lowp", True)
+    ids64, _ = O.route_f64(L, k, "softmax_topk_lowp", True)
+    assert (ids != ids64).any(1).sum() >= 20

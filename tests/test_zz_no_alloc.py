@@ -42,6 +42,26 @@ def test_noalloc_matches_forward_with_workspace(gpu, name, T1, T2):
         assert torch.equal(again, ref), (name, T)
 
 
+def test_noalloc_alternating_streams(gpu):
+    """Calls on two streams in turn (each ordered after the last by an event):
+    each clears the scratch's control region on its own stream first, so
+    every call matches the workspace forward."""
+    syn = S.generate(S.SMALL["c3_fp8"], T=12, seed=31, device=gpu)
+    layer = S.build_layer(syn)
+    ref = layer.forward(syn.x)
+    torch.cuda.synchronize()
+    streams = [torch.cuda.Stream(device=gpu), torch.cuda.Stream(device=gpu)]
+    prev = torch.cuda.current_stream(gpu)
+    for i in range(4):
+        s = streams[i % 2]
+        s.wait_stream(prev)
+        with torch.cuda.stream(s):
+            got = _noalloc(layer, syn.x)
+        prev = s
+        torch.cuda.synchronize()
+        assert torch.equal(got, ref), i
+
+
 def test_noalloc_refuses_layers_beyond_its_scratch(gpu):
     """C3 at 512 tokens needs 41 MiB of workspace, more than the 16 MiB
     scratch: FTM_ERR_WORKSPACE before anything is launched."""
