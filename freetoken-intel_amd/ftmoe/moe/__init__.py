@@ -1,6 +1,9 @@
-"""MoE backend registry (python/freetoken/moe/__init__.py:16,142-171), reduced to
-the hot path: ``fused`` (HBM-resident experts).  The offload slot pool lives in
-:mod:`ftmoe.moe.offload_cache`."""
+"""MoE backend registry (python/freetoken/moe/__init__.py:16,142-171): ``fused``
+(HBM-resident experts, the dense plugin contract) and the engine-selection
+hooks ``offload``, ``cpu`` and ``hybrid`` (:mod:`ftmoe.moe.cpu_offload`), whose
+entry points are the slot pool's :func:`~ftmoe.moe.offload_cache.moe_offload_forward`,
+:class:`~ftmoe.moe.cpu_executor.CpuMoeExecutor` and
+:func:`~ftmoe.moe.hybrid.moe_hybrid_forward`."""
 from __future__ import annotations
 
 from typing import Callable, Dict
@@ -33,6 +36,27 @@ def create_fused_moe_backend():
     from .fused import FusedMoe
 
     return FusedMoe()
+
+
+@SUPPORTED_MOE_BACKENDS.register("offload")
+def create_offload_moe_backend():
+    from .cpu_offload import OffloadMoeBackend
+
+    return OffloadMoeBackend()
+
+
+@SUPPORTED_MOE_BACKENDS.register("cpu")
+def create_cpu_moe_backend():
+    from .cpu_offload import CpuOffloadMoeBackend
+
+    return CpuOffloadMoeBackend()
+
+
+@SUPPORTED_MOE_BACKENDS.register("hybrid")
+def create_hybrid_moe_backend():
+    from .cpu_offload import HybridMoeBackend
+
+    return HybridMoeBackend()
 
 
 def create_moe_backend(backend: str) -> BaseMoeBackend:

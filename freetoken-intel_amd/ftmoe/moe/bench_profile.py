@@ -129,34 +129,52 @@ def gpu_identity() -> tuple:
     return name, uuid
 
 
-def _usable_profile(gpu_name: Optional[str], path, gpu_uuid: Optional[str] = None) -> tuple:
-    """``(profile, source)`` to trust, or ``(None, source)`` (bench_profile.py:
-    138-183).  With no path and no identity given, the identity of GPU 0 keys
-    the per-device file; an explicit path (or the environment variable) is
-    read whatever the identity, but still rejected on a name mismatch."""
-    name, uuid = gpu_name, gpu_uuid
-    if path is None and name is None and uuid is None:
-        name, uuid = gpu_identity()
+# Which calibration profile to trust (the reference's lookup contract,
+# bench_profile.py:138-183, restated as rules):
+#   1. the sources: an explicit path (argument, else $FREETOKEN_BENCHBW_PATH)
+#      is the only source; otherwise this device's file (when its uuid is
+#      known), then the legacy single file;
+#   2. the first source that exists decides: a JSON object is the profile, any
+#      other content (unreadable, not JSON, not an object) means "keep the
+#      default" -- later sources are not consulted;
+#   3. a profile whose recorded device name differs from the known name of
+#      this device is ignored (measurements are hardware-specific);
+#   4. the device identity is queried only when the caller gave neither a path
+#      nor a name nor a uuid.
+# Every outcome is (profile or None, the source that decided or None).
+
+
+def _profile_sources(path, uuid: Optional[str]) -> tuple:
     explicit = path or os.environ.get(ENV_PROFILE_PATH)
     if explicit:
-        candidates = [explicit]
-    else:
-        candidates = ([default_profile_path(uuid)] if uuid else []) + [default_profile_path()]
-    prof = src = None
-    for cand in candidates:
-        prof = _load(cand)
-        if isinstance(prof, dict):
-            src = cand
-            break
-        if os.path.exists(cand):
-            return None, cand  # present but unreadable: keep the default
-    if not isinstance(prof, dict):
+        return (explicit,)
+    return ((default_profile_path(uuid),) if uuid else ()) + (default_profile_path(),)
+
+
+def _recorded_device_name(prof: dict) -> Optional[str]:
+    """The device name a profile was measured on (this build writes ``gpu``,
+    the reference ``xpu``)."""
+    for key in ("gpu", "xpu"):
+        dev = prof.get(key)
+        if isinstance(dev, dict) and dev.get("name"):
+            return str(dev["name"])
+    return None
+
+
+def _usable_profile(gpu_name: Optional[str], path, gpu_uuid: Optional[str] = None) -> tuple:
+    """``(profile, source)`` to trust, or ``(None, source)`` -- see the rules above."""
+    if path is None and gpu_name is None and gpu_uuid is None:
+        gpu_name, gpu_uuid = gpu_identity()
+    decided = next((src for src in _profile_sources(path, gpu_uuid) if os.path.exists(src)), None)
+    if decided is None:
         return None, None
-    dev = prof.get("gpu") or prof.get("xpu") or {}
-    prof_name = dev.get("name") if isinstance(dev, dict) else None
-    if name and prof_name and prof_name != name:
-        return None, src  # measured on another device
-    return prof, src
+    prof = _load(decided)
+    if not isinstance(prof, dict):
+        return None, decided
+    measured_on = _recorded_device_name(prof)
+    if gpu_name and measured_on and measured_on != gpu_name:
+        return None, decided
+    return prof, decided
 
 
 def _keys(quant_format: str) -> list:
