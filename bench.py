@@ -204,12 +204,19 @@ class ConfigBench:
                "bytes": int(b_alg), "GBps": round(b_alg / (med * 1e-6) / 1e9, 1),
                "hbm_frac": round(b_alg / (med * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
         if graphs:
-            res["graph_us_per_layer"], res["graph_bitwise_equal"] = self._graph_point(xs, steps, warmup)
+            g = self._graph_point(xs, steps, warmup)
+            res["graph_us_per_layer"], res["graph_bitwise_equal"] = g["step"], g["bitwise_equal"]
+            res["graph_step_layers"] = g["layers"]
+            res["graph1_us_per_layer"] = g["single"]
         return res
 
-    def _graph_point(self, xs, steps, warmup):
-        """The same steps as HIP-graph replays (one captured forward per
-        (layer, batch) pair), checked bitwise against eager forwards."""
+    def _graph_point(self, xs, steps, warmup, step_layers: int = 48):
+        """HIP-graph replays, as an engine uses them (``MoeGraphRunner``: one
+        graph per decode step): a step of ``step_layers`` forwards (the rotated
+        layers and inputs in turn) captured in one graph and replayed, us per
+        layer; beside it one captured forward per (layer, input) pair replayed
+        in turn (``single``), which pays a graph launch per forward.  Outputs
+        are checked bitwise against eager forwards."""
         import torch
 
         NL, NX = len(self.layers), self.NX
@@ -221,28 +228,50 @@ class ConfigBench:
                 self.layers[l].forward(xs[j])
         torch.cuda.current_stream(self.dev).wait_stream(cap)
         torch.cuda.synchronize()
+
+        def timed(fn, reps):
+            for _ in range(3):
+                fn()
+            torch.cuda.synchronize()
+            f0, f1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            f0.record()
+            for _ in range(reps):
+                fn()
+            f1.record()
+            torch.cuda.synchronize()
+            return f0.elapsed_time(f1) * 1e3 / reps
+
+        seq = [(i % NL, i % NX) for i in range(step_layers)]
+        gstep = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(gstep, stream=cap):
+            outs = [self.layers[l].forward(xs[j]) for l, j in seq]
+        ok = True
+        gstep.replay()
+        for (l, j), o in list(zip(seq, outs))[-3:]:
+            ref = self.layers[l].forward(xs[j])
+            torch.cuda.synchronize()
+            ok = ok and bool(torch.equal(o, ref))
+        step_us = timed(gstep.replay, max(1, steps // step_layers)) / step_layers
         gs = {}
         for l, j in pairs:
             g = torch.cuda.CUDAGraph()
             with torch.cuda.graph(g, stream=cap):
                 o = self.layers[l].forward(xs[j])
             gs[(l, j)] = (g, o)
-        ok = True
         for (l, j), (g, o) in list(gs.items())[:3]:
             g.replay()
             ref = self.layers[l].forward(xs[j])
             torch.cuda.synchronize()
             ok = ok and bool(torch.equal(o, ref))
-        for i in range(warmup):
-            gs[(i % NL, i % NX)][0].replay()
-        torch.cuda.synchronize()
-        f0, f1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        f0.record()
-        for i in range(steps):
-            gs[((warmup + i) % NL, (warmup + i) % NX)][0].replay()
-        f1.record()
-        torch.cuda.synchronize()
-        return round(f0.elapsed_time(f1) * 1e3 / steps, 2), ok
+        order = [gs[((warmup + i) % NL, (warmup + i) % NX)][0] for i in range(steps)]
+        it = iter(range(10 ** 9))
+
+        def one():
+            order[next(it) % len(order)].replay()
+
+        single_us = timed(one, steps)
+        return {"step": round(step_us, 2), "layers": step_layers, "single": round(single_us, 2),
+                "bitwise_equal": ok}
 
     def stage_times(self, T: int, reps: int = 15, passes: int = 4) -> dict:
         """Average duration of each of the five stage launches at T tokens: each

