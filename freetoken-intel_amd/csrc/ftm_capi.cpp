@@ -220,8 +220,8 @@ int ftm_moe_forward(const ftm_moe_layer* layer, const void* x, int32_t num_token
   hipStream_t st = (hipStream_t)stream;
   char* ws = (char*)workspace;
   const int rows = layer->num_experts + (layer->shared_inter > 0 ? 1 : 0);
-  // small decode batches on the lean kernels route inside stage A (no top-k launch)
-  const bool fused = fast_layer(layer, x) && lean_route_ok(*layer, num_tokens);
+  // small decode batches route inside stage A (no top-k launch)
+  const bool fused = fast_layer(layer, x) && route_a_ok(*layer, num_tokens);
   // the router launch also quantises the input of an MXFP4 stage A
   const bool xq = mx_input(*layer, num_tokens);
   if (!fused && route_topk_fused(*layer, num_tokens)) {  // router + top-k in one launch
@@ -232,7 +232,7 @@ int ftm_moe_forward(const ftm_moe_layer* layer, const void* x, int32_t num_token
   hipError_t e = launch_router(*layer, x, num_tokens, 0, rows, ws, wl, st, true);
   if (fused) {
     const RouteOut ro = {topk_ids, topk_w, logits};
-    if (e == hipSuccess) e = launch_experts(*layer, x, num_tokens, out, ws, wl, st, 7, &ro);
+    if (e == hipSuccess) e = launch_experts(*layer, x, num_tokens, out, ws, wl, st, 7, &ro, xq);
     return hip_rc(e);
   }
   if (e == hipSuccess)
@@ -279,7 +279,7 @@ int ftm_moe_forward_stage(const ftm_moe_layer* layer, const void* x, int32_t num
   hipStream_t st = (hipStream_t)stream;
   char* ws = (char*)workspace;
   hipError_t e = hipSuccess;
-  const bool fused = lean_route_ok(*layer, num_tokens);  // routing runs in stage A
+  const bool fused = route_a_ok(*layer, num_tokens);  // routing runs in stage A
   const bool rt = !fused && route_topk_fused(*layer, num_tokens);  // the router launch also routes
   const RouteOut ro = {nullptr, nullptr, nullptr};
   // the router stage quantises the input of an MXFP4 stage A, as ftm_moe_forward's router launch does

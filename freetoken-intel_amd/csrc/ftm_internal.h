@@ -45,7 +45,13 @@ constexpr int kRecMaxT = 256;
 // A record holds every pair of such an expert.
 constexpr int kLeanRouteMaxT = 2;
 constexpr int kLeanRouteMaxK = 16;
-static_assert(kLeanRouteMaxT <= kRecPairs, "records hold all pairs of a routed expert");
+// The same routing inside the GPTQ and LDS-activation stage A kernels
+// (k_stage_a_gq, k_stage_a_xl) up to kRouteAMaxT tokens, while the stage-A
+// grid stays within kRouteAMaxItems workgroups (about one round of them: a
+// second round would pay the routing again).
+constexpr int kRouteAMaxT = 4;
+constexpr int kRouteAMaxItems = 1536;
+static_assert(kLeanRouteMaxT <= kRouteAMaxT && kRouteAMaxT <= kRecPairs, "records hold all pairs of a routed expert");
 constexpr int kCtrlArriveTopk = 0;  // arrivals of the top-k workgroups
 constexpr int kCtrlNRouted = 1;     // routed experts with >= 1 token (written per call)
 constexpr int kCtrlNU = 2;          // nRouted + shared expert
@@ -168,6 +174,12 @@ inline bool lean_ok(const ftm_moe_layer& L, int T) {
 inline bool lean_route_ok(const ftm_moe_layer& L, int T) {
   return lean_ok(L, T) && T <= kLeanRouteMaxT && L.num_experts <= 256 && L.topk <= kLeanRouteMaxK;
 }
+
+// Small decode batches whose stage A routes the tokens itself (route_a): the
+// lean kernels (lean_route_ok), or k_stage_a_gq / k_stage_a_xl with bf16
+// activations and a router matrix, T <= kRouteAMaxT, E <= 256, k <=
+// kLeanRouteMaxK and a stage-A grid of at most kRouteAMaxItems workgroups.
+bool route_a_ok(const ftm_moe_layer& L, int T);
 
 // Router and top-k as one launch (k_route_topk1) for small batches that do
 // not route inside stage A: bf16 activations, a router matrix, T <= 16.

@@ -16,7 +16,7 @@ struct LayerArgs {
   void* out;
   int T, KP, Imax;
   bool lean;        // decode stages use the lean FP8 kernels (they read the work records)
-  bool route_a;     // lean stage A routes the tokens itself (no top-k launch, lean_route_ok)
+  bool route_a;     // stage A routes the tokens itself (no top-k launch, route_a_ok)
   int32_t* ids_out; // route_a: the caller's routing outputs (each may be null)
   float* w_out;
   float* logits_out;

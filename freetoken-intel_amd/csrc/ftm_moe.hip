@@ -1055,6 +1055,168 @@ __global__ __launch_bounds__(kBlock) void k_stage_a(const LayerArgs a) {
   }
 }
 
+// ---------------------------------------------------------------- work records
+// One routed expert's work record: expert id, pair count, bank slot and its
+// first kRecPairs pairs (stage kernels read it with one scalar load).
+struct ExpertRec {
+  int e, cnt, slot;
+  int p[kRecPairs];
+};
+__device__ __forceinline__ ExpertRec load_rec(const LayerArgs& a, int u) {
+  const u32x8 v = sload32(a.recs, (uint32_t)u * (uint32_t)(4 * kRecWords));
+  ExpertRec r;
+  r.e = (int)v[0];
+  r.cnt = (int)v[1];
+  r.slot = (int)v[2];
+#pragma unroll
+  for (int i = 0; i < kRecPairs; ++i) r.p[i] = (int)v[3 + i];
+  return r;
+}
+
+// Rank u of the set bits of m[0..nwords) (-1 if u >= total) and the total.
+__device__ __forceinline__ int mask_rank(const uint32_t* m, int nwords, int u, int& total) {
+  int e = -1, run = 0;
+  for (int w = 0; w < nwords; ++w) {
+    uint32_t b = m[w];
+    const int c = __popc(b);
+    if (e < 0 && u < run + c) {
+      for (int q = 0; q < u - run; ++q) b &= b - 1;
+      e = 32 * w + __builtin_ctz(b);
+    }
+    run += c;
+  }
+  total = run;
+  return e;
+}
+
+// Record of expert e from the LDS selections sel[T * k]: every pair of it (T
+// <= kRecPairs), in token order (per lane: e may differ between lanes).
+__device__ __forceinline__ ExpertRec route_rec(const LayerArgs& a, const int* sel, int e) {
+  const int k = a.L.topk, n = a.T * k;
+  ExpertRec r;
+  r.e = e;
+  r.cnt = 0;
+#pragma unroll
+  for (int q = 0; q < kRecPairs; ++q) r.p[q] = -1;
+  for (int i = 0; i < n; ++i) {
+    if (sel[i] == e) {
+      const int p = (i / k) * a.KP + i % k;
+#pragma unroll
+      for (int q = 0; q < kRecPairs; ++q) r.p[q] = r.cnt == q ? p : r.p[q];
+      ++r.cnt;
+    }
+  }
+  r.slot = a.L.slot_of_expert ? a.L.slot_of_expert[e] : e;
+  return r;
+}
+
+// The same record when every lane asks for the same expert: scalar fields.
+__device__ __forceinline__ ExpertRec route_rec_uniform(const LayerArgs& a, const int* sel, int e) {
+  ExpertRec r = route_rec(a, sel, __builtin_amdgcn_readfirstlane(e));
+  r.e = __builtin_amdgcn_readfirstlane(r.e);
+  r.cnt = __builtin_amdgcn_readfirstlane(r.cnt);
+  r.slot = __builtin_amdgcn_readfirstlane(r.slot);
+#pragma unroll
+  for (int q = 0; q < kRecPairs; ++q) r.p[q] = __builtin_amdgcn_readfirstlane(r.p[q]);
+  return r;
+}
+
+// ---- routing inside stage A for small batches (route_a): every stage-A
+// workgroup routes the call's T <= kRouteAMaxT tokens itself from the router
+// logits (one wave per token, the top-k kernels' arithmetic), ranks the routed
+// experts by id in an LDS bitmap and takes the expert of its item; workgroup
+// 0 publishes what the compaction would have -- the ids, router weights and
+// shared-expert gate weights, the work records, the expert table, the lists
+// and the routed count -- for stage B, the combine and the caller.  This takes
+// the top-k launch out of the chain router -> top-k -> stage A -> ...
+struct RouteA {
+  int sel[kRouteAMaxT * kLeanRouteMaxK];
+  float w[kRouteAMaxT * kLeanRouteMaxK];
+  uint32_t mask[256 / 32];
+};
+
+template <int MODE>
+__device__ __forceinline__ void route_a_token(const LayerArgs& a, RouteA& s, bool lead) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, k = a.L.topk;
+  if (wave >= a.T) return;
+  int sel_e;
+  float sel_w;
+  route_token<MODE, 4>(a, wave, nullptr, 0, nullptr, nullptr, lead ? a.logits_out : nullptr, sel_e, sel_w);
+  if (lane < k) {
+    s.sel[wave * k + lane] = sel_e;
+    s.w[wave * k + lane] = sel_w;
+    atomicOr(&s.mask[sel_e >> 5], 1u << (sel_e & 31));
+  }
+}
+
+// Routes the tokens (whole workgroup; every thread must call it) and returns
+// the number of routed experts.
+__device__ __forceinline__ int route_a_prologue(const LayerArgs& a, RouteA& s, bool lead) {
+  if (threadIdx.x < 256 / 32) s.mask[threadIdx.x] = 0u;
+  __syncthreads();
+  if (a.L.route_mode == FTM_ROUTE_SOFTMAX_TOPK)
+    route_a_token<FTM_ROUTE_SOFTMAX_TOPK>(a, s, lead);
+  else if (a.L.route_mode == FTM_ROUTE_SOFTMAX_TOPK_LOWP)
+    route_a_token<FTM_ROUTE_SOFTMAX_TOPK_LOWP>(a, s, lead);
+  else
+    route_a_token<FTM_ROUTE_TOPK_SOFTMAX>(a, s, lead);
+  __syncthreads();
+  int n;
+  mask_rank(s.mask, (a.L.num_experts + 31) / 32, 0, n);
+  return __builtin_amdgcn_readfirstlane(n);
+}
+
+// Workgroup 0's publication (whole workgroup).
+__device__ void route_a_publish(const LayerArgs& a, const RouteA& s, int nRouted) {
+  const int T = a.T, k = a.L.topk, E = a.L.num_experts, KP = a.KP;
+  const int nw = (E + 31) / 32;
+  for (int i = threadIdx.x; i < T * k; i += blockDim.x) {
+    const int p = (i / k) * KP + i % k;
+    a.wts[p] = s.w[i];
+    a.ids[i] = s.sel[i];
+    if (a.ids_out) a.ids_out[i] = s.sel[i];
+    if (a.w_out) a.w_out[i] = s.w[i];
+  }
+  if (a.L.shared_inter > 0) {
+    for (int t = threadIdx.x; t < T; t += blockDim.x) {
+      const float sl = a.logits[(size_t)t * (E + 1) + E];
+      a.wts[t * KP + k] = round_to(ftm_sigmoidf(sl), a.L.act_dtype);
+    }
+  }
+  for (int u = threadIdx.x; u < nRouted; u += blockDim.x) {
+    int tot;
+    const ExpertRec r = route_rec(a, s.sel, mask_rank(s.mask, nw, u, tot));
+    int32_t* dst = a.recs + (size_t)u * kRecWords;
+    dst[0] = r.e;
+    dst[1] = r.cnt;
+    dst[2] = r.slot;
+#pragma unroll
+    for (int q = 0; q < kRecPairs; ++q) dst[3 + q] = r.p[q];
+    dst[kRecWords - 1] = 0;
+    a.uniq[u] = r.e;
+    a.ucnt[u] = r.cnt;
+#pragma unroll
+    for (int q = 0; q < kRecPairs; ++q)
+      if (q < r.cnt) a.lists[(size_t)r.e * T + q] = r.p[q];
+  }
+  if (threadIdx.x == 0) {
+    a.ctrl[kCtrlNRouted] = nRouted;
+    a.ctrl[kCtrlNU] = nRouted + (a.L.shared_inter > 0 ? 1 : 0);
+  }
+}
+
+// Pair m (< cnt) of a routed expert: from its record when the record holds
+// every pair (route_a), else from its list in global memory.
+__device__ __forceinline__ int pair_rec_or_list(const ExpertRec* rec, Rsrc lres, int m, int cnt, int KP) {
+  if (rec != nullptr) {
+    int p = -1;
+#pragma unroll
+    for (int q = 0; q < kRecPairs; ++q) p = (m == q && m < cnt) ? rec->p[q] : p;
+    return p;
+  }
+  return pair_of_row(lres, true, m, cnt, KP, 0);
+}
+
 // ---------------------------------------------------------------- stage A, GPTQ decode (activations in LDS)
 // The arithmetic of wave_gemm_gptq / stage_a_body (each nibble decoded as
 // 128 + q in bf16, per-group scale and zero-point correction from the group's
@@ -1218,9 +1380,10 @@ struct GqA {
   static size_t lds(int K) { return gq_lds_bytes(2 * KS, K, KS, kRedBytes); }
 };
 
+// rec: null (pairs from list), or a record holding every pair (route_a).
 template <int NT, int KS>
-__device__ void stage_a_gq(const LayerArgs& a, const ProjSlot& W, int Iu, int it, int cnt, const int32_t* list,
-                           f32x4* red) {
+__device__ void stage_a_gq(const LayerArgs& a, const ProjSlot& W, int Iu, int it, int cnt, const ExpertRec* rec,
+                           const int32_t* list, f32x4* red) {
   constexpr int EPI = 16 * NT / GqA<KS>::kThreads;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int rl = lane & 15;
@@ -1253,12 +1416,12 @@ __device__ void stage_a_gq(const LayerArgs& a, const ProjSlot& W, int Iu, int it
     const int nb = min(kGqXT, cnt - mb);
     int pr[kGqXT];
 #pragma unroll
-    for (int i = 0; i < kGqXT; ++i) pr[i] = pair_of_row(lres, true, mb + i, cnt, KP, 0);
+    for (int i = 0; i < kGqXT; ++i) pr[i] = pair_rec_or_list(rec, lres, mb + i, cnt, KP);
     int pe[EPI];
 #pragma unroll
     for (int q = 0; q < EPI; ++q) {
       const int i = (threadIdx.x + q * GqA<KS>::kThreads) / NT;
-      pe[q] = i < kGqXT ? pair_of_row(lres, true, mb + i, cnt, KP, 0) : -1;
+      pe[q] = i < kGqXT ? pair_rec_or_list(rec, lres, mb + i, cnt, KP) : -1;
     }
     f32x4 acc[4];
 #pragma unroll
@@ -1318,9 +1481,35 @@ __global__ __launch_bounds__(GqA<KS>::kThreads) void k_stage_a_gq(const LayerArg
   // aliases the dynamic token-row regions (41 KiB), so a workgroup holds 41
   // KiB of LDS and three fit a CU.
   f32x4* red = (f32x4*)ftm_xl_lds;
+  __shared__ RouteA sra;
   const int I = a.L.inter;
   const int tilesR = I / NT;
   int item = blockIdx.x;
+  if (a.route_a) {
+    // the shared expert's items first (they need no routing), then the routed ones
+    const int nSh = KS == 2 && a.L.shared_inter > 0 ? a.L.shared_inter / 16 : 0;
+    if (item < nSh) {
+      if constexpr (KS == 2) {
+        const int Is = a.L.shared_inter;
+        const ProjSlot W = shared_view(a.L.shared_w13, 2 * Is, a.L.hidden);
+        stage_a_body<FTM_FMT_BF16, FTM_DT_BF16, 16>(a, W, Is, item, a.T, nullptr, a.L.topk, red);
+      }
+      return;
+    }
+    item -= nSh;
+    const int nR = route_a_prologue(a, sra, item == 0);
+    if (item == 0) route_a_publish(a, sra, nR);
+    if (item >= nR * tilesR) return;
+    int tot;
+    const ExpertRec rec = route_rec_uniform(a, sra.sel, mask_rank(sra.mask, (a.L.num_experts + 31) / 32,
+                                                                  item / tilesR, tot));
+    if (rec.slot < 0 || rec.slot >= a.L.w13.num_slots) {
+      if (threadIdx.x == 0) atomicOr(&a.ctrl[kCtrlError], 1);
+      return;
+    }
+    stage_a_gq<NT, KS>(a, proj_slot(a.L.w13, rec.slot), I, item % tilesR, rec.cnt, &rec, nullptr, red);
+    return;
+  }
   const int u = min(item / tilesR, a.L.num_experts), it = item % tilesR;
   const int e = sload_i32(a.uniq, u), cnt = sload_i32(a.ucnt, u);
   const int nRouted = sload_i32(a.ctrl, kCtrlNRouted);
@@ -1330,7 +1519,7 @@ __global__ __launch_bounds__(GqA<KS>::kThreads) void k_stage_a_gq(const LayerArg
       if (threadIdx.x == 0) atomicOr(&a.ctrl[kCtrlError], 1);
       return;
     }
-    stage_a_gq<NT, KS>(a, proj_slot(a.L.w13, slot), I, it, cnt, a.lists + (size_t)e * a.T, red);
+    stage_a_gq<NT, KS>(a, proj_slot(a.L.w13, slot), I, it, cnt, nullptr, a.lists + (size_t)e * a.T, red);
   } else if constexpr (KS == 2) {
     item -= nRouted * tilesR;
     const int Is = a.L.shared_inter;
@@ -1683,20 +1872,6 @@ __device__ __forceinline__ void xl_zero_row(uint16_t* xw, int pitch) {
 }
 
 // Work record of routed expert u (see kRecWords).
-struct ExpertRec {
-  int e, cnt, slot;
-  int p[kRecPairs];
-};
-__device__ __forceinline__ ExpertRec load_rec(const LayerArgs& a, int u) {
-  const u32x8 v = sload32(a.recs, (uint32_t)u * (uint32_t)(4 * kRecWords));
-  ExpertRec r;
-  r.e = (int)v[0];
-  r.cnt = (int)v[1];
-  r.slot = (int)v[2];
-#pragma unroll
-  for (int i = 0; i < kRecPairs; ++i) r.p[i] = (int)v[3 + i];
-  return r;
-}
 
 // Pairs of tokens [mb, mb + kXT) of a routed expert (block 0 from its record,
 // later blocks from its list) or of the shared expert; -1 past cnt.
@@ -1896,10 +2071,39 @@ template <int FMT, int NT, int LPG, int NLWM = kRowsNLW, bool SH = true>
 __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(kXlWaves<FMT, NLWM, SH>))) void k_stage_a_xl(
     const LayerArgs a) {
   __shared__ f32x4 red[NT * 4 * 16];
+  __shared__ RouteA sra;
   const int kp = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int I = a.L.inter;
   const int ti = I / (8 * NT);
-  const int item = blockIdx.x;
+  int item = blockIdx.x;
+  if (a.route_a) {
+    // the shared expert's items first (they need no routing), then the routed ones
+    const int nSh = SH && a.L.shared_inter > 0 ? a.L.shared_inter / (8 * NT) : 0;
+    if (item < nSh) {
+      if constexpr (SH) {
+        const int Is = a.L.shared_inter;
+        const ProjSlot W = shared_view(a.L.shared_w13, 2 * Is, a.L.hidden);
+        stage_a_xl_body<FTM_FMT_BF16, NT, kRowsNLW>(a, W, Is, item * 8 * NT, a.T, nullptr, nullptr, a.L.topk, kp,
+                                                     red);
+      }
+      return;
+    }
+    item -= nSh;
+    const int nR = route_a_prologue(a, sra, item == 0);
+    if (item == 0) route_a_publish(a, sra, nR);
+    if (item >= nR * ti) return;
+    int tot;
+    const ExpertRec rec = route_rec_uniform(a, sra.sel, mask_rank(sra.mask, (a.L.num_experts + 31) / 32,
+                                                                  item / ti, tot));
+    if (rec.slot < 0 || rec.slot >= a.L.w13.num_slots) {
+      if (threadIdx.x == 0) atomicOr(&a.ctrl[kCtrlError], 1);
+      return;
+    }
+    const ProjSlot W = proj_slot(a.L.w13, rec.slot);
+    stage_a_xl_body<FMT, NT, LPG, FMT == FTM_FMT_MXFP4, NLWM>(a, W, I, (item % ti) * 8 * NT, rec.cnt, &rec,
+                                                         a.lists + (size_t)rec.e * a.T, 0, kp, red);
+    return;
+  }
   const int u = min(item / ti, a.L.num_experts);
   const ExpertRec rec = load_rec(a, u);
   const int nRouted = sload_i32(a.ctrl, kCtrlNRouted);
@@ -2405,54 +2609,6 @@ __global__ __launch_bounds__(kBlock) void k_stage_a_lean(const LayerArgs a) {
 // of the routed items publishes ids, weights, records and the routed count for
 // stage B, the combine and the caller.  Replaces the top-k launch.
 
-// Rank u of the set bits of m[0..nwords) (-1 if u >= total) and the total.
-__device__ __forceinline__ int mask_rank(const uint32_t* m, int nwords, int u, int& total) {
-  int e = -1, run = 0;
-  for (int w = 0; w < nwords; ++w) {
-    uint32_t b = m[w];
-    const int c = __popc(b);
-    if (e < 0 && u < run + c) {
-      for (int q = 0; q < u - run; ++q) b &= b - 1;
-      e = 32 * w + __builtin_ctz(b);
-    }
-    run += c;
-  }
-  total = run;
-  return e;
-}
-
-// Record of expert e from the LDS selections sel[T * k]: every pair of it (T
-// <= kRecPairs), in token order (per lane: e may differ between lanes).
-__device__ __forceinline__ ExpertRec route_rec(const LayerArgs& a, const int* sel, int e) {
-  const int k = a.L.topk, n = a.T * k;
-  ExpertRec r;
-  r.e = e;
-  r.cnt = 0;
-#pragma unroll
-  for (int q = 0; q < kRecPairs; ++q) r.p[q] = -1;
-  for (int i = 0; i < n; ++i) {
-    if (sel[i] == e) {
-      const int p = (i / k) * a.KP + i % k;
-#pragma unroll
-      for (int q = 0; q < kRecPairs; ++q) r.p[q] = r.cnt == q ? p : r.p[q];
-      ++r.cnt;
-    }
-  }
-  r.slot = a.L.slot_of_expert ? a.L.slot_of_expert[e] : e;
-  return r;
-}
-
-// The same record when every lane asks for the same expert: scalar fields.
-__device__ __forceinline__ ExpertRec route_rec_uniform(const LayerArgs& a, const int* sel, int e) {
-  ExpertRec r = route_rec(a, sel, __builtin_amdgcn_readfirstlane(e));
-  r.e = __builtin_amdgcn_readfirstlane(r.e);
-  r.cnt = __builtin_amdgcn_readfirstlane(r.cnt);
-  r.slot = __builtin_amdgcn_readfirstlane(r.slot);
-#pragma unroll
-  for (int q = 0; q < kRecPairs; ++q) r.p[q] = __builtin_amdgcn_readfirstlane(r.p[q]);
-  return r;
-}
-
 template <int KR, int NWS, int MODE>
 __global__ __launch_bounds__(kBlock) void k_stage_a_lean_route(const LayerArgs a) {
   __shared__ f32x4 red[4 * 16];
@@ -2831,7 +2987,7 @@ hipError_t launch_router(const ftm_moe_layer& L, const void* x, int T, int row_b
 
 bool route_topk_fused(const ftm_moe_layer& L, int T) {
   return T >= 1 && T <= kTopk1MaxT && L.gate_w != nullptr && L.act_dtype == FTM_DT_BF16 && L.hidden % 8 == 0 &&
-         !lean_route_ok(L, T);
+         !route_a_ok(L, T);
 }
 
 hipError_t launch_route_topk(const ftm_moe_layer& L, const void* x, int T, int32_t* ids_out, float* w_out,
@@ -3157,6 +3313,41 @@ static void launch_stages_dt(const LayerArgs& a, int gridA, int gridB, hipStream
     launch_stages<FMT, FTM_DT_BF16>(a, gridA, gridB, st, which, xq_ready);
 }
 
+bool route_a_ok(const ftm_moe_layer& L, int T) {
+  if (lean_route_ok(L, T)) return true;
+  if (T < 1 || T > kRouteAMaxT || L.gate_w == nullptr || L.act_dtype != FTM_DT_BF16 || L.hidden % 8 != 0)
+    return false;
+  if (L.num_experts > 256 || L.topk > kLeanRouteMaxK || lean_ok(L, T) || gemm_path_ok(L, T)) return false;
+  const int maxU = L.num_experts < T * L.topk ? L.num_experts : T * L.topk;
+  int items;
+  switch (L.w13.fmt) {
+    case FTM_FMT_GPTQ_INT4:
+      if (!gq_ok(L, T)) return false;
+      items = maxU * (L.inter / 64) + (L.shared_inter > 0 ? L.shared_inter / 16 : 0);
+      break;
+    case FTM_FMT_BF16:
+      if (!xl_plan_a<FTM_FMT_BF16, FTM_DT_BF16>(L, T).ok) return false;
+      items = 0;
+      break;
+    case FTM_FMT_FP8_BLOCK:
+      if (!xl_plan_a<FTM_FMT_FP8_BLOCK, FTM_DT_BF16>(L, T).ok) return false;
+      items = 0;
+      break;
+    case FTM_FMT_INT8_PACKED:
+      if (!xl_plan_a<FTM_FMT_INT8_PACKED, FTM_DT_BF16>(L, T).ok) return false;
+      items = 0;
+      break;
+    case FTM_FMT_MXFP4:
+      if (!xl_plan_a<FTM_FMT_MXFP4, FTM_DT_BF16>(L, T).ok) return false;
+      items = 0;
+      break;
+    default: return false;
+  }
+  if (L.w13.fmt != FTM_FMT_GPTQ_INT4)
+    items = maxU * (L.inter / 8) + (L.shared_inter > 0 ? L.shared_inter / 8 : 0);  // k_stage_a_xl, NT = 1
+  return items <= kRouteAMaxItems;
+}
+
 hipError_t launch_experts(const ftm_moe_layer& L, const void* x, int T, void* out, char* ws,
                           const WsLayout& wl, hipStream_t st, int which, const RouteOut* ro, bool xq_ready) {
   if (gemm_path_ok(L, T)) {
@@ -3166,7 +3357,7 @@ hipError_t launch_experts(const ftm_moe_layer& L, const void* x, int T, void* ou
     if (which == 0) return hipGetLastError();
   }
   LayerArgs a = make_args(L, x, out, T, ws, wl);
-  if (ro != nullptr && lean_route_ok(L, T)) {
+  if (ro != nullptr && route_a_ok(L, T)) {
     a.route_a = true;
     a.ids_out = ro->ids;
     a.w_out = ro->w;
@@ -3223,7 +3414,7 @@ const char* stage_kernel_name(const ftm_moe_layer& L, int T, int stage) {
       if (route_topk_fused(L, T)) return "k_route_topk1";
       return T >= kRouterMinT ? "k_router_rows" : "k_router";
     case FTM_STAGE_TOPK:
-      if (lean_route_ok(L, T) || route_topk_fused(L, T)) return "";  // routed inside stage A / the router
+      if (route_a_ok(L, T) || route_topk_fused(L, T)) return "";  // routed inside stage A / the router
       return T <= kTopk1MaxT ? "k_topk1" : T >= kTopkBlkMinT ? "k_topk_blk" : "k_topk";
     case FTM_STAGE_COMBINE: return bc_fused(L, T) ? "" : "k_combine";  // "": done by stage B
     case FTM_STAGE_W13:

@@ -202,6 +202,15 @@ def test_stage_kernel_names_follow_the_dispatch():
     assert name(c3, 0, nat.STAGE_W13) is None
     small = _layer(E=8, H=256, I=128, k=2)
     assert name(small, 4, nat.STAGE_W13) == "k_stage_a_xl"
+    assert name(small, 4, nat.STAGE_ROUTER) == "k_router"  # routed inside k_stage_a_xl
+    assert name(small, 4, nat.STAGE_TOPK) == ""
+    assert name(small, 5, nat.STAGE_ROUTER) == "k_route_topk1"
+    c1 = _layer(E=16, H=1024, I=512, k=2)  # INT8 per-channel, C1's shape
+    c1.w13 = _proj(N=1024, K=1024, num_slots=16, fmt=nat.FMT_INT8_PACKED, group=1024)
+    c1.w2 = _proj(N=1024, K=512, num_slots=16, fmt=nat.FMT_INT8_PACKED, group=512)
+    assert name(c1, 4, nat.STAGE_W13) == "k_stage_a_xl"
+    assert name(c1, 4, nat.STAGE_ROUTER) == "k_router"
+    assert name(c1, 4, nat.STAGE_TOPK) == ""
     assert name(small, 4, nat.STAGE_W2) == "k_stage_b_xl"
     assert name(small, 5, nat.STAGE_W13) == "k_stage_a_rows"
     assert name(small, 5, nat.STAGE_W2) == "k_stage_b_ks"  # K split over the waves up to 32 tokens
@@ -215,6 +224,12 @@ def test_stage_kernel_names_follow_the_dispatch():
     for T in (1, 4, 16):
         assert name(gq, T, nat.STAGE_W13) == "k_stage_a_gq", T
         assert name(gq, T, nat.STAGE_W2) == "k_stage_b_gq", T
+    for T in (1, 2, 4):  # k_stage_a_gq routes the tokens itself: no top-k launch
+        assert name(gq, T, nat.STAGE_ROUTER) == "k_router", T
+        assert name(gq, T, nat.STAGE_TOPK) == "", T
+    for T in (5, 16):
+        assert name(gq, T, nat.STAGE_ROUTER) == "k_route_topk1", T
+        assert name(gq, T, nat.STAGE_TOPK) == "", T
     assert name(gq, 17, nat.STAGE_W13) == "k_stage_a"
     assert name(gq, 32, nat.STAGE_W2) == "k_stage_b_gq"  # stage B keeps LDS rows up to 32 tokens
     assert name(gq, 33, nat.STAGE_W2) == "k_stage_b"
@@ -230,6 +245,11 @@ def test_stage_kernel_names_follow_the_dispatch():
     for T in (1, 8, 32, 64, 128):
         assert name(mx, T, nat.STAGE_W13) == "k_stage_a_xl", T
         assert name(mx, T, nat.STAGE_W2) == "k_stage_b_ks", T
+    # one token: k_stage_a_xl routes it (4 experts x 360 items fit one round of
+    # workgroups); two tokens' 2880 items would not, so they keep the top-k
+    assert name(mx, 1, nat.STAGE_ROUTER) == "k_router"
+    assert name(mx, 1, nat.STAGE_TOPK) == ""
+    assert name(mx, 2, nat.STAGE_ROUTER) == "k_route_topk1"
     assert name(mx, 129, nat.STAGE_W13) == "k_gemm_mx"  # scaled-MFMA tiles (no shared expert)
     assert name(mx, 129, nat.STAGE_W2) == "k_gemm_mx"
     # many experts: the LDS path up to 256 tokens, the register-fed kernels above
