@@ -2230,6 +2230,332 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(kXlWaves
   }
 }
 
+// ---------------------------------------------------------------- token-resident stages
+// For about 6 to 16 tokens per routed expert (MXFP4 decode batches): the
+// LDS-activation kernels above take a token block of kXT rows at a time and
+// split K over the 4 waves of a 16-row item, so every item copies its tokens'
+// rows from L2 once per block -- about four times its weight bytes at 16
+// tokens per expert, in four dependent round trips.  Here a workgroup of 8
+// waves copies one block of up to kTokMaxRows token rows of its expert (bf16,
+// the whole K range) into LDS once, and each wave streams 16 weight rows over
+// the whole K range through registers, two windows of kTokNLW wave-loads in
+// flight, multiplying each window against every token of the block (one or
+// two 16-row MFMA tiles).  The copy is shared by the workgroup's 128 weight
+// rows and no cross-wave reduction is needed.
+//   stage A: wave w takes channels c0 + 8 w .. + 7 (8 gate and the matching 8
+//            up rows of w13) and writes their h;
+//   stage B: wave w takes output columns c0 + 16 w .. + 15 of w2 and writes
+//            router-weighted fp32 rows into the slot buffer (k_combine sums).
+// Blocks beyond kTokMaxRows tokens (or what the LDS holds) stream the weights
+// again.  Formats whose zero byte decodes to 0 (the NOZ contract of
+// rows_consume_lds), no shared expert.  One workgroup fits a CU (the rows take
+// the LDS).  Measured on MI355X (C4, us per layer, T = 64 / 128): 175 / 243
+// on k_stage_a_xl + k_stage_b_ks; here one tile per workgroup 146 / 161, runs
+// of tiles per workgroup 128 / 142.  Not faster: windows of 6, 8 or 12
+// wave-loads (8 and 12: 136 / 156), 12 waves per workgroup (130 / 145), K
+// split over two wave groups (152 / 199) or over four quarters per row group
+// (140 / 216); the weight stream without the MFMAs runs at the same speed
+// (128 / 139), so it is the loads of 16 rows x 64 bytes per wave-load with one
+// workgroup per CU, at ~4 TB/s, that bound it.
+constexpr int kTokWaves = 8;
+constexpr int kTokThreads = 64 * kTokWaves;
+constexpr int kTokMaxRows = 32;  // two MFMA row tiles
+constexpr int kTokNLW = 4;  // wave-loads per window (two windows in flight)
+constexpr int kTokMaxTiles = 8;  // column tiles per workgroup
+constexpr int kTokTileVals = 128;  // bias values per column tile (A: 64 gate + 64 up, B: 128 columns)
+// dynamic LDS: the CU's 160 KiB less the static pairs, router weights and biases
+constexpr int kTokLdsMax = 160 * 1024 - 2 * 4 * kTokMaxRows - 4 * kTokMaxTiles * kTokTileVals - 256;
+
+// LDS row pitch (elements) of K-element bf16 rows read by K-major wave-loads of
+// kload elements: the K range rounded up to whole wave-loads (the tail stays
+// zero), plus 8 so that the 16 rows of one MFMA operand read fall on
+// different banks.
+__host__ __device__ __forceinline__ int tok_pitch(int K, int kload) { return (K + kload - 1) / kload * kload + 8; }
+__host__ __device__ __forceinline__ int tok_rows(int K, int kload) {
+  const int r = kTokLdsMax / (2 * tok_pitch(K, kload));
+  return r < kTokMaxRows ? r : kTokMaxRows;
+}
+
+// Weight row of lane row n (0..15) of wave `wave` in column tile ct: stage A
+// the 8 gate rows of channels c0 .. c0 + 7 then their 8 up rows, stage B
+// output columns c0 .. c0 + 15; -1 past the projection.
+template <bool STB>
+__device__ __forceinline__ int tok_row(const LayerArgs& a, int ct, int wave, int n, int& c0) {
+  const int H = a.L.hidden, I = a.L.inter;
+  if constexpr (STB) {
+    c0 = ct * (16 * kTokWaves) + 16 * wave;
+    return c0 + n < H ? c0 + n : -1;
+  } else {
+    c0 = ct * (8 * kTokWaves) + 8 * wave;
+    return c0 + (n & 7) < I ? (n < 8 ? c0 + n : I + c0 + n - 8) : -1;
+  }
+}
+
+template <int EFMT, bool STB>
+__device__ __forceinline__ RowGeom<EFMT> tok_geom(const LayerArgs& a, const ProjSlot& W, int ct, int wave, int n) {
+  int c0;
+  const int lrow = tok_row<STB>(a, ct, wave, n, c0);
+  const int sb_lo = W.group > 0 ? c0 / W.group : 0;
+  const int sb_hi = W.group > 0 ? (STB ? c0 : a.L.inter + c0) / W.group : 0;
+  return RowGeom<EFMT>(W, lrow, sb_lo, sb_hi);
+}
+
+// The MFMAs of one weight window against one or two 16-row token tiles (TWO)
+// of the resident rows.  Each wave-load's weights are decoded once for both
+// tiles, and the LDS reads of wave-load b + 1 are issued before the MFMAs of b
+// (one wave-load ahead, not the whole window: the registers go to the weight
+// windows in flight).  NOZ semantics of rows_consume_lds: rows >= nb read the
+// tile's first row, wave-loads past L_hi the last one in range against zero
+// weights, lanes past K the zeroed row tails.
+template <int FMT, int NLW, int LPG, bool PAIRED, bool TWO>
+__device__ __forceinline__ void tok_consume(const ProjSlot& W, const RowGeom<FMT>& G, int Lw, int L_hi,
+                                            const RowStream<FMT, NLW>& S, const uint16_t* xs, int pitch, int nb,
+                                            f32x4& acc0, f32x4& acc1) {
+  using F = KMajor<FMT>;
+  static_assert(NLW % LPG == 0, "groups tile the window");
+  constexpr int QM = F::kMfma;
+  const int lane = threadIdx.x & 63;
+  const int g = lane >> 4, m = lane & 15;
+  const bool upper = m >= 8;
+  const uint16_t* x0 = xs + (m < nb ? m : 0) * pitch + F::kLaneK * g;
+  const uint16_t* x1 = xs + (16 + m < nb ? 16 + m : 16) * pitch + F::kLaneK * g;
+  constexpr int NP = F::kPostScale ? NLW / LPG : 1;
+  f32x4 p0[NP], p1[NP];
+#pragma unroll
+  for (int i = 0; i < NP; ++i) p0[i] = p1[i] = (f32x4){0.f, 0.f, 0.f, 0.f};
+  // the first tile's reads run one wave-load ahead; the second tile's are
+  // issued with the wave-load's own MFMAs
+  u32x4 n0[QM];
+  {
+    const int kk = min(Lw, L_hi - 1) * F::kLoadK;
+#pragma unroll
+    for (int q = 0; q < QM; ++q) n0[q] = *(const u32x4*)(x0 + kk + 8 * q);
+  }
+#pragma unroll
+  for (int b = 0; b < NLW; ++b) {
+    u32x4 c0[QM], c1[QM];
+#pragma unroll
+    for (int q = 0; q < QM; ++q) c0[q] = n0[q];
+    if constexpr (TWO) {
+      const int kk = min(Lw + b, L_hi - 1) * F::kLoadK;
+#pragma unroll
+      for (int q = 0; q < QM; ++q) c1[q] = *(const u32x4*)(x1 + kk + 8 * q);
+    }
+    if (b + 1 < NLW) {
+      const int kk = min(Lw + b + 1, L_hi - 1) * F::kLoadK;
+#pragma unroll
+      for (int q = 0; q < QM; ++q) n0[q] = *(const u32x4*)(x0 + kk + 8 * q);
+    }
+    const u32x4 r = S.raw[b];
+    const int pi = F::kPostScale ? b / LPG : 0;
+#pragma unroll
+    for (int q = 0; q < QM; ++q) {
+      u32x4 bq;
+      if constexpr (FMT == FTM_FMT_FP8_BLOCK) {
+        bq = q == 0 ? fp8x8_to_bf16(r.x, r.y) : fp8x8_to_bf16(r.z, r.w);
+      } else if constexpr (FMT == FTM_FMT_MXFP4) {
+        const uint32_t wq = q == 0 ? r.x : q == 1 ? r.y : q == 2 ? r.z : r.w;
+        const uint32_t e8 = ((S.vmask >> b) & 1u) ? (S.sw[b] >> S.sh) & 0xffu : 0u;
+        bq = fp4x8_to_bf16(wq, e8m0_to_f32(e8));
+      } else {
+        bq = r;
+      }
+      p0[pi] = mfma_bf16(c0[q], bq, p0[pi]);
+      if constexpr (TWO) p1[pi] = mfma_bf16(c1[q], bq, p1[pi]);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  if constexpr (F::kPostScale) {
+    const int g0 = Lw / G.lpg;
+#pragma unroll
+    for (int i = 0; i < NP; ++i) {
+      const int b = i * LPG;  // first wave-load of the group
+      uint32_t sidx;
+      if constexpr (FMT == FTM_FMT_FP8_BLOCK)
+        sidx = (((PAIRED && upper) ? G.fp8_hi : G.fp8_lo) / G.sesz) + (uint32_t)(g0 + i);
+      else
+        sidx = G.soff + (uint32_t)(g0 + i);
+      const float s_grp = (Lw + b < L_hi) ? decode_scalar_word(S.sw[b], sidx, W.s_dt) : 0.0f;
+      acc0 += p0[i] * s_grp;
+      if constexpr (TWO) acc1 += p1[i] * s_grp;
+    }
+  } else {
+    acc0 += p0[0];
+    if constexpr (TWO) acc1 += p1[0];
+  }
+}
+
+// One workgroup per (routed expert, group of ni consecutive column tiles):
+// the expert's token rows are copied once and the weight stream runs on
+// through the tiles (the next tile's first windows in flight during the
+// current tile's last), so the launch is about one workgroup per CU, each
+// streaming without a gap between its tiles.
+template <int EFMT, bool STB>
+__global__ __launch_bounds__(kTokThreads) void k_stage_tok(const LayerArgs a, int ni) {
+  using F = KMajor<EFMT>;
+  constexpr int NLW = kTokNLW;
+  constexpr int LPG = F::kPostScale ? 2 : NLW;
+  typedef __attribute__((address_space(1))) const void* GPtr;
+  typedef __attribute__((address_space(3))) void* LPtr;
+  __shared__ int s_pr[kTokMaxRows];
+  __shared__ float s_w[kTokMaxRows];                      // stage B: the block's router weights
+  __shared__ float s_bias[kTokMaxTiles * kTokTileVals];  // the tiles' biases (f32)
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63, n = lane & 15, g = lane >> 4;
+  const int H = a.L.hidden, I = a.L.inter;
+  const int K = STB ? I : H;
+  const int nct = ((STB ? H : I) + (STB ? 16 : 8) * kTokWaves - 1) / ((STB ? 16 : 8) * kTokWaves);
+  const int ngrp = (nct + ni - 1) / ni;
+  const int u = blockIdx.x / ngrp;
+  const int ct0 = (blockIdx.x % ngrp) * ni;
+  const int nti = min(ni, nct - ct0);  // column tiles of this workgroup
+  const int nRouted = sload_i32(a.ctrl, kCtrlNRouted);
+  if (u >= nRouted) return;
+  const ExpertRec rec = load_rec(a, u);
+  const int32_t* list = a.lists + (size_t)rec.e * a.T;
+  const ftm_proj& P = STB ? a.L.w2 : a.L.w13;
+  if (rec.slot < 0 || rec.slot >= P.num_slots) {
+    // non-resident expert: stage B contributes zeros; both flag the error
+    if constexpr (STB) {
+      for (int it = 0; it < nti; ++it) {
+        int c0;
+        (void)tok_row<true>(a, ct0 + it, wave, 0, c0);
+        for (int idx = lane; idx < rec.cnt * 16; idx += 64) {
+          const int col = c0 + idx % 16;
+          if (col < H) a.ybuf[(size_t)sload_i32(list, idx / 16) * H + col] = 0.0f;
+        }
+      }
+    }
+    if (threadIdx.x == 0) atomicOr(&a.ctrl[kCtrlError], 1);
+    return;
+  }
+  const ProjSlot W = proj_slot(P, rec.slot);
+  const int nL = fmt_loads<EFMT>(K);
+  const int nwin = ((nL + NLW - 1) / NLW + 1) / 2 * 2;  // windows per tile, even (a pad window loads nothing)
+  const int pitch = tok_pitch(K, F::kLoadK);
+  const int rows_max = tok_rows(K, F::kLoadK);
+  const uint32_t pb = 2u * (uint32_t)pitch;  // row pitch in bytes
+  uint16_t* xs = ftm_xl_lds;
+  // the rows' tails [K, pitch) are never copied: zero them once
+  {
+    const int tq = (pitch - K) / 8;  // 16-byte pieces per tail
+    for (int i = threadIdx.x; i < rows_max * tq; i += kTokThreads) {
+      const int r = i / tq, q = i % tq;
+      *(u32x4*)(xs + r * pitch + K + 8 * q) = (u32x4){0u, 0u, 0u, 0u};
+    }
+  }
+  const char* src = STB ? (const char*)a.hbuf : (const char*)a.x;
+  const size_t src_row = STB ? 2u * (size_t)a.Imax : 2u * (size_t)H;  // bytes per source row
+  const int div = STB ? 1 : a.KP;                                      // source row of pair p: p / div
+  for (int mb = 0; mb < rec.cnt; mb += rows_max) {
+    const int nb = min(rows_max, rec.cnt - mb);
+    const bool two = nb > 16;
+    __syncthreads();  // the previous block's reads of s_pr and the rows are done
+    // The epilogues take the pairs, router weights and biases from LDS: a
+    // vector load used after the window loop would wait for the next tile's
+    // windows in flight.  The loads issue here and land with the copies.
+    float wv = 0.0f;
+    if (threadIdx.x < nb) {
+      const int m = mb + threadIdx.x;
+      int p = -1;
+#pragma unroll
+      for (int q = 0; q < kRecPairs; ++q) p = m == q ? rec.p[q] : p;
+      p = m < kRecPairs ? p : list[m];
+      s_pr[threadIdx.x] = p;
+      if constexpr (STB) wv = a.wts[p];
+    }
+    uint32_t bv[2] = {0u, 0u};  // raw bits, converted once the copies have landed
+    if (W.bias != nullptr) {
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {
+        const int i = threadIdx.x + q * kTokThreads;
+        const int it = i / kTokTileVals, j = i % kTokTileVals;
+        int col = -1;
+        if (it < nti) {
+          if constexpr (STB) {
+            col = (ct0 + it) * kTokTileVals + j;
+            col = col < H ? col : -1;
+          } else {
+            const int c = (ct0 + it) * (8 * kTokWaves) + (j & 63);
+            col = c < I ? (j < 64 ? c : I + c) : -1;
+          }
+        }
+        if (col >= 0) bv[q] = load_bits(W.bias, col, W.bias_dt);
+      }
+    }
+    // the first tile's first two windows, then the block's rows
+    RowGeom<EFMT> G[1] = {tok_geom<EFMT, STB>(a, W, ct0, wave, n)};
+    RowStream<EFMT, NLW> S0[1], S1[1];
+    rows_issue<EFMT, NLW, !STB>(W, G[0], 0, nL, S0[0]);
+    rows_issue<EFMT, NLW, !STB>(W, G[0], NLW, nL, S1[0]);
+    __syncthreads();  // s_pr
+    const uint32_t nbytes = (uint32_t)nb * pb;
+    for (uint32_t c = (uint32_t)wave * 1024u; c < nbytes; c += 1024u * kTokWaves) {
+      const uint32_t d = c + 16u * (uint32_t)lane;
+      const uint32_t r = d / pb, off = d - r * pb;
+      if (r < (uint32_t)nb && off < 2u * (uint32_t)K) {
+        const char* row = src + (size_t)(s_pr[r] / div) * src_row + off;
+        __builtin_amdgcn_global_load_lds((GPtr)row, (LPtr)((char*)xs + c), 16, 0, 0);
+      }
+    }
+    __builtin_amdgcn_s_waitcnt(0);  // this wave's copies (and the first windows) have landed
+    if (STB && threadIdx.x < nb) s_w[threadIdx.x] = wv;
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const int i = threadIdx.x + q * kTokThreads;
+      if (i < kTokMaxTiles * kTokTileVals) s_bias[i] = bits_to_f32(opaque_bits(bv[q]), W.bias_dt);
+    }
+    __syncthreads();                // every wave's copies
+    for (int it = 0; it < nti; ++it) {
+      // acc0 / acc1: tokens 0-15 / 16-31 of the block (MFMA row tiles)
+      f32x4 acc0[1] = {(f32x4){0.f, 0.f, 0.f, 0.f}}, acc1[1] = {(f32x4){0.f, 0.f, 0.f, 0.f}};
+      const RowGeom<EFMT> Gc[1] = {G[0]};
+      // the windows after this tile's last two are the next tile's first two
+      const RowGeom<EFMT> Gn = tok_geom<EFMT, STB>(a, W, ct0 + it + 1, wave, n);
+      int c0;
+      const int lrow = tok_row<STB>(a, ct0 + it, wave, n, c0);
+      for (int w = 0; w < nwin; w += 2) {
+        const bool last = w + 2 >= nwin;
+        const int Lw = w * NLW;
+        if (two)
+          tok_consume<EFMT, NLW, LPG, !STB, true>(W, Gc[0], Lw, nL, S0[0], xs, pitch, nb, acc0[0], acc1[0]);
+        else
+          tok_consume<EFMT, NLW, LPG, !STB, false>(W, Gc[0], Lw, nL, S0[0], xs, pitch, nb, acc0[0], acc1[0]);
+        // unconditional: past the tiles and past K the loads fetch nothing
+        rows_issue<EFMT, NLW, !STB>(W, last ? Gn : Gc[0], last ? 0 : Lw + 2 * NLW, nL, S0[0]);
+        if (two)
+          tok_consume<EFMT, NLW, LPG, !STB, true>(W, Gc[0], Lw + NLW, nL, S1[0], xs, pitch, nb, acc0[0], acc1[0]);
+        else
+          tok_consume<EFMT, NLW, LPG, !STB, false>(W, Gc[0], Lw + NLW, nL, S1[0], xs, pitch, nb, acc0[0], acc1[0]);
+        rows_issue<EFMT, NLW, !STB>(W, last ? Gn : Gc[0], last ? NLW : Lw + 3 * NLW, nL, S1[0]);
+      }
+      G[0] = Gn;
+      // MFMA lane (g, n) holds tokens 4 g + r (r = 0..3) of its tile, weight row n of the wave's 16
+      const float* sb = s_bias + it * kTokTileVals;
+      const float bgf = STB ? sb[16 * wave + n] : sb[8 * wave + (n & 7)];
+      const float buf = STB ? 0.0f : sb[64 + 8 * wave + (n & 7)];
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        const f32x4 acc = t == 0 ? acc0[0] : acc1[0];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int tok = 16 * t + 4 * g + r;
+          if constexpr (STB) {
+            if (tok < nb && lrow >= 0) a.ybuf[(size_t)s_pr[tok] * H + c0 + n] = (acc[r] + bgf) * s_w[tok];
+          } else {
+            const float gs = acc[r] + bgf;
+            const float us = dpp_f<kDppRowShl8>(acc[r]) + buf;
+            if (n < 8 && tok < nb && lrow >= 0) {
+              const float h = act_fn(a.L.act, gs, us, a.L.swiglu_alpha, a.L.swiglu_limit);
+              store_scalar(a.hbuf, (size_t)s_pr[tok] * a.Imax + c0 + n, FTM_DT_BF16, h);
+            }
+          }
+        }
+      }
+    }
+  }
+}
+
 // GPTQ stage B: the shared expert's items first, 16 output columns each with
 // K split over the 4 waves (stage_b_ks_body) and its tokens in blocks of
 // kGqBShXT, one workgroup per (block, 16 columns); then the routed experts'
@@ -3111,8 +3437,54 @@ static XlPlan xl_plan_a(const ftm_moe_layer& L, int T) {
   }
 }
 
+// Compute units of the current device (cached per device).
+static int device_cus() {
+  static int cus[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cus[dev] == 0) {
+    int v = 0;
+    cus[dev] = hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0 ? v : 256;
+  }
+  return cus[dev];
+}
+
+// Token-resident stages (k_stage_tok) for both projections: MXFP4 layers with
+// bf16 activations and no shared expert, below the GEMM crossover, from
+// kTokMinAvg tokens per routed expert on average (up to kRecMaxT tokens: the
+// kernels read the work records).
+constexpr int kTokMinAvg = 6;
+static bool tok_ok(const ftm_moe_layer& L, int T) {
+  if (L.w13.fmt != FTM_FMT_MXFP4 || L.w2.fmt != FTM_FMT_MXFP4 || L.act_dtype != FTM_DT_BF16) return false;
+  if (L.shared_inter > 0 || L.hidden % 8 != 0 || L.inter % 8 != 0 || T > kRecMaxT || gemm_path_ok(L, T)) return false;
+  const long pairs = (long)T * L.topk;
+  const long maxU = L.num_experts < pairs ? L.num_experts : pairs;
+  if (pairs < (long)kTokMinAvg * maxU) return false;
+  return tok_rows(L.hidden, 128) >= 16 && tok_rows(L.inter, 128) >= 16;
+}
+
+template <int FMT, bool STB>
+static void launch_tok(const LayerArgs& a, int maxU, hipStream_t st) {
+  constexpr int kload = FMT == FTM_FMT_MXFP4 ? 128 : FMT == FTM_FMT_BF16 ? 32 : 64;
+  const int K = STB ? a.L.inter : a.L.hidden;
+  const size_t lds = (size_t)tok_rows(K, kload) * 2u * (size_t)tok_pitch(K, kload);
+  static bool attr = false;
+  if (!attr) {
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&k_stage_tok<FMT, STB>),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, kTokLdsMax);
+    attr = true;
+  }
+  const int cols = STB ? 16 * kTokWaves : 8 * kTokWaves;
+  const int nct = ((STB ? a.L.hidden : a.L.inter) + cols - 1) / cols;
+  // column tiles per workgroup: about one workgroup per CU (one fits a CU's LDS)
+  int ni = (maxU * nct + device_cus() - 1) / device_cus();
+  ni = ni < kTokMaxTiles ? ni : kTokMaxTiles;
+  const int ngrp = (nct + ni - 1) / ni;
+  hipLaunchKernelGGL((k_stage_tok<FMT, STB>), dim3(maxU * ngrp), dim3(kTokThreads), lds, st, a, ni);
+}
+
 bool mx_stage_a(const ftm_moe_layer& L, int T) {
-  return L.w13.fmt == FTM_FMT_MXFP4 && L.act_dtype == FTM_DT_BF16 && !gemm_path_ok(L, T) &&
+  return L.w13.fmt == FTM_FMT_MXFP4 && L.act_dtype == FTM_DT_BF16 && !gemm_path_ok(L, T) && !tok_ok(L, T) &&
          xl_plan_a<FTM_FMT_MXFP4, FTM_DT_BF16>(L, T).ok;
 }
 
@@ -3219,7 +3591,11 @@ static void launch_stages(const LayerArgs& a, int gridA, int gridB, hipStream_t 
       const int maxU = a.L.num_experts < a.T * a.L.topk ? a.L.num_experts : a.T * a.L.topk;
       const int items = maxU * (a.L.inter / 8) + (a.L.shared_inter > 0 ? a.L.shared_inter / 8 : 0);
       const XlPlan pa = xl_plan_a<FMT, AT>(a.L, a.T);
-      if (pa.ok) {
+      bool tok = false;
+      if constexpr (FMT == FTM_FMT_MXFP4 && AT == FTM_DT_BF16) tok = tok_ok(a.L, a.T);
+      if (tok) {
+        if constexpr (FMT == FTM_FMT_MXFP4 && AT == FTM_DT_BF16) launch_tok<FMT, false>(a, maxU, st);
+      } else if (pa.ok) {
         size_t lds = 4u * kXR * (size_t)xl_pitch(a.L.hidden, 4) * 2u;
         if (FMT == FTM_FMT_MXFP4) {
           // routed MXFP4 rows on scaled MFMAs: quantise the input first; the
@@ -3255,7 +3631,14 @@ static void launch_stages(const LayerArgs& a, int gridA, int gridB, hipStream_t 
   }
   if (which & 2) {
     const XlPlan pb = xl_plan_b<FMT, AT>(a.L, a.T);
-    if constexpr (FMT == FTM_FMT_GPTQ_INT4) {
+    bool tok = false;
+    if constexpr (FMT == FTM_FMT_MXFP4 && AT == FTM_DT_BF16) tok = tok_ok(a.L, a.T);
+    if (tok) {
+      if constexpr (FMT == FTM_FMT_MXFP4 && AT == FTM_DT_BF16) {
+        const int maxU = a.L.num_experts < a.T * a.L.topk ? a.L.num_experts : a.T * a.L.topk;
+        launch_tok<FMT, true>(a, maxU, st);
+      }
+    } else if constexpr (FMT == FTM_FMT_GPTQ_INT4) {
       if (gq_b_ok(a.L, a.T) && AT == FTM_DT_BF16) {
         // the shared expert's (token block, 16 columns) items + routed items of 128 columns
         const size_t lds_r = gq_lds_bytes(4, a.L.inter, 2, kGqBRedBytes);
@@ -3394,10 +3777,12 @@ static const char* expert_kernel_name(const ftm_moe_layer& L, int T, int stage) 
   if (stage == FTM_STAGE_W13) {
     if (lean) return lean_route_ok(L, T) ? "k_stage_a_lean_route" : "k_stage_a_lean";
     if (FMT == FTM_FMT_GPTQ_INT4) return AT == FTM_DT_BF16 && gq_ok(L, T) ? "k_stage_a_gq" : "k_stage_a";
+    if (AT == FTM_DT_BF16 && tok_ok(L, T)) return "k_stage_tok";
     return xl_plan_a<FMT, AT>(L, T).ok ? "k_stage_a_xl" : "k_stage_a_rows";
   }
   if (lean) return L.topk + (L.shared_inter > 0 ? 1 : 0) <= kBcMaxKP && T <= kBcMaxT ? "k_stage_bc_lean" : "k_stage_b_lean";
   if (FMT == FTM_FMT_GPTQ_INT4) return AT == FTM_DT_BF16 && gq_b_ok(L, T) ? "k_stage_b_gq" : "k_stage_b";
+  if (AT == FTM_DT_BF16 && tok_ok(L, T)) return "k_stage_tok";
   if (xl_plan_b<FMT, AT>(L, T).ok) return "k_stage_b_xl";
   return ks_plan_b<FMT, AT>(L, T).ok ? "k_stage_b_ks" : "k_stage_b";
 }

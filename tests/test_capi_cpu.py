@@ -237,14 +237,18 @@ def test_stage_kernel_names_follow_the_dispatch():
     gq.w13.K, gq.w2.N = 2176, 2176
     assert name(gq, 4, nat.STAGE_W13) == "k_stage_a"
     # MXFP4 (C4 shape): stage A on scaled MFMAs with activations in LDS and
-    # stage B with w2's 2880-wide K split over the waves, up to 16 tokens per
-    # expert (T = 128 on 32 experts, top-4); the GEMM tiles above
+    # stage B with w2's 2880-wide K split over the waves below 6 tokens per
+    # expert, the token-resident stages from 6 up to 16 (T = 128 on 32
+    # experts, top-4); the GEMM tiles above
     mx = _layer(E=32, H=2880, I=2880, k=4)
     mx.w13 = _proj(N=2 * 2880, K=2880, num_slots=8, fmt=nat.FMT_MXFP4, group=32)
     mx.w2 = _proj(N=2880, K=2880, num_slots=8, fmt=nat.FMT_MXFP4, group=32)
-    for T in (1, 8, 32, 64, 128):
+    for T in (1, 8, 32, 47):
         assert name(mx, T, nat.STAGE_W13) == "k_stage_a_xl", T
         assert name(mx, T, nat.STAGE_W2) == "k_stage_b_ks", T
+    for T in (48, 64, 128):  # 6 to 16 tokens per expert: token rows resident in LDS, both stages
+        assert name(mx, T, nat.STAGE_W13) == "k_stage_tok", T
+        assert name(mx, T, nat.STAGE_W2) == "k_stage_tok", T
     # one token: k_stage_a_xl routes it (4 experts x 360 items fit one round of
     # workgroups); two tokens' 2880 items would not, so they keep the top-k
     assert name(mx, 1, nat.STAGE_ROUTER) == "k_router"

@@ -14,6 +14,7 @@ import torch
 import ftm_oracle as O
 from ftm_helpers import ATOL, MX_REL_RMS, RTOL, assert_close, np_, oracle_spec, rel_rms, to_f32, wide_range_x
 
+from ftmoe import _native as nat
 from ftmoe import synthetic as S
 
 pytestmark = pytest.mark.gpu
@@ -150,6 +151,28 @@ def test_mxfp4_many_experts_lds_path(gpu, T):
 
     syn = S.generate(replace(S.SMALL["c4_mxfp4"], E=128, k=2), T=T, seed=60 + T)
     _run_and_check(syn, gpu)
+
+
+@pytest.mark.parametrize("T,hot", [(24, False), (48, False), (64, False), (64, True)])
+def test_mxfp4_token_resident_stages(gpu, T, hot):
+    """MXFP4 at 6 to 16 tokens per routed expert: both projections on
+    k_stage_tok (one block of up to 32 token rows of an expert in LDS per
+    workgroup, 8 waves of 16 weight rows each over the whole K, 320 and 192
+    not multiples of the 128-wide wave-loads).  hot: a gate bias of 8 on
+    expert 0 routes every token to it, so its 64 tokens take two blocks and
+    its weights are streamed twice."""
+    from dataclasses import replace
+
+    syn = S.generate(S.SMALL["c4_mxfp4"], T=T, seed=80 + T)
+    if hot:
+        gb = syn.gate_b.clone()
+        gb[0] = 8.0
+        syn = replace(syn, gate_b=gb)
+    layer, _, ref, _ = _run_and_check(syn, gpu)
+    assert layer.stage_kernel(T, nat.STAGE_W13) == "k_stage_tok"
+    assert layer.stage_kernel(T, nat.STAGE_W2) == "k_stage_tok"
+    if hot:
+        assert (ref["ids"] == 0).any(axis=1).all()
 
 
 def test_c4_mxfp4_full_shape_wide_range_inputs(gpu, c4_full):
