@@ -2278,16 +2278,17 @@ __host__ __device__ __forceinline__ int tok_rows(int K, int kload) {
 
 // Weight row of lane row n (0..15) of wave `wave` in column tile ct: stage A
 // the 8 gate rows of channels c0 .. c0 + 7 then their 8 up rows, stage B
-// output columns c0 .. c0 + 15; -1 past the projection.
+// output columns c0 .. c0 + 15; -1 past the projection or for ct < 0 (a tile
+// past the workgroup's run, whose prefetch must load nothing).
 template <bool STB>
 __device__ __forceinline__ int tok_row(const LayerArgs& a, int ct, int wave, int n, int& c0) {
   const int H = a.L.hidden, I = a.L.inter;
   if constexpr (STB) {
     c0 = ct * (16 * kTokWaves) + 16 * wave;
-    return c0 + n < H ? c0 + n : -1;
+    return ct >= 0 && c0 + n < H ? c0 + n : -1;
   } else {
     c0 = ct * (8 * kTokWaves) + 8 * wave;
-    return c0 + (n & 7) < I ? (n < 8 ? c0 + n : I + c0 + n - 8) : -1;
+    return ct >= 0 && c0 + (n & 7) < I ? (n < 8 ? c0 + n : I + c0 + n - 8) : -1;
   }
 }
 
@@ -2511,7 +2512,8 @@ __global__ __launch_bounds__(kTokThreads) void k_stage_tok(const LayerArgs a, in
       f32x4 acc0[1] = {(f32x4){0.f, 0.f, 0.f, 0.f}}, acc1[1] = {(f32x4){0.f, 0.f, 0.f, 0.f}};
       const RowGeom<EFMT> Gc[1] = {G[0]};
       // the windows after this tile's last two are the next tile's first two
-      const RowGeom<EFMT> Gn = tok_geom<EFMT, STB>(a, W, ct0 + it + 1, wave, n);
+      // (nothing past the run: those tiles are another workgroup's)
+      const RowGeom<EFMT> Gn = tok_geom<EFMT, STB>(a, W, it + 1 < nti ? ct0 + it + 1 : -1, wave, n);
       int c0;
       const int lrow = tok_row<STB>(a, ct0 + it, wave, n, c0);
       for (int w = 0; w < nwin; w += 2) {
