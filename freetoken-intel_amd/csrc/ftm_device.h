@@ -299,6 +299,14 @@ __device__ __forceinline__ u32x4 bload16(Rsrc r, uint32_t off) {
 __device__ __forceinline__ uint32_t bload4(Rsrc r, uint32_t off) {
   return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
 }
+// XCD-aware order: consecutive workgroups go to different XCDs (round robin),
+// so workgroup b runs item xcd * per + min(xcd, rem) + b / 8, which keeps
+// runs of consecutive items on one XCD's L2 (a bijection on [0, G)).
+__device__ __forceinline__ int xcd_item(int b, int G) {
+  const int xcd = b & 7, per = G >> 3, rem = G & 7;
+  return xcd * per + (xcd < rem ? xcd : rem) + (b >> 3);
+}
+
 // Device-coherent accesses (the SC1 cache-policy bit): the load misses every
 // cache another XCD's writes could leave stale, the store is written through
 // to where every XCD reads it.  Data one workgroup hands to another inside a

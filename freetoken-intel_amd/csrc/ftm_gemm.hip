@@ -335,14 +335,6 @@ __device__ __forceinline__ void wait_ring(int stages) {
   else wait_vm<0>();
 }
 
-// XCD-aware order: consecutive workgroups go to different XCDs (round robin),
-// so workgroup b runs item xcd * per + min(xcd, rem) + b / 8, which keeps
-// runs of consecutive items (the N tiles of one M tile) on one XCD's L2.
-__device__ __forceinline__ int xcd_item(int b, int G) {
-  const int xcd = b & 7, per = G >> 3, rem = G & 7;
-  return xcd * per + (xcd < rem ? xcd : rem) + (b >> 3);
-}
-
 // One 64-token x NWR-row tile over the whole K range (FP8, INT8 or bf16
 // weights).  Wave w owns tile rows 64 j + 16 w .. + 15 (j < NWR / 64: for
 // stage A the gate rows and the matching up rows) for all 64 tokens, so each

@@ -2392,7 +2392,7 @@ __device__ __forceinline__ void tok_consume(const ProjSlot& W, const RowGeom<FMT
 // current tile's last), so the launch is about one workgroup per CU, each
 // streaming without a gap between its tiles.
 template <int EFMT, bool STB>
-__global__ __launch_bounds__(kTokThreads) void k_stage_tok(const LayerArgs a, int ni) {
+__device__ __forceinline__ void stage_tok_body(const LayerArgs& a, int ni) {
   using F = KMajor<EFMT>;
   constexpr int NLW = kTokNLW;
   constexpr int LPG = F::kPostScale ? 2 : NLW;
@@ -2407,8 +2407,10 @@ __global__ __launch_bounds__(kTokThreads) void k_stage_tok(const LayerArgs a, in
   const int K = STB ? I : H;
   const int nct = ((STB ? H : I) + (STB ? 16 : 8) * kTokWaves - 1) / ((STB ? 16 : 8) * kTokWaves);
   const int ngrp = (nct + ni - 1) / ni;
-  const int u = blockIdx.x / ngrp;
-  const int ct0 = (blockIdx.x % ngrp) * ni;
+  // an expert's runs on one XCD: its token rows are fetched into one L2
+  const int b = xcd_item((int)blockIdx.x, (int)gridDim.x);
+  const int u = b / ngrp;
+  const int ct0 = (b % ngrp) * ni;
   const int nti = min(ni, nct - ct0);  // column tiles of this workgroup
   const int nRouted = sload_i32(a.ctrl, kCtrlNRouted);
   if (u >= nRouted) return;
@@ -2556,6 +2558,16 @@ __global__ __launch_bounds__(kTokThreads) void k_stage_tok(const LayerArgs a, in
       }
     }
   }
+}
+
+// Stage A (w13 + activation) and stage B (w2) on the token-resident body.
+template <int EFMT>
+__global__ __launch_bounds__(kTokThreads) void k_stage_tok_a(const LayerArgs a, int ni) {
+  stage_tok_body<EFMT, false>(a, ni);
+}
+template <int EFMT>
+__global__ __launch_bounds__(kTokThreads) void k_stage_tok_b(const LayerArgs a, int ni) {
+  stage_tok_body<EFMT, true>(a, ni);
 }
 
 // GPTQ stage B: the shared expert's items first, 16 output columns each with
@@ -3451,7 +3463,7 @@ static int device_cus() {
   return cus[dev];
 }
 
-// Token-resident stages (k_stage_tok) for both projections: MXFP4 layers with
+// Token-resident stages (k_stage_tok_a / _b) for both projections: MXFP4 layers with
 // bf16 activations and no shared expert, below the GEMM crossover, from
 // kTokMinAvg tokens per routed expert on average (up to kRecMaxT tokens: the
 // kernels read the work records).
@@ -3472,8 +3484,9 @@ static void launch_tok(const LayerArgs& a, int maxU, hipStream_t st) {
   const size_t lds = (size_t)tok_rows(K, kload) * 2u * (size_t)tok_pitch(K, kload);
   static bool attr = false;
   if (!attr) {
-    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&k_stage_tok<FMT, STB>),
-                              hipFuncAttributeMaxDynamicSharedMemorySize, kTokLdsMax);
+    const void* fn = STB ? reinterpret_cast<const void*>(&k_stage_tok_b<FMT>)
+                         : reinterpret_cast<const void*>(&k_stage_tok_a<FMT>);
+    (void)hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, kTokLdsMax);
     attr = true;
   }
   const int cols = STB ? 16 * kTokWaves : 8 * kTokWaves;
@@ -3482,7 +3495,10 @@ static void launch_tok(const LayerArgs& a, int maxU, hipStream_t st) {
   int ni = (maxU * nct + device_cus() - 1) / device_cus();
   ni = ni < kTokMaxTiles ? ni : kTokMaxTiles;
   const int ngrp = (nct + ni - 1) / ni;
-  hipLaunchKernelGGL((k_stage_tok<FMT, STB>), dim3(maxU * ngrp), dim3(kTokThreads), lds, st, a, ni);
+  if constexpr (STB)
+    hipLaunchKernelGGL((k_stage_tok_b<FMT>), dim3(maxU * ngrp), dim3(kTokThreads), lds, st, a, ni);
+  else
+    hipLaunchKernelGGL((k_stage_tok_a<FMT>), dim3(maxU * ngrp), dim3(kTokThreads), lds, st, a, ni);
 }
 
 bool mx_stage_a(const ftm_moe_layer& L, int T) {
@@ -3779,12 +3795,12 @@ static const char* expert_kernel_name(const ftm_moe_layer& L, int T, int stage) 
   if (stage == FTM_STAGE_W13) {
     if (lean) return lean_route_ok(L, T) ? "k_stage_a_lean_route" : "k_stage_a_lean";
     if (FMT == FTM_FMT_GPTQ_INT4) return AT == FTM_DT_BF16 && gq_ok(L, T) ? "k_stage_a_gq" : "k_stage_a";
-    if (AT == FTM_DT_BF16 && tok_ok(L, T)) return "k_stage_tok";
+    if (AT == FTM_DT_BF16 && tok_ok(L, T)) return "k_stage_tok_a";
     return xl_plan_a<FMT, AT>(L, T).ok ? "k_stage_a_xl" : "k_stage_a_rows";
   }
   if (lean) return L.topk + (L.shared_inter > 0 ? 1 : 0) <= kBcMaxKP && T <= kBcMaxT ? "k_stage_bc_lean" : "k_stage_b_lean";
   if (FMT == FTM_FMT_GPTQ_INT4) return AT == FTM_DT_BF16 && gq_b_ok(L, T) ? "k_stage_b_gq" : "k_stage_b";
-  if (AT == FTM_DT_BF16 && tok_ok(L, T)) return "k_stage_tok";
+  if (AT == FTM_DT_BF16 && tok_ok(L, T)) return "k_stage_tok_b";
   if (xl_plan_b<FMT, AT>(L, T).ok) return "k_stage_b_xl";
   return ks_plan_b<FMT, AT>(L, T).ok ? "k_stage_b_ks" : "k_stage_b";
 }

@@ -247,8 +247,8 @@ def test_stage_kernel_names_follow_the_dispatch():
         assert name(mx, T, nat.STAGE_W13) == "k_stage_a_xl", T
         assert name(mx, T, nat.STAGE_W2) == "k_stage_b_ks", T
     for T in (48, 64, 128):  # 6 to 16 tokens per expert: token rows resident in LDS, both stages
-        assert name(mx, T, nat.STAGE_W13) == "k_stage_tok", T
-        assert name(mx, T, nat.STAGE_W2) == "k_stage_tok", T
+        assert name(mx, T, nat.STAGE_W13) == "k_stage_tok_a", T
+        assert name(mx, T, nat.STAGE_W2) == "k_stage_tok_b", T
     # one token: k_stage_a_xl routes it (4 experts x 360 items fit one round of
     # workgroups); two tokens' 2880 items would not, so they keep the top-k
     assert name(mx, 1, nat.STAGE_ROUTER) == "k_router"

@@ -156,7 +156,7 @@ def test_mxfp4_many_experts_lds_path(gpu, T):
 @pytest.mark.parametrize("T,hot", [(24, False), (48, False), (64, False), (64, True)])
 def test_mxfp4_token_resident_stages(gpu, T, hot):
     """MXFP4 at 6 to 16 tokens per routed expert: both projections on
-    k_stage_tok (one block of up to 32 token rows of an expert in LDS per
+    k_stage_tok_a / _b (one block of up to 32 token rows of an expert in LDS per
     workgroup, 8 waves of 16 weight rows each over the whole K, 320 and 192
     not multiples of the 128-wide wave-loads).  hot: a gate bias of 8 on
     expert 0 routes every token to it, so its 64 tokens take two blocks and
@@ -169,8 +169,8 @@ def test_mxfp4_token_resident_stages(gpu, T, hot):
         gb[0] = 8.0
         syn = replace(syn, gate_b=gb)
     layer, _, ref, _ = _run_and_check(syn, gpu)
-    assert layer.stage_kernel(T, nat.STAGE_W13) == "k_stage_tok"
-    assert layer.stage_kernel(T, nat.STAGE_W2) == "k_stage_tok"
+    assert layer.stage_kernel(T, nat.STAGE_W13) == "k_stage_tok_a"
+    assert layer.stage_kernel(T, nat.STAGE_W2) == "k_stage_tok_b"
     if hot:
         assert (ref["ids"] == 0).any(axis=1).all()
 
