@@ -3466,8 +3466,11 @@ static int device_cus() {
 // Token-resident stages (k_stage_tok_a / _b) for both projections: MXFP4 layers with
 // bf16 activations and no shared expert, below the GEMM crossover, from
 // kTokMinAvg tokens per routed expert on average (up to kRecMaxT tokens: the
-// kernels read the work records).
-constexpr int kTokMinAvg = 6;
+// kernels read the work records).  Measured on MI355X (C4, us per layer,
+// against k_stage_a_xl + k_stage_b_ks): 2 tokens per expert (T=16) 113.4
+// against 96.9, 3 (T=24) 113.7 / 109.9, 4 (T=32) 116.9 / 123.2, 5 (T=40)
+// 117.8 / 133.4.
+constexpr int kTokMinAvg = 4;
 static bool tok_ok(const ftm_moe_layer& L, int T) {
   if (L.w13.fmt != FTM_FMT_MXFP4 || L.w2.fmt != FTM_FMT_MXFP4 || L.act_dtype != FTM_DT_BF16) return false;
   if (L.shared_inter > 0 || L.hidden % 8 != 0 || L.inter % 8 != 0 || T > kRecMaxT || gemm_path_ok(L, T)) return false;

@@ -237,16 +237,16 @@ def test_stage_kernel_names_follow_the_dispatch():
     gq.w13.K, gq.w2.N = 2176, 2176
     assert name(gq, 4, nat.STAGE_W13) == "k_stage_a"
     # MXFP4 (C4 shape): stage A on scaled MFMAs with activations in LDS and
-    # stage B with w2's 2880-wide K split over the waves below 6 tokens per
-    # expert, the token-resident stages from 6 up to 16 (T = 128 on 32
+    # stage B with w2's 2880-wide K split over the waves below 4 tokens per
+    # expert, the token-resident stages from 4 up to 16 (T = 128 on 32
     # experts, top-4); the GEMM tiles above
     mx = _layer(E=32, H=2880, I=2880, k=4)
     mx.w13 = _proj(N=2 * 2880, K=2880, num_slots=8, fmt=nat.FMT_MXFP4, group=32)
     mx.w2 = _proj(N=2880, K=2880, num_slots=8, fmt=nat.FMT_MXFP4, group=32)
-    for T in (1, 8, 32, 47):
+    for T in (1, 8, 31):
         assert name(mx, T, nat.STAGE_W13) == "k_stage_a_xl", T
         assert name(mx, T, nat.STAGE_W2) == "k_stage_b_ks", T
-    for T in (48, 64, 128):  # 6 to 16 tokens per expert: token rows resident in LDS, both stages
+    for T in (32, 64, 128):  # 4 to 16 tokens per expert: token rows resident in LDS, both stages
         assert name(mx, T, nat.STAGE_W13) == "k_stage_tok_a", T
         assert name(mx, T, nat.STAGE_W2) == "k_stage_tok_b", T
     # one token: k_stage_a_xl routes it (4 experts x 360 items fit one round of
@@ -258,8 +258,10 @@ def test_stage_kernel_names_follow_the_dispatch():
     assert name(mx, 129, nat.STAGE_W2) == "k_gemm_mx"
     # many experts: the LDS path up to 256 tokens, the register-fed kernels above
     mx.num_experts = 256
-    assert name(mx, 256, nat.STAGE_W13) == "k_stage_a_xl"
-    assert name(mx, 256, nat.STAGE_W2) == "k_stage_b_ks"
+    assert name(mx, 200, nat.STAGE_W13) == "k_stage_a_xl"  # about 3 tokens per expert
+    assert name(mx, 200, nat.STAGE_W2) == "k_stage_b_ks"
+    assert name(mx, 256, nat.STAGE_W13) == "k_stage_tok_a"  # 4 per expert
+    assert name(mx, 256, nat.STAGE_W2) == "k_stage_tok_b"
     assert name(mx, 257, nat.STAGE_W13) == "k_stage_a_rows"
     assert name(mx, 257, nat.STAGE_W2) == "k_stage_b"
     f32 = _layer(E=8, H=256, I=128, k=2, act_dtype=nat.DT_F32)
