@@ -116,39 +116,41 @@ __global__ __launch_bounds__(kBlock) void k_quant_mx(const uint16_t* __restrict_
 constexpr int kRouterTPW = 4;  // tokens per wave
 constexpr int kRouterSteps = 4;  // 512-element chunk steps per load group
 
-// Logits of row r for tokens tb + 4 i (i < kRouterTPW), by one wave (COH:
-// stored device-coherent, for a reader in the same launch).
-template <bool COH = false>
-__device__ __forceinline__ void router_row_tile(const LayerArgs& a, int r, int tb) {
+// Logits of row r for tokens tb + ts i (i < NT), by one wave, NS chunk steps
+// per load group (COH: stored device-coherent, for a reader in the same
+// launch).  NT, ts and NS change which loads are in flight together, not the
+// order of any sum.
+template <bool COH = false, int NT = kRouterTPW, int NS = kRouterSteps>
+__device__ __forceinline__ void router_row_tile(const LayerArgs& a, int r, int tb, int ts = 4) {
   const int E = a.L.num_experts, H = a.L.hidden, T = a.T;
   const void* grow = (r < E) ? (const void*)((const uint16_t*)a.L.gate_w + (size_t)r * H) : a.L.shared_gate;
   const int lane = threadIdx.x & 63;
   const Rsrc gres = make_rsrc(grow, (uint32_t)H * 2u);
   const Rsrc xres = make_rsrc(a.x, (uint32_t)T * (uint32_t)H * 2u);
   const int nsteps = (H + 511) / 512;
-  float acc[kRouterTPW];
+  float acc[NT];
 #pragma unroll
-  for (int i = 0; i < kRouterTPW; ++i) acc[i] = 0.0f;
-  for (int s0 = 0; s0 < nsteps; s0 += kRouterSteps) {
-    u32x4 gv[kRouterSteps], xv[kRouterSteps][kRouterTPW];
+  for (int i = 0; i < NT; ++i) acc[i] = 0.0f;
+  for (int s0 = 0; s0 < nsteps; s0 += NS) {
+    u32x4 gv[NS], xv[NS][NT];
 #pragma unroll
-    for (int q = 0; q < kRouterSteps; ++q) {
+    for (int q = 0; q < NS; ++q) {
       const int c = lane + 64 * (s0 + q);
       const bool ok = (s0 + q < nsteps) && (8 * c < H);
       gv[q] = bload16(gres, ok ? 16u * (uint32_t)c : kOOB);
 #pragma unroll
-      for (int i = 0; i < kRouterTPW; ++i) {
-        const int t = tb + 4 * i;
+      for (int i = 0; i < NT; ++i) {
+        const int t = tb + ts * i;
         xv[q][i] = bload16(xres, (ok && t < T) ? ((uint32_t)t * (uint32_t)H + 8u * (uint32_t)c) * 2u : kOOB);
       }
     }
 #pragma unroll
-    for (int q = 0; q < kRouterSteps; ++q) {
+    for (int q = 0; q < NS; ++q) {
       const int c = lane + 64 * (s0 + q);
       const bool ok = (s0 + q < nsteps) && (8 * c < H);
       const uint32_t gw[4] = {gv[q].x, gv[q].y, gv[q].z, gv[q].w};
 #pragma unroll
-      for (int i = 0; i < kRouterTPW; ++i) {
+      for (int i = 0; i < NT; ++i) {
         const uint32_t xw[4] = {xv[q][i].x, xv[q][i].y, xv[q][i].z, xv[q][i].w};
         float t8 = acc[i];
 #pragma unroll
@@ -161,9 +163,9 @@ __device__ __forceinline__ void router_row_tile(const LayerArgs& a, int r, int t
     }
   }
 #pragma unroll
-  for (int i = 0; i < kRouterTPW; ++i) {
+  for (int i = 0; i < NT; ++i) {
     const float v = wave_sum(acc[i]);
-    const int t = tb + 4 * i;
+    const int t = tb + ts * i;
     if (lane == 0 && t < T) {
       float z = v;
       if (r < E && a.L.gate_b != nullptr) z = v + bf16_to_f32(((const uint16_t*)a.L.gate_b)[r]);
@@ -757,30 +759,36 @@ __global__ __launch_bounds__(64 * kTopk1Waves) void k_topk1(const LayerArgs a, c
 }
 
 // Router and top-k in one launch for T <= kTopk1MaxT: workgroup g computes
-// the logits of rows [4 g, 4 g + 4) for every token, each of its 16 waves
-// one (row, token quad) exactly as a k_router wave does (router_row_tile: all
-// of a step group's loads in flight, the same fp32 order), and the last
-// workgroup to arrive runs k_topk1's body -- one wave per token, per-expert
-// counters in LDS, compaction and work records.  Takes the top-k launch and
-// its ramp out of the chain router -> top-k -> stage A.
-constexpr int kRouteRows = 4;  // router rows per k_route_topk1 workgroup
-template <int MODE, int NV>
-__global__ __launch_bounds__(64 * kTopk1Waves) void k_route_topk1(const LayerArgs a, int row_end, int32_t* ids_out,
-                                                                  float* w_out, float* logits_out) {
+// the logits of rows [rpw g, rpw g + rpw) for every token (route_rpw: about
+// 128 workgroups), wpr = 16 / rpw waves per row; wave w takes row rpw g + w /
+// wpr and tokens w % wpr + wpr i (i < NT) exactly as a k_router wave does
+// (router_row_tile: the loads of every chunk of the gate row and the tokens
+// in flight, the same fp32 order).  The last workgroup to arrive runs
+// k_topk1's body -- one wave per token, per-expert counters in LDS,
+// compaction and work records.  Takes the top-k launch and its ramp out of
+// the chain router -> top-k -> stage A.
+constexpr int kRouteWgs = 136;  // router workgroups aimed at
+__host__ __device__ constexpr int route_rpw(int rows) {
+  return rows <= kRouteWgs ? 1 : rows <= 2 * kRouteWgs ? 2 : 4;
+}
+template <int MODE, int NV, int NT>
+__global__ __launch_bounds__(64 * kTopk1Waves) void k_route_topk1(
+    const LayerArgs a, int row_end, int32_t* ids_out, float* w_out, float* logits_out) {
   __shared__ int32_t s_cnt[kMaxExperts];
   __shared__ int32_t s_first[kMaxExperts * kRecPairs];
   __shared__ int s_wsum[kTopk1Waves];
   __shared__ int s_last;
-  const int wave = threadIdx.x >> 6;
-  static_assert(kRouteRows * 4 == kTopk1Waves && 4 * kRouterTPW >= kTopk1MaxT, "16 waves: 4 rows x 16 tokens");
-  const int nrwg = (row_end + kRouteRows - 1) / kRouteRows;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: scalar gate-row descriptors
+  static_assert(kTopk1Waves == 16 && kTopk1MaxT <= 16, "16 waves: wpr >= 4 waves per row, NT <= 4 tokens each");
+  const int rpw = route_rpw(row_end), wpr = kTopk1Waves / rpw;
+  const int nrwg = (row_end + rpw - 1) / rpw;
   if ((int)blockIdx.x >= nrwg) {  // workgroups past the router's quantise the input (as in k_router)
     quant_mx_piece((const uint16_t*)a.x, a.T, a.L.hidden, a.xq,
                    ((int)blockIdx.x - nrwg) * (64 * kTopk1Waves) + threadIdx.x);
     return;
   }
-  const int r = (int)blockIdx.x * kRouteRows + (wave & 3);
-  if (r < row_end) router_row_tile<true>(a, r, wave >> 2);
+  const int r = (int)blockIdx.x * rpw + wave / wpr, tb = wave % wpr;
+  if (r < row_end && tb < a.T) router_row_tile<true, NT, 4>(a, r, tb, wpr);
   // publish this workgroup's logits (device-coherent stores, acknowledged
   // before the arrival); the last arrival reads every workgroup's
   __builtin_amdgcn_s_waitcnt(0);
@@ -3335,18 +3343,28 @@ hipError_t launch_route_topk(const ftm_moe_layer& L, const void* x, int T, int32
   const LayerArgs a = make_args(L, x, nullptr, T, ws, wl);
   const int rows = L.num_experts + (L.shared_inter > 0 ? 1 : 0);
   const int nq = quant && mx_input(L, T) ? (quant_mx_threads(T, L.hidden) + 64 * kTopk1Waves - 1) / (64 * kTopk1Waves) : 0;
-  const dim3 grid((rows + kRouteRows - 1) / kRouteRows + nq), block(64 * kTopk1Waves);
-#define FTM_RT_NV(M)                                                                                         \
-  if (L.num_experts <= 256)                                                                                  \
-    hipLaunchKernelGGL((k_route_topk1<M, 4>), grid, block, 0, st, a, rows, ids_out, w_out, logits_out);     \
-  else                                                                                                       \
-    hipLaunchKernelGGL((k_route_topk1<M, 8>), grid, block, 0, st, a, rows, ids_out, w_out, logits_out);
+  const int rpw = route_rpw(rows), wpr = kTopk1Waves / rpw, nt = (T + wpr - 1) / wpr;
+  const dim3 grid((rows + rpw - 1) / rpw + nq), block(64 * kTopk1Waves);
+#define FTM_RT_NT(M, NV)                                                                                       \
+  if (nt <= 1)                                                                                                 \
+    hipLaunchKernelGGL((k_route_topk1<M, NV, 1>), grid, block, 0, st, a, rows, ids_out, w_out, logits_out);   \
+  else if (nt <= 2)                                                                                            \
+    hipLaunchKernelGGL((k_route_topk1<M, NV, 2>), grid, block, 0, st, a, rows, ids_out, w_out, logits_out);   \
+  else                                                                                                         \
+    hipLaunchKernelGGL((k_route_topk1<M, NV, 4>), grid, block, 0, st, a, rows, ids_out, w_out, logits_out);
+#define FTM_RT_NV(M)      \
+  if (L.num_experts <= 256) { \
+    FTM_RT_NT(M, 4)       \
+  } else {                \
+    FTM_RT_NT(M, 8)       \
+  }
   switch (L.route_mode) {
     case FTM_ROUTE_SOFTMAX_TOPK: FTM_RT_NV(FTM_ROUTE_SOFTMAX_TOPK) break;
     case FTM_ROUTE_SOFTMAX_TOPK_LOWP: FTM_RT_NV(FTM_ROUTE_SOFTMAX_TOPK_LOWP) break;
     default: FTM_RT_NV(FTM_ROUTE_TOPK_SOFTMAX) break;
   }
 #undef FTM_RT_NV
+#undef FTM_RT_NT
   return hipGetLastError();
 }
 
