@@ -199,7 +199,16 @@ __global__ __launch_bounds__(kBlock) void k_router(const LayerArgs a, int row_be
 // elements each, in order) with one fma chain, and the wave sums the 64
 // partials with the same xor-32..1 butterfly (wave_sum).
 constexpr int kRouterRB = 8;   // expert rows per WG
-constexpr int kRouterMinT = 64;  // from here on k_router_rows (x re-reads dominate k_router)
+constexpr int kRouterMinT = 64;  // from here on k_router_rows (x re-reads dominate k_router) ...
+// ... once k_router's input re-reads (rows x T x H elements, one pass of x per
+// row) pass 40 M elements.  Measured on MI355X, k_router against
+// k_router_rows in us: C4 (32 rows, H 2880) T=64/128/256 5.7/5.8/8.5 against
+// 9.8/9.8/10.0, T=512 13.0 against 11.9; C2 (128 rows) T=64/128 5.2/6.9
+// against 7.4/7.5; C3 (257 rows) T=64 7.5 against 7.9, T=128 11.2 against 9.2.
+constexpr double kRouterRowsMinElems = 40e6;
+__host__ __forceinline__ bool router_by_rows(int rows, int T, int H) {
+  return T >= kRouterMinT && (double)rows * T * H > kRouterRowsMinElems;
+}
 
 // One level of the transposing butterfly: lanes with bit M set keep values
 // [N, 2N), the others [0, N); each adds the partner's copy of what it keeps.
@@ -3324,7 +3333,7 @@ hipError_t launch_router(const ftm_moe_layer& L, const void* x, int T, int row_b
   // quantisation blocks spread over the grid's token-block rows (ceil(nq / ty) columns)
   const int nq = quant && mx_input(L, T) ? (quant_mx_threads(T, L.hidden) + kBlock - 1) / kBlock : 0;
   const int qx = (nq + ty - 1) / ty;
-  if (T >= kRouterMinT)
+  if (router_by_rows(row_end - row_begin, T, L.hidden))
     hipLaunchKernelGGL(k_router_rows, dim3((row_end - row_begin + kRouterRB - 1) / kRouterRB + qx, ty),
                        dim3(kBlock), 0, st, a, row_begin, row_end);
   else
@@ -3836,7 +3845,7 @@ const char* stage_kernel_name(const ftm_moe_layer& L, int T, int stage) {
   switch (stage) {
     case FTM_STAGE_ROUTER:
       if (route_topk_fused(L, T)) return "k_route_topk1";
-      return T >= kRouterMinT ? "k_router_rows" : "k_router";
+      return router_by_rows(L.num_experts + (L.shared_inter > 0 ? 1 : 0), T, L.hidden) ? "k_router_rows" : "k_router";
     case FTM_STAGE_TOPK:
       if (route_a_ok(L, T) || route_topk_fused(L, T)) return "";  // routed inside stage A / the router
       return T <= kTopk1MaxT ? "k_topk1" : T >= kTopkBlkMinT ? "k_topk_blk" : "k_topk";

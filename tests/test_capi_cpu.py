@@ -196,7 +196,9 @@ def test_stage_kernel_names_follow_the_dispatch():
     assert name(c3, 255, nat.STAGE_TOPK) == "k_topk"
     assert name(c3, 256, nat.STAGE_TOPK) == "k_topk_blk"
     assert name(c3, 17, nat.STAGE_ROUTER) == "k_router"
-    assert name(c3, 64, nat.STAGE_ROUTER) == "k_router_rows"
+    # k_router_rows once k_router would re-read x more than 40 M elements (rows x T x H)
+    assert name(c3, 64, nat.STAGE_ROUTER) == "k_router"
+    assert name(c3, 128, nat.STAGE_ROUTER) == "k_router_rows"
     assert name(c3, 17, nat.STAGE_COMBINE) == "k_combine"
     assert name(c3, 16, 5) is None
     assert name(c3, 0, nat.STAGE_W13) is None
@@ -254,6 +256,8 @@ def test_stage_kernel_names_follow_the_dispatch():
     assert name(mx, 1, nat.STAGE_ROUTER) == "k_router"
     assert name(mx, 1, nat.STAGE_TOPK) == ""
     assert name(mx, 2, nat.STAGE_ROUTER) == "k_route_topk1"
+    assert name(mx, 128, nat.STAGE_ROUTER) == "k_router"  # 32 rows: one row per workgroup
+    assert name(mx, 512, nat.STAGE_ROUTER) == "k_router_rows"
     assert name(mx, 129, nat.STAGE_W13) == "k_gemm_mx"  # scaled-MFMA tiles (no shared expert)
     assert name(mx, 129, nat.STAGE_W2) == "k_gemm_mx"
     # many experts: the LDS path up to 256 tokens, the register-fed kernels above
