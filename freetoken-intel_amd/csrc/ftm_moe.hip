@@ -1382,6 +1382,31 @@ __device__ __forceinline__ void gq_pipeline(Rsrc wres, Rsrc sres, Rsrc zres, uin
   }
 }
 
+// Small batches (a workgroup or two per CU): every group of the wave's range
+// [lo, hi), at most NG, issued at once before the token-row copy -- one
+// round trip instead of one per group pair -- then multiplied in order (the
+// same arithmetic as gq_pipeline).
+template <int NG>
+__device__ __forceinline__ void gq_issue_all(Rsrc wres, Rsrc sres, Rsrc zres, uint32_t ncol, int N, uint32_t sbytes,
+                                             int lo, int hi, GqGroup (&G)[NG]) {
+#pragma unroll
+  for (int i = 0; i < NG; ++i) gq_issue(wres, sres, zres, lo + i < hi ? ncol : kOOB, N, lo + i, sbytes, G[i]);
+}
+template <int NG>
+__device__ __forceinline__ void gq_run_all(uint32_t ncol, uint32_t sbytes, int s_dt, int lo, int hi,
+                                           const uint16_t* xrow, const GqGroup (&G)[NG], f32x4 (&acc)[4]) {
+  __builtin_amdgcn_s_waitcnt(0);  // every group and the copy landed
+#pragma unroll
+  for (int i = 0; i < NG; ++i)
+    if (lo + i < hi) gq_group(G[i], xrow, i * 128, ncol, sbytes, s_dt, acc);
+}
+// Measured on MI355X (C2, us): stage A (k_stage_a_gq<4>, one or two
+// tokens) T=1 13.5 -> 12.8, T=2 15.4 -> 14.8; stage B T=1 7.8 -> 7.4, T=2
+// 8.9 either way, T=3 / 4 10.1 / 10.7 -> 10.5 / 11.2 (two workgroups per CU
+// at 188 registers), so stage B issues them all for one token only.
+constexpr int kGqAllNG = 4;   // groups per wave issued at once
+constexpr int kGqBAllMaxT = 1;  // stage B issues them all up to this many tokens
+
 // Item: 64 channels of one expert; waves [0, KS) take the 64 gate columns and
 // waves [KS, 2 KS) the 64 up columns, each over 1 / KS of the K groups (KS = 2:
 // a 256-thread workgroup, rows of up to kGqMaxKR elements per wave; KS = 4: 512
@@ -1444,11 +1469,18 @@ __device__ void stage_a_gq(const LayerArgs& a, const ProjSlot& W, int Iu, int it
 #pragma unroll
     for (int c = 0; c < 4; ++c) acc[c] = (f32x4){0.f, 0.f, 0.f, 0.f};
     if (hi > lo) {
-      GqGroup GA;
-      gq_issue(wres, sres, zres, ncol, N, lo, sbytes, GA);  // weights first,
-      gq_fill(pr, nb, a.x, KP, H, k0, kr, pitch, xw);       // then the token rows
       const uint16_t* xrow = rl < nb ? xw + rl * pitch : zrow;
-      gq_pipeline(wres, sres, zres, ncol, N, sbytes, W.s_dt, lo, hi, xrow, GA, acc);
+      if constexpr (KS == 4) {  // one or two tokens: a wave's <= 4 groups in flight at once
+        GqGroup G[kGqAllNG];
+        gq_issue_all<kGqAllNG>(wres, sres, zres, ncol, N, sbytes, lo, hi, G);
+        gq_fill(pr, nb, a.x, KP, H, k0, kr, pitch, xw);
+        gq_run_all<kGqAllNG>(ncol, sbytes, W.s_dt, lo, hi, xrow, G, acc);
+      } else {
+        GqGroup GA;
+        gq_issue(wres, sres, zres, ncol, N, lo, sbytes, GA);  // weights first,
+        gq_fill(pr, nb, a.x, KP, H, k0, kr, pitch, xw);       // then the token rows
+        gq_pipeline(wres, sres, zres, ncol, N, sbytes, W.s_dt, lo, hi, xrow, GA, acc);
+      }
     }
     __syncthreads();  // red aliases the token rows: every wave is past its MFMAs
 #pragma unroll
@@ -1560,6 +1592,7 @@ constexpr int kGqBRedBytes = 16384;  // its reduction buffer: 4 waves x 4 sub-ti
 // 56.5, so it stops at 32 tokens.
 constexpr int kGqBMaxT = 32;
 
+template <bool ALL>
 __device__ void stage_b_gq(const LayerArgs& a, const ProjSlot& W, int it, int cnt, const int32_t* list,
                            f32x4* red) {
   constexpr int EPI = kGqXT * kGqNB / kBlock;
@@ -1607,11 +1640,18 @@ __device__ void stage_b_gq(const LayerArgs& a, const ProjSlot& W, int it, int cn
 #pragma unroll
     for (int c = 0; c < 4; ++c) acc[c] = (f32x4){0.f, 0.f, 0.f, 0.f};
     if (hi > lo) {
-      GqGroup GA;
-      gq_issue(wres, sres, zres, ncol, N, lo, sbytes, GA);       // weights first,
-      gq_fill(pr, nb, a.hbuf, 1, a.Imax, k0, kr, pitch, xw);     // then the h rows
       const uint16_t* xrow = rl < nb ? xw + rl * pitch : zrow;
-      gq_pipeline(wres, sres, zres, ncol, N, sbytes, W.s_dt, lo, hi, xrow, GA, acc);
+      if constexpr (ALL) {
+        GqGroup G[kGqAllNG];
+        gq_issue_all<kGqAllNG>(wres, sres, zres, ncol, N, sbytes, lo, hi, G);
+        gq_fill(pr, nb, a.hbuf, 1, a.Imax, k0, kr, pitch, xw);
+        gq_run_all<kGqAllNG>(ncol, sbytes, W.s_dt, lo, hi, xrow, G, acc);
+      } else {
+        GqGroup GA;
+        gq_issue(wres, sres, zres, ncol, N, lo, sbytes, GA);       // weights first,
+        gq_fill(pr, nb, a.hbuf, 1, a.Imax, k0, kr, pitch, xw);     // then the h rows
+        gq_pipeline(wres, sres, zres, ncol, N, sbytes, W.s_dt, lo, hi, xrow, GA, acc);
+      }
     }
     __syncthreads();  // red aliases the h rows: every wave is past its MFMAs
 #pragma unroll
@@ -2614,6 +2654,7 @@ static bool gq_b_ok(const ftm_moe_layer& L, int T) {
   return (L.inter / 128 + 1) / 2 * 128 <= kGqMaxKR;
 }
 
+template <bool ALL>
 __global__ __launch_bounds__(kBlock) void k_stage_b_gq(const LayerArgs a) {
   // routed items: the reduction buffer (16 KiB) aliases the h-row regions;
   // the shared expert's K-split items keep a small one of their own (their
@@ -2647,7 +2688,7 @@ __global__ __launch_bounds__(kBlock) void k_stage_b_gq(const LayerArgs a) {
     if (threadIdx.x == 0) atomicOr(&a.ctrl[kCtrlError], 1);
     return;
   }
-  stage_b_gq(a, proj_slot(a.L.w2, slot), it, cnt, list, (f32x4*)ftm_xl_lds);
+  stage_b_gq<ALL>(a, proj_slot(a.L.w2, slot), it, cnt, list, (f32x4*)ftm_xl_lds);
 }
 
 // Stage B item body: NT x 64 output columns of one expert; in each 64-column
@@ -3693,7 +3734,12 @@ static void launch_stages(const LayerArgs& a, int gridA, int gridB, hipStream_t 
         const size_t lds_s = a.L.shared_inter > 0 ? 4u * kXR * (size_t)xl_pitch(a.Imax, 4) * 2u : 0u;
         const int maxU = a.L.num_experts < a.T * a.L.topk ? a.L.num_experts : a.T * a.L.topk;
         const int grid = gq_b_sh_items(a.L, a.T) + maxU * (a.L.hidden / kGqNB);
-        hipLaunchKernelGGL(k_stage_b_gq, dim3(grid), dim3(kBlock), lds_r > lds_s ? lds_r : lds_s, st, a);
+        // a wave's half of the K groups issued at once for a few tokens (a
+        // workgroup or two per CU), two groups in flight above
+        if (a.T <= kGqBAllMaxT && ((a.L.inter + 127) / 128 + 1) / 2 <= kGqAllNG)
+          hipLaunchKernelGGL(k_stage_b_gq<true>, dim3(grid), dim3(kBlock), lds_r > lds_s ? lds_r : lds_s, st, a);
+        else
+          hipLaunchKernelGGL(k_stage_b_gq<false>, dim3(grid), dim3(kBlock), lds_r > lds_s ? lds_r : lds_s, st, a);
       } else {
         hipLaunchKernelGGL((k_stage_b<FMT, AT>), dim3(gridB), dim3(kBlock), 0, st, a);
       }
