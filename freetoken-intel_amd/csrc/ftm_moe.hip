@@ -184,13 +184,28 @@ __device__ __forceinline__ void router_quant_block(const LayerArgs& a, int qb) {
   quant_mx_piece((const uint16_t*)a.x, a.T, a.L.hidden, a.xq, qb * kBlock + threadIdx.x);
 }
 
+// NT = 1: wave w takes token 4 blockIdx.y + w alone, with every chunk step of
+// the row in one load group (a 2880-wide row is 6 steps: one round trip
+// instead of two), while the grid stays within kRouterOneMaxWgs workgroups.
+// Measured on MI355X against four tokens per wave (us): C4 (32 rows) T=1 /
+// 17 / 32 / 64 / 128 2.9 / 3.3 / 3.3 / 3.7 / 4.9 against 4.8 / 5.8 / 5.9 / 5.9 /
+// 6.0; C2 (128 rows) T=1 2.8 against 3.7, T=17 3.8 against 4.4, T=32 4.5 both,
+// T=64 6.6 against 5.5; C3 (257 rows) T=1 2.8 against 4.0, T=17 5.2 against
+// 5.5, T=32 7.3 against 6.0.
+constexpr int kRouterOneMaxWgs = 1300;
+template <int NT>
 __global__ __launch_bounds__(kBlock) void k_router(const LayerArgs a, int row_begin, int rows) {
-  const int wave = threadIdx.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   if ((int)blockIdx.x >= rows) {
     router_quant_block(a, ((int)blockIdx.x - rows) * (int)gridDim.y + (int)blockIdx.y);
     return;
   }
-  router_row_tile(a, row_begin + blockIdx.x, blockIdx.y * 4 * kRouterTPW + wave);
+  if constexpr (NT == 1) {
+    const int t = 4 * (int)blockIdx.y + wave;
+    if (t < a.T) router_row_tile<false, 1, 8>(a, row_begin + blockIdx.x, t);
+  } else {
+    router_row_tile(a, row_begin + blockIdx.x, blockIdx.y * 4 * kRouterTPW + wave);
+  }
 }
 
 // Large T: one WG per (8 expert rows, 16 tokens), so x is read once per 8
@@ -3369,7 +3384,8 @@ hipError_t launch_router(const ftm_moe_layer& L, const void* x, int T, int row_b
                          const WsLayout& wl, hipStream_t st, bool quant) {
   const LayerArgs a = make_args(L, x, nullptr, T, ws, wl);
   if (row_end - row_begin <= 0 || T <= 0) return hipSuccess;
-  const int tpb = 4 * kRouterTPW;
+  const bool one = (row_end - row_begin) * ((T + 3) / 4) <= kRouterOneMaxWgs;  // k_router<1>: 4 tokens per workgroup
+  const int tpb = one ? 4 : 4 * kRouterTPW;
   const int ty = (T + tpb - 1) / tpb;
   // quantisation blocks spread over the grid's token-block rows (ceil(nq / ty) columns)
   const int nq = quant && mx_input(L, T) ? (quant_mx_threads(T, L.hidden) + kBlock - 1) / kBlock : 0;
@@ -3377,8 +3393,11 @@ hipError_t launch_router(const ftm_moe_layer& L, const void* x, int T, int row_b
   if (router_by_rows(row_end - row_begin, T, L.hidden))
     hipLaunchKernelGGL(k_router_rows, dim3((row_end - row_begin + kRouterRB - 1) / kRouterRB + qx, ty),
                        dim3(kBlock), 0, st, a, row_begin, row_end);
+  else if (one)
+    hipLaunchKernelGGL(k_router<1>, dim3(row_end - row_begin + qx, ty), dim3(kBlock), 0, st, a, row_begin,
+                       row_end - row_begin);
   else
-    hipLaunchKernelGGL(k_router, dim3(row_end - row_begin + qx, ty), dim3(kBlock), 0, st, a, row_begin,
+    hipLaunchKernelGGL(k_router<kRouterTPW>, dim3(row_end - row_begin + qx, ty), dim3(kBlock), 0, st, a, row_begin,
                        row_end - row_begin);
   return hipGetLastError();
 }
