@@ -602,6 +602,50 @@ def test_c3_shape_route_modes(gpu, mode, T):
     _run_and_check(syn, gpu)
 
 
+# ---------------------------------------------------------------- router layouts
+@pytest.mark.parametrize("E,shared,H,T", [
+    (136, False, 2880, 16),  # k_route_topk1: one row per workgroup, rows in two load groups (6 chunk steps)
+    (137, False, 320, 13),   # two rows per workgroup, the last one alone; a partial chunk step
+    (272, True, 256, 9),     # 273 rows: four per workgroup, the shared-gate row in the last
+    (40, False, 2880, 3),    # one row per workgroup, three of its waves busy
+    (64, True, 2880, 1),     # one token
+    (64, False, 1152, 20),   # k_router, one token per wave over five token blocks
+    (300, True, 640, 40),    # k_router, four tokens per wave (301 x 10 blocks > 1300)
+])
+def test_router_layouts_bit_exact(gpu, E, shared, H, T):
+    """Every layout the router kernels pick (rows per workgroup, tokens per
+    wave, chunk steps per load group) keeps the fp32 summation order the
+    oracle replays: logits, ids and weights bit-exact against it."""
+    from ftmoe.banks import Proj
+    from ftmoe.layer import MoeLayer
+
+    I, k = 16, 4
+    rng = np.random.RandomState(E + T)
+    gate = O.f32_to_bf16_bits((rng.randn(E, H) * 0.05).astype(np.float32))
+    x = O.f32_to_bf16_bits(rng.randn(T, H).astype(np.float32))
+    shd = None
+    if shared:  # the shared-gate row rides in the router launch (rows = E + 1)
+        sgate = O.f32_to_bf16_bits((rng.randn(1, H) * 0.05).astype(np.float32))
+        shd = {"w13": torch.zeros(2 * I, H, dtype=torch.bfloat16, device=gpu),
+               "w2": torch.zeros(H, I, dtype=torch.bfloat16, device=gpu),
+               "gate": torch.from_numpy(sgate.view(np.int16)).view(torch.bfloat16).to(gpu)}
+    w13 = Proj("bf16", torch.zeros(E, 2 * I, H, dtype=torch.bfloat16, device=gpu), 2 * I, H)
+    w2 = Proj("bf16", torch.zeros(E, H, I, dtype=torch.bfloat16, device=gpu), H, I)
+    g = torch.from_numpy(gate.view(np.int16)).view(torch.bfloat16).to(gpu)
+    layer = MoeLayer(w13=w13, w2=w2, num_experts=E, hidden=H, inter=I, topk=k, gate_w=g, shared=shd,
+                     act_dtype=torch.bfloat16)
+    xd = torch.from_numpy(x.view(np.int16)).view(torch.bfloat16).to(gpu)
+    out, ids, w, logits = layer.forward(xd, return_routing=True)
+    torch.cuda.synchronize()
+    ref_logits = O.router_logits(x, gate)
+    rid, rw = O.route(ref_logits, k, "softmax_topk", True)
+    kern = layer.stage_kernel(T, nat.STAGE_ROUTER)
+    np.testing.assert_array_equal(to_f32(logits), ref_logits, err_msg=f"router logits ({kern})")
+    np.testing.assert_array_equal(ids.cpu().numpy(), rid, err_msg=f"routing indices ({kern})")
+    np.testing.assert_array_equal(w.cpu().numpy(), rw, err_msg=f"router weights ({kern})")
+    assert torch.count_nonzero(out) == 0  # zero banks: only the routing is under test
+
+
 # ---------------------------------------------------------------- LOWP routing on adversarial logits
 def _route_only_layer(gpu, E, k, renorm, mode="softmax_topk_lowp"):
     from ftmoe.banks import Proj
