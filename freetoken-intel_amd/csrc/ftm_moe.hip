@@ -409,6 +409,20 @@ __device__ __forceinline__ uint32_t wave_max_u32(uint32_t x) {
   return max(max(r0, r1), max(r2, r3));
 }
 
+// Wave max of a u32 in every lane without a scalar round trip: DPP within
+// rows, then the gfx950 row swaps (v_permlane16_swap: rows 0 <-> 1, 2 <-> 3;
+// v_permlane32_swap: halves) -- eight VALU instructions.
+__device__ __forceinline__ uint32_t wave_max_u32_v(uint32_t x) {
+  x = max(x, (uint32_t)dpp_i<kDppXor1>((int)x));
+  x = max(x, (uint32_t)dpp_i<kDppXor2>((int)x));
+  x = max(x, (uint32_t)dpp_i<kDppHalfMirror>((int)x));
+  x = max(x, (uint32_t)dpp_i<kDppMirror>((int)x));
+  const auto r16 = __builtin_amdgcn_permlane16_swap(x, x, false, false);
+  x = max((uint32_t)r16[0], (uint32_t)r16[1]);
+  const auto r32 = __builtin_amdgcn_permlane32_swap(x, x, false, false);
+  return max((uint32_t)r32[0], (uint32_t)r32[1]);
+}
+
 __device__ __forceinline__ void cas_desc(uint64_t& a, uint64_t& b) {
   const uint64_t hi = umax64(a, b), lo = a > b ? b : a;
   a = hi;
@@ -574,15 +588,24 @@ __device__ __forceinline__ void route_token_pre(const LayerArgs& a, int t, const
 #pragma unroll
     for (int i = 0; i < NV; ++i) lst[i] = (lane + 64 * i < E) ? pack_key32(key[i], lane + 64 * i) : 0u;
     sort_desc32<NV>(lst);
-    uint32_t mine = 0u, first = 0u;
+    // k rounds: the wave max of the lanes' heads is the next key (in every
+    // lane), the lane holding it pops its head
+    uint32_t mine = 0u;
+    const uint32_t first = wave_max_u32_v(lst[0]);
     for (int j = 0; j < k; ++j) {
-      const uint32_t best = wave_max_u32(lst[0]);
-      first = j == 0 ? best : first;
+      const uint32_t best = j == 0 ? first : wave_max_u32_v(lst[0]);
       mine = lane == j ? best : mine;
-      const bool pop = lst[0] == best;
+      // the lane holding the key pops its head: one select per candidate,
+      // written out so the shift stays NV v_cndmask (left to itself the
+      // compiler tracks the rotation with index compares, ~2x the VALU); the
+      // s_nop gives the VALU-written mask the two wait states the compiler
+      // puts between a v_cmp and its v_cndmask on this target
+      const uint64_t pop = __ballot(lst[0] == best);
+      asm volatile("s_nop 1\n\tv_cndmask_b32_e64 %0, %0, %1, %2" : "+v"(lst[0]) : "v"(lst[1]), "s"(pop));
 #pragma unroll
-      for (int i = 0; i + 1 < NV; ++i) lst[i] = pop ? lst[i + 1] : lst[i];
-      lst[NV - 1] = pop ? 0u : lst[NV - 1];
+      for (int i = 1; i + 1 < NV; ++i)
+        asm volatile("v_cndmask_b32_e64 %0, %0, %1, %2" : "+v"(lst[i]) : "v"(lst[i + 1]), "s"(pop));
+      asm volatile("v_cndmask_b32_e64 %0, %0, 0, %1" : "+v"(lst[NV - 1]) : "s"(pop));
     }
     top0 = key32_value(first);
     if (lane < k) {
