@@ -270,6 +270,27 @@ __device__ __forceinline__ u32x4 gptq_word_to_bf16(uint32_t w) {
   r.w = ((w >> 12) & 0x000f000fu) | 0x43004300u;
   return r;
 }
+// The same with the mask and the 128.0 pattern in VGPRs (gq_decode_consts):
+// each value is one v_and_or_b32 (after a shift) instead of an AND and an OR
+// with literal operands -- a VOP3 on this target takes no literal.  7 VALU
+// per word instead of 11.
+struct GqConsts {
+  uint32_t m, c;
+};
+__device__ __forceinline__ GqConsts gq_decode_consts() {
+  GqConsts k;
+  asm("v_mov_b32 %0, 0xf000f" : "=v"(k.m));
+  asm("v_mov_b32 %0, 0x43004300" : "=v"(k.c));
+  return k;
+}
+__device__ __forceinline__ u32x4 gptq_word_to_bf16(uint32_t w, GqConsts k) {
+  u32x4 r;
+  r.x = (w & k.m) | k.c;
+  r.y = ((w >> 4) & k.m) | k.c;
+  r.z = ((w >> 8) & k.m) | k.c;
+  r.w = ((w >> 12) & k.m) | k.c;
+  return r;
+}
 
 // Reorder 8 bf16 activations x0..x7 to [x0,x4,x1,x5,x2,x6,x3,x7] (the GPTQ
 // element order above).
@@ -1070,7 +1091,7 @@ __device__ __forceinline__ void wave_gemm_gptq(const ProjSlot& W, const int (&co
           const uint32_t wv[4] = {raw[r][b].x, raw[r][b].y, raw[r][b].z, raw[r][b].w};
 #pragma unroll
           for (int c = 0; c < 4; ++c) {
-            const u32x4 bq = gptq_word_to_bf16(wv[c]);
+            const u32x4 bq = gptq_word_to_bf16(wv[c], gq_decode_consts());
             tmp[r][c] = mfma_bf16(ahi[b], bq, tmp[r][c]);
             if constexpr (SPLIT) tmp[r][c] = mfma_bf16(alo[b], bq, tmp[r][c]);
           }

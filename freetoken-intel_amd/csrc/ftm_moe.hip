@@ -1339,6 +1339,7 @@ __device__ __forceinline__ void gq_group(const GqGroup& G, const uint16_t* xrow,
                                          uint32_t sbytes, int s_dt, f32x4 (&acc)[4]) {
   const int lane = threadIdx.x & 63, g = lane >> 4;
   const u32x4 ones = (u32x4){0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u};  // bf16 1.0
+  const GqConsts kc = gq_decode_consts();
   f32x4 tmp[4];
 #pragma unroll
   for (int c = 0; c < 4; ++c) tmp[c] = (f32x4){0.f, 0.f, 0.f, 0.f};
@@ -1349,7 +1350,7 @@ __device__ __forceinline__ void gq_group(const GqGroup& G, const uint16_t* xrow,
     sxr = mfma_bf16(av, ones, sxr);
     const uint32_t wv[4] = {G.raw[b].x, G.raw[b].y, G.raw[b].z, G.raw[b].w};
 #pragma unroll
-    for (int c = 0; c < 4; ++c) tmp[c] = mfma_bf16(av, gptq_word_to_bf16(wv[c]), tmp[c]);
+    for (int c = 0; c < 4; ++c) tmp[c] = mfma_bf16(av, gptq_word_to_bf16(wv[c], kc), tmp[c]);
   }
   const uint32_t sw[4] = {G.scv.x, G.scv.y, G.scv.z, G.scv.w};
 #pragma unroll
@@ -1561,8 +1562,13 @@ static int gq_ks(const ftm_moe_layer& L, int T) {
 }
 static bool gq_ok(const ftm_moe_layer& L, int T) { return gq_ks(L, T) != 0; }
 
+// KS = 2: three 4-wave workgroups' worth of waves per SIMD (amdgpu_waves_per_eu
+// 3: 147 VGPRs and no accumulators parked in AGPRs, against 156 + 20 and two
+// waves per SIMD left to the compiler): C2 w13 T=16 / 32 35.7 / 60.2 ->
+// 35.4 / 60.0 us, w2 (the same for k_stage_b_gq) 21.1 / 30.1 -> 20.8 / 29.5.
 template <int KS>
-__global__ __launch_bounds__(GqA<KS>::kThreads) void k_stage_a_gq(const LayerArgs a) {
+__global__ __launch_bounds__(GqA<KS>::kThreads) __attribute__((amdgpu_waves_per_eu(KS == 2 ? 3 : 1))) void k_stage_a_gq(
+    const LayerArgs a) {
   constexpr int NT = 64;
   // The reduction buffer (16 KiB routed, 32 KiB for the shared-expert body)
   // aliases the dynamic token-row regions (41 KiB), so a workgroup holds 41
@@ -2693,7 +2699,7 @@ static bool gq_b_ok(const ftm_moe_layer& L, int T) {
 }
 
 template <bool ALL>
-__global__ __launch_bounds__(kBlock) void k_stage_b_gq(const LayerArgs a) {
+__global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(ALL ? 1 : 3))) void k_stage_b_gq(const LayerArgs a) {
   // routed items: the reduction buffer (16 KiB) aliases the h-row regions;
   // the shared expert's K-split items keep a small one of their own (their
   // waves' regions are in use while other waves reduce)
