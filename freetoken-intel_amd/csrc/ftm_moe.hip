@@ -1311,22 +1311,34 @@ __device__ __forceinline__ void gq_zero_row(uint16_t* zrow, int kr) {
   for (int e = 8 * lane; e < kr; e += 8 * 64) *(u32x4*)(zrow + e) = (u32x4){0u, 0u, 0u, 0u};
 }
 
-struct GqGroup {
-  u32x4 raw[4];  // 4 wave-loads of 32 K: lane (g, rl) holds k8 row 4 b + g, columns ncol .. ncol + 3
-  u32x4 scv;
+// NCOL columns per lane: 4 (a wave covers 64 columns, 16-byte loads) or 2
+// (32 columns, 8-byte loads: twice the items for one or two tokens).
+template <int NCOL>
+struct GqGroupT {
+  typedef uint32_t V __attribute__((ext_vector_type(NCOL)));
+  V raw[4];  // 4 wave-loads of 32 K: lane (g, rl) holds k8 row 4 b + g, columns ncol .. ncol + NCOL - 1
+  V scv;     // the columns' scales (fp32: NCOL words; fp16 / bf16: NCOL halves in the first words)
   uint32_t zw;
 };
+typedef GqGroupT<4> GqGroup;
 
+template <int NCOL>
+__device__ __forceinline__ typename GqGroupT<NCOL>::V gq_bload(Rsrc r, uint32_t off) {
+  if constexpr (NCOL == 4) return bload16(r, off);
+  else return __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0);
+}
+
+template <int NCOL = 4>
 __device__ __forceinline__ void gq_issue(Rsrc wres, Rsrc sres, Rsrc zres, uint32_t ncol, int N, int grp,
-                                         uint32_t sbytes, GqGroup& G) {
+                                         uint32_t sbytes, GqGroupT<NCOL>& G) {
   const int g = (threadIdx.x & 63) >> 4;
   const bool ok = ncol != kOOB;
 #pragma unroll
   for (int b = 0; b < 4; ++b) {
     const uint32_t prow = (uint32_t)(grp * 16 + 4 * b + g);
-    G.raw[b] = bload16(wres, ok ? (prow * (uint32_t)N + ncol) * 4u : kOOB);
+    G.raw[b] = gq_bload<NCOL>(wres, ok ? (prow * (uint32_t)N + ncol) * 4u : kOOB);
   }
-  G.scv = bload16(sres, ok ? ((uint32_t)grp * (uint32_t)N + ncol) * sbytes : kOOB);
+  G.scv = gq_bload<NCOL>(sres, ok ? ((uint32_t)grp * (uint32_t)N + ncol) * sbytes : kOOB);
   G.zw = bload4(zres, ok ? ((uint32_t)grp * (uint32_t)(N / 8) + ncol / 8) * 4u : kOOB);
 }
 constexpr int kGqLoads = 6;  // vector loads per gq_issue
@@ -1335,26 +1347,28 @@ constexpr int kGqLoads = 6;  // vector loads per gq_issue
 // The token rows' sums over the group come from one more MFMA per wave-load
 // against a tile of ones, already in the output layout (lane (g, j) holds
 // rows 4 g .. 4 g + 3), instead of VALU sums and cross-lane shuffles.
-__device__ __forceinline__ void gq_group(const GqGroup& G, const uint16_t* xrow, int kofs, uint32_t ncol,
-                                         uint32_t sbytes, int s_dt, f32x4 (&acc)[4]) {
+template <int NCOL = 4>
+__device__ __forceinline__ void gq_group(const GqGroupT<NCOL>& G, const uint16_t* xrow, int kofs, uint32_t ncol,
+                                         uint32_t sbytes, int s_dt, f32x4 (&acc)[NCOL]) {
   const int lane = threadIdx.x & 63, g = lane >> 4;
   const u32x4 ones = (u32x4){0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u};  // bf16 1.0
   const GqConsts kc = gq_decode_consts();
-  f32x4 tmp[4];
+  f32x4 tmp[NCOL];
 #pragma unroll
-  for (int c = 0; c < 4; ++c) tmp[c] = (f32x4){0.f, 0.f, 0.f, 0.f};
+  for (int c = 0; c < NCOL; ++c) tmp[c] = (f32x4){0.f, 0.f, 0.f, 0.f};
   f32x4 sxr = (f32x4){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int b = 0; b < 4; ++b) {
     const u32x4 av = perm_gptq(*(const u32x4*)(xrow + kofs + 32 * b + 8 * g));
     sxr = mfma_bf16(av, ones, sxr);
-    const uint32_t wv[4] = {G.raw[b].x, G.raw[b].y, G.raw[b].z, G.raw[b].w};
 #pragma unroll
-    for (int c = 0; c < 4; ++c) tmp[c] = mfma_bf16(av, gptq_word_to_bf16(wv[c], kc), tmp[c]);
+    for (int c = 0; c < NCOL; ++c) tmp[c] = mfma_bf16(av, gptq_word_to_bf16(G.raw[b][c], kc), tmp[c]);
   }
-  const uint32_t sw[4] = {G.scv.x, G.scv.y, G.scv.z, G.scv.w};
+  uint32_t sw[NCOL];
 #pragma unroll
-  for (int c = 0; c < 4; ++c) {
+  for (int c = 0; c < NCOL; ++c) sw[c] = G.scv[c];
+#pragma unroll
+  for (int c = 0; c < NCOL; ++c) {
     float sc;
     if (sbytes == 4u) {
       sc = __uint_as_float(sw[c]);
@@ -1425,24 +1439,26 @@ __device__ __forceinline__ void gq_pipeline(Rsrc wres, Rsrc sres, Rsrc zres, uin
 // [lo, hi), at most NG, issued at once before the token-row copy -- one
 // round trip instead of one per group pair -- then multiplied in order (the
 // same arithmetic as gq_pipeline).
-template <int NG>
+template <int NG, int NCOL>
 __device__ __forceinline__ void gq_issue_all(Rsrc wres, Rsrc sres, Rsrc zres, uint32_t ncol, int N, uint32_t sbytes,
-                                             int lo, int hi, GqGroup (&G)[NG]) {
+                                             int lo, int hi, GqGroupT<NCOL> (&G)[NG]) {
 #pragma unroll
-  for (int i = 0; i < NG; ++i) gq_issue(wres, sres, zres, lo + i < hi ? ncol : kOOB, N, lo + i, sbytes, G[i]);
+  for (int i = 0; i < NG; ++i) gq_issue<NCOL>(wres, sres, zres, lo + i < hi ? ncol : kOOB, N, lo + i, sbytes, G[i]);
 }
-template <int NG>
+template <int NG, int NCOL>
 __device__ __forceinline__ void gq_run_all(uint32_t ncol, uint32_t sbytes, int s_dt, int lo, int hi,
-                                           const uint16_t* xrow, const GqGroup (&G)[NG], f32x4 (&acc)[4]) {
+                                           const uint16_t* xrow, const GqGroupT<NCOL> (&G)[NG],
+                                           f32x4 (&acc)[NCOL]) {
   __builtin_amdgcn_s_waitcnt(0);  // every group and the copy landed
 #pragma unroll
   for (int i = 0; i < NG; ++i)
-    if (lo + i < hi) gq_group(G[i], xrow, i * 128, ncol, sbytes, s_dt, acc);
+    if (lo + i < hi) gq_group<NCOL>(G[i], xrow, i * 128, ncol, sbytes, s_dt, acc);
 }
 // Measured on MI355X (C2, us): stage A (k_stage_a_gq<4>, one or two
 // tokens) T=1 13.5 -> 12.8, T=2 15.4 -> 14.8; stage B T=1 7.8 -> 7.4, T=2
 // 8.9 either way, T=3 / 4 10.1 / 10.7 -> 10.5 / 11.2 (two workgroups per CU
-// at 188 registers), so stage B issues them all for one token only.
+// at 188 registers), so stage B issues them all for one token only, on
+// items of 64 columns (6.9 -> 6.3 against 128: twice the workgroups).
 constexpr int kGqAllNG = 4;   // groups per wave issued at once
 constexpr int kGqBAllMaxT = 1;  // stage B issues them all up to this many tokens
 
@@ -1451,6 +1467,11 @@ constexpr int kGqBAllMaxT = 1;  // stage B issues them all up to this many token
 // a 256-thread workgroup, rows of up to kGqMaxKR elements per wave; KS = 4: 512
 // threads, half the rows per wave, twice the waves -- and bytes in flight --
 // per CU at the same LDS).
+// Channels per stage-A item: 32 for one token (twice the items, so twice
+// the CUs stream the eight experts: C2 w13 T=1 11.9 -> 10.9 us; at T=2 the
+// 64-channel items are 0.2 us faster), else 64.
+__host__ __device__ constexpr int gq_nt(int ks, int T) { return ks == 4 && T == 1 ? 32 : 64; }
+
 template <int KS>
 struct GqA {
   static constexpr int kThreads = 2 * KS * 64;
@@ -1466,6 +1487,8 @@ template <int NT, int KS>
 __device__ void stage_a_gq(const LayerArgs& a, const ProjSlot& W, int Iu, int it, int cnt, const ExpertRec* rec,
                            const int32_t* list, f32x4* red) {
   constexpr int EPI = 16 * NT / GqA<KS>::kThreads;
+  constexpr int NCOL = NT / 16;  // columns per lane
+  static_assert(NCOL == 4 || (NCOL == 2 && KS == 4), "64-column tiles, or 32 with every group issued at once");
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int rl = lane & 15;
   const int H = a.L.hidden, KP = a.KP, N = W.N;
@@ -1479,7 +1502,7 @@ __device__ void stage_a_gq(const LayerArgs& a, const ProjSlot& W, int Iu, int it
   const Rsrc zres = make_rsrc(W.z, (uint32_t)ngroups * (uint32_t)(N / 8) * 4u);
   const Rsrc sres = make_rsrc(W.s, (uint32_t)ngroups * (uint32_t)N * sbytes);
   const int col0 = (tile == 0 ? 0 : Iu) + it * NT;
-  const uint32_t ncol = col0 + 4 * rl < N ? (uint32_t)(col0 + 4 * rl) : kOOB;
+  const uint32_t ncol = col0 + NCOL * rl < N ? (uint32_t)(col0 + NCOL * rl) : kOOB;
   const Rsrc lres = make_rsrc(list, (uint32_t)cnt * 4u);
   const int kr_max = gq_wave_kr(W.K, KS);
   const int pitch = gq_pitch(kr_max);
@@ -1504,16 +1527,16 @@ __device__ void stage_a_gq(const LayerArgs& a, const ProjSlot& W, int Iu, int it
       const int i = (threadIdx.x + q * GqA<KS>::kThreads) / NT;
       pe[q] = i < kGqXT ? pair_rec_or_list(rec, lres, mb + i, cnt, KP) : -1;
     }
-    f32x4 acc[4];
+    f32x4 acc[NCOL];
 #pragma unroll
-    for (int c = 0; c < 4; ++c) acc[c] = (f32x4){0.f, 0.f, 0.f, 0.f};
+    for (int c = 0; c < NCOL; ++c) acc[c] = (f32x4){0.f, 0.f, 0.f, 0.f};
     if (hi > lo) {
       const uint16_t* xrow = rl < nb ? xw + rl * pitch : zrow;
       if constexpr (KS == 4) {  // one or two tokens: a wave's <= 4 groups in flight at once
-        GqGroup G[kGqAllNG];
-        gq_issue_all<kGqAllNG>(wres, sres, zres, ncol, N, sbytes, lo, hi, G);
+        GqGroupT<NCOL> G[kGqAllNG];
+        gq_issue_all<kGqAllNG, NCOL>(wres, sres, zres, ncol, N, sbytes, lo, hi, G);
         gq_fill(pr, nb, a.x, KP, H, k0, kr, pitch, xw);
-        gq_run_all<kGqAllNG>(ncol, sbytes, W.s_dt, lo, hi, xrow, G, acc);
+        gq_run_all<kGqAllNG, NCOL>(ncol, sbytes, W.s_dt, lo, hi, xrow, G, acc);
       } else {
         GqGroup GA;
         gq_issue(wres, sres, zres, ncol, N, lo, sbytes, GA);  // weights first,
@@ -1523,19 +1546,19 @@ __device__ void stage_a_gq(const LayerArgs& a, const ProjSlot& W, int Iu, int it
     }
     __syncthreads();  // red aliases the token rows: every wave is past its MFMAs
 #pragma unroll
-    for (int c = 0; c < 4; ++c) red[(wave * 4 + c) * 64 + lane] = acc[c];
+    for (int c = 0; c < NCOL; ++c) red[(wave * NCOL + c) * 64 + lane] = acc[c];
     __syncthreads();
 #pragma unroll
     for (int q = 0; q < EPI; ++q) {
       const int idx = threadIdx.x + q * GqA<KS>::kThreads;
       const int i = idx / NT, j = idx % NT;
-      const int c = j & 3, jj = j >> 2;
+      const int c = j % NCOL, jj = j / NCOL;
       const int ln = jj + 16 * (i >> 2), rr = i & 3;
       float g4 = 0.0f, u4 = 0.0f;
 #pragma unroll
       for (int p = 0; p < KS; ++p) {
-        g4 += red[(p * 4 + c) * 64 + ln][rr];
-        u4 += red[((KS + p) * 4 + c) * 64 + ln][rr];
+        g4 += red[(p * NCOL + c) * 64 + ln][rr];
+        u4 += red[((KS + p) * NCOL + c) * 64 + ln][rr];
       }
       const float gs = W.bias != nullptr ? g4 + bias_g[q] : g4;
       const float us = W.bias != nullptr ? u4 + bias_u[q] : u4;
@@ -1566,10 +1589,9 @@ static bool gq_ok(const ftm_moe_layer& L, int T) { return gq_ks(L, T) != 0; }
 // 3: 147 VGPRs and no accumulators parked in AGPRs, against 156 + 20 and two
 // waves per SIMD left to the compiler): C2 w13 T=16 / 32 35.7 / 60.2 ->
 // 35.4 / 60.0 us, w2 (the same for k_stage_b_gq) 21.1 / 30.1 -> 20.8 / 29.5.
-template <int KS>
+template <int KS, int NT>
 __global__ __launch_bounds__(GqA<KS>::kThreads) __attribute__((amdgpu_waves_per_eu(KS == 2 ? 3 : 1))) void k_stage_a_gq(
     const LayerArgs a) {
-  constexpr int NT = 64;
   // The reduction buffer (16 KiB routed, 32 KiB for the shared-expert body)
   // aliases the dynamic token-row regions (41 KiB), so a workgroup holds 41
   // KiB of LDS and three fit a CU.
@@ -1630,16 +1652,19 @@ __global__ __launch_bounds__(GqA<KS>::kThreads) __attribute__((amdgpu_waves_per_
 // summed through LDS, router-weighted, and written to the slot buffer rows
 // (k_combine sums them).
 constexpr int kGqNB = 128;  // output columns per stage-B item
+constexpr int kGqNB1 = 64;  // ... for one token (every group issued at once)
 constexpr int kGqBRedBytes = 16384;  // its reduction buffer: 4 waves x 4 sub-tiles x 64 lanes x 16 B
 // Measured on C2 (w2, against the register-fed k_stage_b): T=4 18.6 -> 11.6
 // us, T=16 39.5 -> 29.3, T=24 46.3 -> 36.0, T=32 49.6 -> 41.0; T=64 55.3 ->
 // 56.5, so it stops at 32 tokens.
 constexpr int kGqBMaxT = 32;
 
-template <bool ALL>
+template <bool ALL, int NB>
 __device__ void stage_b_gq(const LayerArgs& a, const ProjSlot& W, int it, int cnt, const int32_t* list,
                            f32x4* red) {
-  constexpr int EPI = kGqXT * kGqNB / kBlock;
+  constexpr int EPI = kGqXT * NB / kBlock;
+  constexpr int NCOL = NB / 32;  // columns per lane: two column halves of NB / 2
+  static_assert(NCOL == 4 || (NCOL == 2 && ALL), "128-column items, or 64 with every group issued at once");
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int rl = lane & 15;
   const int H = a.L.hidden, KP = a.KP, N = W.N;
@@ -1652,8 +1677,8 @@ __device__ void stage_b_gq(const LayerArgs& a, const ProjSlot& W, int it, int cn
   const Rsrc wres = make_rsrc(W.w, (uint32_t)(W.K / 8) * (uint32_t)N * 4u);
   const Rsrc zres = make_rsrc(W.z, (uint32_t)ngroups * (uint32_t)(N / 8) * 4u);
   const Rsrc sres = make_rsrc(W.s, (uint32_t)ngroups * (uint32_t)N * sbytes);
-  const int col0 = it * kGqNB + 64 * tile;
-  const uint32_t ncol = col0 + 4 * rl < N ? (uint32_t)(col0 + 4 * rl) : kOOB;
+  const int col0 = it * NB + (NB / 2) * tile;
+  const uint32_t ncol = col0 + NCOL * rl < N ? (uint32_t)(col0 + NCOL * rl) : kOOB;
   const Rsrc lres = make_rsrc(list, (uint32_t)cnt * 4u);
   const Rsrc wtres = make_rsrc(a.wts, (uint32_t)a.T * (uint32_t)KP * 4u);
   const int kr_max = gq_wave_kr(W.K, 2);
@@ -1664,7 +1689,7 @@ __device__ void stage_b_gq(const LayerArgs& a, const ProjSlot& W, int it, int cn
   float bias_n[EPI];
 #pragma unroll
   for (int q = 0; q < EPI; ++q) {
-    const int n = it * kGqNB + (threadIdx.x + q * kBlock) % kGqNB;
+    const int n = it * NB + (threadIdx.x + q * kBlock) % NB;
     bias_n[q] = (W.bias != nullptr && n < H) ? load_scalar(W.bias, n, W.bias_dt) : 0.0f;
   }
   for (int mb = 0; mb < cnt; mb += kGqXT) {
@@ -1676,20 +1701,20 @@ __device__ void stage_b_gq(const LayerArgs& a, const ProjSlot& W, int it, int cn
     float we[EPI];
 #pragma unroll
     for (int q = 0; q < EPI; ++q) {
-      const int i = (threadIdx.x + q * kBlock) / kGqNB;
+      const int i = (threadIdx.x + q * kBlock) / NB;
       pe[q] = pair_of_row(lres, true, mb + i, cnt, KP, 0);
       we[q] = __uint_as_float(bload4(wtres, pe[q] >= 0 ? 4u * (uint32_t)pe[q] : kOOB));
     }
-    f32x4 acc[4];
+    f32x4 acc[NCOL];
 #pragma unroll
-    for (int c = 0; c < 4; ++c) acc[c] = (f32x4){0.f, 0.f, 0.f, 0.f};
+    for (int c = 0; c < NCOL; ++c) acc[c] = (f32x4){0.f, 0.f, 0.f, 0.f};
     if (hi > lo) {
       const uint16_t* xrow = rl < nb ? xw + rl * pitch : zrow;
       if constexpr (ALL) {
-        GqGroup G[kGqAllNG];
-        gq_issue_all<kGqAllNG>(wres, sres, zres, ncol, N, sbytes, lo, hi, G);
+        GqGroupT<NCOL> G[kGqAllNG];
+        gq_issue_all<kGqAllNG, NCOL>(wres, sres, zres, ncol, N, sbytes, lo, hi, G);
         gq_fill(pr, nb, a.hbuf, 1, a.Imax, k0, kr, pitch, xw);
-        gq_run_all<kGqAllNG>(ncol, sbytes, W.s_dt, lo, hi, xrow, G, acc);
+        gq_run_all<kGqAllNG, NCOL>(ncol, sbytes, W.s_dt, lo, hi, xrow, G, acc);
       } else {
         GqGroup GA;
         gq_issue(wres, sres, zres, ncol, N, lo, sbytes, GA);       // weights first,
@@ -1699,16 +1724,16 @@ __device__ void stage_b_gq(const LayerArgs& a, const ProjSlot& W, int it, int cn
     }
     __syncthreads();  // red aliases the h rows: every wave is past its MFMAs
 #pragma unroll
-    for (int c = 0; c < 4; ++c) red[(wave * 4 + c) * 64 + lane] = acc[c];
+    for (int c = 0; c < NCOL; ++c) red[(wave * NCOL + c) * 64 + lane] = acc[c];
     __syncthreads();
 #pragma unroll
     for (int q = 0; q < EPI; ++q) {
       const int idx = threadIdx.x + q * kBlock;
-      const int i = idx / kGqNB, j = idx % kGqNB;
-      const int t = j >> 6, jl = j & 63;
-      const int c = jl & 3, ln = (jl >> 2) + 16 * (i >> 2), rr = i & 3;
-      const int n = it * kGqNB + j;
-      float y = red[((2 * t) * 4 + c) * 64 + ln][rr] + red[((2 * t + 1) * 4 + c) * 64 + ln][rr];
+      const int i = idx / NB, j = idx % NB;
+      const int t = j / (NB / 2), jl = j % (NB / 2);
+      const int c = jl % NCOL, ln = jl / NCOL + 16 * (i >> 2), rr = i & 3;
+      const int n = it * NB + j;
+      float y = red[((2 * t) * NCOL + c) * 64 + ln][rr] + red[((2 * t + 1) * NCOL + c) * 64 + ln][rr];
       if (pe[q] >= 0 && n < H) {
         if (W.bias != nullptr) y += bias_n[q];
         a.ybuf[(size_t)pe[q] * H + n] = y * we[q];
@@ -2698,14 +2723,14 @@ static bool gq_b_ok(const ftm_moe_layer& L, int T) {
   return (L.inter / 128 + 1) / 2 * 128 <= kGqMaxKR;
 }
 
-template <bool ALL>
+template <bool ALL, int NB>
 __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(ALL ? 1 : 3))) void k_stage_b_gq(const LayerArgs a) {
   // routed items: the reduction buffer (16 KiB) aliases the h-row regions;
   // the shared expert's K-split items keep a small one of their own (their
   // waves' regions are in use while other waves reduce)
   __shared__ f32x4 red_s[4 * 16];
   const int H = a.L.hidden;
-  const int tilesR = H / kGqNB;
+  const int tilesR = H / NB;
   const int nSh = gq_b_sh_items(a.L, a.T);
   const int item = (int)blockIdx.x;
   if (item < nSh) {
@@ -2725,14 +2750,14 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(ALL ? 1 
   const int slot = a.L.slot_of_expert ? sload_i32(a.L.slot_of_expert, e) : e;
   if (slot < 0 || slot >= a.L.w2.num_slots) {
     // non-resident expert: contribute zeros, flag the error
-    for (int idx = threadIdx.x; idx < cnt * kGqNB; idx += kBlock) {
-      const int m = idx / kGqNB, n = it * kGqNB + idx % kGqNB;
+    for (int idx = threadIdx.x; idx < cnt * NB; idx += kBlock) {
+      const int m = idx / NB, n = it * NB + idx % NB;
       a.ybuf[(size_t)list[m] * H + n] = 0.0f;
     }
     if (threadIdx.x == 0) atomicOr(&a.ctrl[kCtrlError], 1);
     return;
   }
-  stage_b_gq<ALL>(a, proj_slot(a.L.w2, slot), it, cnt, list, (f32x4*)ftm_xl_lds);
+  stage_b_gq<ALL, NB>(a, proj_slot(a.L.w2, slot), it, cnt, list, (f32x4*)ftm_xl_lds);
 }
 
 // Stage B item body: NT x 64 output columns of one expert; in each 64-column
@@ -3716,10 +3741,12 @@ static void launch_stages(const LayerArgs& a, int gridA, int gridB, hipStream_t 
   if (which & 1) {
     if constexpr (FMT == FTM_FMT_GPTQ_INT4) {
       if (const int ks = gq_ks(a.L, a.T); ks != 0 && AT == FTM_DT_BF16) {
-        if (ks == 4)
-          hipLaunchKernelGGL(k_stage_a_gq<4>, dim3(gridA), dim3(GqA<4>::kThreads), GqA<4>::lds(a.L.hidden), st, a);
+        if (ks == 4 && gq_nt(ks, a.T) == 32)
+          hipLaunchKernelGGL((k_stage_a_gq<4, 32>), dim3(gridA), dim3(GqA<4>::kThreads), GqA<4>::lds(a.L.hidden), st, a);
+        else if (ks == 4)
+          hipLaunchKernelGGL((k_stage_a_gq<4, 64>), dim3(gridA), dim3(GqA<4>::kThreads), GqA<4>::lds(a.L.hidden), st, a);
         else
-          hipLaunchKernelGGL(k_stage_a_gq<2>, dim3(gridA), dim3(GqA<2>::kThreads), GqA<2>::lds(a.L.hidden), st, a);
+          hipLaunchKernelGGL((k_stage_a_gq<2, 64>), dim3(gridA), dim3(GqA<2>::kThreads), GqA<2>::lds(a.L.hidden), st, a);
       } else {
         hipLaunchKernelGGL((k_stage_a<FMT, AT>), dim3(gridA), dim3(kBlock), 0, st, a);
       }
@@ -3781,13 +3808,17 @@ static void launch_stages(const LayerArgs& a, int gridA, int gridB, hipStream_t 
         const size_t lds_r = gq_lds_bytes(4, a.L.inter, 2, kGqBRedBytes);
         const size_t lds_s = a.L.shared_inter > 0 ? 4u * kXR * (size_t)xl_pitch(a.Imax, 4) * 2u : 0u;
         const int maxU = a.L.num_experts < a.T * a.L.topk ? a.L.num_experts : a.T * a.L.topk;
-        const int grid = gq_b_sh_items(a.L, a.T) + maxU * (a.L.hidden / kGqNB);
+        const size_t lds = lds_r > lds_s ? lds_r : lds_s;
         // a wave's half of the K groups issued at once for a few tokens (a
-        // workgroup or two per CU), two groups in flight above
-        if (a.T <= kGqBAllMaxT && ((a.L.inter + 127) / 128 + 1) / 2 <= kGqAllNG)
-          hipLaunchKernelGGL(k_stage_b_gq<true>, dim3(grid), dim3(kBlock), lds_r > lds_s ? lds_r : lds_s, st, a);
-        else
-          hipLaunchKernelGGL(k_stage_b_gq<false>, dim3(grid), dim3(kBlock), lds_r > lds_s ? lds_r : lds_s, st, a);
+        // workgroup or two per CU), two groups in flight above; one token
+        // takes 64-column items (twice the CUs stream the eight experts)
+        if (a.T <= kGqBAllMaxT && ((a.L.inter + 127) / 128 + 1) / 2 <= kGqAllNG) {
+          const int grid = gq_b_sh_items(a.L, a.T) + maxU * (a.L.hidden / kGqNB1);
+          hipLaunchKernelGGL((k_stage_b_gq<true, kGqNB1>), dim3(grid), dim3(kBlock), lds, st, a);
+        } else {
+          const int grid = gq_b_sh_items(a.L, a.T) + maxU * (a.L.hidden / kGqNB);
+          hipLaunchKernelGGL((k_stage_b_gq<false, kGqNB>), dim3(grid), dim3(kBlock), lds, st, a);
+        }
       } else {
         hipLaunchKernelGGL((k_stage_b<FMT, AT>), dim3(gridB), dim3(kBlock), 0, st, a);
       }
@@ -3848,7 +3879,7 @@ bool route_a_ok(const ftm_moe_layer& L, int T) {
   switch (L.w13.fmt) {
     case FTM_FMT_GPTQ_INT4:
       if (!gq_ok(L, T)) return false;
-      items = maxU * (L.inter / 64) + (L.shared_inter > 0 ? L.shared_inter / 16 : 0);
+      items = maxU * (L.inter / gq_nt(gq_ks(L, T), T)) + (L.shared_inter > 0 ? L.shared_inter / 16 : 0);
       break;
     case FTM_FMT_BF16:
       if (!xl_plan_a<FTM_FMT_BF16, FTM_DT_BF16>(L, T).ok) return false;
@@ -3889,7 +3920,7 @@ hipError_t launch_experts(const ftm_moe_layer& L, const void* x, int T, void* ou
     a.logits_out = ro->logits;
   }
   const int maxU = L.num_experts < T * L.topk ? L.num_experts : T * L.topk;
-  const int NT = L.w13.fmt == FTM_FMT_GPTQ_INT4 ? 64 : 16;
+  const int NT = L.w13.fmt == FTM_FMT_GPTQ_INT4 ? gq_nt(gq_ks(L, T), T) : 16;
   const int has_sh = L.shared_inter > 0 ? 1 : 0;
   const int gridA = maxU * (L.inter / NT) + (has_sh ? L.shared_inter / 16 : 0);
   const int gridB = (maxU + has_sh) * (L.hidden / 64);
