@@ -2188,13 +2188,13 @@ __device__ void stage_a_xl_body(const LayerArgs& a, const ProjSlot& W, int Iu, i
 // compiler's choice.  Measured on MI355X (C4 MXFP4 T=32, k_stage_a_xl with
 // scaled-MFMA rows): 72.2 us against 76.8 at the compiler's 116 registers
 // (4 waves) and 92.2 at 6 waves (spills).
-template <int FMT, int NLW, bool SH>
-constexpr int kXlWaves = (FMT == FTM_FMT_MXFP4 && NLW <= 6 && !SH) ? 5 : 1;
+template <int FMT, int NLW, bool SH, int NT = 1>
+constexpr int kXlWaves = (FMT == FTM_FMT_MXFP4 && NLW <= 6 && !SH) ? (NT == 1 ? 5 : 3) : 1;
 
 // NT x 8 channels per workgroup: routed items first, then the shared expert's
 // (SH = false: a layer without one, and no bf16 body in the kernel).
 template <int FMT, int NT, int LPG, int NLWM = kRowsNLW, bool SH = true>
-__global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(kXlWaves<FMT, NLWM, SH>))) void k_stage_a_xl(
+__global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(kXlWaves<FMT, NLWM, SH, NT>))) void k_stage_a_xl(
     const LayerArgs a) {
   __shared__ f32x4 red[NT * 4 * 16];
   __shared__ RouteA sra;
@@ -3572,6 +3572,18 @@ static int xl_lpg(const ftm_proj& P, int split) {
   return two ? 2 : one ? kRowsNLW : 0;
 }
 
+// Compute units of the current device (cached per device).
+static int device_cus() {
+  static int cus[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cus[dev] == 0) {
+    int v = 0;
+    cus[dev] = hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0 ? v : 256;
+  }
+  return cus[dev];
+}
+
 template <int FMT, int AT>
 static XlPlan xl_plan_a(const ftm_moe_layer& L, int T) {
   XlPlan p{false, 1, kRowsNLW};
@@ -3586,22 +3598,20 @@ static XlPlan xl_plan_a(const ftm_moe_layer& L, int T) {
     if (FMT == FTM_FMT_MXFP4 && 4 * kXT * mx_pitch((L.hidden + 127) / 128, 4) > kDynLdsMax) return p;
     p.lpg = xl_lpg<FMT>(L.w13, 4);
     if (p.lpg == 0) return p;
+    // MXFP4 without a shared expert: 16-channel items (5 workgroups per CU at
+    // 8 channels, 3 at 16: kXlWaves) where the 8-channel grid would need a
+    // second round of workgroups and the 16-channel one fits one.  Measured on
+    // MI355X (C4, w13 us): T = 1 (1,440 / 720 workgroups) 13.5 -> 11.9; T = 2
+    // (two rounds either way) 15.8 -> 20.9.
     p.nt = 1;
+    if (FMT == FTM_FMT_MXFP4 && L.shared_inter == 0 && L.inter % 16 == 0) {
+      const int maxU = L.num_experts < T * L.topk ? L.num_experts : T * L.topk;
+      const int items = maxU * (L.inter / 8), cus = device_cus();
+      if (items > 5 * cus && items / 2 <= 3 * cus) p.nt = 2;
+    }
     p.ok = true;
     return p;
   }
-}
-
-// Compute units of the current device (cached per device).
-static int device_cus() {
-  static int cus[64] = {0};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (cus[dev] == 0) {
-    int v = 0;
-    cus[dev] = hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0 ? v : 256;
-  }
-  return cus[dev];
 }
 
 // Token-resident stages (k_stage_tok_a / _b) for both projections: MXFP4 layers with
@@ -3777,6 +3787,8 @@ static void launch_stages(const LayerArgs& a, int gridA, int gridB, hipStream_t 
 #define FTM_XLM(NLW)                                                                                          \
   if (a.L.shared_inter > 0)                                                                                   \
     hipLaunchKernelGGL((k_stage_a_xl<FMT, 1, kRowsNLW, NLW, true>), dim3(itemsx), dim3(kBlock), lds, st, a); \
+  else if (nt == 2)                                                                                           \
+    hipLaunchKernelGGL((k_stage_a_xl<FMT, 2, kRowsNLW, NLW, false>), dim3(itemsx), dim3(kBlock), lds, st, a); \
   else                                                                                                        \
     hipLaunchKernelGGL((k_stage_a_xl<FMT, 1, kRowsNLW, NLW, false>), dim3(itemsx), dim3(kBlock), lds, st, a)
         if constexpr (FMT == FTM_FMT_MXFP4) {
@@ -3875,7 +3887,7 @@ bool route_a_ok(const ftm_moe_layer& L, int T) {
     return false;
   if (L.num_experts > 256 || L.topk > kLeanRouteMaxK || lean_ok(L, T) || gemm_path_ok(L, T)) return false;
   const int maxU = L.num_experts < T * L.topk ? L.num_experts : T * L.topk;
-  int items;
+  int items, nt = 1;
   switch (L.w13.fmt) {
     case FTM_FMT_GPTQ_INT4:
       if (!gq_ok(L, T)) return false;
@@ -3893,14 +3905,17 @@ bool route_a_ok(const ftm_moe_layer& L, int T) {
       if (!xl_plan_a<FTM_FMT_INT8_PACKED, FTM_DT_BF16>(L, T).ok) return false;
       items = 0;
       break;
-    case FTM_FMT_MXFP4:
-      if (!xl_plan_a<FTM_FMT_MXFP4, FTM_DT_BF16>(L, T).ok) return false;
+    case FTM_FMT_MXFP4: {
+      const XlPlan p = xl_plan_a<FTM_FMT_MXFP4, FTM_DT_BF16>(L, T);
+      if (!p.ok) return false;
+      nt = p.nt;
       items = 0;
       break;
+    }
     default: return false;
   }
-  if (L.w13.fmt != FTM_FMT_GPTQ_INT4)
-    items = maxU * (L.inter / 8) + (L.shared_inter > 0 ? L.shared_inter / 8 : 0);  // k_stage_a_xl, NT = 1
+  if (L.w13.fmt != FTM_FMT_GPTQ_INT4)  // k_stage_a_xl, NT x 8 channels an item
+    items = maxU * (L.inter / (8 * nt)) + (L.shared_inter > 0 ? L.shared_inter / (8 * nt) : 0);
   return items <= kRouteAMaxItems;
 }
 

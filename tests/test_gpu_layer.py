@@ -118,8 +118,8 @@ def c4_full(gpu):
 def test_c4_mxfp4_full_shape_matches_oracle(gpu, c4_full, T):
     """MXFP4 at the C4 shape (H = I = 2880, 32 experts, top-4 on biased logits,
     clamped SwiGLU with biases): stage A on scaled MFMAs with activations in
-    LDS and stage B with K split over the waves up to 16 tokens per expert
-    (T = 128)."""
+    LDS (16-channel items at T = 1, 8-channel above) and stage B with K split
+    over the waves up to 16 tokens per expert (T = 128)."""
     from dataclasses import replace
 
     _run_and_check(replace(c4_full, x=c4_full.x[:T].contiguous()), gpu)
