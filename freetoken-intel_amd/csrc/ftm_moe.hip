@@ -3274,7 +3274,11 @@ __global__ __launch_bounds__(kBlock) void k_stage_b_lean(const LayerArgs a) {
 // unit against split by token block: T=8 17.2 -> 15.8 us, T=16 25.5 -> 24.0.
 // Neither a software pipeline over a wave's experts (8 waves, 198 VGPRs: the
 // compiler's vmcnt tracking across the loop still serialises the loads; 18.3
-// and 28.9 us) nor 16 waves (128 VGPRs; 18.6 and 28.1 us) was faster.
+// and 28.9 us) nor 16 waves (128 VGPRs; 18.6 and 28.1 us) was faster, nor two
+// routed experts per wave in the 16 MFMA rows (8 weight rows each, twice the
+// bytes in flight for the same registers): a pair took 3.8 us where one unit
+// takes 2.0 (s_memrealtime per unit, T=16), so the CU's memory pipeline, not
+// a wave's latency, bounds the loop (stage B + combine T=16 23.3 -> 24.3 us).
 constexpr int kBcWaves = 12;  // 768 threads: 170 VGPRs per lane (16 waves spill at 128)
 constexpr int kBcCols = 8;    // output columns per workgroup: H / 8 workgroups fill the CUs
 // Measured on MI355X (C3), stage B + combine: T=5 12.7 us against 12.2 + 4.8,
@@ -3288,25 +3292,27 @@ __global__ __launch_bounds__(64 * kBcWaves) void k_stage_bc_lean(const LayerArgs
   const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int H = a.L.hidden, T = a.T, KP = a.KP;
   const int col0 = blockIdx.x * kBcCols;
-  // slots of pairs without an expert stay zero (as their slot-buffer rows would be)
-  for (int i = threadIdx.x; i < T * KP * 16; i += 64 * kBcWaves) s_y[i] = 0.0f;
-  __syncthreads();
-  const int nRouted = sload_i32(a.ctrl, kCtrlNRouted);
   const int nSh = a.L.shared_inter > 0 ? (T + kLeanXT - 1) / kLeanXT : 0;
-  const int nU = nSh + nRouted;
   // Each routed unit's record is loaded one unit ahead, one word a lane
   // (lanes 0..kRecWords-1, a vector load the current unit's full wait
   // covers), so a unit's weight loads issue without waiting for its record
   // (a scalar prefetch was waited for at the loop head: its registers are
-  // recycled).  C3 stage B + combine: T=16 23.5 -> 22.6-23.4 us, T=4-8 within
-  // 0.3 us.
-  const Rsrc rres = make_rsrc(a.recs, (uint32_t)nRouted * (uint32_t)(4 * kRecWords));
+  // recycled); the first one is requested beside the routed count (any of
+  // the E + 1 records: the loop reads it only for a routed unit).  C3 stage
+  // B + combine, us: T=16 23.5 -> 22.9, T=8 14.5 -> 13.9, T=1 5.5 -> 5.4.
   const int rl = threadIdx.x & 63;
+  const Rsrc rall = make_rsrc(a.recs, (uint32_t)(a.L.num_experts + 1) * (uint32_t)(4 * kRecWords));
+  uint32_t nrec = bload4(rall, wv >= nSh && rl < kRecWords ? (uint32_t)((wv - nSh) * kRecWords + rl) * 4u : kOOB);
+  const int nRouted = sload_i32(a.ctrl, kCtrlNRouted);
+  // slots of pairs without an expert stay zero (as their slot-buffer rows would be)
+  for (int i = threadIdx.x; i < T * KP * 16; i += 64 * kBcWaves) s_y[i] = 0.0f;
+  __syncthreads();
+  const int nU = nSh + nRouted;
+  const Rsrc rres = make_rsrc(a.recs, (uint32_t)nRouted * (uint32_t)(4 * kRecWords));
   auto rec_load = [&](int uu) {
     const int u = uu - nSh;
     return bload4(rres, uu < nU && u >= 0 && rl < kRecWords ? (uint32_t)(u * kRecWords + rl) * 4u : kOOB);
   };
-  uint32_t nrec = rec_load(wv);
   for (int uu = wv; uu < nU; uu += kBcWaves) {
     ExpertRec rec;
     rec.e = __builtin_amdgcn_readlane((int)nrec, 0);
