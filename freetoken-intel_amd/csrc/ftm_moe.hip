@@ -680,7 +680,8 @@ __device__ __forceinline__ void zero_skipped_slots(const LayerArgs& a, int t, bo
 // the expert's list (cnt: per-expert counters, in LDS or global memory;
 // s_first: null, or an LDS copy of each list's first kRecPairs entries).
 __device__ __forceinline__ void emit_token(const LayerArgs& a, int t, int sel_e, float sel_w, int32_t* ids_out,
-                                           float* w_out, int32_t* cnt, int32_t* s_first = nullptr) {
+                                           float* w_out, int32_t* cnt, int32_t* s_first = nullptr,
+                                           const float* sh_logit = nullptr) {
   const int E = a.L.num_experts, k = a.L.topk, T = a.T, KP = a.KP;
   const int lane = threadIdx.x & 63;
   bool listed = false;
@@ -711,7 +712,8 @@ __device__ __forceinline__ void emit_token(const LayerArgs& a, int t, int sel_e,
   // every slot no stage writes is zeroed (k_combine sums all of a token's slots)
   zero_skipped_slots(a, t, lane < k && !listed);
   if (lane == 0 && a.L.shared_inter > 0) {
-    const float sl = load_dev(&a.logits[(size_t)t * (E + 1) + E]);  // k_route_topk1: another workgroup's logit
+    // k_route_topk1: another workgroup's logit (sh_logit: loaded with the routing logits)
+    const float sl = sh_logit != nullptr ? *sh_logit : load_dev(&a.logits[(size_t)t * (E + 1) + E]);
     a.wts[t * KP + k] = round_to(ftm_sigmoidf(sl), a.L.act_dtype);
   }
 }
@@ -849,8 +851,10 @@ __global__ __launch_bounds__(64 * kTopk1Waves) void k_route_topk1(
   for (int t = wave; t < T; t += kTopk1Waves) {
     int sel_e;
     float sel_w;
+    // the shared-gate logit requested before the routing logits (one round trip for both)
+    const float shl = a.L.shared_inter > 0 ? load_dev(&a.logits[(size_t)t * (E + 1) + E]) : 0.0f;
     route_token<MODE, NV, true>(a, t, nullptr, 0, nullptr, nullptr, logits_out, sel_e, sel_w);
-    emit_token(a, t, sel_e, sel_w, ids_out, w_out, s_cnt, s_first);
+    emit_token(a, t, sel_e, sel_w, ids_out, w_out, s_cnt, s_first, &shl);
   }
   __syncthreads();
   compact_experts<kTopk1Waves>(a, s_cnt, false, s_wsum, s_first);
