@@ -2260,9 +2260,13 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(kXlWaves
 // leave CUs idle and whose rows are too long for one window per wave.
 // NLW: wave-loads per prefetch window; NOZ: regions of kXT rows without the
 // zero row (rows_consume_lds), their tails past K cleared once here.
-template <int EFMT, int LPG, int NLW = kRowsNLW, bool NOZ = false>
+// PART: one token block (cnt <= kXT) and no reduction here -- lanes 0..15 store
+// this wave's accumulator at red[kp * 16 + lane] and the caller sums the K
+// quarters (k_stage_bc_ks); rg: the wave's LDS region (-1: kp).
+template <int EFMT, int LPG, int NLW = kRowsNLW, bool NOZ = false, bool PART = false>
 __device__ void stage_b_ks_body(const LayerArgs& a, const ProjSlot& W, int c0, int cnt, const ExpertRec* rec,
-                                const int32_t* list, int shared_col, int kp, f32x4* red, int mb0 = 0) {
+                                const int32_t* list, int shared_col, int kp, f32x4* red, int mb0 = 0,
+                                int rg = -1) {
   using F = KMajor<EFMT>;
   constexpr int KS = 4;
   const int lane = threadIdx.x & 63;
@@ -2276,8 +2280,9 @@ __device__ void stage_b_ks_body(const LayerArgs& a, const ProjSlot& W, int c0, i
   G[0] = RowGeom<EFMT>(W, c0 + n, W.group > 0 ? c0 / W.group : 0, W.group > 0 ? (c0 + 8) / W.group : 0);
   rows_issue<EFMT, NLW, true>(W, G[0], L_lo, L_hi, S[0]);
   const int pitch = xl_pitch(a.Imax, KS);
-  uint16_t* xw = ftm_xl_lds + kp * (NOZ ? kXT : kXR) * pitch;
+  uint16_t* xw = ftm_xl_lds + (rg < 0 ? kp : rg) * (NOZ ? kXT : kXR) * pitch;
   const int k0 = L_lo * F::kLoadK, k1 = min(L_hi * F::kLoadK, W.K);
+  if constexpr (PART) cnt = min(cnt, mb0 + kXT);
   if constexpr (NOZ) {
     // elements [k1, L_hi * kLoadK) of each row (the last wave's only): read by
     // lanes past K, never filled
@@ -2305,6 +2310,7 @@ __device__ void stage_b_ks_body(const LayerArgs& a, const ProjSlot& W, int c0, i
     }
     // MFMA rows 0..kXT-1 (the block's tokens) live in lanes 0..15, lane n = column c0 + n
     if (lane < 16) red[kp * 16 + lane] = acc[0];
+    if constexpr (PART) continue;
     __syncthreads();
     if (kp == 0 && lane < 16) {
       f32x4 v = red[n];
@@ -2357,6 +2363,92 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(kXlWaves
     if (Is <= 0 || sitem >= tn) return;
     const ProjSlot W = shared_view(a.L.shared_w2, H, Is);
     stage_b_ks_body<FTM_FMT_BF16, kRowsNLW>(a, W, sitem * 16, a.T, nullptr, nullptr, a.L.topk, kp, red);
+  }
+}
+
+// ---- K-split stage B and the combine in one launch for up to kXT tokens (no
+// shared expert): one workgroup of kBcKsWaves waves per 16 output columns
+// takes every routed expert.  Wave w streams K quarter w % 4 of the experts
+// w / 4, w / 4 + 4, ... (stage_b_ks_body, PART); the quarters are summed in
+// order with the bias and the router weight as k_stage_b_ks does, into the
+// pair's slot row in LDS, and the workgroup sums each token's slots in slot
+// order (k_combine's order and rounding) into the output.  Saves the combine
+// launch and the slot buffer's round trip: at one token the two launches are
+// each a ramp and a few dependent round trips over a few MB.  Up to two
+// routed experts per wave: measured on MI355X (C4, stage B + combine, us per
+// layer): T=1 (4 experts) 26.4 -> 24.4, T=2 (8) 36.9 -> 35.9-36.5, T=4 (16,
+// four a wave, one after another) 50.3 -> 50.9-51.2.
+constexpr int kBcKsWaves = 16;
+constexpr int kBcKsMaxU = 8;    // routed experts (two per wave group of four)
+constexpr int kBcKsMaxKP = 64;  // top-k (no shared expert)
+template <int FMT, int LPG, int NLW>
+__global__ __launch_bounds__(64 * kBcKsWaves) void k_stage_bc_ks(const LayerArgs a) {
+  constexpr bool NOZ = kKsNoz<FMT>;
+  __shared__ f32x4 red[kBcKsMaxU * 4 * 16];
+  __shared__ float s_y[kXT * kBcKsMaxKP * 16];
+  __shared__ uint32_t s_bias[kBcKsMaxU * 16];
+  __shared__ float s_wr[kBcKsMaxU * kXT];
+  __shared__ int s_pr[kBcKsMaxU * kXT];
+  __shared__ int s_cnt[kBcKsMaxU];
+  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int kp = wv & 3, ug = wv >> 2;
+  const int lane = threadIdx.x & 63;
+  const int H = a.L.hidden, T = a.T, KP = a.KP;
+  const int c0 = blockIdx.x * 16;
+  const int nRouted = sload_i32(a.ctrl, kCtrlNRouted);
+  // slots of pairs without an expert stay zero (as their slot-buffer rows would be)
+  for (int i = threadIdx.x; i < T * KP * 16; i += 64 * kBcKsWaves) s_y[i] = 0.0f;
+  for (int u = ug; u < nRouted; u += 4) {
+    const ExpertRec rec = load_rec(a, u);
+    const bool ok = rec.slot >= 0 && rec.slot < a.L.w2.num_slots;
+    if (!ok) {  // non-resident expert: contributes zeros, flags the error
+      if (kp == 0 && lane == 0) {
+        s_cnt[u] = 0;
+        atomicOr(&a.ctrl[kCtrlError], 1);
+      }
+      continue;
+    }
+    const ProjSlot W = proj_slot(a.L.w2, rec.slot);
+    // the epilogue's operands, requested before the weights' wait in the body
+    uint32_t bb = 0u;
+    float wr = 0.0f;
+    int pr = -1;
+    if (kp == 0) {
+      if (W.bias != nullptr && lane < 16) bb = load_bits(W.bias, c0 + lane, W.bias_dt);
+      pr = lane == 0 ? rec.p[0] : lane == 1 ? rec.p[1] : lane == 2 ? rec.p[2] : rec.p[3];
+      if (lane < kXT && lane < rec.cnt) wr = a.wts[pr];
+    }
+    stage_b_ks_body<FMT, LPG, NLW, NOZ, true>(a, W, c0, rec.cnt, &rec, a.lists + (size_t)rec.e * T, 0, kp,
+                                              red + u * 4 * 16, 0, wv);
+    if (kp == 0) {
+      if (lane < 16) s_bias[u * 16 + lane] = bb;
+      if (lane < kXT) {
+        s_wr[u * kXT + lane] = wr;
+        s_pr[u * kXT + lane] = pr;
+      }
+      if (lane == 0) s_cnt[u] = rec.cnt;
+    }
+  }
+  __syncthreads();
+  // slot rows: the K quarters in order, + bias, x router weight (k_stage_b_ks's epilogue)
+  for (int i = threadIdx.x; i < nRouted * 16; i += 64 * kBcKsWaves) {
+    const int u = i >> 4, n = i & 15;
+    const int cnt = s_cnt[u];
+    if (cnt == 0) continue;
+    f32x4 v = red[(u * 4) * 16 + n];
+#pragma unroll
+    for (int j = 1; j < 4; ++j) v += red[(u * 4 + j) * 16 + n];
+    const float bnf = bits_to_f32(opaque_bits(s_bias[u * 16 + n]), a.L.w2.bias_dtype);
+#pragma unroll
+    for (int r = 0; r < kXT; ++r)
+      if (r < cnt) s_y[s_pr[u * kXT + r] * 16 + n] = (v[r] + bnf) * s_wr[u * kXT + r];
+  }
+  __syncthreads();
+  for (int i = threadIdx.x; i < T * 16; i += 64 * kBcKsWaves) {
+    const int t = i >> 4, n = i & 15;
+    float sum = s_y[(t * KP) * 16 + n];
+    for (int j = 1; j < KP; ++j) sum += s_y[(t * KP + j) * 16 + n];
+    ((uint16_t*)a.out)[(size_t)t * H + c0 + n] = f32_to_bf16(sum);
   }
 }
 
@@ -3743,6 +3835,53 @@ static XlPlan ks_plan_b(const ftm_moe_layer& L, int T) {
   }
 }
 
+// K-split stage B and the combine as one launch (k_stage_bc_ks): bf16
+// activations, stage B on k_stage_b_ks, no shared expert, up to kBcKsMaxT
+// tokens (one token block: kXT), at most kBcKsMaxU routed experts (min(E, T
+// k)) and kBcKsMaxKP slots a token, the 16 wave regions within the CU's LDS.
+constexpr int kBcKsMaxT = kXT;
+constexpr size_t kBcKsLdsMax = 160u * 1024u - 40u * 1024u;  // the CU's LDS less the kernel's static arrays
+template <int FMT>
+static size_t bcks_lds(const ftm_moe_layer& L) {
+  return (size_t)kBcKsWaves * (kKsNoz<FMT> ? kXT : kXR) * (size_t)xl_pitch(L.inter, 4) * 2u;
+}
+template <int FMT>
+static bool bcks_ok(const ftm_moe_layer& L, int T) {
+  if constexpr (FMT == FTM_FMT_GPTQ_INT4) {
+    return false;
+  } else {
+    if (L.act_dtype != FTM_DT_BF16 || L.shared_inter > 0 || T < 1 || T > kBcKsMaxT) return false;
+    const int maxU = L.num_experts < T * L.topk ? L.num_experts : T * L.topk;
+    if (maxU > kBcKsMaxU || L.topk > kBcKsMaxKP || bcks_lds<FMT>(L) > kBcKsLdsMax) return false;
+    if (FMT == FTM_FMT_FP8_BLOCK && lean_ok(L, T)) return false;
+    if constexpr (FMT == FTM_FMT_MXFP4) {
+      if (tok_ok(L, T)) return false;
+    }
+    return !xl_plan_b<FMT, FTM_DT_BF16>(L, T).ok && ks_plan_b<FMT, FTM_DT_BF16>(L, T).ok;
+  }
+}
+static bool bcks_fused(const ftm_moe_layer& L, int T) {
+  if (gemm_path_ok(L, T)) return false;
+  switch (L.w13.fmt) {
+    case FTM_FMT_BF16: return bcks_ok<FTM_FMT_BF16>(L, T);
+    case FTM_FMT_FP8_BLOCK: return bcks_ok<FTM_FMT_FP8_BLOCK>(L, T);
+    case FTM_FMT_INT8_PACKED: return bcks_ok<FTM_FMT_INT8_PACKED>(L, T);
+    case FTM_FMT_MXFP4: return bcks_ok<FTM_FMT_MXFP4>(L, T);
+    default: return false;
+  }
+}
+template <int FMT, int LPG, int NLW>
+static void launch_bcks(const LayerArgs& a, hipStream_t st) {
+  static bool attr = false;
+  if (!attr) {
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&k_stage_bc_ks<FMT, LPG, NLW>),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)kBcKsLdsMax);
+    attr = true;
+  }
+  hipLaunchKernelGGL((k_stage_bc_ks<FMT, LPG, NLW>), dim3(a.L.hidden / 16), dim3(64 * kBcKsWaves), bcks_lds<FMT>(a.L),
+                     st, a);
+}
+
 // which: bit 0 = stage A (w13 + act), bit 1 = stage B (w2), bit 2 = combine
 template <int FMT, int AT>
 static void launch_stages(const LayerArgs& a, int gridA, int gridB, hipStream_t st, int which, bool xq_ready) {
@@ -3834,6 +3973,8 @@ static void launch_stages(const LayerArgs& a, int gridA, int gridB, hipStream_t 
       }
     }
   }
+  bool bcks = false;  // stage B and the combine in one launch
+  if constexpr (AT == FTM_DT_BF16) bcks = bcks_ok<FMT>(a.L, a.T);
   if (which & 2) {
     const XlPlan pb = xl_plan_b<FMT, AT>(a.L, a.T);
     bool tok = false;
@@ -3878,7 +4019,9 @@ static void launch_stages(const LayerArgs& a, int gridA, int gridB, hipStream_t 
       const size_t lds = 4u * (sh || !kKsNoz<FMT> ? kXR : kXT) * (size_t)xl_pitch(a.Imax, 4) * 2u;
       const int gridk = (maxU + (sh ? 1 : 0)) * (a.L.hidden / 16);
 #define FTM_KSB(LPG, NLW)                                                                          \
-  if (sh)                                                                                          \
+  if (bcks)                                                                                        \
+    launch_bcks<FMT, LPG, NLW>(a, st);                                                             \
+  else if (sh)                                                                                     \
     hipLaunchKernelGGL((k_stage_b_ks<FMT, LPG, NLW, true>), dim3(gridk), dim3(kBlock), lds, st, a); \
   else                                                                                             \
     hipLaunchKernelGGL((k_stage_b_ks<FMT, LPG, NLW, false>), dim3(gridk), dim3(kBlock), lds, st, a)
@@ -3896,7 +4039,7 @@ static void launch_stages(const LayerArgs& a, int gridA, int gridB, hipStream_t 
       hipLaunchKernelGGL((k_stage_b<FMT, AT>), dim3(gridB), dim3(kBlock), 0, st, a);
     }
   }
-  if (which & 4) {
+  if ((which & 4) && !bcks) {
     const int n4 = a.T * (a.L.hidden / 4);
     hipLaunchKernelGGL((k_combine<AT>), dim3((n4 + kBlock - 1) / kBlock), dim3(kBlock), 0, st, a);
   }
@@ -4001,6 +4144,7 @@ static const char* expert_kernel_name(const ftm_moe_layer& L, int T, int stage) 
   if (FMT == FTM_FMT_GPTQ_INT4) return AT == FTM_DT_BF16 && gq_b_ok(L, T) ? "k_stage_b_gq" : "k_stage_b";
   if (AT == FTM_DT_BF16 && tok_ok(L, T)) return "k_stage_tok_b";
   if (xl_plan_b<FMT, AT>(L, T).ok) return "k_stage_b_xl";
+  if (AT == FTM_DT_BF16 && bcks_ok<FMT>(L, T)) return "k_stage_bc_ks";
   return ks_plan_b<FMT, AT>(L, T).ok ? "k_stage_b_ks" : "k_stage_b";
 }
 
@@ -4018,7 +4162,7 @@ const char* stage_kernel_name(const ftm_moe_layer& L, int T, int stage) {
     case FTM_STAGE_TOPK:
       if (route_a_ok(L, T) || route_topk_fused(L, T)) return "";  // routed inside stage A / the router
       return T <= kTopk1MaxT ? "k_topk1" : T >= kTopkBlkMinT ? "k_topk_blk" : "k_topk";
-    case FTM_STAGE_COMBINE: return bc_fused(L, T) ? "" : "k_combine";  // "": done by stage B
+    case FTM_STAGE_COMBINE: return bc_fused(L, T) || bcks_fused(L, T) ? "" : "k_combine";  // "": done by stage B
     case FTM_STAGE_W13:
     case FTM_STAGE_W2: break;
     default: return nullptr;

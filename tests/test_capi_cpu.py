@@ -247,7 +247,12 @@ def test_stage_kernel_names_follow_the_dispatch():
     mx.w2 = _proj(N=2880, K=2880, num_slots=8, fmt=nat.FMT_MXFP4, group=32)
     for T in (1, 8, 31):
         assert name(mx, T, nat.STAGE_W13) == "k_stage_a_xl", T
+    for T in (1, 2):  # up to 8 routed experts stage B and the combine run as one launch
+        assert name(mx, T, nat.STAGE_W2) == "k_stage_bc_ks", T
+        assert name(mx, T, nat.STAGE_COMBINE) == "", T
+    for T in (3, 5, 8, 31):
         assert name(mx, T, nat.STAGE_W2) == "k_stage_b_ks", T
+        assert name(mx, T, nat.STAGE_COMBINE) == "k_combine", T
     for T in (32, 64, 128):  # 4 to 16 tokens per expert: token rows resident in LDS, both stages
         assert name(mx, T, nat.STAGE_W13) == "k_stage_tok_a", T
         assert name(mx, T, nat.STAGE_W2) == "k_stage_tok_b", T

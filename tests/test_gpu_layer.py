@@ -713,3 +713,63 @@ def test_fused_backend_on_adversarial_lowp_logits(gpu):
                                                False)
     ref = _fused_ref(x, w1, w2, gating, K, True, "silu", False, torch.bfloat16)
     assert_close(got.float().cpu().numpy(), ref, ATOL, RTOL, what="fused bf16, adversarial routing")
+
+
+def _ks_layer(name, I, T, seed):
+    """A small layer whose w2 rows need the K-split stage B (too long for one
+    wave's window, short enough for a quarter of them): I = 2880 for MXFP4,
+    1024 for INT8 and FP8; no shared expert."""
+    from dataclasses import replace
+
+    cfg = replace(S.SMALL[name], E=12, H=256, I=I, k=4, shared_inter=0)
+    return S.generate(cfg, T=T, seed=seed)
+
+
+@pytest.mark.parametrize("name,I,T", [("c4_mxfp4", 2880, 1), ("c4_mxfp4", 2880, 2), ("c1_int8", 1024, 2),
+                                      ("c3_fp8", 1024, 1), ("c4_mxfp4", 2880, 3), ("c4_mxfp4", 2880, 5)])
+def test_k_split_stage_b_with_combine(gpu, name, I, T):
+    """Up to 8 routed experts (top-4: two tokens) the K-split stage B and the
+    combine run as one launch (k_stage_bc_ks: one workgroup per 16 columns
+    over every routed expert, the slot rows summed in LDS); above,
+    k_stage_b_ks and k_combine.  Both against the oracle, for MXFP4 (with the
+    gpt-oss biases), INT8 and FP8 rows."""
+    layer, _, _, _ = _run_and_check(_ks_layer(name, I, T, 90 + T), gpu)
+    fused = T <= 2
+    assert layer.stage_kernel(T, nat.STAGE_W2) == ("k_stage_bc_ks" if fused else "k_stage_b_ks")
+    assert layer.stage_kernel(T, nat.STAGE_COMBINE) == ("" if fused else "k_combine")
+
+
+@pytest.mark.parametrize("T", [1, 2])
+def test_k_split_stage_b_with_combine_skipped_and_missing(gpu, T):
+    """k_stage_bc_ks with caller routing: pairs with id -1 contribute nothing,
+    a routed expert without a slot contributes nothing and sets the error
+    bit, and a second call on the same workspace gives the same output."""
+    from ftmoe.layer import workspace
+
+    syn = _ks_layer("c4_mxfp4", 2880, T, 120 + T)
+    spec = oracle_spec(syn)
+    ref_full = O.layer_reference(spec, np_(syn.x))
+    ids = ref_full["ids"].astype(np.int32)
+    w = ref_full["w"].astype(np.float32)
+    missing = int(ids[0, 1])
+    ids_in = ids.copy()
+    ids_in[-1, -1] = -1  # one pair without an expert
+    w_ref = np.where((ids == missing) | (ids_in < 0), 0.0, w).astype(np.float32)
+    ref = O.layer_reference(spec, np_(syn.x), ids=ids, w=w_ref)
+    dsyn = syn.to(gpu)
+    slots = torch.arange(syn.cfg.E, dtype=torch.int32, device=gpu)
+    slots[missing] = -1
+    layer = S.build_layer(dsyn, slot_of_expert=slots)
+    ws = workspace(gpu, layer.workspace_bytes(T))
+    ws[:16].zero_()
+    ids_d, w_d = torch.from_numpy(ids_in).to(gpu), torch.from_numpy(w).to(gpu)
+    out = layer.forward_routed(dsyn.x, ids_d, w_d)
+    torch.cuda.synchronize()
+    err = int(ws[12:16].view(torch.int32).item())
+    ws[12:16].zero_()
+    assert err & 1, "error bit for a non-resident routed expert"
+    assert_close(to_f32(out), ref["out"], what="k_stage_bc_ks without the missing expert and the skipped pair")
+    again = layer.forward_routed(dsyn.x, ids_d, w_d)
+    torch.cuda.synchronize()
+    ws[12:16].zero_()
+    assert torch.equal(out, again)
