@@ -3857,7 +3857,12 @@ static bool bcks_ok(const ftm_moe_layer& L, int T) {
     if constexpr (FMT == FTM_FMT_MXFP4) {
       if (tok_ok(L, T)) return false;
     }
-    return !xl_plan_b<FMT, FTM_DT_BF16>(L, T).ok && ks_plan_b<FMT, FTM_DT_BF16>(L, T).ok;
+    if (!ks_plan_b<FMT, FTM_DT_BF16>(L, T).ok) return false;
+    // Where a w2 row fits one wave's window (k_stage_b_xl, H / 64 workgroups
+    // per expert) only up to 2 routed experts: measured on MI355X (C1, H =
+    // 1024, us per layer) T=1 (2 experts) 18.3 -> 17.4, T=2 (4) 18.5 -> 19.4,
+    // T=4 (8) 19.9 -> 23.0.
+    return maxU <= 2 || !xl_plan_b<FMT, FTM_DT_BF16>(L, T).ok;
   }
 }
 static bool bcks_fused(const ftm_moe_layer& L, int T) {
@@ -4004,7 +4009,7 @@ static void launch_stages(const LayerArgs& a, int gridA, int gridB, hipStream_t 
       } else {
         hipLaunchKernelGGL((k_stage_b<FMT, AT>), dim3(gridB), dim3(kBlock), 0, st, a);
       }
-    } else if (pb.ok) {
+    } else if (pb.ok && !bcks) {
       const size_t lds = 4u * kXR * (size_t)xl_pitch(a.Imax, 1) * 2u;
       const int nt = pb.nt;
       const int maxU = a.L.num_experts < a.T * a.L.topk ? a.L.num_experts : a.T * a.L.topk;
@@ -4143,8 +4148,8 @@ static const char* expert_kernel_name(const ftm_moe_layer& L, int T, int stage) 
   if (lean) return L.topk + (L.shared_inter > 0 ? 1 : 0) <= kBcMaxKP && T <= kBcMaxT ? "k_stage_bc_lean" : "k_stage_b_lean";
   if (FMT == FTM_FMT_GPTQ_INT4) return AT == FTM_DT_BF16 && gq_b_ok(L, T) ? "k_stage_b_gq" : "k_stage_b";
   if (AT == FTM_DT_BF16 && tok_ok(L, T)) return "k_stage_tok_b";
-  if (xl_plan_b<FMT, AT>(L, T).ok) return "k_stage_b_xl";
   if (AT == FTM_DT_BF16 && bcks_ok<FMT>(L, T)) return "k_stage_bc_ks";
+  if (xl_plan_b<FMT, AT>(L, T).ok) return "k_stage_b_xl";
   return ks_plan_b<FMT, AT>(L, T).ok ? "k_stage_b_ks" : "k_stage_b";
 }
 

@@ -214,6 +214,8 @@ def test_stage_kernel_names_follow_the_dispatch():
     assert name(c1, 4, nat.STAGE_ROUTER) == "k_router"
     assert name(c1, 4, nat.STAGE_TOPK) == ""
     assert name(small, 4, nat.STAGE_W2) == "k_stage_b_xl"
+    assert name(small, 1, nat.STAGE_W2) == "k_stage_bc_ks"  # two routed experts: stage B with the combine
+    assert name(small, 1, nat.STAGE_COMBINE) == ""
     assert name(small, 5, nat.STAGE_W13) == "k_stage_a_rows"
     assert name(small, 5, nat.STAGE_W2) == "k_stage_b_ks"  # K split over the waves up to 32 tokens
     assert name(small, 33, nat.STAGE_W2) == "k_stage_b"

@@ -773,3 +773,14 @@ def test_k_split_stage_b_with_combine_skipped_and_missing(gpu, T):
     torch.cuda.synchronize()
     ws[12:16].zero_()
     assert torch.equal(out, again)
+
+
+@pytest.mark.parametrize("name", ["c1_int8", "c4_mxfp4"])
+def test_two_routed_experts_stage_b_with_combine(gpu, name):
+    """One token on two experts of a layer whose w2 rows fit one wave's
+    window: k_stage_bc_ks replaces k_stage_b_xl + k_combine (INT8 and MXFP4
+    rows), against the oracle."""
+    layer, _, _, _ = _run_and_check(S.generate(S.SMALL[name], T=1, seed=140), gpu)
+    assert layer.stage_kernel(1, nat.STAGE_W2) == "k_stage_bc_ks"
+    assert layer.stage_kernel(1, nat.STAGE_COMBINE) == ""
+    assert layer.stage_kernel(2, nat.STAGE_W2) == "k_stage_b_xl"
