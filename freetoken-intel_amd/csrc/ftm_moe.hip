@@ -3385,6 +3385,7 @@ constexpr int kBcMaxKP = 65;  // top-k <= 64, + the shared expert
 template <int KB, int NWS>
 __global__ __launch_bounds__(64 * kBcWaves) void k_stage_bc_lean(const LayerArgs a) {
   __shared__ float s_y[kBcMaxT * kBcMaxKP * 16];
+  __shared__ int s_next;  // the next unit a wave takes
   const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int H = a.L.hidden, T = a.T, KP = a.KP;
   const int col0 = blockIdx.x * kBcCols;
@@ -3402,6 +3403,7 @@ __global__ __launch_bounds__(64 * kBcWaves) void k_stage_bc_lean(const LayerArgs
   const int nRouted = sload_i32(a.ctrl, kCtrlNRouted);
   // slots of pairs without an expert stay zero (as their slot-buffer rows would be)
   for (int i = threadIdx.x; i < T * KP * 16; i += 64 * kBcWaves) s_y[i] = 0.0f;
+  if (threadIdx.x == 0) s_next = kBcWaves;
   __syncthreads();
   const int nU = nSh + nRouted;
   const Rsrc rres = make_rsrc(a.recs, (uint32_t)nRouted * (uint32_t)(4 * kRecWords));
@@ -3409,14 +3411,21 @@ __global__ __launch_bounds__(64 * kBcWaves) void k_stage_bc_lean(const LayerArgs
     const int u = uu - nSh;
     return bload4(rres, uu < nU && u >= 0 && rl < kRecWords ? (uint32_t)(u * kRecWords + rl) * 4u : kOOB);
   };
-  for (int uu = wv; uu < nU; uu += kBcWaves) {
+  // units handed out on demand: wave w starts with unit w, then takes the next
+  // free one (an LDS counter), so waves whose units ran short take more (C3
+  // stage B + combine, us: T=16 23.0 -> 22.7, T=8 14.1 -> 13.8, T=4 9.4 -> 9.3)
+  int nx = 0;
+  for (int uu = wv; uu < nU; uu = nx) {
     ExpertRec rec;
     rec.e = __builtin_amdgcn_readlane((int)nrec, 0);
     rec.cnt = __builtin_amdgcn_readlane((int)nrec, 1);
     rec.slot = __builtin_amdgcn_readlane((int)nrec, 2);
 #pragma unroll
     for (int i = 0; i < kRecPairs; ++i) rec.p[i] = __builtin_amdgcn_readlane((int)nrec, 3 + i);
-    nrec = rec_load(uu + kBcWaves);
+    int t = 0;
+    if (rl == 0) t = atomicAdd(&s_next, 1);
+    nx = __builtin_amdgcn_readfirstlane(t);
+    nrec = rec_load(nx);
     if (uu >= nSh) {
       if (rec.slot < 0 || rec.slot >= a.L.w2.num_slots) {  // non-resident: contributes zeros
         if ((threadIdx.x & 63) == 0) atomicOr(&a.ctrl[kCtrlError], 1);
