@@ -41,7 +41,9 @@ constexpr int kRecMaxT = 256;
 // chain of dependent launches.  Every stage-A workgroup then spends ~3 us
 // routing before its weight loads, which pays while the grid fits one round
 // of workgroups: measured on MI355X (C3), T = 1: 27.0 us per layer against
-// 29.6 with the top-k launch; T = 4: 47.8 against 42.7 (2,112 workgroups).
+// 29.6 with the top-k launch; T = 4: 47.8 against 42.7 (2,112 workgroups);
+// measured again beside k_route_topk1 (us per layer): T = 3 30.5 against
+// 29.5, T = 4 34.6 against 32.5.
 // A record holds every pair of such an expert.
 constexpr int kLeanRouteMaxT = 2;
 constexpr int kLeanRouteMaxK = 16;
