@@ -2366,9 +2366,9 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(kXlWaves
   }
 }
 
-// ---- K-split stage B and the combine in one launch for up to kXT tokens (no
-// shared expert): one workgroup of kBcKsWaves waves per 16 output columns
-// takes every routed expert.  Wave w streams K quarter w % 4 of the experts
+// ---- K-split stage B and the combine in one launch for up to kBcKsMaxU
+// routed experts and kXT tokens (no shared expert; bcks_ok): one workgroup of
+// kBcKsWaves waves per 16 output columns takes every routed expert.  Wave w streams K quarter w % 4 of the experts
 // w / 4, w / 4 + 4, ... (stage_b_ks_body, PART); the quarters are summed in
 // order with the bias and the router weight as k_stage_b_ks does, into the
 // pair's slot row in LDS, and the workgroup sums each token's slots in slot
